@@ -1,0 +1,260 @@
+"""Benchmark of the paged KV-cache decode step on one MI355X.
+
+Workload (the headline configuration): paged decode append + full block-table
+gather, bf16 MLA-style latent rows of 512 + 64 dims (1152 B per token), one
+layer, batch 64, context lengths uniform in [1024, 32768], block size 64,
+physical pages a random permutation of a 200k-page pool (14.7 GB), one new
+token per sequence per step, values N(0,1).  Each step = reserve (page
+allocation) + fused append+gather of every sequence into a packed buffer.
+
+Prints one JSON line (see the keys below).  Progress goes to stderr.
+
+Algorithmic bytes per step (read + write of every gathered row, the appended
+row read + written, one int32 block-table entry per page):
+    2 * sum(L) * 1152 + B * 2 * 1152 + sum(ceil(L / 64)) * 4
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+for _p in (ROOT / "saint-llm_amd", ROOT):
+    if str(_p) not in sys.path:
+        sys.path.insert(0, str(_p))
+
+import numpy as np  # noqa: E402
+import torch  # noqa: E402
+
+HBM_PEAK_GBS = 8000.0  # MI355X HBM3E peak, 8 TB/s
+ROW = 576  # 512 latent + 64 rope, bf16
+ROW_BYTES = ROW * 2
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def alg_bytes_append_gather(lens: np.ndarray, bs: int) -> int:
+    L = lens.astype(np.int64)
+    return int(2 * L.sum() * ROW_BYTES + len(L) * 2 * ROW_BYTES + (-(-L // bs)).sum() * 4)
+
+
+def copy_bandwidth(dev: torch.device, nbytes: int = 2 << 30, iters: int = 20) -> float:
+    """Read+write GB/s of torch's device copy over nbytes (the plain-copy yardstick)."""
+    a = torch.empty(nbytes // 2, dtype=torch.bfloat16, device=dev).normal_()
+    b = torch.empty_like(a)
+    for _ in range(3):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(iters):
+        b.copy_(a)
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / iters
+    del a, b
+    return 2 * nbytes / (ms * 1e-3) / 1e9
+
+
+class PagedDecode:
+    """Device state of the paged-append+gather workload."""
+
+    def __init__(self, dev: torch.device, batch: int, lmin: int, lmax: int, bs: int,
+                 n_pages: int, steps_total: int, seed: int = 0) -> None:
+        from saint_kv import ops
+
+        self.ops = ops
+        rng = np.random.default_rng(seed)
+        self.bs = bs
+        self.batch = batch
+        self.lens0 = rng.integers(lmin, lmax + 1, size=batch).astype(np.int32)
+        max_pages = int(-(-(int(self.lens0.max()) + steps_total) // bs))
+        order = rng.permutation(n_pages).astype(np.int32)
+        self.stack = torch.empty(n_pages, dtype=torch.int32, device=dev)
+        self.top = torch.empty(1, dtype=torch.int32, device=dev)
+        ops.free_stack_init(self.stack, self.top, torch.as_tensor(order, device=dev))
+        self.bt = torch.full((batch, max_pages), -1, dtype=torch.int32, device=dev)
+        self.lens = torch.zeros(batch, dtype=torch.int32, device=dev)
+        self.status = torch.zeros(1, dtype=torch.int32, device=dev)
+        gen = torch.Generator(device=dev).manual_seed(seed)
+        self.pool = torch.empty(n_pages, bs, ROW, dtype=torch.bfloat16, device=dev)
+        for chunk in self.pool.split(8192):
+            chunk.normal_(generator=gen)
+        # prefill: map pages for the initial contexts (content is the N(0,1) pool)
+        ops.reserve(self.stack, self.top, self.bt, self.lens,
+                    torch.as_tensor(self.lens0, device=dev), bs, self.status)
+        cap = self.lens0.astype(np.int64) + steps_total
+        self.offsets = torch.as_tensor(np.concatenate([[0], np.cumsum(cap)[:-1]]), device=dev)
+        self.out = torch.empty(int(cap.sum()), ROW, dtype=torch.bfloat16, device=dev)
+        self.tokens = torch.empty(steps_total, batch, 1, ROW, dtype=torch.bfloat16, device=dev)
+        self.tokens.normal_(generator=gen)
+        self.step_idx = 0
+        torch.cuda.synchronize()
+        if int(self.status.item()) != 0:
+            raise RuntimeError(f"prefill reserve refused: status {int(self.status.item())}")
+
+    def host_lens(self) -> np.ndarray:
+        return self.lens0 + self.step_idx
+
+    def step(self, ev: tuple | None = None) -> None:
+        self.ops.reserve(self.stack, self.top, self.bt, self.lens, 1, self.bs, self.status)
+        if ev is not None:
+            ev[0].record()
+        self.ops.append_gather(self.pool, self.bt, self.lens, self.tokens[self.step_idx], 1,
+                               self.out, self.offsets)
+        if ev is not None:
+            ev[1].record()
+        self.step_idx += 1
+
+
+def cpu_baseline(seconds: float = 10.0, seed: int = 0) -> dict:
+    """The oracle's paged append+gather on host cores, on a bounded sample."""
+    from oracle import reference_cpu as ref
+
+    rng = np.random.default_rng(seed)
+    threads = torch.get_num_threads()
+    bs, n_seq = 64, 8
+    lens = rng.integers(1024, 32769, size=n_seq).astype(np.int32)
+    pages_needed = int((-(-(lens.astype(np.int64) + 64) // bs)).sum())
+    n_pages = pages_needed + 16
+    stack, top = ref.free_stack_init(n_pages, rng.permutation(n_pages).astype(np.int32))
+    bt = np.full((n_seq, int(-(-(int(lens.max()) + 64) // bs))), -1, dtype=np.int32)
+    cur = np.zeros(n_seq, dtype=np.int32)
+    _, top = ref.reserve(stack, top, bt, cur, lens, bs)
+    pool = torch.randn(n_pages, bs, ROW).to(torch.bfloat16)
+    out = torch.empty(n_seq, int(lens.max()) + 64, ROW, dtype=torch.bfloat16)
+    tok = torch.randn(n_seq, 1, ROW).to(torch.bfloat16)
+    done_bytes, t0, steps = 0, time.perf_counter(), 0
+    while time.perf_counter() - t0 < seconds and steps < 10000:
+        _, top = ref.reserve(stack, top, bt, cur, 1, bs)
+        ref.paged_append(pool, bt, cur, tok, 1)
+        ref.paged_gather(pool, bt, cur, out)
+        done_bytes += alg_bytes_append_gather(cur, bs)
+        steps += 1
+    dt = time.perf_counter() - t0
+    return {
+        "value": round(done_bytes / dt / 1e9, 3),
+        "unit": "GB/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"{steps} decode steps of 8 sequences (L~U[1k,32k], sum L={int(lens.sum())}) "
+                  f"of the same append+gather, torch-eager CPU oracle, {dt:.1f} s",
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); the cache shards by "
+              "sequence with no per-step exchange, so N GPUs run N independent copies.",
+              file=sys.stderr)
+        return 2
+    if not torch.cuda.is_available():
+        print("bench.py needs a ROCm GPU", file=sys.stderr)
+        return 2
+    dev = torch.device("cuda:0")
+    from saint_kv import _lib
+
+    _lib.load()
+    log(f"device {torch.cuda.get_device_name(dev)}")
+    copy_gbs = copy_bandwidth(dev)
+    log(f"torch copy_ yardstick {copy_gbs:.0f} GB/s")
+
+    batch, bs, n_pages = 64, 64, 200_000
+    total_steps = args.warmup + args.steps
+    w = PagedDecode(dev, batch, 1024, 32768, bs, n_pages, total_steps)
+    log(f"prefilled {batch} sequences, sum L = {int(w.lens0.sum())}")
+    for _ in range(args.warmup):
+        w.step()
+    torch.cuda.synchronize()
+
+    stream = torch.cuda.current_stream(dev)
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in range(args.steps)]
+    t_start, t_end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    alg_total = 0
+    lens_steps = []
+    for i in range(args.steps):
+        lens_steps.append(w.host_lens() + i + 1)
+    torch.cuda.synchronize()
+    t_start.record(stream)
+    for i in range(args.steps):
+        w.step(evs[i])
+    t_end.record(stream)
+    torch.cuda.synchronize()
+    total_ms = t_start.elapsed_time(t_end)
+    kern_ms = np.array([a.elapsed_time(b) for a, b in evs])
+    for L in lens_steps:
+        alg_total += alg_bytes_append_gather(L, bs)
+    ms_per_step = total_ms / args.steps
+    value = alg_total / (total_ms * 1e-3) / 1e9
+    alg_per_launch = alg_total / args.steps
+    kern_avg_ms = float(kern_ms.mean())
+    achieved = alg_per_launch / (kern_avg_ms * 1e-3) / 1e9
+    tokens_per_step = float(np.mean([L.sum() for L in lens_steps]))
+    log(f"step {ms_per_step * 1e3:.1f} us, kernel {kern_avg_ms * 1e3:.1f} us, "
+        f"{value:.0f} GB/s, kernel {achieved:.0f} GB/s")
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        log("timing the CPU oracle baseline")
+        cpu = cpu_baseline(args.cpu_seconds)
+        log(f"cpu baseline {cpu['value']} GB/s on {cpu['cores']} threads")
+
+    rec = {
+        "metric": "KV append+gather GB/s (% of HBM peak) and decode-step KV tokens/s at 64k ctx",
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic N(0,1) KV rows, seeded; random-permutation page pool",
+        "config": {
+            "workload": "paged decode append + full block-table gather (B=64, L~U[1k,32k], "
+                        "latent 512+64 bf16, bs=64, 200k-page pool, 1 token/seq/step)",
+            "batch": batch,
+            "block_size": bs,
+            "row_bytes": ROW_BYTES,
+            "pool_pages": n_pages,
+            "parallelism": "single GPU",
+        },
+        "pct_hbm_peak": round(100 * value / HBM_PEAK_GBS, 2),
+        "kv_tokens_per_s": round(tokens_per_step / (ms_per_step * 1e-3), 1),
+        "copy_yardstick_gbs": round(copy_gbs, 1),
+        "roofline": {
+            "bound": "hbm",
+            "kernel": "k_paged_copy<2> (skv_append_gather)",
+            "achieved": round(achieved, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": None,
+            "alg_bytes_per_launch": int(alg_per_launch),
+            "avg_launch_us": round(kern_avg_ms * 1e3, 2),
+        },
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(rec), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

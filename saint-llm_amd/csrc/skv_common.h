@@ -1,0 +1,158 @@
+// Shared device/host helpers for the saint-kv HIP kernels (gfx950, wave64).
+//
+// Everything here is written for CDNA4 directly: 64-lane wavefronts, 16-byte
+// vector memory operations, LDS-backed block scans.  No CUDA shims, no
+// alternative back ends.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "saintkv.h"
+
+namespace skv {
+
+constexpr int kWave = 64;
+
+// 16-byte vector used for every bulk copy: one global_load_dwordx4 /
+// global_store_dwordx4 per lane.
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+// ---------------------------------------------------------------------------
+// Error reporting for the C ABI.  A thread-local message plus a negative
+// status code; the Python layer maps codes onto ValueError / RuntimeError.
+// ---------------------------------------------------------------------------
+int set_error(int code, const char* fmt, ...);
+int check_launch(const char* what);
+
+// ---------------------------------------------------------------------------
+// Streaming loads/stores.  Page copies touch every byte exactly once, so they
+// use non-temporal hints to keep L2/MALL for the block tables and scores.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ u32x4 ld_stream(const u32x4* p) {
+  return __builtin_nontemporal_load(p);
+}
+__device__ __forceinline__ void st_stream(u32x4* p, u32x4 v) {
+  __builtin_nontemporal_store(v, p);
+}
+
+// ---------------------------------------------------------------------------
+// bf16 <-> fp32.  Round-to-nearest-even with quiet-NaN canonicalisation,
+// the rounding torch applies in Tensor.to(torch.bfloat16).
+// ---------------------------------------------------------------------------
+__host__ __device__ __forceinline__ float bf16_to_f32(uint16_t h) {
+  uint32_t u = static_cast<uint32_t>(h) << 16;
+  float f;
+  __builtin_memcpy(&f, &u, 4);
+  return f;
+}
+
+__host__ __device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+  uint32_t u;
+  __builtin_memcpy(&u, &f, 4);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x0040u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return static_cast<uint16_t>(u >> 16);
+}
+
+// ---------------------------------------------------------------------------
+// OCP FP8 E4M3FN (bias 7, no infinities, S.1111.111 = NaN, max 448).
+//
+// encode: round-to-nearest-even of a finite fp32 whose magnitude is already
+// clamped to <= 448 (the quantiser clamps first).  Written from the format
+// definition: subnormal range by exact power-of-two scaling + RNE to an
+// integer; normal range by RNE on the fp32 mantissa (drop 20 bits) and an
+// exponent rebias.  NaN maps to the E4M3FN NaN code.
+// ---------------------------------------------------------------------------
+__host__ __device__ __forceinline__ uint8_t f32_to_e4m3fn(float x) {
+  uint32_t u;
+  __builtin_memcpy(&u, &x, 4);
+  const uint32_t sign = (u >> 24) & 0x80u;
+  const uint32_t a = u & 0x7fffffffu;
+  if (a > 0x7f800000u) return static_cast<uint8_t>(sign | 0x7fu);  // NaN
+  if (a >= 0x43e00000u) return static_cast<uint8_t>(sign | 0x7eu);  // >= 448 saturates
+  if (a < 0x3c800000u) {
+    // |x| < 2^-6: subnormal target.  a * 2^9 is exact in fp32; rint is RNE.
+    float af;
+    __builtin_memcpy(&af, &a, 4);
+    const float q = __builtin_rintf(af * 512.0f);  // 0..8, 8 == min normal
+    return static_cast<uint8_t>(sign | static_cast<uint32_t>(q));
+  }
+  // normal: keep 3 mantissa bits, RNE on the 20 dropped bits.
+  const uint32_t r = a + 0x7ffffu + ((a >> 20) & 1u);
+  const uint32_t e = (r >> 23) - 127u + 7u;
+  const uint32_t m = (r >> 20) & 7u;
+  return static_cast<uint8_t>(sign | (e << 3) | m);
+}
+
+__host__ __device__ __forceinline__ float e4m3fn_to_f32(uint8_t c) {
+  const uint32_t sign = (static_cast<uint32_t>(c) & 0x80u) << 24;
+  const uint32_t e = (c >> 3) & 0xfu;
+  const uint32_t m = c & 7u;
+  uint32_t u;
+  if (e == 0) {
+    float f = static_cast<float>(m) * (1.0f / 512.0f);  // exact
+    __builtin_memcpy(&u, &f, 4);
+    u |= sign;
+  } else if (e == 15 && m == 7) {
+    u = sign | 0x7fc00000u;
+  } else {
+    u = sign | ((e - 7u + 127u) << 23) | (m << 20);
+  }
+  float f;
+  __builtin_memcpy(&f, &u, 4);
+  return f;
+}
+
+constexpr float kE4M3Max = 448.0f;
+constexpr float kF32Tiny = 1.17549435082228750797e-38f;  // FLT_MIN
+
+// ---------------------------------------------------------------------------
+// Block-wide exclusive scan over int32 (blockDim.x a multiple of 64, <=1024).
+// Wave-level inclusive scan through __shfl_up, wave totals through LDS.
+// Returns the exclusive prefix; *total receives the block sum.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ int wave_inclusive_scan(int v) {
+  const int lane = threadIdx.x & (kWave - 1);
+#pragma unroll
+  for (int d = 1; d < kWave; d <<= 1) {
+    const int t = __shfl_up(v, d, kWave);
+    if (lane >= d) v += t;
+  }
+  return v;
+}
+
+__device__ __forceinline__ int block_exclusive_scan(int v, int* lds16, int* total) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wid = threadIdx.x / kWave;
+  const int nw = blockDim.x / kWave;
+  const int inc = wave_inclusive_scan(v);
+  if (lane == kWave - 1) lds16[wid] = inc;
+  __syncthreads();
+  if (wid == 0) {
+    int w = (lane < nw) ? lds16[lane] : 0;
+    const int winc = wave_inclusive_scan(w);
+    if (lane < nw) lds16[lane] = winc - w;  // exclusive wave offsets
+    if (lane == nw - 1) lds16[16] = winc;
+  }
+  __syncthreads();
+  const int res = lds16[wid] + inc - v;
+  *total = lds16[16];
+  __syncthreads();
+  return res;
+}
+
+__device__ __forceinline__ int block_reduce_sum(int v, int* lds16) {
+  int total;
+  (void)block_exclusive_scan(v, lds16, &total);
+  return total;
+}
+
+__host__ __device__ __forceinline__ int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+// Grid size for persistent grid-stride kernels: enough workgroups to cover
+// all 256 CUs several times over.
+constexpr int kPersistentBlocks = 2048;
+
+}  // namespace skv

@@ -1,0 +1,84 @@
+"""The C-ABI library loads on a CPU-only host and exports what the header declares.
+
+No compute call is made here (no GPU needed).
+"""
+
+from __future__ import annotations
+
+import re
+import subprocess
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADERS = sorted((ROOT / "include").glob("*.h"))
+
+
+def _declared() -> set[str]:
+    names: set[str] = set()
+    for h in HEADERS:
+        text = re.sub(r"/\*.*?\*/", "", h.read_text(), flags=re.S)
+        names.update(re.findall(r"^\s*(?:const\s+)?\w+\**\s+\**(skv_\w+)\s*\(", text, flags=re.M))
+    return names
+
+
+def test_header_declares_entry_points() -> None:
+    names = _declared()
+    assert "skv_abi_version" in names and "skv_last_error" in names
+    assert len(names) >= 7
+
+
+def test_library_exports_every_declared_symbol() -> None:
+    from saint_kv import _lib
+
+    lib = _lib.load()
+    for name in _declared():
+        assert hasattr(lib, name), f"{name} declared in include/ but not exported"
+    out = subprocess.run(["nm", "-D", "--defined-only", str(_lib.LIB_PATH)],
+                         capture_output=True, text=True, check=True).stdout
+    exported = set(re.findall(r"\bT (skv_\w+)", out))
+    assert _declared() <= exported
+    # every exported skv_ symbol is declared in a header (no hidden ABI)
+    assert exported <= _declared()
+
+
+def test_python_signatures_cover_the_header() -> None:
+    from saint_kv import _lib
+
+    assert set(_lib.SIGNATURES) | {"skv_last_error"} == _declared()
+
+
+def test_abi_version_and_error_text() -> None:
+    from saint_kv import _lib
+
+    lib = _lib.load()
+    assert lib.skv_abi_version() == 1
+    # an argument error is reported without touching the GPU
+    rc = lib.skv_free_stack_init(None, None, None, 0, None)
+    assert rc == _lib.SKV_EINVAL
+    assert "n_pages" in _lib.last_error()
+    with pytest.raises(ValueError, match="n_pages"):
+        _lib.check(rc, "skv_free_stack_init")
+
+
+def test_argument_errors_map_to_value_error() -> None:
+    from saint_kv import _lib
+
+    lib = _lib.load()
+    rc = lib.skv_paged_gather(None, None, 0, 0, None, 24, 16, 1, None, 1, None, 1, None)
+    assert rc == _lib.SKV_EINVAL and "row_bytes" in _lib.last_error()
+    rc = lib.skv_reserve(None, None, 8, None, 4, 8, None, None, 1, 1, 16, None, None)
+    assert rc == _lib.SKV_EINVAL and "max_pages" in _lib.last_error()
+
+
+def test_single_hip_runtime_mapped() -> None:
+    """The library binds to the HIP runtime torch already mapped (one libamdhip64)."""
+    import torch  # noqa: F401
+
+    from saint_kv import _lib
+
+    _lib.load()
+    maps = Path("/proc/self/maps").read_text()
+    libs = {ln.split()[-1] for ln in maps.splitlines() if "libamdhip64" in ln}
+    assert len(libs) == 1, libs
