@@ -146,7 +146,7 @@ def _dst_args(out: torch.Tensor, rb: int, batch: int,
         return row_offsets.data_ptr(), 0, cap
     if out.dim() < 3 or out.shape[0] != batch:
         raise ValueError(f"out must be [batch={batch}, rows, *row]; got {tuple(out.shape)}")
-    if math.prod(out.shape[2:]) * es != rb or not out[0].is_contiguous():
+    if math.prod(out.shape[2:]) * es != rb or (batch and not out[0].is_contiguous()):
         raise ValueError("out rows must be dense and match the pool row size")
     seq_stride_bytes = out.stride(0) * es
     if seq_stride_bytes % rb:
