@@ -44,6 +44,14 @@ extern "C" {
 #define SKV_EHIP (-4)       /* HIP runtime error (launch / memcpy)          */
 #define SKV_ESTATE (-5)     /* illegal state transition (double free, sink) */
 
+/* Entry formats of compressed caches. */
+#define SKV_FMT_BF16 0 /* entry = channels bf16 values (2*channels bytes) */
+#define SKV_FMT_FP8 1  /* entry = e4m3fn codes of the main dims, one fp32 scale
+                        * per 128 main dims, then SKV_FP8_ROPE_DIMS bf16 dims */
+#define SKV_FP8_ROPE_DIMS 64
+#define SKV_FP8_ENTRY_BYTES(channels) \
+  (((channels) - SKV_FP8_ROPE_DIMS) + ((channels) - SKV_FP8_ROPE_DIMS) / 128 * 4 + 2 * SKV_FP8_ROPE_DIMS)
+
 /* Device-side status words written by kernels that can refuse work
  * (bit flags, 0 = success). */
 #define SKV_STATUS_MAX_PAGES 1 /* a sequence would exceed bt_stride pages   */
@@ -107,6 +115,117 @@ int skv_append_gather(void* dst, const int64_t* dst_row_offsets, int64_t dst_seq
                       int64_t bt_stride, const int32_t* seq_lens, const int32_t* n_new,
                       int32_t n_new_uniform, const void* src, int64_t src_seq_stride,
                       int64_t src_row_stride, int64_t src_len, int64_t batch, void* stream);
+
+/* ---- SWA ring -------------------------------------------------------------
+ * ring: [batch, window, row_bytes]; token at position p of sequence b lives
+ * in slot p % window.  skv_ring_append writes the n_new[b] newest tokens
+ * (positions [seq_lens[b]-n_new[b], seq_lens[b]); seq_lens already include
+ * them); when n_new > window only the last window tokens are written.
+ * skv_ring_read copies the last min(window, seq_lens[b]) tokens in position
+ * order to dst row b*dst_seq_stride_rows + r.  Replaces the window mask over
+ * the full history (swa.py:115-125, csa.py:352-360). */
+int skv_ring_append(void* ring, int64_t window, int64_t row_bytes, const int32_t* seq_lens,
+                    const int32_t* n_new, int32_t n_new_uniform, const void* src,
+                    int64_t src_seq_stride, int64_t src_row_stride, int64_t src_len,
+                    int64_t batch, void* stream);
+int skv_ring_read(void* dst, int64_t dst_seq_stride_rows, int64_t dst_capacity_rows,
+                  const void* ring, int64_t window, int64_t row_bytes, const int32_t* seq_lens,
+                  int64_t batch, void* stream);
+
+/* ---- compression ----------------------------------------------------------
+ * Append n_new tokens' compressor projections (c, z: bf16 [batch, T, channels]
+ * with byte strides in_seq_stride / in_row_stride, T = in_len) of sequences
+ * whose token counts are now seq_lens.  Every block of m tokens completed by
+ * this call is pooled, out[j] = sum_i softmax_i(z[i,j] + bias[i,j]) * c[i,j]
+ * (bias fp32 [m, channels]; fp32 math, rounded to bf16), and written as entry
+ * floor(p/m) of the paged compressed cache (format SKV_FMT_BF16 or
+ * SKV_FMT_FP8, quantized on write).  Tokens of the incomplete block are
+ * staged in tail_c / tail_z (bf16 [batch, m, channels], slot = p % m).
+ * Pages for the new entries must be reserved beforehand.
+ * Replaces TokenLevelCompressor pooling (csa.py:79-87) and the block-emission
+ * state machine of HCAKVCacheLayer/CSAKVCacheLayer.append
+ * (kv_cache.py:170-195, 291-315). */
+int skv_compress_append(void* pool, int64_t entry_bytes, int64_t block_size, int64_t n_pages,
+                        const int32_t* block_table, int64_t bt_stride, void* tail_c, void* tail_z,
+                        const void* c_new, const void* z_new, int64_t in_seq_stride,
+                        int64_t in_row_stride, int64_t in_len, const float* bias,
+                        const int32_t* seq_lens, const int32_t* n_new, int32_t n_new_uniform,
+                        int64_t m, int64_t channels, int32_t format, int64_t batch, void* stream);
+
+/* ---- FP8 quantize-on-write --------------------------------------------------
+ * skv_paged_append for SKV_FMT_FP8 entries: bf16 source rows of `channels`
+ * dims are quantized per 1x128 block on the way into the pool
+ * (cast_to_fp8, quant/reference.py:75-111; rope dims kept bf16). */
+int skv_fp8_quant_append(void* pool, int64_t entry_bytes, int64_t block_size, int64_t n_pages,
+                         const int32_t* block_table, int64_t bt_stride, const int32_t* seq_lens,
+                         const int32_t* n_new, int32_t n_new_uniform, const void* src,
+                         int64_t src_seq_stride, int64_t src_row_stride, int64_t src_len,
+                         int64_t channels, int64_t batch, void* stream);
+
+/* Host-side access to the e4m3fn codec the kernels use (CPU, no GPU), for
+ * exhaustive codec checks.  No reference counterpart. */
+int skv_fp8_encode_host(const float* x, uint8_t* codes, int64_t n);
+int skv_fp8_decode_host(const uint8_t* codes, float* x, int64_t n);
+
+/* ---- top-k selection --------------------------------------------------------
+ * Row r of fp32 scores (row stride score_stride elements) has n_cols[r]
+ * columns (n_cols == NULL: n_cols_uniform) of which the first n_valid[r] are
+ * causally valid.  Writes k indices per row (row stride out_stride): the
+ * min(k, n_cols, n_valid) best valid columns ordered by score descending,
+ * ties by ascending index; a pick whose score is not finite is -1, and ranks
+ * past that count are -1.  Replaces the mask + topk + isfinite of
+ * CSA._indexer_topk_cached (csa.py:411-422).  k <= 2048. */
+int skv_topk_select(const float* scores, int64_t score_stride, int64_t rows,
+                    const int32_t* n_valid, const int32_t* n_cols, int32_t n_cols_uniform,
+                    int64_t k, int32_t* out_idx, int64_t out_stride, void* stream);
+
+/* Decode form: row b is the query at position seq_lens[b]-1 of sequence b,
+ * n_cols = seq_lens[b] / m and n_valid = (seq_lens[b]-1) / m (a block s is
+ * visible iff s*m + m - 1 < q_pos; kernels/attention.py:53-57). */
+int skv_topk_select_decode(const float* scores, int64_t score_stride, int64_t batch,
+                           const int32_t* seq_lens, int64_t m, int64_t k, int32_t* out_idx,
+                           int64_t out_stride, void* stream);
+
+/* ---- top-k gather -----------------------------------------------------------
+ * dst[r, j] = entry max(idx[r*idx_stride + j], 0) of sequence row_seq[r]
+ * (row_seq == NULL: r) from the paged compressed cache; a -1 pick reads
+ * entry 0 (clamp(min=0), csa.py:328-331).  Picks at or past n_entries[b]
+ * (including every pick of a sequence with no entries) produce zero rows.
+ * SKV_FMT_BF16 copies entries; SKV_FMT_FP8 dequantizes them to bf16
+ * (code * scale rounded to bf16; quant/reference.py:114-116).
+ * dst: [rows, k, out_row] with out_row = entry_bytes (bf16) or 2*channels. */
+int skv_topk_gather(void* dst, const void* pool, int64_t entry_bytes, int64_t block_size,
+                    int64_t n_pages, const int32_t* block_table, int64_t bt_stride,
+                    const int32_t* n_entries, const int32_t* idx, int64_t idx_stride, int64_t k,
+                    int64_t rows, const int32_t* row_seq, int64_t channels, int32_t format,
+                    void* stream);
+
+/* ---- eviction and compaction --------------------------------------------------
+ * skv_release: push every page of each sequence with release_mask[b] != 0 back
+ * on the free stack (ascending b; within b from the last logical page to the
+ * first), set its block-table row to -1 and its length to 0.  Refuses
+ * (status SKV_STATUS_STACK / BADARG, nothing written) if the stack would
+ * overflow or a released page id is invalid.  No reference counterpart. */
+int skv_release(int32_t* free_stack, int32_t* free_top, int64_t n_pages, int32_t* block_table,
+                int64_t bt_stride, int32_t* seq_lens, const uint8_t* release_mask, int64_t batch,
+                int64_t block_size, int32_t* status, void* stream);
+
+/* A pool whose pages share one block table (e.g. the main and indexer streams
+ * of a CSA cache); page p of the pool is at base + p*page_bytes. */
+typedef struct skv_pool_ref {
+  void* base;
+  int64_t page_bytes;
+} skv_pool_ref;
+
+/* skv_compact: defragment up to 4 pools sharing one block table.  Live pages
+ * with id >= n_live move into the free ids < n_live (both ascending), the
+ * tables are rewritten and the free stack rebuilt so pops return n_live,
+ * n_live+1, ...  workspace: int32 [3*n_pages]; info: int32 [2] receives
+ * {n_live, n_moved}.  No reference counterpart. */
+int skv_compact(const skv_pool_ref* pools, int32_t n_pools, int32_t* block_table,
+                int64_t bt_stride, const int32_t* seq_lens, int64_t batch, int64_t block_size,
+                int64_t n_pages, int32_t* free_stack, int32_t* free_top, int32_t* workspace,
+                int32_t* info, void* stream);
 
 #ifdef __cplusplus
 }

@@ -341,6 +341,42 @@ def compress_pool(c: Tensor, z: Tensor, bias: Tensor) -> Tensor:
     return (w * c.float()).sum(dim=-2)  # csa.py:87
 
 
+def compress_append(pool: Tensor, block_table: np.ndarray, tail_c: Tensor, tail_z: Tensor,
+                    c_new: Tensor, z_new: Tensor, bias: Tensor, seq_lens: np.ndarray,
+                    n_new: np.ndarray | int, fp8: bool = False) -> list[tuple[int, int, Tensor]]:
+    """Emission state machine of kv_cache.py:170-195 / 291-315 on paged entries.
+
+    seq_lens are token counts after the append.  Every block of m tokens
+    completed by the n_new tokens is pooled (compress_pool, rounded to bf16)
+    into entry floor(p/m); the incomplete block's new tokens go to the tails
+    (slot p % m).  Returns [(b, entry, bf16 value)] of the emitted entries.
+    """
+    m = tail_c.shape[1]
+    bs = pool.shape[1]
+    n = np.broadcast_to(np.asarray(n_new), (block_table.shape[0],))
+    emitted = []
+    for b in range(block_table.shape[0]):
+        L, k = int(seq_lens[b]), int(n[b])
+        if k <= 0:
+            continue
+        first_new = L - k
+
+        def row(t: Tensor, tail: Tensor, p: int) -> Tensor:
+            return tail[b, p % m] if p < first_new else t[b, p - first_new]
+
+        for e in range(first_new // m, L // m):
+            cs = torch.stack([row(c_new, tail_c, e * m + i) for i in range(m)])
+            zs = torch.stack([row(z_new, tail_z, e * m + i) for i in range(m)])
+            val = compress_pool(cs, zs, bias).to(torch.bfloat16)
+            page, slot = int(block_table[b, e // bs]), e % bs
+            pool[page, slot] = fp8_pack_entries(val.unsqueeze(0))[0] if fp8 else val
+            emitted.append((b, e, val))
+        for p in range(max(first_new, (L // m) * m), L):
+            tail_c[b, p % m] = c_new[b, p - first_new]
+            tail_z[b, p % m] = z_new[b, p - first_new]
+    return emitted
+
+
 def compress_pool_bf16_module(c: Tensor, z: Tensor, bias: Tensor) -> Tensor:
     """The same pooling with the rounding a bf16 module applies at every op
     (z + bias, softmax and the product each rounded to bf16; csa.py:82-87)."""
@@ -372,7 +408,7 @@ def topk_select(scores: np.ndarray, n_valid: np.ndarray, k: int, n_blocks: int) 
 
     Entries s >= n_valid[r] are masked to -inf (causal mask, csa.py:411-415);
     the order is descending score, ties by ascending index; picks whose score
-    is -inf become -1 (csa.py:420-422).
+    is not finite (NaN, +inf or -inf) become -1 (isfinite, csa.py:420-422).
     """
     scores = np.asarray(scores, dtype=np.float32)[:, :n_blocks]
     rows = scores.shape[0]
@@ -386,7 +422,7 @@ def topk_select(scores: np.ndarray, n_valid: np.ndarray, k: int, n_blocks: int) 
         key = order_key(s)
         idx = np.arange(n_blocks)
         order = np.lexsort((idx, ~key))[:k_eff]
-        picks = np.where(np.isneginf(s[order]), -1, order)
+        picks = np.where(~np.isfinite(s[order]), -1, order)
         out[r] = picks
     return out
 

@@ -1,0 +1,371 @@
+// Top-k block selection over fp32 indexer scores and the block-table gather
+// of the selected compressed entries (with optional FP8 -> bf16 dequant).
+//
+// Reference semantics:
+//   CSA._indexer_topk_cached (csa.py:411-422), kernels/attention.py:53-89:
+//     scores[s] = -inf where s*m + m - 1 >= q_pos (causal block mask)
+//     k_eff = min(top_k, n_blocks); topk(k_eff) sorted descending;
+//     picks whose score is not finite become -1.
+//   Sparse gather (csa.py:326-331): idx.clamp(min=0) then torch.gather, so a
+//   -1 pick copies entry 0 (masked later by the consumer).
+//   dequant_from_fp8 (quant/reference.py:114-116): code * scale, then bf16.
+// Order of equal scores: ascending index (a total order; torch leaves ties
+// unspecified).
+#include "skv_common.h"
+
+namespace skv {
+
+constexpr int kTopkThreads = 1024;
+constexpr int kTopkWaves = kTopkThreads / kWave;
+constexpr int kLdsKeys = 28672;  // rows with at most this many valid scores are staged in LDS
+constexpr int kMaxTopK = 2048;
+
+constexpr uint32_t kKeyNaN = 0xffffffffu;
+constexpr uint32_t kKeyPosInf = 0xff800000u;
+constexpr uint32_t kKeyNegInf = 0x007fffffu;
+
+// Order-preserving map fp32 -> uint32 (larger float -> larger key); -0.0 is
+// folded onto +0.0 and every NaN onto the largest key (torch.topk ranks NaN
+// above +inf).
+__device__ __forceinline__ uint32_t score_key(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return kKeyNaN;
+  if (u == 0x80000000u) u = 0u;
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+__device__ __forceinline__ bool key_finite(uint32_t k) {
+  return k != kKeyNaN && k != kKeyPosInf && k != kKeyNegInf;
+}
+
+struct TopkArgs {
+  const float* scores;
+  int64_t stride;
+  const int32_t* n_valid;
+  const int32_t* n_cols;
+  int n_cols_uni;
+  const int32_t* lens;  // decode mode: n_cols = L/m, n_valid = (L-1)/m
+  int m;
+  int k;
+  int32_t* out;
+  int64_t out_stride;
+};
+
+__global__ __launch_bounds__(kTopkThreads) void k_topk_select(TopkArgs a) {
+  __shared__ uint32_t keys[kLdsKeys];
+  __shared__ int whist[kTopkWaves][256];
+  __shared__ int hist[256];
+  __shared__ uint32_t cand_key[kMaxTopK];
+  __shared__ int cand_idx[kMaxTopK];
+  __shared__ int scan_lds[17];
+  __shared__ int sh_digit, sh_above, sh_cnt;
+
+  const int r = blockIdx.x;
+  const int tid = threadIdx.x;
+  const int wid = tid / kWave;
+  int n_cols, n_valid;
+  if (a.lens) {
+    const int L = max(a.lens[r], 0);
+    n_cols = L / a.m;
+    n_valid = L > 0 ? (L - 1) / a.m : 0;
+  } else {
+    n_cols = a.n_cols ? a.n_cols[r] : a.n_cols_uni;
+    n_valid = a.n_valid[r];
+  }
+  n_cols = max(n_cols, 0);
+  n_valid = max(0, min(n_valid, n_cols));
+  const int k_eff = min(a.k, n_cols);
+  const int sel = min(k_eff, n_valid);
+  int32_t* out = a.out + r * a.out_stride;
+  for (int j = sel + tid; j < a.k; j += kTopkThreads) out[j] = -1;
+  if (sel == 0) return;
+
+  const float* row = a.scores + r * a.stride;
+  const bool in_lds = n_valid <= kLdsKeys;
+  if (in_lds) {
+    for (int i = tid; i < n_valid; i += kTopkThreads) keys[i] = score_key(row[i]);
+    __syncthreads();
+  }
+  auto key_at = [&](int i) -> uint32_t { return in_lds ? keys[i] : score_key(row[i]); };
+
+  // ---- radix select: the sel-th largest key, 8 bits per pass ---------------
+  uint32_t prefix = 0, pmask = 0;
+  int remaining = sel;  // rank (1-based) of the target among keys matching prefix
+  int eq_total = 0;
+  for (int pass = 0; pass < 4; ++pass) {
+    const int shift = 24 - 8 * pass;
+    for (int i = tid; i < kTopkWaves * 256; i += kTopkThreads) (&whist[0][0])[i] = 0;
+    __syncthreads();
+    for (int i = tid; i < n_valid; i += kTopkThreads) {
+      const uint32_t key = key_at(i);
+      if ((key & pmask) == prefix) atomicAdd(&whist[wid][(key >> shift) & 255u], 1);
+    }
+    __syncthreads();
+    if (tid < 256) {
+      int s = 0;
+#pragma unroll
+      for (int w = 0; w < kTopkWaves; ++w) s += whist[w][tid];
+      hist[tid] = s;
+    }
+    __syncthreads();
+    // suffix counts: above(d) = sum of hist[d+1..255]; thread t owns bin 255-t
+    {
+      const int bin = 255 - tid;
+      const int v = (tid < 256) ? hist[bin] : 0;
+      int tot;
+      const int ex = block_exclusive_scan(v, scan_lds, &tot);  // count of bins > bin
+      if (tid < 256 && ex < remaining && remaining <= ex + v) {
+        sh_digit = bin;
+        sh_above = ex;
+      }
+      __syncthreads();
+    }
+    const int d = sh_digit;
+    remaining -= sh_above;
+    prefix |= static_cast<uint32_t>(d) << shift;
+    pmask |= 255u << shift;
+    eq_total = hist[d];
+    __syncthreads();
+  }
+  const uint32_t T = prefix;
+  const int need_eq = remaining;  // keys == T to take (smallest indices first)
+  const int n_gt = sel - need_eq;
+
+  // ---- collect the sel winners ------------------------------------------------
+  if (tid == 0) sh_cnt = 0;
+  __syncthreads();
+  for (int i = tid; i < n_valid; i += kTopkThreads) {
+    const uint32_t key = key_at(i);
+    if (key > T || (key == T && eq_total == need_eq)) {
+      const int slot = atomicAdd(&sh_cnt, 1);
+      cand_key[slot] = key;
+      cand_idx[slot] = i;
+    }
+  }
+  __syncthreads();
+  if (eq_total != need_eq) {
+    // ties at the threshold: take the need_eq smallest indices, in index order
+    int carry = 0;
+    for (int base = 0; base < n_valid; base += kTopkThreads) {
+      const int i = base + tid;
+      const int is_eq = (i < n_valid && key_at(i) == T) ? 1 : 0;
+      int tot;
+      const int rank = carry + block_exclusive_scan(is_eq, scan_lds, &tot);
+      if (is_eq && rank < need_eq) {
+        cand_key[n_gt + rank] = T;
+        cand_idx[n_gt + rank] = i;
+      }
+      carry += tot;
+      if (carry >= need_eq) break;  // uniform: carry is the same on every thread
+    }
+    __syncthreads();
+  }
+
+  // ---- order the winners: key descending, index ascending ------------------
+  for (int c = tid; c < sel; c += kTopkThreads) {
+    const uint32_t kc = cand_key[c];
+    const int ic = cand_idx[c];
+    int rank = 0;
+    for (int j = 0; j < sel; ++j) {
+      const uint32_t kj = cand_key[j];
+      rank += (kj > kc) || (kj == kc && cand_idx[j] < ic);
+    }
+    out[rank] = key_finite(kc) ? ic : -1;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Gather of selected entries through the block table.
+// ---------------------------------------------------------------------------
+constexpr int kGatherThreads = 256;
+constexpr int kGatherEntries = 8;
+
+struct TopkGatherArgs {
+  uint8_t* dst;
+  const uint8_t* pool;
+  int64_t entry_bytes;
+  int bs;
+  int64_t n_pages;
+  const int32_t* bt;
+  int64_t bt_stride;
+  const int32_t* n_entries;
+  const int32_t* idx;
+  int64_t idx_stride;
+  int k;
+  const int32_t* row_seq;
+  int channels;
+  int format;
+  int fp8_main;
+  int64_t out_row_bytes;
+};
+
+// Entry address of pick j of row r, or nullptr when no entry exists.
+__device__ __forceinline__ const uint8_t* pick_entry(const TopkGatherArgs& a, int r, int j) {
+  const int b = a.row_seq ? a.row_seq[r] : r;
+  int e = a.idx[r * a.idx_stride + j];
+  if (e < 0) e = 0;  // clamp(min=0): a -1 pick reads entry 0
+  const int n_ent = a.n_entries[b];
+  if (e >= n_ent) return nullptr;
+  const int64_t p = e / a.bs;
+  if (p >= a.bt_stride) return nullptr;
+  const int32_t page = a.bt[b * a.bt_stride + p];
+  if (page < 0 || page >= a.n_pages) return nullptr;
+  return a.pool + (static_cast<int64_t>(page) * a.bs + e % a.bs) * a.entry_bytes;
+}
+
+// grid: (ceil(k / kGatherEntries), rows)
+__global__ __launch_bounds__(kGatherThreads) void k_topk_gather(TopkGatherArgs a) {
+  const int r = blockIdx.y;
+  const int j0 = blockIdx.x * kGatherEntries;
+  const int nj = min(kGatherEntries, a.k - j0);
+  if (nj <= 0) return;
+  uint8_t* out_base = a.dst + (static_cast<int64_t>(r) * a.k + j0) * a.out_row_bytes;
+  if (a.format == SKV_FMT_BF16) {
+    const int chunks = static_cast<int>(a.entry_bytes >> 4);
+    const int total = nj * chunks;
+    for (int t = threadIdx.x; t < total; t += kGatherThreads) {
+      const int jj = t / chunks;
+      const int c = t - jj * chunks;
+      const uint8_t* src = pick_entry(a, r, j0 + jj);
+      u32x4 v = {0u, 0u, 0u, 0u};
+      if (src) v = *(reinterpret_cast<const u32x4*>(src) + c);
+      st_stream(reinterpret_cast<u32x4*>(out_base + jj * a.out_row_bytes) + c, v);
+    }
+    return;
+  }
+  // FP8 entry: [fp8_main codes][fp8_main/128 fp32 scales][rope bf16]
+  const int code_chunks = a.fp8_main >> 4;             // 16 codes each -> 2 output chunks
+  const int rope_chunks = (a.channels - a.fp8_main) >> 3;  // 8 bf16 each
+  const int per_entry = code_chunks + rope_chunks;
+  const int total = nj * per_entry;
+  for (int t = threadIdx.x; t < total; t += kGatherThreads) {
+    const int jj = t / per_entry;
+    const int c = t - jj * per_entry;
+    const uint8_t* src = pick_entry(a, r, j0 + jj);
+    uint8_t* orow = out_base + jj * a.out_row_bytes;
+    if (c < code_chunks) {
+      u32x4 o0 = {0u, 0u, 0u, 0u}, o1 = {0u, 0u, 0u, 0u};
+      if (src) {
+        const u32x4 codes = *(reinterpret_cast<const u32x4*>(src) + c);
+        const float scale = *reinterpret_cast<const float*>(src + a.fp8_main + (c >> 3) * 4);
+        float f[16];
+#pragma unroll
+        for (int q = 0; q < 16; ++q) {
+          const uint8_t code = static_cast<uint8_t>(codes[q >> 2] >> (8 * (q & 3)));
+          f[q] = e4m3fn_to_f32(code) * scale;
+        }
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          o0[q] = f32_to_bf16(f[2 * q]) | (static_cast<uint32_t>(f32_to_bf16(f[2 * q + 1])) << 16);
+          o1[q] = f32_to_bf16(f[8 + 2 * q]) | (static_cast<uint32_t>(f32_to_bf16(f[8 + 2 * q + 1])) << 16);
+        }
+      }
+      st_stream(reinterpret_cast<u32x4*>(orow) + 2 * c, o0);
+      st_stream(reinterpret_cast<u32x4*>(orow) + 2 * c + 1, o1);
+    } else {
+      const int rc = c - code_chunks;
+      u32x4 v = {0u, 0u, 0u, 0u};
+      if (src) {
+        v = *reinterpret_cast<const u32x4*>(src + a.fp8_main + (a.fp8_main >> 7) * 4 + rc * 16);
+      }
+      st_stream(reinterpret_cast<u32x4*>(orow + a.fp8_main * 2) + rc, v);
+    }
+  }
+}
+
+}  // namespace skv
+
+using namespace skv;
+
+static int launch_topk(const TopkArgs& a, int64_t rows, void* stream, const char* what) {
+  if (a.k < 0 || a.k > kMaxTopK) {
+    return set_error(SKV_EINVAL, "%s: k must be in [0, %d]; got %d", what, kMaxTopK, a.k);
+  }
+  if (rows < 0 || rows > INT32_MAX) return set_error(SKV_EINVAL, "%s: bad rows", what);
+  if (!a.out || a.out_stride < a.k) return set_error(SKV_EINVAL, "%s: out_stride must be >= k", what);
+  if (rows == 0 || a.k == 0) return SKV_OK;
+  hipLaunchKernelGGL(k_topk_select, dim3(static_cast<unsigned>(rows)), dim3(kTopkThreads), 0,
+                     static_cast<hipStream_t>(stream), a);
+  return check_launch(what);
+}
+
+extern "C" int skv_topk_select(const float* scores, int64_t score_stride, int64_t rows,
+                               const int32_t* n_valid, const int32_t* n_cols,
+                               int32_t n_cols_uniform, int64_t k, int32_t* out_idx,
+                               int64_t out_stride, void* stream) {
+  if (!n_valid) return set_error(SKV_EINVAL, "skv_topk_select: n_valid is NULL");
+  TopkArgs a{};
+  a.scores = scores;
+  a.stride = score_stride;
+  a.n_valid = n_valid;
+  a.n_cols = n_cols;
+  a.n_cols_uni = n_cols_uniform;
+  a.k = static_cast<int>(k);
+  a.out = out_idx;
+  a.out_stride = out_stride;
+  return launch_topk(a, rows, stream, "skv_topk_select");
+}
+
+extern "C" int skv_topk_select_decode(const float* scores, int64_t score_stride, int64_t batch,
+                                      const int32_t* seq_lens, int64_t m, int64_t k,
+                                      int32_t* out_idx, int64_t out_stride, void* stream) {
+  if (m <= 0) return set_error(SKV_EINVAL, "skv_topk_select_decode: compression_rate must be positive; got %lld", (long long)m);
+  if (!seq_lens) return set_error(SKV_EINVAL, "skv_topk_select_decode: seq_lens is NULL");
+  TopkArgs a{};
+  a.scores = scores;
+  a.stride = score_stride;
+  a.lens = seq_lens;
+  a.m = static_cast<int>(m);
+  a.k = static_cast<int>(k);
+  a.out = out_idx;
+  a.out_stride = out_stride;
+  return launch_topk(a, batch, stream, "skv_topk_select_decode");
+}
+
+extern "C" int skv_topk_gather(void* dst, const void* pool, int64_t entry_bytes, int64_t block_size,
+                               int64_t n_pages, const int32_t* block_table, int64_t bt_stride,
+                               const int32_t* n_entries, const int32_t* idx, int64_t idx_stride,
+                               int64_t k, int64_t rows, const int32_t* row_seq, int64_t channels,
+                               int32_t format, void* stream) {
+  const char* what = "skv_topk_gather";
+  if (entry_bytes <= 0 || (entry_bytes & 15) || block_size <= 0 || bt_stride <= 0) {
+    return set_error(SKV_EINVAL, "%s: bad entry_bytes/block_size/bt_stride", what);
+  }
+  if (k < 0 || k > INT32_MAX || rows < 0 || rows > 65535 || idx_stride < k) {
+    return set_error(SKV_EINVAL, "%s: need 0 <= k <= idx_stride and rows <= 65535", what);
+  }
+  if ((reinterpret_cast<uintptr_t>(dst) | reinterpret_cast<uintptr_t>(pool)) & 15) {
+    return set_error(SKV_EINVAL, "%s: dst and pool must be 16-byte aligned", what);
+  }
+  TopkGatherArgs a{};
+  a.dst = static_cast<uint8_t*>(dst);
+  a.pool = static_cast<const uint8_t*>(pool);
+  a.entry_bytes = entry_bytes;
+  a.bs = static_cast<int>(block_size);
+  a.n_pages = n_pages;
+  a.bt = block_table;
+  a.bt_stride = bt_stride;
+  a.n_entries = n_entries;
+  a.idx = idx;
+  a.idx_stride = idx_stride;
+  a.k = static_cast<int>(k);
+  a.row_seq = row_seq;
+  a.channels = static_cast<int>(channels);
+  a.format = format;
+  if (format == SKV_FMT_BF16) {
+    a.out_row_bytes = entry_bytes;
+  } else if (format == SKV_FMT_FP8) {
+    a.fp8_main = static_cast<int>(channels - SKV_FP8_ROPE_DIMS);
+    if (a.fp8_main <= 0 || (a.fp8_main % 128) || entry_bytes != SKV_FP8_ENTRY_BYTES(channels)) {
+      return set_error(SKV_EINVAL, "%s: fp8 entries need channels = 128*q + %d and entry_bytes = %lld",
+                       what, SKV_FP8_ROPE_DIMS, (long long)SKV_FP8_ENTRY_BYTES(channels));
+    }
+    a.out_row_bytes = channels * 2;
+  } else {
+    return set_error(SKV_EINVAL, "%s: unknown format %d", what, format);
+  }
+  if (rows == 0 || k == 0) return SKV_OK;
+  const dim3 grid(static_cast<unsigned>(ceil_div(k, kGatherEntries)), static_cast<unsigned>(rows));
+  hipLaunchKernelGGL(k_topk_gather, grid, dim3(kGatherThreads), 0, static_cast<hipStream_t>(stream), a);
+  return check_launch(what);
+}

@@ -47,7 +47,41 @@ SIGNATURES: dict[str, list] = {
         _P, _P, _I64, _I64, _P, _I64, _I64, _I64, _P, _I64, _P, _P, _I32, _P, _I64, _I64, _I64,
         _I64, _P,
     ],
+    "skv_ring_append": [_P, _I64, _I64, _P, _P, _I32, _P, _I64, _I64, _I64, _I64, _P],
+    "skv_ring_read": [_P, _I64, _I64, _P, _I64, _I64, _P, _I64, _P],
+    "skv_compress_append": [
+        _P, _I64, _I64, _I64, _P, _I64, _P, _P, _P, _P, _I64, _I64, _I64, _P, _P, _P, _I32, _I64,
+        _I64, _I32, _I64, _P,
+    ],
+    "skv_fp8_quant_append": [
+        _P, _I64, _I64, _I64, _P, _I64, _P, _P, _I32, _P, _I64, _I64, _I64, _I64, _I64, _P,
+    ],
+    "skv_fp8_encode_host": [_P, _P, _I64],
+    "skv_fp8_decode_host": [_P, _P, _I64],
+    "skv_topk_select": [_P, _I64, _I64, _P, _P, _I32, _I64, _P, _I64, _P],
+    "skv_topk_select_decode": [_P, _I64, _I64, _P, _I64, _I64, _P, _I64, _P],
+    "skv_topk_gather": [
+        _P, _P, _I64, _I64, _I64, _P, _I64, _P, _P, _I64, _I64, _I64, _P, _I64, _I32, _P,
+    ],
+    "skv_release": [_P, _P, _I64, _P, _I64, _P, _P, _I64, _I64, _P, _P],
+    "skv_compact": [ctypes.c_void_p, _I32, _P, _I64, _P, _I64, _I64, _I64, _P, _P, _P, _P, _P],
 }
+
+# Entry formats and the FP8 entry layout (include/saintkv.h).
+SKV_FMT_BF16 = 0
+SKV_FMT_FP8 = 1
+SKV_FP8_ROPE_DIMS = 64
+
+
+def fp8_entry_bytes(channels: int) -> int:
+    main = channels - SKV_FP8_ROPE_DIMS
+    return main + main // 128 * 4 + 2 * SKV_FP8_ROPE_DIMS
+
+
+class PoolRef(ctypes.Structure):
+    """skv_pool_ref: one pool sharing a block table."""
+
+    _fields_ = [("base", ctypes.c_void_p), ("page_bytes", ctypes.c_int64)]
 
 _lib: ctypes.CDLL | None = None
 

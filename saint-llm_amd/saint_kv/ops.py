@@ -7,6 +7,7 @@ Nothing here computes on the CPU; the wrappers only describe memory.
 
 from __future__ import annotations
 
+import ctypes
 import math
 
 import torch
@@ -186,3 +187,259 @@ def append_gather(pool: torch.Tensor, block_table: torch.Tensor, seq_lens: torch
               bs, n_pages, block_table.data_ptr(), bt_stride, seq_lens.data_ptr(), n_ptr, n_uni,
               src.data_ptr(), s_seq, s_row, src.shape[1], batch, _lib.stream_handle(pool.device))
     return out
+
+
+# ---------------------------------------------------------------------------
+# SWA ring
+# ---------------------------------------------------------------------------
+def _check_ring(ring: torch.Tensor) -> tuple[int, int, int]:
+    _require_gpu(ring, "ring")
+    if ring.dim() < 3 or not ring.is_contiguous():
+        raise ValueError(f"ring must be a contiguous [batch, window, *row]; got {tuple(ring.shape)}")
+    rb = math.prod(ring.shape[2:]) * ring.element_size()
+    return ring.shape[0], ring.shape[1], rb
+
+
+def ring_append(ring: torch.Tensor, seq_lens: torch.Tensor, src: torch.Tensor,
+                n_new: int | torch.Tensor) -> None:
+    """Write the newest ``n_new`` tokens (``seq_lens`` already counts them) into the ring."""
+    batch, window, rb = _check_ring(ring)
+    _require_i32(seq_lens, "seq_lens", (batch,))
+    _require_gpu(src, "src")
+    if src.shape[0] != batch:
+        raise ValueError(f"src batch {src.shape[0]} != ring batch {batch}")
+    s_seq, s_row = _row_view_strides(src, rb, "src")
+    n_ptr, n_uni = _n_new_args(n_new, batch)
+    _lib.call("skv_ring_append", ring.data_ptr(), window, rb, seq_lens.data_ptr(), n_ptr, n_uni,
+              src.data_ptr(), s_seq, s_row, src.shape[1], batch, _lib.stream_handle(ring.device))
+
+
+def ring_read(ring: torch.Tensor, seq_lens: torch.Tensor, out: torch.Tensor) -> torch.Tensor:
+    """out[b, r] = token at position L-n+r, n = min(window, L), in position order."""
+    batch, window, rb = _check_ring(ring)
+    _require_i32(seq_lens, "seq_lens", (batch,))
+    _, seq_rows, cap = _dst_args(out, rb, batch, None)
+    _lib.call("skv_ring_read", out.data_ptr(), seq_rows, cap, ring.data_ptr(), window, rb,
+              seq_lens.data_ptr(), batch, _lib.stream_handle(ring.device))
+    return out
+
+
+# ---------------------------------------------------------------------------
+# Compression pooling into a paged compressed cache
+# ---------------------------------------------------------------------------
+def _entry_format(pool: torch.Tensor, channels: int) -> int:
+    rb = row_bytes_of(pool)
+    if pool.dtype == torch.bfloat16 and rb == 2 * channels:
+        return _lib.SKV_FMT_BF16
+    if pool.dtype == torch.uint8 and rb == _lib.fp8_entry_bytes(channels):
+        return _lib.SKV_FMT_FP8
+    raise ValueError(
+        f"pool rows of {rb} bytes ({pool.dtype}) match neither bf16 entries of {channels} "
+        f"channels nor fp8 entries of {_lib.fp8_entry_bytes(channels)} bytes",
+    )
+
+
+def compress_append(pool: torch.Tensor, block_table: torch.Tensor, tail_c: torch.Tensor,
+                    tail_z: torch.Tensor, c_new: torch.Tensor, z_new: torch.Tensor,
+                    bias: torch.Tensor, seq_lens: torch.Tensor, n_new: int | torch.Tensor) -> int:
+    """Pool every block of m tokens completed by this append into the paged cache.
+
+    ``pool`` is bf16 [n_pages, bs, C] (bf16 entries) or uint8 [n_pages, bs, E]
+    (fp8 entries); ``tail_c``/``tail_z`` bf16 [B, m, C]; ``c_new``/``z_new``
+    bf16 [B, T, C] with identical strides; ``bias`` fp32 [m, C].  Returns the
+    entry format used.
+    """
+    n_pages, bs, rb = _check_pool(pool)
+    _require_i32(block_table, "block_table")
+    batch, bt_stride = block_table.shape
+    _require_i32(seq_lens, "seq_lens", (batch,))
+    channels = c_new.shape[-1]
+    fmt = _entry_format(pool, channels)
+    m = tail_c.shape[1]
+    for name, t in (("tail_c", tail_c), ("tail_z", tail_z)):
+        _require_gpu(t, name)
+        if t.dtype != torch.bfloat16 or tuple(t.shape) != (batch, m, channels) or not t.is_contiguous():
+            raise ValueError(f"{name} must be contiguous bf16 [{batch}, {m}, {channels}]")
+    for name, t in (("c_new", c_new), ("z_new", z_new)):
+        _require_gpu(t, name)
+        if t.dtype != torch.bfloat16 or t.dim() != 3 or t.shape[0] != batch or t.stride(-1) != 1:
+            raise ValueError(f"{name} must be bf16 [batch, T, channels] with dense rows")
+    if c_new.shape != z_new.shape or c_new.stride() != z_new.stride():
+        raise ValueError("c_new and z_new must have the same shape and strides")
+    _require_gpu(bias, "bias")
+    if bias.dtype != torch.float32 or tuple(bias.shape) != (m, channels) or not bias.is_contiguous():
+        raise ValueError(f"bias must be contiguous fp32 [{m}, {channels}]")
+    n_ptr, n_uni = _n_new_args(n_new, batch)
+    es = c_new.element_size()
+    _lib.call("skv_compress_append", pool.data_ptr(), rb, bs, n_pages, block_table.data_ptr(),
+              bt_stride, tail_c.data_ptr(), tail_z.data_ptr(), c_new.data_ptr(), z_new.data_ptr(),
+              c_new.stride(0) * es, c_new.stride(1) * es, c_new.shape[1], bias.data_ptr(),
+              seq_lens.data_ptr(), n_ptr, n_uni, m, channels, fmt, batch,
+              _lib.stream_handle(pool.device))
+    return fmt
+
+
+def fp8_quant_append(pool: torch.Tensor, block_table: torch.Tensor, seq_lens: torch.Tensor,
+                     src: torch.Tensor, n_new: int | torch.Tensor) -> None:
+    """Quantize bf16 rows [B, T, C] into fp8 entries (uint8 pool [n_pages, bs, E])."""
+    n_pages, bs, rb = _check_pool(pool)
+    _require_i32(block_table, "block_table")
+    batch, bt_stride = block_table.shape
+    _require_i32(seq_lens, "seq_lens", (batch,))
+    _require_gpu(src, "src")
+    if src.dtype != torch.bfloat16 or src.dim() != 3 or src.shape[0] != batch or src.stride(-1) != 1:
+        raise ValueError("src must be bf16 [batch, T, channels] with dense rows")
+    channels = src.shape[-1]
+    if pool.dtype != torch.uint8 or rb != _lib.fp8_entry_bytes(channels):
+        raise ValueError(f"fp8 pool rows must be {_lib.fp8_entry_bytes(channels)} uint8")
+    n_ptr, n_uni = _n_new_args(n_new, batch)
+    es = src.element_size()
+    _lib.call("skv_fp8_quant_append", pool.data_ptr(), rb, bs, n_pages, block_table.data_ptr(),
+              bt_stride, seq_lens.data_ptr(), n_ptr, n_uni, src.data_ptr(), src.stride(0) * es,
+              src.stride(1) * es, src.shape[1], channels, batch, _lib.stream_handle(pool.device))
+
+
+def fp8_encode_host(x: torch.Tensor) -> torch.Tensor:
+    """e4m3fn codes of fp32 CPU values through the library's own codec (no GPU)."""
+    if x.device.type != "cpu" or x.dtype != torch.float32:
+        raise ValueError("fp8_encode_host takes a CPU float32 tensor")
+    x = x.contiguous()
+    out = torch.empty(x.shape, dtype=torch.uint8)
+    _lib.call("skv_fp8_encode_host", x.data_ptr(), out.data_ptr(), x.numel())
+    return out
+
+
+def fp8_decode_host(codes: torch.Tensor) -> torch.Tensor:
+    if codes.device.type != "cpu" or codes.dtype != torch.uint8:
+        raise ValueError("fp8_decode_host takes a CPU uint8 tensor")
+    codes = codes.contiguous()
+    out = torch.empty(codes.shape, dtype=torch.float32)
+    _lib.call("skv_fp8_decode_host", codes.data_ptr(), out.data_ptr(), codes.numel())
+    return out
+
+
+# ---------------------------------------------------------------------------
+# Top-k selection and gather
+# ---------------------------------------------------------------------------
+def _check_scores(scores: torch.Tensor, rows: int) -> None:
+    _require_gpu(scores, "scores")
+    if scores.dtype != torch.float32 or scores.dim() != 2 or scores.stride(1) != 1:
+        raise ValueError("scores must be fp32 [rows, n] with unit column stride")
+    if scores.shape[0] != rows:
+        raise ValueError(f"scores has {scores.shape[0]} rows, expected {rows}")
+
+
+def _check_idx_out(out: torch.Tensor, rows: int, k: int) -> None:
+    _require_gpu(out, "out")
+    if out.dtype != torch.int32 or out.dim() != 2 or out.shape[0] != rows or out.shape[1] < k:
+        raise ValueError(f"out must be int32 [{rows}, >={k}]")
+    if out.stride(1) != 1:
+        raise ValueError("out must have unit column stride")
+
+
+def topk_select(scores: torch.Tensor, n_valid: torch.Tensor, n_cols: int | torch.Tensor, k: int,
+                out: torch.Tensor) -> torch.Tensor:
+    """Per row: the min(k, n_cols, n_valid) best valid columns, -1 padded to k."""
+    rows = n_valid.shape[0]
+    _require_i32(n_valid, "n_valid", (rows,))
+    _check_scores(scores, rows)
+    _check_idx_out(out, rows, k)
+    if isinstance(n_cols, torch.Tensor):
+        _require_i32(n_cols, "n_cols", (rows,))
+        nc_ptr, nc_uni = n_cols.data_ptr(), 0
+    else:
+        nc_ptr, nc_uni = None, int(n_cols)
+        if nc_uni > scores.shape[1]:
+            raise ValueError(f"n_cols={nc_uni} exceeds the score row length {scores.shape[1]}")
+    _lib.call("skv_topk_select", scores.data_ptr(), scores.stride(0), rows, n_valid.data_ptr(),
+              nc_ptr, nc_uni, k, out.data_ptr(), out.stride(0), _lib.stream_handle(scores.device))
+    return out
+
+
+def topk_select_decode(scores: torch.Tensor, seq_lens: torch.Tensor, m: int, k: int,
+                       out: torch.Tensor) -> torch.Tensor:
+    """Decode query at position L-1 of each sequence: causal block mask from seq_lens."""
+    batch = seq_lens.shape[0]
+    _require_i32(seq_lens, "seq_lens", (batch,))
+    _check_scores(scores, batch)
+    _check_idx_out(out, batch, k)
+    _lib.call("skv_topk_select_decode", scores.data_ptr(), scores.stride(0), batch,
+              seq_lens.data_ptr(), m, k, out.data_ptr(), out.stride(0),
+              _lib.stream_handle(scores.device))
+    return out
+
+
+def topk_gather(pool: torch.Tensor, block_table: torch.Tensor, n_entries: torch.Tensor,
+                idx: torch.Tensor, out: torch.Tensor, channels: int,
+                row_seq: torch.Tensor | None = None) -> torch.Tensor:
+    """out[r, j] = entry max(idx[r, j], 0) of the row's sequence (fp8 entries dequantized)."""
+    n_pages, bs, rb = _check_pool(pool)
+    _require_i32(block_table, "block_table")
+    batch, bt_stride = block_table.shape
+    _require_i32(n_entries, "n_entries", (batch,))
+    _require_gpu(idx, "idx")
+    if idx.dtype != torch.int32 or idx.dim() != 2 or idx.stride(1) != 1:
+        raise ValueError("idx must be int32 [rows, k] with unit column stride")
+    rows, k = idx.shape
+    if row_seq is None:
+        if rows != batch:
+            raise ValueError("without row_seq, idx must have one row per sequence")
+    else:
+        _require_i32(row_seq, "row_seq", (rows,))
+    fmt = _entry_format(pool, channels)
+    out_row = rb if fmt == _lib.SKV_FMT_BF16 else 2 * channels
+    _require_gpu(out, "out")
+    if not out.is_contiguous() or out.numel() * out.element_size() != rows * k * out_row:
+        raise ValueError(f"out must be contiguous with {rows}x{k} rows of {out_row} bytes")
+    _lib.call("skv_topk_gather", out.data_ptr(), pool.data_ptr(), rb, bs, n_pages,
+              block_table.data_ptr(), bt_stride, n_entries.data_ptr(), idx.data_ptr(),
+              idx.stride(0), k, rows, _lib.ptr(row_seq), channels, fmt,
+              _lib.stream_handle(pool.device))
+    return out
+
+
+# ---------------------------------------------------------------------------
+# Eviction and compaction
+# ---------------------------------------------------------------------------
+def release(free_stack: torch.Tensor, free_top: torch.Tensor, block_table: torch.Tensor,
+            seq_lens: torch.Tensor, mask: torch.Tensor, block_size: int,
+            status: torch.Tensor | None = None) -> None:
+    """Return every page of the sequences with mask[b] to the free stack."""
+    _require_i32(free_stack, "free_stack")
+    _require_i32(free_top, "free_top", (1,))
+    _require_i32(block_table, "block_table")
+    batch, bt_stride = block_table.shape
+    _require_i32(seq_lens, "seq_lens", (batch,))
+    _require_gpu(mask, "mask")
+    if mask.dtype not in (torch.uint8, torch.bool) or tuple(mask.shape) != (batch,):
+        raise ValueError("mask must be uint8/bool [batch]")
+    if status is not None:
+        _require_i32(status, "status", (1,))
+    _lib.call("skv_release", free_stack.data_ptr(), free_top.data_ptr(), free_stack.numel(),
+              block_table.data_ptr(), bt_stride, seq_lens.data_ptr(), mask.contiguous().data_ptr(),
+              batch, block_size, _lib.ptr(status), _lib.stream_handle(block_table.device))
+
+
+def compact(pools: list[torch.Tensor], block_table: torch.Tensor, seq_lens: torch.Tensor,
+            block_size: int, free_stack: torch.Tensor, free_top: torch.Tensor,
+            workspace: torch.Tensor, info: torch.Tensor) -> None:
+    """Defragment ``pools`` (sharing ``block_table``) so live pages occupy [0, n_live)."""
+    n_pages = free_stack.numel()
+    refs = (_lib.PoolRef * len(pools))()
+    for i, p in enumerate(pools):
+        pn, pbs, rb = _check_pool(p)
+        if pn != n_pages or pbs != block_size:
+            raise ValueError("every pool must have n_pages pages of block_size rows")
+        refs[i].base = p.data_ptr()
+        refs[i].page_bytes = pbs * rb
+    _require_i32(block_table, "block_table")
+    batch, bt_stride = block_table.shape
+    _require_i32(seq_lens, "seq_lens", (batch,))
+    _require_i32(free_stack, "free_stack")
+    _require_i32(free_top, "free_top", (1,))
+    _require_i32(workspace, "workspace", (3 * n_pages,))
+    _require_i32(info, "info", (2,))
+    _lib.call("skv_compact", ctypes.cast(refs, ctypes.c_void_p), len(pools), block_table.data_ptr(), bt_stride,
+              seq_lens.data_ptr(), batch, block_size, n_pages, free_stack.data_ptr(),
+              free_top.data_ptr(), workspace.data_ptr(), info.data_ptr(),
+              _lib.stream_handle(block_table.device))

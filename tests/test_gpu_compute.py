@@ -1,0 +1,311 @@
+"""GPU parity of the SWA ring, compression pooling, FP8 codec, top-k select,
+top-k gather, release and compaction against the CPU oracle.
+
+Bit-exact for indices, tables, copies and FP8 codes; pooled values within
+rtol=1e-2, atol=1e-2 of the fp32 oracle (bf16 output).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import reference_cpu as ref
+
+pytestmark = pytest.mark.gpu
+
+POOL_RTOL = 1e-2
+POOL_ATOL = 1e-2
+
+
+def _np(t: torch.Tensor) -> np.ndarray:
+    return t.detach().cpu().numpy()
+
+
+def _i32(a, dev) -> torch.Tensor:
+    return torch.as_tensor(np.asarray(a, dtype=np.int32), device=dev)
+
+
+# ------------------------------------------------------------------- ring ----
+def test_ring_append_read_ragged(dev) -> None:
+    from saint_kv import ops
+
+    g = torch.Generator().manual_seed(0)
+    batch, w, d = 5, 128, 576
+    ring = torch.zeros(batch, w, d, dtype=torch.bfloat16, device=dev)
+    r_ring = torch.zeros(batch, w, d, dtype=torch.bfloat16)
+    lens = np.zeros(batch, dtype=np.int32)
+    for n_step in ([3, 0, 130, 1, 64], [1, 1, 1, 1, 1], [300, 7, 0, 128, 2], [1, 0, 1, 0, 1]):
+        n = np.array(n_step, dtype=np.int32)
+        src = torch.randn(batch, int(n.max()), d, generator=g).to(torch.bfloat16)
+        before = lens.copy()
+        lens = lens + n
+        ops.ring_append(ring, _i32(lens, dev), src.to(dev), _i32(n, dev))
+        ref.ring_append(r_ring, before, src, n)
+        out = torch.zeros(batch, w, d, dtype=torch.bfloat16, device=dev)
+        ops.ring_read(ring, _i32(lens, dev), out)
+        r_out = ref.ring_read(r_ring, lens, torch.zeros(batch, w, d, dtype=torch.bfloat16))
+        torch.cuda.synchronize()
+        assert torch.equal(ring.cpu(), r_ring)
+        assert torch.equal(out.cpu(), r_out)
+
+
+# ---------------------------------------------------------------- pooling ----
+def _compress_case(dev, batch, m, channels, chunks, fp8, seed):
+    from saint_kv import ops
+
+    g = torch.Generator().manual_seed(seed)
+    rng = np.random.default_rng(seed)
+    bs, n_pages, max_pages = 16, 256, 64
+    order = rng.permutation(n_pages).astype(np.int32)
+    stack = torch.empty(n_pages, dtype=torch.int32, device=dev)
+    top = torch.empty(1, dtype=torch.int32, device=dev)
+    ops.free_stack_init(stack, top, _i32(order, dev))
+    bt = torch.full((batch, max_pages), -1, dtype=torch.int32, device=dev)
+    n_ent = torch.zeros(batch, dtype=torch.int32, device=dev)
+    r_stack, r_top = ref.free_stack_init(n_pages, order)
+    r_bt = np.full((batch, max_pages), -1, dtype=np.int32)
+    r_ent = np.zeros(batch, dtype=np.int32)
+    row = ref.FP8_ENTRY_BYTES if fp8 else channels
+    dt = torch.uint8 if fp8 else torch.bfloat16
+    pool = torch.zeros(n_pages, bs, row, dtype=dt, device=dev)
+    pool_bf = torch.zeros(n_pages, bs, channels, dtype=torch.bfloat16, device=dev)
+    r_pool = torch.zeros(n_pages, bs, channels, dtype=torch.bfloat16)
+    tail = [torch.zeros(batch, m, channels, dtype=torch.bfloat16, device=dev) for _ in range(4)]
+    r_tc = torch.zeros(batch, m, channels, dtype=torch.bfloat16)
+    r_tz = torch.zeros(batch, m, channels, dtype=torch.bfloat16)
+    bias = torch.randn(m, channels, generator=g)
+    lens = np.zeros(batch, dtype=np.int32)
+    for n_step in chunks:
+        n = np.asarray(n_step, dtype=np.int32)
+        t = max(int(n.max()), 1)
+        c = torch.randn(batch, t, channels, generator=g).to(torch.bfloat16)
+        z = torch.randn(batch, t, channels, generator=g).to(torch.bfloat16)
+        new_ent = (lens + n) // m - lens // m
+        lens = lens + n
+        ops.reserve(stack, top, bt, n_ent, _i32(new_ent, dev), bs)
+        r_status, r_top = ref.reserve(r_stack, r_top, r_bt, r_ent, new_ent, bs)
+        assert r_status == 0
+        # same staging, two formats: the fp8 run must quantize the bf16 run's values
+        ops.compress_append(pool_bf, bt, tail[0], tail[1], c.to(dev), z.to(dev), bias.to(dev),
+                            _i32(lens, dev), _i32(n, dev))
+        ops.compress_append(pool, bt, tail[2], tail[3], c.to(dev), z.to(dev), bias.to(dev),
+                            _i32(lens, dev), _i32(n, dev))
+        ref.compress_append(r_pool, r_bt, r_tc, r_tz, c, z, bias, lens, n)
+    torch.cuda.synchronize()
+    assert np.array_equal(_np(bt), r_bt) and np.array_equal(_np(n_ent), r_ent)
+    assert torch.equal(tail[0].cpu(), r_tc) and torch.equal(tail[1].cpu(), r_tz)
+    assert torch.equal(tail[2].cpu(), r_tc)
+    got = torch.zeros(batch, int(r_ent.max()), channels, dtype=torch.bfloat16, device=dev)
+    ops.paged_gather(pool_bf, bt, n_ent, got)
+    exp = ref.paged_gather(r_pool, r_bt, r_ent, torch.zeros(got.shape, dtype=torch.bfloat16))
+    torch.testing.assert_close(got.cpu().float(), exp.float(), rtol=POOL_RTOL, atol=POOL_ATOL)
+    if fp8:
+        live = ref.live_pages(r_bt, r_ent, bs)
+        q_exp = ref.fp8_pack_entries(pool_bf.cpu()[live].reshape(-1, channels))
+        # only filled slots of each live page are compared
+        filled = torch.zeros(len(live), bs, dtype=torch.bool)
+        k = 0
+        for b in range(batch):
+            for j in range(int(-(-r_ent[b] // bs))):
+                filled[k, : min(bs, int(r_ent[b]) - j * bs)] = True
+                k += 1
+        assert torch.equal(pool.cpu()[live].reshape(-1, row)[filled.reshape(-1)],
+                           q_exp[filled.reshape(-1)])
+    return r_ent
+
+
+@pytest.mark.parametrize("m,channels", [(4, 128), (4, 576), (128, 576)])
+def test_compress_decode_steps(dev, m, channels) -> None:
+    steps = [[1] * 3] * (3 * m + 5)
+    ent = _compress_case(dev, 3, m, channels, steps, fp8=False, seed=m + channels)
+    assert ent.tolist() == [(3 * m + 5) // m] * 3
+
+
+def test_compress_ragged_chunks_fp8(dev) -> None:
+    chunks = [[3, 0, 9], [6, 4, 1], [1, 13, 0], [5, 4, 4], [0, 1, 2], [9, 9, 9]]
+    _compress_case(dev, 3, 4, 576, chunks, fp8=True, seed=7)
+
+
+def test_compress_long_prefill_hca(dev) -> None:
+    _compress_case(dev, 2, 128, 576, [[700, 333], [1, 1], [200, 5]], fp8=True, seed=8)
+
+
+# -------------------------------------------------------------------- FP8 ----
+def test_fp8_quant_append_bit_exact(dev) -> None:
+    from saint_kv import ops
+
+    g = torch.Generator().manual_seed(12)
+    batch, bs, n_pages, n = 4, 8, 64, 37
+    x = torch.randn(batch, n, 576, generator=g)
+    outl = torch.rand(batch, n, 576, generator=g) < 0.01
+    x = torch.where(outl, x * 20, x)
+    x[0, 0, :128] = 0.0                      # zero block -> scale FLT_MIN, codes 0
+    x[1, 2, 128:256] *= 1e-30                # subnormal-range codes
+    x[2, 3, 256:384] = 3e38                  # huge but finite
+    x = x.to(torch.bfloat16)
+    stack = torch.empty(n_pages, dtype=torch.int32, device=dev)
+    top = torch.empty(1, dtype=torch.int32, device=dev)
+    ops.free_stack_init(stack, top)
+    bt = torch.full((batch, 8), -1, dtype=torch.int32, device=dev)
+    lens = torch.zeros(batch, dtype=torch.int32, device=dev)
+    ops.reserve(stack, top, bt, lens, n, bs)
+    pool = torch.zeros(n_pages, bs, 656, dtype=torch.uint8, device=dev)
+    ops.fp8_quant_append(pool, bt, lens, x.to(dev), n)
+    torch.cuda.synchronize()
+    got = torch.zeros(batch, n, 656, dtype=torch.uint8, device=dev)
+    ops.paged_gather(pool, bt, lens, got)
+    exp = ref.fp8_pack_entries(x.reshape(-1, 576)).reshape(batch, n, 656)
+    assert torch.equal(got.cpu(), exp)
+
+
+# ------------------------------------------------------------------ top-k ----
+@pytest.mark.parametrize("n,k", [(64, 16), (16384, 512), (20000, 1024), (100_000, 1024), (5000, 2048)])
+def test_topk_select_distinct(dev, n, k) -> None:
+    from saint_kv import ops
+
+    rng = np.random.default_rng(n + k)
+    rows = 6
+    s = rng.standard_normal((rows, n)).astype(np.float32)
+    n_valid = rng.integers(0, n + 1, size=rows).astype(np.int32)
+    n_valid[0], n_valid[1] = n, min(k // 2, n)
+    out = torch.full((rows, k), -7, dtype=torch.int32, device=dev)
+    ops.topk_select(torch.from_numpy(s).to(dev), _i32(n_valid, dev), n, k, out)
+    exp = ref.topk_select(s, n_valid, k, n)
+    torch.cuda.synchronize()
+    got = _np(out)[:, : exp.shape[1]]
+    assert np.array_equal(got, exp)
+    assert (_np(out)[:, exp.shape[1]:] == -1).all()
+    exp_t = ref.topk_select_torch(torch.from_numpy(s), n_valid, k, n).numpy()
+    assert np.array_equal(got, exp_t)  # distinct scores: identical to torch.topk
+
+
+def test_topk_select_ties_nonfinite_ragged_cols(dev) -> None:
+    from saint_kv import ops
+
+    rng = np.random.default_rng(13)
+    rows, n, k = 5, 40000, 512
+    s = rng.standard_normal((rows, n)).astype(np.float32)
+    s[0] = 0.0                                              # all ties
+    s[1, ::3] = 1.5                                         # many ties at the threshold
+    s[2, :10] = [np.nan, np.inf, -np.inf, 0.0, -0.0, np.nan, 5.0, np.inf, -np.inf, 7.0]
+    s[3] = np.round(s[3] * 4) / 4                           # heavy ties, in LDS range below
+    n_cols = np.array([n, n, 30000, 20000, 100], dtype=np.int32)
+    n_valid = np.array([n, 39000, 30000, 20000, 50], dtype=np.int32)
+    out = torch.full((rows, k), -7, dtype=torch.int32, device=dev)
+    ops.topk_select(torch.from_numpy(s).to(dev), _i32(n_valid, dev), _i32(n_cols, dev), k, out)
+    torch.cuda.synchronize()
+    for r in range(rows):
+        exp = ref.topk_select(s[r:r + 1], n_valid[r:r + 1], k, int(n_cols[r]))[0]
+        assert np.array_equal(_np(out)[r, : len(exp)], exp), r
+        assert (_np(out)[r, len(exp):] == -1).all()
+
+
+def test_topk_select_decode_masks(dev) -> None:
+    from saint_kv import ops
+
+    rng = np.random.default_rng(14)
+    m, k = 4, 512
+    lens = np.array([0, 1, 4, 5, 8, 2049, 65536, 12345], dtype=np.int32)
+    n = int(lens.max() // m)
+    s = rng.standard_normal((len(lens), n)).astype(np.float32)
+    out = torch.full((len(lens), k), -7, dtype=torch.int32, device=dev)
+    ops.topk_select_decode(torch.from_numpy(s).to(dev), _i32(lens, dev), m, k, out)
+    torch.cuda.synchronize()
+    for b, L in enumerate(lens):
+        n_cols = int(L) // m
+        exp = ref.topk_select(s[b:b + 1], np.array([ref.n_valid_blocks(int(L) - 1, m)]), k, n_cols)[0]
+        assert np.array_equal(_np(out)[b, : len(exp)], exp), b
+        assert (_np(out)[b, len(exp):] == -1).all()
+
+
+# ----------------------------------------------------------- top-k gather ----
+@pytest.mark.parametrize("fp8", [False, True])
+def test_topk_gather_paged(dev, fp8) -> None:
+    from saint_kv import ops
+
+    g = torch.Generator().manual_seed(15)
+    rng = np.random.default_rng(15)
+    batch, bs, n_pages, k = 4, 64, 400, 96
+    ent = np.array([5000, 0, 1, 777], dtype=np.int32)
+    stack = torch.empty(n_pages, dtype=torch.int32, device=dev)
+    top = torch.empty(1, dtype=torch.int32, device=dev)
+    order = rng.permutation(n_pages).astype(np.int32)
+    ops.free_stack_init(stack, top, _i32(order, dev))
+    bt = torch.full((batch, 100), -1, dtype=torch.int32, device=dev)
+    n_ent = torch.zeros(batch, dtype=torch.int32, device=dev)
+    ops.reserve(stack, top, bt, n_ent, _i32(ent, dev), bs)
+    x = torch.randn(batch, int(ent.max()), 576, generator=g).to(torch.bfloat16)
+    if fp8:
+        pool = torch.zeros(n_pages, bs, 656, dtype=torch.uint8, device=dev)
+        ops.fp8_quant_append(pool, bt, n_ent, x.to(dev), _i32(ent, dev))
+    else:
+        pool = torch.zeros(n_pages, bs, 576, dtype=torch.bfloat16, device=dev)
+        ops.paged_append(pool, bt, n_ent, x.to(dev), _i32(ent, dev))
+    idx = np.stack([rng.integers(-1, max(int(e), 1), size=k) for e in ent]).astype(np.int32)
+    idx[0, :5] = [-1, 0, 4999, 4998, -1]
+    out = torch.full((batch, k, 576), 9.0, dtype=torch.bfloat16, device=dev)
+    ops.topk_gather(pool, bt, n_ent, _i32(idx, dev), out, 576)
+    torch.cuda.synchronize()
+    src = ref.fp8_unpack_entries(ref.fp8_pack_entries(x.reshape(-1, 576))).reshape(x.shape) if fp8 else x
+    for b in range(batch):
+        for j in range(k):
+            e = max(int(idx[b, j]), 0)
+            exp = src[b, e] if e < ent[b] else torch.zeros(576, dtype=torch.bfloat16)
+            assert torch.equal(out[b, j].cpu(), exp), (b, j)
+
+
+# ------------------------------------------------------ release / compact ----
+def test_release_and_compact(dev) -> None:
+    from saint_kv import ops
+
+    g = torch.Generator().manual_seed(16)
+    rng = np.random.default_rng(16)
+    batch, bs, n_pages = 10, 16, 600
+    order = rng.permutation(n_pages).astype(np.int32)
+    stack = torch.empty(n_pages, dtype=torch.int32, device=dev)
+    top = torch.empty(1, dtype=torch.int32, device=dev)
+    ops.free_stack_init(stack, top, _i32(order, dev))
+    bt = torch.full((batch, 60), -1, dtype=torch.int32, device=dev)
+    lens = torch.zeros(batch, dtype=torch.int32, device=dev)
+    r_stack, r_top = ref.free_stack_init(n_pages, order)
+    r_bt = np.full((batch, 60), -1, dtype=np.int32)
+    r_lens = np.zeros(batch, dtype=np.int32)
+    n = rng.integers(1, 900, size=batch).astype(np.int32)
+    ops.reserve(stack, top, bt, lens, _i32(n, dev), bs)
+    ref.reserve(r_stack, r_top, r_bt, r_lens, n, bs)
+    pool_a = torch.randn(n_pages, bs, 128, generator=g).to(torch.bfloat16).to(dev)
+    pool_b = torch.randint(0, 255, (n_pages, bs, 656), generator=g, dtype=torch.uint8).to(dev)
+    r_pools = [pool_a.cpu(), pool_b.cpu()]
+    before = ref.paged_gather(r_pools[0], r_bt, r_lens, torch.zeros(batch, int(n.max()), 128, dtype=torch.bfloat16))
+    mask = np.zeros(batch, dtype=np.uint8)
+    mask[rng.choice(batch, size=3, replace=False)] = 1
+    status = torch.full((1,), -7, dtype=torch.int32, device=dev)
+    ops.release(stack, top, bt, lens, torch.as_tensor(mask, device=dev), bs, status)
+    st, r_top = ref.release(r_stack, r_top, r_bt, r_lens, mask, bs)
+    torch.cuda.synchronize()
+    assert st == 0 and int(status.item()) == 0
+    assert int(top.item()) == r_top and np.array_equal(_np(stack)[:r_top], r_stack[:r_top])
+    assert np.array_equal(_np(bt), r_bt) and np.array_equal(_np(lens), r_lens)
+    ws = torch.empty(3 * n_pages, dtype=torch.int32, device=dev)
+    info = torch.zeros(2, dtype=torch.int32, device=dev)
+    ops.compact([pool_a, pool_b], bt, lens, bs, stack, top, ws, info)
+    r_stack, r_top, moved = ref.compact(r_pools, r_bt, r_lens, bs)
+    torch.cuda.synchronize()
+    assert np.array_equal(_np(bt), r_bt)
+    assert int(top.item()) == r_top and np.array_equal(_np(stack)[:r_top], r_stack[:r_top])
+    assert _np(info).tolist() == [len(ref.live_pages(r_bt, r_lens, bs)), moved]
+    live = ref.live_pages(r_bt, r_lens, bs)
+    assert torch.equal(pool_a.cpu()[live], r_pools[0][live])
+    assert torch.equal(pool_b.cpu()[live], r_pools[1][live])
+    after = torch.zeros_like(before, device=dev)
+    ops.paged_gather(pool_a, bt, lens, after)
+    for b in range(batch):
+        if not mask[b]:
+            assert torch.equal(after[b, : n[b]].cpu(), before[b, : n[b]])
+    # a double release is refused without touching anything
+    ops.release(stack, top, bt, torch.full_like(lens, 10 * n_pages), torch.ones(batch, dtype=torch.uint8, device=dev), bs, status)
+    torch.cuda.synchronize()
+    assert int(status.item()) in (ref.STATUS_STACK, ref.STATUS_BADARG)
+    assert int(top.item()) == r_top
