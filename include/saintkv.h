@@ -139,14 +139,16 @@ int skv_ring_read(void* dst, int64_t dst_seq_stride_rows, int64_t dst_capacity_r
  * this call is pooled, out[j] = sum_i softmax_i(z[i,j] + bias[i,j]) * c[i,j]
  * (bias fp32 [m, channels]; fp32 math, rounded to bf16), and written as entry
  * floor(p/m) of the paged compressed cache (format SKV_FMT_BF16 or
- * SKV_FMT_FP8, quantized on write).  Tokens of the incomplete block are
- * staged in tail_c / tail_z (bf16 [batch, m, channels], slot = p % m).
- * Pages for the new entries must be reserved beforehand.
+ * SKV_FMT_FP8, quantized on write).  The incomplete block is carried in
+ * tail_state (fp32 [batch, 3, channels]: running max, sum of weights and
+ * weighted sum of its tokens' online softmax), so a block split over several
+ * calls pools to the same value as one call.  Pages for the new entries must
+ * be reserved beforehand.
  * Replaces TokenLevelCompressor pooling (csa.py:79-87) and the block-emission
  * state machine of HCAKVCacheLayer/CSAKVCacheLayer.append
  * (kv_cache.py:170-195, 291-315). */
 int skv_compress_append(void* pool, int64_t entry_bytes, int64_t block_size, int64_t n_pages,
-                        const int32_t* block_table, int64_t bt_stride, void* tail_c, void* tail_z,
+                        const int32_t* block_table, int64_t bt_stride, float* tail_state,
                         const void* c_new, const void* z_new, int64_t in_seq_stride,
                         int64_t in_row_stride, int64_t in_len, const float* bias,
                         const int32_t* seq_lens, const int32_t* n_new, int32_t n_new_uniform,
@@ -217,7 +219,7 @@ typedef struct skv_pool_ref {
   int64_t page_bytes;
 } skv_pool_ref;
 
-/* skv_compact: defragment up to 4 pools sharing one block table.  Live pages
+/* skv_compact: defragment up to 16 pools sharing one block table.  Live pages
  * with id >= n_live move into the free ids < n_live (both ascending), the
  * tables are rewritten and the free stack rebuilt so pops return n_live,
  * n_live+1, ...  workspace: int32 [3*n_pages]; info: int32 [2] receives
@@ -226,6 +228,91 @@ int skv_compact(const skv_pool_ref* pools, int32_t n_pools, int32_t* block_table
                 int64_t bt_stride, const int32_t* seq_lens, int64_t batch, int64_t block_size,
                 int64_t n_pages, int32_t* free_stack, int32_t* free_top, int32_t* workspace,
                 int32_t* info, void* stream);
+
+/* ---- fused decode step ----------------------------------------------------
+ * One decode step (one new token per sequence) of a stack of heterogeneous
+ * layers in four launches, whatever the layer count:
+ *   1 plan    : every sequence's token count +1; for each page group, reserve
+ *               the page of any compressed entry this token completes
+ *               (skv_reserve policy, groups in order; all-or-nothing: on a
+ *               refusal nothing changes and *status gets SKV_STATUS_* bits).
+ *   2 append  : per layer, the token's latent row into its SWA ring; HCA/CSA
+ *               layers fold (c, z) into the running pooling state and emit the
+ *               entry when the block completes (bf16 or fp8); CSA layers do
+ *               the same for the indexer stream (bf16 entries).
+ *   3 top-k   : per CSA layer, skv_topk_select_decode over its score row.
+ *   4 gather  : CSA layers gather their top_k picks (fp8 dequantized to bf16;
+ *               -1 reads entry 0, picks without an entry give zero rows); HCA
+ *               layers copy all their entries (dense read, rows past the
+ *               sequence's entries are left untouched); every layer copies the
+ *               last min(window, L) tokens of its ring in position order.
+ * Mirrors one cached step of CSA/HCA/SWAttention.forward over a
+ * KVCacheBundle (model.py:294-315; csa.py:299-331; hca.py:110-141;
+ * swa.py:107-125).  The kernels read the descriptor from device memory:
+ * device_desc must hold a copy of *host_desc (uploaded by the caller).
+ * batch <= 1024, up to 16 layers and 4 page groups. */
+#define SKV_MAX_LAYERS 16
+#define SKV_MAX_GROUPS 4
+#define SKV_LAYER_SWA 0
+#define SKV_LAYER_HCA 1
+#define SKV_LAYER_CSA 2
+
+typedef struct skv_page_group {
+  int32_t* free_stack;  /* [n_pages] */
+  int32_t* free_top;    /* [1] */
+  int64_t n_pages;
+  int32_t* block_table; /* [batch, bt_stride] */
+  int64_t bt_stride;
+  int32_t* n_entries;   /* [batch] compressed entries per sequence */
+  int32_t m;            /* compression rate of every layer of the group */
+  int32_t block_size;   /* entries per page */
+} skv_page_group;
+
+typedef struct skv_decode_layer {
+  int32_t kind;           /* SKV_LAYER_* */
+  int32_t group;          /* page group of an HCA/CSA layer */
+  int32_t format;         /* SKV_FMT_* of the main compressed stream */
+  int32_t top_k;          /* CSA: picks per query (<= 2048) */
+  void* ring;             /* [batch, window, latent] bf16 */
+  void* pool;             /* main stream pages: [n_pages, block_size, entry_bytes] */
+  int64_t entry_bytes;
+  float* state;           /* [batch, 3, latent] fp32 pooling state */
+  const float* bias;      /* [m, latent] fp32 */
+  void* idx_pool;         /* CSA indexer stream: [n_pages, block_size, c_indexer] bf16 */
+  float* idx_state;       /* [batch, 3, c_indexer] */
+  const float* idx_bias;  /* [m, c_indexer] */
+  const void* kv_new;     /* [batch, latent] bf16: the new token's latent row */
+  const void* c_new;      /* [batch, latent] bf16: compressor projections */
+  const void* z_new;
+  const void* ci_new;     /* [batch, c_indexer] bf16: indexer compressor projections */
+  const void* zi_new;
+  const float* scores;    /* CSA: [batch, score_stride] fp32 indexer scores */
+  int64_t score_stride;
+  int32_t* topk_idx;      /* CSA out: [batch, top_k] */
+  void* out_entries;      /* CSA: [batch, top_k, latent]; HCA: [batch, out_rows, latent] bf16 */
+  int64_t out_rows;       /* HCA: rows per sequence of out_entries */
+  void* out_window;       /* [batch, window, latent] bf16 */
+} skv_decode_layer;
+
+typedef struct skv_decode_desc {
+  int32_t batch;
+  int32_t n_layers;
+  int32_t n_groups;
+  int32_t latent;         /* channels of the ring rows and main entries (multiple of 8) */
+  int32_t c_indexer;      /* channels of the indexer stream (multiple of 8) */
+  int32_t window;         /* SWA ring rows */
+  int32_t* tok_lens;      /* [batch] tokens per sequence */
+  int32_t* status;        /* [1] */
+  skv_page_group groups[SKV_MAX_GROUPS];
+  skv_decode_layer layers[SKV_MAX_LAYERS];
+} skv_decode_desc;
+
+int skv_decode_step(const skv_decode_desc* host_desc, const skv_decode_desc* device_desc,
+                    void* stream);
+
+/* sizeof(skv_decode_desc), sizeof(skv_decode_layer), sizeof(skv_page_group)
+ * written to out[0..2], so bindings can check their struct layout. */
+int skv_decode_desc_sizes(int64_t* out);
 
 #ifdef __cplusplus
 }

@@ -9,15 +9,13 @@
 //     combined = cat(h_buffer[:, :cnt], h_new); n_complete = total // m;
 //     blocks -> compressed[:, nb:nb+n_complete]; leftover -> h_buffer
 //   FP8 quantize-on-write (quant/reference.py:75-110) on each 128-dim block.
-// Here the buffered state is the per-token (c, z) pair of the incomplete block
-// (the projections are per-token, so buffering them is equivalent to
-// buffering h and projecting at emission).
-#include "skv_entry.h"
+// Here the buffered state of the incomplete block is the running online-softmax
+// state of each channel (max, sum, weighted sum; fp32 [batch, 3, channels]),
+// so a decode step costs O(channels) whatever m is, and a block emits from
+// that state the same value a one-shot pooling of its m tokens gives.
+#include "skv_pool_state.h"
 
 namespace skv {
-
-constexpr int kPoolWave = 64;
-constexpr int kMaxGroups = 4;  // 8-channel groups per lane: channels <= 64*8*4 = 2048
 
 struct CompressArgs {
   uint8_t* pool;
@@ -26,8 +24,7 @@ struct CompressArgs {
   int64_t n_pages;
   const int32_t* bt;
   int64_t bt_stride;
-  uint16_t* tail_c;
-  uint16_t* tail_z;
+  float* state;  // [batch, 3, channels]: running max, sum of weights, weighted sum
   const uint8_t* c_new;
   const uint8_t* z_new;
   int64_t in_seq_stride;
@@ -43,19 +40,32 @@ struct CompressArgs {
   int fp8_main;  // main (quantized) channels in FP8 format
 };
 
-// Row pointer of token position p of sequence b (tail slot or new input row).
-__device__ __forceinline__ const uint16_t* token_row(const CompressArgs& a, const uint16_t* tail,
-                                                     const uint8_t* in, int b, int64_t p,
-                                                     int64_t first_new) {
-  if (p < first_new) {
-    return tail + (static_cast<int64_t>(b) * a.m + (p % a.m)) * a.channels;
-  }
-  const int64_t i = p - first_new;
-  return reinterpret_cast<const uint16_t*>(in + b * a.in_seq_stride + i * a.in_row_stride);
+__device__ __forceinline__ void state_emit(const PoolState& st, const CompressArgs& a, int b, int64_t e,
+                                           int lane, int groups) {
+  const int64_t page_idx = e / a.bs;
+  const int32_t page = (page_idx < a.bt_stride) ? a.bt[b * a.bt_stride + page_idx] : -1;
+  if (page < 0 || page >= a.n_pages) return;  // wave-uniform
+  uint8_t* entry = a.pool + (static_cast<int64_t>(page) * a.bs + e % a.bs) * a.entry_bytes;
+  state_emit_entry(st, entry, lane, groups, a.format, a.fp8_main);
 }
 
-// grid: (units, batch); block: one wave.  Unit k of sequence b pools completed
-// block e0 + k; unit 0 then stages the incomplete block's new tokens.
+// Token rows [p0, p1) of sequence b (all new in this call) folded into st.
+__device__ __forceinline__ void fold_tokens(PoolState& st, const CompressArgs& a, int b, int64_t first_new,
+                                            int64_t p0, int64_t p1, int lane, int groups) {
+  for (int64_t p = p0; p < p1; ++p) {
+    const int64_t i = p - first_new;
+    const uint16_t* crow = reinterpret_cast<const uint16_t*>(a.c_new + b * a.in_seq_stride + i * a.in_row_stride);
+    const uint16_t* zrow = reinterpret_cast<const uint16_t*>(a.z_new + b * a.in_seq_stride + i * a.in_row_stride);
+    state_update(st, crow, zrow, a.bias + (p % a.m) * a.channels, lane, groups);
+  }
+}
+
+// grid: (units, batch); block: one wave.
+//   unit 0      : block e0 (continuing from the stored state when the previous
+//                 call left it incomplete); then, if further blocks complete and
+//                 the last one stays incomplete, the state of that last block.
+//   unit k >= 1 : complete block e0 + k (only new tokens).
+// Only unit 0 touches the state buffer of its sequence.
 __global__ __launch_bounds__(kPoolWave) void k_compress_append(CompressArgs a) {
   const int b = blockIdx.y;
   const int k = blockIdx.x;
@@ -69,82 +79,35 @@ __global__ __launch_bounds__(kPoolWave) void k_compress_append(CompressArgs a) {
   const int64_t nb = e1 - e0;
   if (k >= max<int64_t>(nb, 1)) return;
   const int groups = a.channels >> 3;
-
-  if (k < nb) {
-    const int64_t e = e0 + k;
-    float acc[kMaxGroups][8], mx[kMaxGroups][8], sum[kMaxGroups][8];
-#pragma unroll
-    for (int g = 0; g < kMaxGroups; ++g)
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        acc[g][j] = 0.f;
-        mx[g][j] = -INFINITY;
-        sum[g][j] = 0.f;
-      }
-    for (int i = 0; i < a.m; ++i) {
-      const int64_t p = e * a.m + i;
-      const uint16_t* crow = token_row(a, a.tail_c, a.c_new, b, p, first_new);
-      const uint16_t* zrow = token_row(a, a.tail_z, a.z_new, b, p, first_new);
-      const float* brow = a.bias + static_cast<int64_t>(i) * a.channels;
-#pragma unroll
-      for (int g = 0; g < kMaxGroups; ++g) {
-        const int grp = lane + g * kPoolWave;
-        if (grp >= groups) break;
-        float c[8], z[8];
-        unpack8_bf16(*reinterpret_cast<const u32x4*>(crow + grp * 8), c);
-        unpack8_bf16(*reinterpret_cast<const u32x4*>(zrow + grp * 8), z);
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          const float v = z[j] + brow[grp * 8 + j];
-          // online softmax over the m tokens of this channel
-          if (v > mx[g][j]) {
-            const float s = expf(mx[g][j] - v);
-            sum[g][j] = sum[g][j] * s + 1.f;
-            acc[g][j] = acc[g][j] * s + c[j];
-            mx[g][j] = v;
-          } else {
-            const float w = expf(v - mx[g][j]);
-            sum[g][j] += w;
-            acc[g][j] += w * c[j];
-          }
-        }
-      }
-    }
-    const int64_t page_idx = e / a.bs;
-    const int32_t page = (page_idx < a.bt_stride) ? a.bt[b * a.bt_stride + page_idx] : -1;
-    if (page >= 0 && page < a.n_pages) {
-      uint8_t* entry = a.pool + (static_cast<int64_t>(page) * a.bs + e % a.bs) * a.entry_bytes;
-#pragma unroll
-      for (int g = 0; g < kMaxGroups; ++g) {
-        const int grp = lane + g * kPoolWave;
-        // every lane takes part in the shuffles; only lanes with a group store
-        float out[8];
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          const float r = (grp < groups) ? acc[g][j] / sum[g][j] : 0.f;
-          out[j] = bf16_to_f32(f32_to_bf16(r));  // the compressor emits bf16 entries
-        }
-        store_entry_group(entry, out, grp, groups, a.format, a.fp8_main);
-      }
-    }
-  }
-
+  float* sbase = a.state + static_cast<int64_t>(b) * 3 * a.channels;
+  PoolState st;
   if (k == 0) {
-    // Stage the new tokens of the still-incomplete block e1 (positions >= e1*m).
-    // Each lane rewrites only the channels it read above, after its own loads.
-    __syncthreads();
-    const int64_t p0 = max(first_new, e1 * a.m);
-    for (int64_t p = p0; p < L; ++p) {
-      const int64_t i = p - first_new;
-      const int64_t slot = (static_cast<int64_t>(b) * a.m + (p % a.m)) * a.channels;
-      const uint16_t* crow = reinterpret_cast<const uint16_t*>(a.c_new + b * a.in_seq_stride + i * a.in_row_stride);
-      const uint16_t* zrow = reinterpret_cast<const uint16_t*>(a.z_new + b * a.in_seq_stride + i * a.in_row_stride);
-      for (int grp = lane; grp < groups; grp += kPoolWave) {
-        *reinterpret_cast<u32x4*>(a.tail_c + slot + grp * 8) = *reinterpret_cast<const u32x4*>(crow + grp * 8);
-        *reinterpret_cast<u32x4*>(a.tail_z + slot + grp * 8) = *reinterpret_cast<const u32x4*>(zrow + grp * 8);
-      }
+    if (first_new % a.m != 0) {
+      state_load(st, sbase, a.channels, lane, groups);
+    } else {
+      state_reset(st);
     }
+    const int64_t p1 = min(L, (e0 + 1) * a.m);
+    fold_tokens(st, a, b, first_new, first_new, p1, lane, groups);
+    if (p1 == (e0 + 1) * a.m) {
+      state_emit(st, a, b, e0, lane, groups);
+      if (nb >= 1 && L % a.m != 0) {
+        // the incomplete last block e1 starts fresh; its state replaces the
+        // one loaded above (same lanes, after the loads retired)
+        __syncthreads();
+        state_reset(st);
+        fold_tokens(st, a, b, first_new, e1 * a.m, L, lane, groups);
+        state_store(st, sbase, a.channels, lane, groups);
+      }
+    } else {
+      state_store(st, sbase, a.channels, lane, groups);
+    }
+    return;
   }
+  const int64_t e = e0 + k;
+  state_reset(st);
+  fold_tokens(st, a, b, first_new, e * a.m, (e + 1) * a.m, lane, groups);
+  state_emit(st, a, b, e, lane, groups);
 }
 
 }  // namespace skv
@@ -153,7 +116,7 @@ using namespace skv;
 
 extern "C" int skv_compress_append(void* pool, int64_t entry_bytes, int64_t block_size,
                                    int64_t n_pages, const int32_t* block_table, int64_t bt_stride,
-                                   void* tail_c, void* tail_z, const void* c_new, const void* z_new,
+                                   float* tail_state, const void* c_new, const void* z_new,
                                    int64_t in_seq_stride, int64_t in_row_stride, int64_t in_len,
                                    const float* bias, const int32_t* seq_lens, const int32_t* n_new,
                                    int32_t n_new_uniform, int64_t m, int64_t channels,
@@ -175,8 +138,8 @@ extern "C" int skv_compress_append(void* pool, int64_t entry_bytes, int64_t bloc
                      what, (long long)entry_bytes, format, (long long)channels, SKV_FP8_ROPE_DIMS,
                      (long long)SKV_FP8_ENTRY_BYTES(channels));
   }
-  const uintptr_t align = reinterpret_cast<uintptr_t>(pool) | reinterpret_cast<uintptr_t>(tail_c) |
-                          reinterpret_cast<uintptr_t>(tail_z) | reinterpret_cast<uintptr_t>(c_new) |
+  const uintptr_t align = reinterpret_cast<uintptr_t>(pool) | reinterpret_cast<uintptr_t>(tail_state) |
+                          reinterpret_cast<uintptr_t>(c_new) |
                           reinterpret_cast<uintptr_t>(z_new) | static_cast<uintptr_t>(in_seq_stride) |
                           static_cast<uintptr_t>(in_row_stride);
   if (align & 15) return set_error(SKV_EINVAL, "%s: pointers and strides must be 16-byte aligned", what);
@@ -190,8 +153,7 @@ extern "C" int skv_compress_append(void* pool, int64_t entry_bytes, int64_t bloc
   a.n_pages = n_pages;
   a.bt = block_table;
   a.bt_stride = bt_stride;
-  a.tail_c = static_cast<uint16_t*>(tail_c);
-  a.tail_z = static_cast<uint16_t*>(tail_z);
+  a.state = tail_state;
   a.c_new = static_cast<const uint8_t*>(c_new);
   a.z_new = static_cast<const uint8_t*>(z_new);
   a.in_seq_stride = in_seq_stride;

@@ -1,0 +1,363 @@
+// Fused decode step over a stack of heterogeneous layers: four launches per
+// step whatever the number of layers (plan, append/compress, top-k, gather).
+//
+// Reference: one cached decode call of SaintLLM.forward walks the blocks and
+// hands each attention its cache layer (model.py:294-315); the per-layer cache
+// work is SWAKVCacheLayer/HCAKVCacheLayer/CSAKVCacheLayer.append
+// (kv_cache.py:63-83, 138-202, 266-322), the CSA indexer top-k
+// (csa.py:377-422), the sparse gather (csa.py:326-331), the HCA dense read
+// (hca.py:126-141) and the SWA window (swa.py:115-125).
+#include "skv_pool_state.h"
+#include "skv_topk.h"
+
+namespace skv {
+
+constexpr int kDecodeMaxBatch = 1024;
+constexpr int kPlanThreads = 1024;
+constexpr int kGatherThreadsD = 256;
+constexpr int kGatherRowsD = 8;
+
+// ---------------------------------------------------------------------------
+// 1. plan: token counts +1 and page reservation of every group.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(kPlanThreads) void k_decode_plan(const skv_decode_desc* __restrict__ d) {
+  __shared__ int off[SKV_MAX_GROUPS][kDecodeMaxBatch + 1];
+  __shared__ int first[SKV_MAX_GROUPS][kDecodeMaxBatch];
+  __shared__ int total[SKV_MAX_GROUPS];
+  __shared__ int scan_lds[17];
+  __shared__ int bad_all;
+  const int tid = threadIdx.x;
+  const int batch = d->batch;
+  if (tid == 0) bad_all = 0;
+  __syncthreads();
+  int bad = 0;
+  for (int g = 0; g < d->n_groups; ++g) {
+    const skv_page_group& G = d->groups[g];
+    int need = 0;
+    if (tid < batch) {
+      const int L1 = d->tok_lens[tid] + 1;
+      const int cur = G.n_entries[tid];
+      const int target = L1 / G.m;
+      if (target < cur) {
+        bad |= SKV_STATUS_BADARG;
+      } else {
+        const int64_t p0 = ceil_div(cur, G.block_size);
+        const int64_t p1 = ceil_div(target, G.block_size);
+        if (p1 > G.bt_stride) bad |= SKV_STATUS_MAX_PAGES;
+        need = static_cast<int>(p1 - p0);
+        first[g][tid] = static_cast<int>(p0);
+      }
+    }
+    int tot;
+    const int ex = block_exclusive_scan(need, scan_lds, &tot);
+    if (tid < batch) off[g][tid] = ex;
+    if (tid == 0) {
+      off[g][batch] = tot;
+      total[g] = tot;
+    }
+    const int top = *G.free_top;
+    if (top < 0 || top > G.n_pages) bad |= SKV_STATUS_BADARG;
+    else if (tot > top) bad |= SKV_STATUS_NOSPC;
+  }
+  if (bad) atomicOr(&bad_all, bad);
+  __syncthreads();
+  if (bad_all) {
+    if (tid == 0) *d->status = bad_all;
+    return;
+  }
+  for (int g = 0; g < d->n_groups; ++g) {
+    const skv_page_group& G = d->groups[g];
+    const int top = *G.free_top;
+    const int tot = total[g];
+    for (int t = tid; t < tot; t += kPlanThreads) {
+      int lo = 0, hi = batch;
+      while (hi - lo > 1) {
+        const int mid = (lo + hi) >> 1;
+        if (off[g][mid] <= t) lo = mid; else hi = mid;
+      }
+      G.block_table[static_cast<int64_t>(lo) * G.bt_stride + first[g][lo] + (t - off[g][lo])] =
+          G.free_stack[top - 1 - t];
+    }
+    __syncthreads();  // every thread has read free_top before it moves
+    if (tid < batch) G.n_entries[tid] = (d->tok_lens[tid] + 1) / G.m;
+    if (tid == 0) *G.free_top = top - tot;
+  }
+  __syncthreads();  // n_entries used the old token count
+  if (tid < batch) d->tok_lens[tid] += 1;
+  if (tid == 0) *d->status = 0;
+}
+
+// ---------------------------------------------------------------------------
+// 2. append: ring row, pooling state fold / entry emission.  grid (batch, layers)
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ void decode_fold(const skv_page_group& G, int b, int64_t p, void* pool,
+                                            int64_t entry_bytes, float* state, const float* bias,
+                                            const void* c_all, const void* z_all, int channels,
+                                            int format, int fp8_main, int lane) {
+  const int groups = channels >> 3;
+  float* sbase = state + static_cast<int64_t>(b) * 3 * channels;
+  const uint16_t* crow = static_cast<const uint16_t*>(c_all) + static_cast<int64_t>(b) * channels;
+  const uint16_t* zrow = static_cast<const uint16_t*>(z_all) + static_cast<int64_t>(b) * channels;
+  PoolState st;
+  if (p % G.m != 0) {
+    state_load(st, sbase, channels, lane, groups);
+  } else {
+    state_reset(st);
+  }
+  state_update(st, crow, zrow, bias + (p % G.m) * channels, lane, groups);
+  if ((p + 1) % G.m == 0) {
+    const int64_t e = (p + 1) / G.m - 1;
+    const int64_t pi = e / G.block_size;
+    const int32_t page = (pi < G.bt_stride) ? G.block_table[b * G.bt_stride + pi] : -1;
+    if (page >= 0 && page < G.n_pages) {
+      uint8_t* entry = static_cast<uint8_t*>(pool) +
+                       (static_cast<int64_t>(page) * G.block_size + e % G.block_size) * entry_bytes;
+      state_emit_entry(st, entry, lane, groups, format, fp8_main);
+    }
+  } else {
+    state_store(st, sbase, channels, lane, groups);
+  }
+}
+
+__global__ __launch_bounds__(kPoolWave) void k_decode_append(const skv_decode_desc* __restrict__ d) {
+  const int b = blockIdx.x;
+  const skv_decode_layer& Ly = d->layers[blockIdx.y];
+  const int lane = threadIdx.x;
+  const int L = d->tok_lens[b];
+  if (L <= 0) return;
+  const int64_t p = L - 1;
+  // ring row of the token
+  const int row_chunks = d->latent >> 3;  // 16-byte chunks of a bf16 row
+  const u32x4* src = static_cast<const u32x4*>(Ly.kv_new) + static_cast<int64_t>(b) * row_chunks;
+  u32x4* dst = static_cast<u32x4*>(Ly.ring) + (static_cast<int64_t>(b) * d->window + p % d->window) * row_chunks;
+  for (int c = lane; c < row_chunks; c += kPoolWave) dst[c] = src[c];
+  if (Ly.kind == SKV_LAYER_SWA) return;
+  const skv_page_group& G = d->groups[Ly.group];
+  const int fp8_main = (Ly.format == SKV_FMT_FP8) ? d->latent - SKV_FP8_ROPE_DIMS : 0;
+  decode_fold(G, b, p, Ly.pool, Ly.entry_bytes, Ly.state, Ly.bias, Ly.c_new, Ly.z_new, d->latent,
+              Ly.format, fp8_main, lane);
+  if (Ly.kind == SKV_LAYER_CSA && Ly.idx_pool) {
+    decode_fold(G, b, p, Ly.idx_pool, static_cast<int64_t>(d->c_indexer) * 2, Ly.idx_state, Ly.idx_bias,
+                Ly.ci_new, Ly.zi_new, d->c_indexer, SKV_FMT_BF16, 0, lane);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// 3. top-k: grid (batch, CSA layers)
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(kTopkThreads) void k_decode_topk(const skv_decode_desc* __restrict__ d) {
+  __shared__ TopkSmem sm;
+  const int b = blockIdx.x;
+  int want = blockIdx.y, li = 0;
+  for (; li < d->n_layers; ++li) {
+    if (d->layers[li].kind == SKV_LAYER_CSA && want-- == 0) break;
+  }
+  if (li >= d->n_layers) return;  // uniform over the workgroup
+  const skv_decode_layer& Ly = d->layers[li];
+  const skv_page_group& G = d->groups[Ly.group];
+  const int L = d->tok_lens[b];
+  const int n_cols = L / G.m;
+  const int n_valid = L > 0 ? (L - 1) / G.m : 0;
+  topk_row(sm, Ly.scores + static_cast<int64_t>(b) * Ly.score_stride, n_cols, n_valid, Ly.top_k,
+           Ly.topk_idx + static_cast<int64_t>(b) * Ly.top_k);
+}
+
+// ---------------------------------------------------------------------------
+// 4. gather: grid (tiles, batch, layers); a tile is 8 output rows of the
+//    layer's row space [entries (top_k or out_rows) | window].
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ void dequant_chunk(const uint8_t* entry, int fp8_main, int c, u32x4& o0, u32x4& o1) {
+  const u32x4 codes = *(reinterpret_cast<const u32x4*>(entry) + c);
+  const float scale = *reinterpret_cast<const float*>(entry + fp8_main + (c >> 3) * 4);
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    float f[4];
+#pragma unroll
+    for (int h = 0; h < 4; ++h) f[h] = e4m3fn_to_f32(static_cast<uint8_t>(codes[q] >> (8 * h))) * scale;
+    const uint32_t lo = f32_to_bf16(f[0]) | (static_cast<uint32_t>(f32_to_bf16(f[1])) << 16);
+    const uint32_t hi = f32_to_bf16(f[2]) | (static_cast<uint32_t>(f32_to_bf16(f[3])) << 16);
+    if (q < 2) {
+      o0[2 * q] = lo;
+      o0[2 * q + 1] = hi;
+    } else {
+      o1[2 * (q - 2)] = lo;
+      o1[2 * (q - 2) + 1] = hi;
+    }
+  }
+}
+
+__global__ __launch_bounds__(kGatherThreadsD) void k_decode_gather(const skv_decode_desc* __restrict__ d) {
+  __shared__ const uint8_t* src_row[kGatherRowsD];
+  __shared__ uint8_t* dst_row[kGatherRowsD];
+  __shared__ int row_kind[kGatherRowsD];  // 0 skip, 1 copy bf16 row, 2 dequant fp8 entry, 3 zero row
+  const int b = blockIdx.y;
+  const skv_decode_layer& Ly = d->layers[blockIdx.z];
+  const int latent = d->latent;
+  const int64_t out_row = static_cast<int64_t>(latent) * 2;
+  const int L = d->tok_lens[b];
+  int n_entry_rows = 0;
+  if (Ly.kind == SKV_LAYER_CSA) n_entry_rows = Ly.top_k;
+  else if (Ly.kind == SKV_LAYER_HCA) n_entry_rows = static_cast<int>(Ly.out_rows);
+  const int n_rows = n_entry_rows + d->window;
+  const int r0 = blockIdx.x * kGatherRowsD;
+  if (r0 >= n_rows) return;
+  if (threadIdx.x < kGatherRowsD) {
+    const int r = r0 + threadIdx.x;
+    int kind = 0;
+    const uint8_t* s = nullptr;
+    uint8_t* o = nullptr;
+    if (r < n_entry_rows) {
+      const skv_page_group& G = d->groups[Ly.group];
+      const int n_ent = G.n_entries[b];
+      int e;
+      if (Ly.kind == SKV_LAYER_CSA) {
+        e = Ly.topk_idx[static_cast<int64_t>(b) * Ly.top_k + r];
+        if (e < 0) e = 0;  // clamp(min=0): a -1 pick reads entry 0
+        o = static_cast<uint8_t*>(Ly.out_entries) + (static_cast<int64_t>(b) * Ly.top_k + r) * out_row;
+        kind = 3;
+      } else {
+        e = r;
+        o = static_cast<uint8_t*>(Ly.out_entries) + (static_cast<int64_t>(b) * Ly.out_rows + r) * out_row;
+        kind = 0;  // dense rows past the entries stay untouched
+      }
+      if (e < n_ent) {
+        const int64_t pi = e / G.block_size;
+        const int32_t page = (pi < G.bt_stride) ? G.block_table[b * G.bt_stride + pi] : -1;
+        if (page >= 0 && page < G.n_pages) {
+          s = static_cast<const uint8_t*>(Ly.pool) +
+              (static_cast<int64_t>(page) * G.block_size + e % G.block_size) * Ly.entry_bytes;
+          kind = (Ly.format == SKV_FMT_FP8) ? 2 : 1;
+        }
+      }
+    } else if (r < n_rows) {
+      const int w = r - n_entry_rows;
+      const int cnt = min(max(L, 0), d->window);
+      if (w < cnt) {
+        const int64_t slot = (static_cast<int64_t>(L) - cnt + w) % d->window;
+        s = static_cast<const uint8_t*>(Ly.ring) + (static_cast<int64_t>(b) * d->window + slot) * out_row;
+        o = static_cast<uint8_t*>(Ly.out_window) + (static_cast<int64_t>(b) * d->window + w) * out_row;
+        kind = 1;
+      }
+    }
+    src_row[threadIdx.x] = s;
+    dst_row[threadIdx.x] = o;
+    row_kind[threadIdx.x] = kind;
+  }
+  __syncthreads();
+  const int bf_chunks = latent >> 3;                 // 16-byte chunks of an output row
+  const int fp8_main = latent - SKV_FP8_ROPE_DIMS;
+  const int code_chunks = fp8_main >> 4;             // 16 codes -> 2 output chunks
+  const int rope_chunks = SKV_FP8_ROPE_DIMS >> 3;
+  const int fp8_tasks = code_chunks + rope_chunks;
+  // bf16 copies and zero rows: one task per output chunk
+  for (int t = threadIdx.x; t < kGatherRowsD * bf_chunks; t += kGatherThreadsD) {
+    const int rr = t / bf_chunks;
+    const int c = t - rr * bf_chunks;
+    const int kind = row_kind[rr];
+    if (kind == 1) {
+      st_stream(reinterpret_cast<u32x4*>(dst_row[rr]) + c, *(reinterpret_cast<const u32x4*>(src_row[rr]) + c));
+    } else if (kind == 3) {
+      st_stream(reinterpret_cast<u32x4*>(dst_row[rr]) + c, u32x4{0u, 0u, 0u, 0u});
+    }
+  }
+  // fp8 entries: one task per 16 codes (two output chunks) or per rope chunk
+  for (int t = threadIdx.x; t < kGatherRowsD * fp8_tasks; t += kGatherThreadsD) {
+    const int rr = t / fp8_tasks;
+    if (row_kind[rr] != 2) continue;
+    const int c = t - rr * fp8_tasks;
+    const uint8_t* s = src_row[rr];
+    u32x4* o = reinterpret_cast<u32x4*>(dst_row[rr]);
+    if (c < code_chunks) {
+      u32x4 o0, o1;
+      dequant_chunk(s, fp8_main, c, o0, o1);
+      st_stream(o + 2 * c, o0);
+      st_stream(o + 2 * c + 1, o1);
+    } else {
+      const int rc = c - code_chunks;
+      st_stream(o + (fp8_main >> 3) + rc,
+                *reinterpret_cast<const u32x4*>(s + fp8_main + (fp8_main >> 7) * 4 + rc * 16));
+    }
+  }
+}
+
+}  // namespace skv
+
+using namespace skv;
+
+extern "C" int skv_decode_desc_sizes(int64_t* out) {
+  if (!out) return set_error(SKV_EINVAL, "skv_decode_desc_sizes: out is NULL");
+  out[0] = sizeof(skv_decode_desc);
+  out[1] = sizeof(skv_decode_layer);
+  out[2] = sizeof(skv_page_group);
+  return SKV_OK;
+}
+
+extern "C" int skv_decode_step(const skv_decode_desc* h, const skv_decode_desc* dd, void* stream) {
+  const char* what = "skv_decode_step";
+  if (!h || !dd) return set_error(SKV_EINVAL, "%s: NULL descriptor", what);
+  if (h->batch < 0 || h->batch > kDecodeMaxBatch) {
+    return set_error(SKV_EINVAL, "%s: batch must be in [0, %d]; got %d", what, kDecodeMaxBatch, h->batch);
+  }
+  if (h->n_layers < 0 || h->n_layers > SKV_MAX_LAYERS || h->n_groups < 0 || h->n_groups > SKV_MAX_GROUPS) {
+    return set_error(SKV_EINVAL, "%s: n_layers <= %d and n_groups <= %d", what, SKV_MAX_LAYERS, SKV_MAX_GROUPS);
+  }
+  if (h->latent <= 0 || (h->latent & 7) || h->latent > kPoolWave * 8 * kMaxGroups ||
+      h->c_indexer < 0 || (h->c_indexer & 7) || h->c_indexer > kPoolWave * 8 * kMaxGroups ||
+      h->window <= 0) {
+    return set_error(SKV_EINVAL, "%s: latent/c_indexer must be multiples of 8 in range and window > 0", what);
+  }
+  if (!h->tok_lens || !h->status) return set_error(SKV_EINVAL, "%s: NULL tok_lens/status", what);
+  for (int g = 0; g < h->n_groups; ++g) {
+    const skv_page_group& G = h->groups[g];
+    if (!G.free_stack || !G.free_top || !G.block_table || !G.n_entries || G.m <= 0 ||
+        G.block_size <= 0 || G.bt_stride <= 0 || G.n_pages <= 0) {
+      return set_error(SKV_EINVAL, "%s: page group %d is incomplete", what, g);
+    }
+  }
+  int n_csa = 0, max_rows = 0;
+  for (int l = 0; l < h->n_layers; ++l) {
+    const skv_decode_layer& Ly = h->layers[l];
+    if (!Ly.ring || !Ly.kv_new || !Ly.out_window) return set_error(SKV_EINVAL, "%s: layer %d lacks ring/kv_new/out_window", what, l);
+    int rows = h->window;
+    if (Ly.kind == SKV_LAYER_HCA || Ly.kind == SKV_LAYER_CSA) {
+      if (Ly.group < 0 || Ly.group >= h->n_groups) return set_error(SKV_EINVAL, "%s: layer %d group out of range", what, l);
+      if (!Ly.pool || !Ly.state || !Ly.bias || !Ly.c_new || !Ly.z_new || !Ly.out_entries) {
+        return set_error(SKV_EINVAL, "%s: layer %d lacks pool/state/bias/c/z/out", what, l);
+      }
+      if (entry_layout(Ly.format, h->latent, Ly.entry_bytes) < 0) {
+        return set_error(SKV_EINVAL, "%s: layer %d entry_bytes %lld does not match format %d", what, l,
+                         (long long)Ly.entry_bytes, Ly.format);
+      }
+      if (Ly.kind == SKV_LAYER_CSA) {
+        if (Ly.top_k <= 0 || Ly.top_k > kMaxTopK || !Ly.scores || !Ly.topk_idx) {
+          return set_error(SKV_EINVAL, "%s: CSA layer %d needs 0 < top_k <= %d, scores and topk_idx", what, l, kMaxTopK);
+        }
+        if (Ly.idx_pool && (!Ly.idx_state || !Ly.idx_bias || !Ly.ci_new || !Ly.zi_new || h->c_indexer <= 0)) {
+          return set_error(SKV_EINVAL, "%s: CSA layer %d indexer stream incomplete", what, l);
+        }
+        ++n_csa;
+        rows += Ly.top_k;
+      } else {
+        if (Ly.out_rows <= 0) return set_error(SKV_EINVAL, "%s: HCA layer %d needs out_rows > 0", what, l);
+        rows += static_cast<int>(Ly.out_rows);
+      }
+    } else if (Ly.kind != SKV_LAYER_SWA) {
+      return set_error(SKV_EINVAL, "%s: layer %d has unknown kind %d", what, l, Ly.kind);
+    }
+    max_rows = max(max_rows, rows);
+  }
+  if (h->batch == 0 || h->n_layers == 0) return SKV_OK;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  hipLaunchKernelGGL(k_decode_plan, dim3(1), dim3(kPlanThreads), 0, s, dd);
+  int rc = check_launch(what);
+  if (rc) return rc;
+  hipLaunchKernelGGL(k_decode_append, dim3(h->batch, h->n_layers), dim3(kPoolWave), 0, s, dd);
+  if ((rc = check_launch(what))) return rc;
+  if (n_csa > 0) {
+    hipLaunchKernelGGL(k_decode_topk, dim3(h->batch, n_csa), dim3(kTopkThreads), 0, s, dd);
+    if ((rc = check_launch(what))) return rc;
+  }
+  const dim3 ggrid(static_cast<unsigned>(ceil_div(max_rows, kGatherRowsD)), h->batch, h->n_layers);
+  hipLaunchKernelGGL(k_decode_gather, ggrid, dim3(kGatherThreadsD), 0, s, dd);
+  return check_launch(what);
+}

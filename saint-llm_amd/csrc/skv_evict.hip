@@ -19,7 +19,7 @@ namespace skv {
 
 constexpr int kEvictThreads = 1024;
 constexpr int kEvictMaxBatch = 4096;
-constexpr int kMaxPools = 4;
+constexpr int kMaxPools = 16;
 
 __device__ __forceinline__ int owner_of(const int* off, int batch, int t) {
   int lo = 0, hi = batch;  // off[lo] <= t < off[hi]

@@ -11,32 +11,9 @@
 //   dequant_from_fp8 (quant/reference.py:114-116): code * scale, then bf16.
 // Order of equal scores: ascending index (a total order; torch leaves ties
 // unspecified).
-#include "skv_common.h"
+#include "skv_topk.h"
 
 namespace skv {
-
-constexpr int kTopkThreads = 1024;
-constexpr int kTopkWaves = kTopkThreads / kWave;
-constexpr int kLdsKeys = 28672;  // rows with at most this many valid scores are staged in LDS
-constexpr int kMaxTopK = 2048;
-
-constexpr uint32_t kKeyNaN = 0xffffffffu;
-constexpr uint32_t kKeyPosInf = 0xff800000u;
-constexpr uint32_t kKeyNegInf = 0x007fffffu;
-
-// Order-preserving map fp32 -> uint32 (larger float -> larger key); -0.0 is
-// folded onto +0.0 and every NaN onto the largest key (torch.topk ranks NaN
-// above +inf).
-__device__ __forceinline__ uint32_t score_key(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return kKeyNaN;
-  if (u == 0x80000000u) u = 0u;
-  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-}
-
-__device__ __forceinline__ bool key_finite(uint32_t k) {
-  return k != kKeyNaN && k != kKeyPosInf && k != kKeyNegInf;
-}
 
 struct TopkArgs {
   const float* scores;
@@ -52,17 +29,8 @@ struct TopkArgs {
 };
 
 __global__ __launch_bounds__(kTopkThreads) void k_topk_select(TopkArgs a) {
-  __shared__ uint32_t keys[kLdsKeys];
-  __shared__ int whist[kTopkWaves][256];
-  __shared__ int hist[256];
-  __shared__ uint32_t cand_key[kMaxTopK];
-  __shared__ int cand_idx[kMaxTopK];
-  __shared__ int scan_lds[17];
-  __shared__ int sh_digit, sh_above, sh_cnt;
-
+  __shared__ TopkSmem sm;
   const int r = blockIdx.x;
-  const int tid = threadIdx.x;
-  const int wid = tid / kWave;
   int n_cols, n_valid;
   if (a.lens) {
     const int L = max(a.lens[r], 0);
@@ -72,106 +40,7 @@ __global__ __launch_bounds__(kTopkThreads) void k_topk_select(TopkArgs a) {
     n_cols = a.n_cols ? a.n_cols[r] : a.n_cols_uni;
     n_valid = a.n_valid[r];
   }
-  n_cols = max(n_cols, 0);
-  n_valid = max(0, min(n_valid, n_cols));
-  const int k_eff = min(a.k, n_cols);
-  const int sel = min(k_eff, n_valid);
-  int32_t* out = a.out + r * a.out_stride;
-  for (int j = sel + tid; j < a.k; j += kTopkThreads) out[j] = -1;
-  if (sel == 0) return;
-
-  const float* row = a.scores + r * a.stride;
-  const bool in_lds = n_valid <= kLdsKeys;
-  if (in_lds) {
-    for (int i = tid; i < n_valid; i += kTopkThreads) keys[i] = score_key(row[i]);
-    __syncthreads();
-  }
-  auto key_at = [&](int i) -> uint32_t { return in_lds ? keys[i] : score_key(row[i]); };
-
-  // ---- radix select: the sel-th largest key, 8 bits per pass ---------------
-  uint32_t prefix = 0, pmask = 0;
-  int remaining = sel;  // rank (1-based) of the target among keys matching prefix
-  int eq_total = 0;
-  for (int pass = 0; pass < 4; ++pass) {
-    const int shift = 24 - 8 * pass;
-    for (int i = tid; i < kTopkWaves * 256; i += kTopkThreads) (&whist[0][0])[i] = 0;
-    __syncthreads();
-    for (int i = tid; i < n_valid; i += kTopkThreads) {
-      const uint32_t key = key_at(i);
-      if ((key & pmask) == prefix) atomicAdd(&whist[wid][(key >> shift) & 255u], 1);
-    }
-    __syncthreads();
-    if (tid < 256) {
-      int s = 0;
-#pragma unroll
-      for (int w = 0; w < kTopkWaves; ++w) s += whist[w][tid];
-      hist[tid] = s;
-    }
-    __syncthreads();
-    // suffix counts: above(d) = sum of hist[d+1..255]; thread t owns bin 255-t
-    {
-      const int bin = 255 - tid;
-      const int v = (tid < 256) ? hist[bin] : 0;
-      int tot;
-      const int ex = block_exclusive_scan(v, scan_lds, &tot);  // count of bins > bin
-      if (tid < 256 && ex < remaining && remaining <= ex + v) {
-        sh_digit = bin;
-        sh_above = ex;
-      }
-      __syncthreads();
-    }
-    const int d = sh_digit;
-    remaining -= sh_above;
-    prefix |= static_cast<uint32_t>(d) << shift;
-    pmask |= 255u << shift;
-    eq_total = hist[d];
-    __syncthreads();
-  }
-  const uint32_t T = prefix;
-  const int need_eq = remaining;  // keys == T to take (smallest indices first)
-  const int n_gt = sel - need_eq;
-
-  // ---- collect the sel winners ------------------------------------------------
-  if (tid == 0) sh_cnt = 0;
-  __syncthreads();
-  for (int i = tid; i < n_valid; i += kTopkThreads) {
-    const uint32_t key = key_at(i);
-    if (key > T || (key == T && eq_total == need_eq)) {
-      const int slot = atomicAdd(&sh_cnt, 1);
-      cand_key[slot] = key;
-      cand_idx[slot] = i;
-    }
-  }
-  __syncthreads();
-  if (eq_total != need_eq) {
-    // ties at the threshold: take the need_eq smallest indices, in index order
-    int carry = 0;
-    for (int base = 0; base < n_valid; base += kTopkThreads) {
-      const int i = base + tid;
-      const int is_eq = (i < n_valid && key_at(i) == T) ? 1 : 0;
-      int tot;
-      const int rank = carry + block_exclusive_scan(is_eq, scan_lds, &tot);
-      if (is_eq && rank < need_eq) {
-        cand_key[n_gt + rank] = T;
-        cand_idx[n_gt + rank] = i;
-      }
-      carry += tot;
-      if (carry >= need_eq) break;  // uniform: carry is the same on every thread
-    }
-    __syncthreads();
-  }
-
-  // ---- order the winners: key descending, index ascending ------------------
-  for (int c = tid; c < sel; c += kTopkThreads) {
-    const uint32_t kc = cand_key[c];
-    const int ic = cand_idx[c];
-    int rank = 0;
-    for (int j = 0; j < sel; ++j) {
-      const uint32_t kj = cand_key[j];
-      rank += (kj > kc) || (kj == kc && cand_idx[j] < ic);
-    }
-    out[rank] = key_finite(kc) ? ic : -1;
-  }
+  topk_row(sm, a.scores + r * a.stride, n_cols, n_valid, a.k, a.out + r * a.out_stride);
 }
 
 // ---------------------------------------------------------------------------

@@ -50,8 +50,8 @@ SIGNATURES: dict[str, list] = {
     "skv_ring_append": [_P, _I64, _I64, _P, _P, _I32, _P, _I64, _I64, _I64, _I64, _P],
     "skv_ring_read": [_P, _I64, _I64, _P, _I64, _I64, _P, _I64, _P],
     "skv_compress_append": [
-        _P, _I64, _I64, _I64, _P, _I64, _P, _P, _P, _P, _I64, _I64, _I64, _P, _P, _P, _I32, _I64,
-        _I64, _I32, _I64, _P,
+        _P, _I64, _I64, _I64, _P, _I64, _P, _P, _P, _I64, _I64, _I64, _P, _P, _P, _I32, _I64, _I64,
+        _I32, _I64, _P,
     ],
     "skv_fp8_quant_append": [
         _P, _I64, _I64, _I64, _P, _I64, _P, _P, _I32, _P, _I64, _I64, _I64, _I64, _I64, _P,
@@ -64,6 +64,8 @@ SIGNATURES: dict[str, list] = {
         _P, _P, _I64, _I64, _I64, _P, _I64, _P, _P, _I64, _I64, _I64, _P, _I64, _I32, _P,
     ],
     "skv_release": [_P, _P, _I64, _P, _I64, _P, _P, _I64, _I64, _P, _P],
+    "skv_decode_step": [_P, _P, _P],
+    "skv_decode_desc_sizes": [_P],
     "skv_compact": [ctypes.c_void_p, _I32, _P, _I64, _P, _I64, _I64, _I64, _P, _P, _P, _P, _P],
 }
 

@@ -1,0 +1,350 @@
+"""Heterogeneous paged KV cache for batched decode (ragged sequences).
+
+``DecodeCache`` holds, for a stack of CSA / HCA / SWA layers:
+
+* per layer an SWA ring of the last ``window`` latent rows (bf16);
+* per CSA/HCA layer a paged compressed cache (bf16 or FP8 entries) whose page
+  ids come from the free stack of the layer's page group (one group per
+  compression rate; layers of a group share the block table, as their entry
+  counts advance in lockstep), plus the fp32 running pooling state of the
+  block being filled;
+* per CSA layer the indexer stream (bf16 entries, same pages).
+
+``step()`` runs one decode step for every sequence through the fused C-ABI
+entry point ``skv_decode_step`` (four launches).  The per-step inputs live in
+fixed device buffers (``inputs``), so a sequence of steps can be captured in a
+HIP graph and replayed.
+
+Reference: the per-layer caches of kv_cache.py:32-327 composed as
+KVCacheBundle (kv_cache.py:333-427) and driven by the cached decode loop
+(generate.py:113-126, model.py:294-315).
+"""
+
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass
+
+import numpy as np
+import torch
+
+from saint_kv import _lib, ops
+
+KIND = {"swa": 0, "hca": 1, "csa": 2}
+MAX_LAYERS = 16
+MAX_GROUPS = 4
+MAX_BATCH = 1024
+
+_P = ctypes.c_void_p
+
+
+class PageGroupC(ctypes.Structure):
+    _fields_ = [
+        ("free_stack", _P), ("free_top", _P), ("n_pages", ctypes.c_int64),
+        ("block_table", _P), ("bt_stride", ctypes.c_int64), ("n_entries", _P),
+        ("m", ctypes.c_int32), ("block_size", ctypes.c_int32),
+    ]
+
+
+class DecodeLayerC(ctypes.Structure):
+    _fields_ = [
+        ("kind", ctypes.c_int32), ("group", ctypes.c_int32), ("format", ctypes.c_int32),
+        ("top_k", ctypes.c_int32), ("ring", _P), ("pool", _P), ("entry_bytes", ctypes.c_int64),
+        ("state", _P), ("bias", _P), ("idx_pool", _P), ("idx_state", _P), ("idx_bias", _P),
+        ("kv_new", _P), ("c_new", _P), ("z_new", _P), ("ci_new", _P), ("zi_new", _P),
+        ("scores", _P), ("score_stride", ctypes.c_int64), ("topk_idx", _P),
+        ("out_entries", _P), ("out_rows", ctypes.c_int64), ("out_window", _P),
+    ]
+
+
+class DecodeDescC(ctypes.Structure):
+    _fields_ = [
+        ("batch", ctypes.c_int32), ("n_layers", ctypes.c_int32), ("n_groups", ctypes.c_int32),
+        ("latent", ctypes.c_int32), ("c_indexer", ctypes.c_int32), ("window", ctypes.c_int32),
+        ("tok_lens", _P), ("status", _P),
+        ("groups", PageGroupC * MAX_GROUPS), ("layers", DecodeLayerC * MAX_LAYERS),
+    ]
+
+
+def check_struct_layout() -> None:
+    """Raise if the ctypes mirrors disagree with the library's struct sizes."""
+    sizes = (ctypes.c_int64 * 3)()
+    _lib.call("skv_decode_desc_sizes", ctypes.cast(sizes, ctypes.c_void_p))
+    mine = (ctypes.sizeof(DecodeDescC), ctypes.sizeof(DecodeLayerC), ctypes.sizeof(PageGroupC))
+    if tuple(sizes) != mine:
+        raise RuntimeError(f"decode descriptor layout mismatch: library {tuple(sizes)} vs ctypes {mine}")
+
+
+@dataclass(frozen=True)
+class LayerSpec:
+    """One attention layer's cache: kind "csa" | "hca" | "swa"."""
+
+    kind: str
+    m: int = 4
+    top_k: int = 512
+    fp8: bool = False
+    indexer: bool = True
+
+
+@dataclass
+class _Group:
+    m: int
+    n_pages: int
+    free_stack: torch.Tensor
+    free_top: torch.Tensor
+    block_table: torch.Tensor
+    n_entries: torch.Tensor
+
+
+class DecodeCache:
+    """Paged heterogeneous cache of ``batch`` ragged sequences on one GPU."""
+
+    def __init__(self, layers: list[LayerSpec], batch: int, max_len: int, *,
+                 latent: int = 576, c_indexer: int = 128, window: int = 128,
+                 block_size: int = 64, device: torch.device | str | None = None,
+                 page_order_seed: int | None = 0, pages_per_group: dict[int, int] | None = None,
+                 hca_out_rows: int | None = None) -> None:
+        if not 0 < len(layers) <= MAX_LAYERS:
+            raise ValueError(f"1..{MAX_LAYERS} layers supported; got {len(layers)}")
+        if not 0 < batch <= MAX_BATCH:
+            raise ValueError(f"batch must be in [1, {MAX_BATCH}]; got {batch}")
+        if max_len <= 0:
+            raise ValueError(f"max_len must be positive; got {max_len}")
+        dev = torch.device("cuda", torch.cuda.current_device()) if device is None else torch.device(device)
+        if dev.type != "cuda":
+            raise RuntimeError("DecodeCache runs only on a ROCm GPU (no CPU fallback)")
+        _lib.load()
+        check_struct_layout()
+        self.device = dev
+        self.layers = list(layers)
+        self.batch, self.max_len = batch, max_len
+        self.latent, self.c_indexer, self.window, self.block_size = latent, c_indexer, window, block_size
+        self.tok_lens = torch.zeros(batch, dtype=torch.int32, device=dev)
+        self.status = torch.zeros(1, dtype=torch.int32, device=dev)
+        self.host_lens = np.zeros(batch, dtype=np.int64)
+
+        # page groups: one per compression rate
+        rates = sorted({s.m for s in layers if s.kind in ("csa", "hca")})
+        if len(rates) > MAX_GROUPS:
+            raise ValueError(f"at most {MAX_GROUPS} distinct compression rates")
+        self.groups: list[_Group] = []
+        self.group_of_rate = {}
+        rng = np.random.default_rng(page_order_seed) if page_order_seed is not None else None
+        for m in rates:
+            max_entries = max_len // m
+            bt_stride = max(1, -(-max_entries // block_size))
+            n_pages = (pages_per_group or {}).get(m, batch * bt_stride)
+            stack = torch.empty(n_pages, dtype=torch.int32, device=dev)
+            top = torch.empty(1, dtype=torch.int32, device=dev)
+            order = None if rng is None else torch.as_tensor(
+                rng.permutation(n_pages).astype(np.int32), device=dev)
+            ops.free_stack_init(stack, top, order)
+            self.group_of_rate[m] = len(self.groups)
+            self.groups.append(_Group(
+                m=m, n_pages=n_pages, free_stack=stack, free_top=top,
+                block_table=torch.full((batch, bt_stride), -1, dtype=torch.int32, device=dev),
+                n_entries=torch.zeros(batch, dtype=torch.int32, device=dev)))
+
+        bf = torch.bfloat16
+        self.ring, self.pool, self.state, self.bias = [], [], [], []
+        self.idx_pool, self.idx_state, self.idx_bias = [], [], []
+        self.inputs: list[dict[str, torch.Tensor]] = []
+        self.scores, self.topk_idx, self.out_entries, self.out_window = [], [], [], []
+        for spec in layers:
+            if spec.kind not in KIND:
+                raise ValueError(f"unknown layer kind {spec.kind!r}")
+            self.ring.append(torch.zeros(batch, window, latent, dtype=bf, device=dev))
+            self.out_window.append(torch.zeros(batch, window, latent, dtype=bf, device=dev))
+            inp = {"kv": torch.zeros(batch, latent, dtype=bf, device=dev)}
+            pool = state = bias = ipool = istate = ibias = sc = tk = oe = None
+            if spec.kind in ("csa", "hca"):
+                g = self.groups[self.group_of_rate[spec.m]]
+                if spec.fp8:
+                    pool = torch.zeros(g.n_pages, block_size, _lib.fp8_entry_bytes(latent),
+                                       dtype=torch.uint8, device=dev)
+                else:
+                    pool = torch.zeros(g.n_pages, block_size, latent, dtype=bf, device=dev)
+                state = torch.zeros(batch, 3, latent, dtype=torch.float32, device=dev)
+                bias = torch.zeros(spec.m, latent, dtype=torch.float32, device=dev)
+                inp["c"] = torch.zeros(batch, latent, dtype=bf, device=dev)
+                inp["z"] = torch.zeros(batch, latent, dtype=bf, device=dev)
+                if spec.kind == "csa":
+                    if spec.indexer:
+                        ipool = torch.zeros(g.n_pages, block_size, c_indexer, dtype=bf, device=dev)
+                        istate = torch.zeros(batch, 3, c_indexer, dtype=torch.float32, device=dev)
+                        ibias = torch.zeros(spec.m, c_indexer, dtype=torch.float32, device=dev)
+                        inp["ci"] = torch.zeros(batch, c_indexer, dtype=bf, device=dev)
+                        inp["zi"] = torch.zeros(batch, c_indexer, dtype=bf, device=dev)
+                    sc = torch.zeros(batch, max(1, max_len // spec.m), dtype=torch.float32, device=dev)
+                    tk = torch.full((batch, spec.top_k), -1, dtype=torch.int32, device=dev)
+                    oe = torch.zeros(batch, spec.top_k, latent, dtype=bf, device=dev)
+                else:
+                    rows = hca_out_rows or max(1, max_len // spec.m)
+                    oe = torch.zeros(batch, rows, latent, dtype=bf, device=dev)
+            self.pool.append(pool)
+            self.state.append(state)
+            self.bias.append(bias)
+            self.idx_pool.append(ipool)
+            self.idx_state.append(istate)
+            self.idx_bias.append(ibias)
+            self.inputs.append(inp)
+            self.scores.append(sc)
+            self.topk_idx.append(tk)
+            self.out_entries.append(oe)
+        self._build_desc()
+
+    # ----------------------------------------------------------- descriptor --
+    def _build_desc(self) -> None:
+        d = DecodeDescC()
+        d.batch, d.n_layers, d.n_groups = self.batch, len(self.layers), len(self.groups)
+        d.latent, d.c_indexer, d.window = self.latent, self.c_indexer, self.window
+        d.tok_lens, d.status = self.tok_lens.data_ptr(), self.status.data_ptr()
+        for i, g in enumerate(self.groups):
+            G = d.groups[i]
+            G.free_stack, G.free_top, G.n_pages = g.free_stack.data_ptr(), g.free_top.data_ptr(), g.n_pages
+            G.block_table, G.bt_stride = g.block_table.data_ptr(), g.block_table.shape[1]
+            G.n_entries, G.m, G.block_size = g.n_entries.data_ptr(), g.m, self.block_size
+        p = _lib.ptr
+        for i, spec in enumerate(self.layers):
+            Ly = d.layers[i]
+            Ly.kind = KIND[spec.kind]
+            Ly.ring, Ly.out_window = p(self.ring[i]), p(self.out_window[i])
+            Ly.kv_new = p(self.inputs[i]["kv"])
+            if spec.kind in ("csa", "hca"):
+                Ly.group = self.group_of_rate[spec.m]
+                Ly.format = _lib.SKV_FMT_FP8 if spec.fp8 else _lib.SKV_FMT_BF16
+                Ly.pool, Ly.entry_bytes = p(self.pool[i]), ops.row_bytes_of(self.pool[i])
+                Ly.state, Ly.bias = p(self.state[i]), p(self.bias[i])
+                Ly.c_new, Ly.z_new = p(self.inputs[i]["c"]), p(self.inputs[i]["z"])
+                Ly.out_entries = p(self.out_entries[i])
+                if spec.kind == "csa":
+                    Ly.top_k = spec.top_k
+                    Ly.scores, Ly.score_stride = p(self.scores[i]), self.scores[i].shape[1]
+                    Ly.topk_idx = p(self.topk_idx[i])
+                    if spec.indexer:
+                        Ly.idx_pool, Ly.idx_state = p(self.idx_pool[i]), p(self.idx_state[i])
+                        Ly.idx_bias = p(self.idx_bias[i])
+                        Ly.ci_new, Ly.zi_new = p(self.inputs[i]["ci"]), p(self.inputs[i]["zi"])
+                else:
+                    Ly.out_rows = self.out_entries[i].shape[1]
+        self._desc = d
+        raw = bytes(memoryview(d))
+        self._desc_dev = torch.tensor(list(raw), dtype=torch.uint8, device=self.device)
+
+    # ------------------------------------------------------------------ step --
+    def step(self) -> None:
+        """One decode step of every sequence from the current ``inputs`` and ``scores``."""
+        if (self.host_lens + 1 > self.max_len).any():
+            raise RuntimeError(f"DecodeCache overflow: a sequence would exceed max_len={self.max_len}")
+        _lib.call("skv_decode_step", ctypes.addressof(self._desc), self._desc_dev.data_ptr(),
+                  _lib.stream_handle(self.device))
+        self.host_lens += 1
+
+    def check_status(self) -> None:
+        """Synchronise and raise if a page reservation was refused."""
+        st = int(self.status.item())
+        if st:
+            raise RuntimeError(f"DecodeCache page reservation refused (status bits {st})")
+
+    # --------------------------------------------------------------- prefill --
+    def prefill(self, lens: np.ndarray, generator: torch.Generator | None = None,
+                data: dict | None = None) -> None:
+        """Bring every sequence from empty to ``lens[b]`` tokens.
+
+        With ``data`` (per layer dicts of bf16 [B, T, ...] tensors "kv", "c", "z",
+        "ci", "zi") the caches are built through the kernels exactly as decode
+        would build them.  Without it the compressed entries and rings are
+        filled with N(0,1) values (synthetic contexts for benchmarking) and the
+        incomplete blocks' states are folded from N(0,1) tokens.
+        """
+        lens = np.asarray(lens, dtype=np.int64)
+        if lens.shape != (self.batch,) or (lens < 0).any() or (lens > self.max_len).any():
+            raise ValueError("lens must be [batch] in [0, max_len]")
+        if (self.host_lens != 0).any():
+            raise RuntimeError("prefill needs empty sequences")
+        dev = self.device
+        lens_t = torch.as_tensor(lens.astype(np.int32), device=dev)
+        for g in self.groups:
+            n_ent = torch.as_tensor((lens // g.m).astype(np.int32), device=dev)
+            ops.reserve(g.free_stack, g.free_top, g.block_table, g.n_entries, n_ent,
+                        self.block_size, self.status)
+        for i, spec in enumerate(self.layers):
+            if data is not None:
+                src = data[i]["kv"]
+                ops.ring_append(self.ring[i], lens_t, src, lens_t)
+            else:
+                self.ring[i].normal_(generator=generator)
+            if spec.kind == "swa":
+                continue
+            g = self.groups[self.group_of_rate[spec.m]]
+            streams = [(self.pool[i], self.state[i], self.bias[i], "c", "z", self.latent)]
+            if spec.kind == "csa" and spec.indexer:
+                streams.append((self.idx_pool[i], self.idx_state[i], self.idx_bias[i], "ci", "zi",
+                                self.c_indexer))
+            for pool, state, bias, kc, kz, ch in streams:
+                if data is not None:
+                    ops.compress_append(pool, g.block_table, state, data[i][kc], data[i][kz], bias,
+                                        lens_t, lens_t)
+                    continue
+                self._fill_entries(pool, g, lens // spec.m, ch, generator)
+                tail = lens % spec.m
+                if tail.max() > 0:
+                    t = int(tail.max())
+                    c = torch.randn(self.batch, t, ch, generator=generator, device=dev).to(torch.bfloat16)
+                    z = torch.randn(self.batch, t, ch, generator=generator, device=dev).to(torch.bfloat16)
+                    ops.compress_append(pool, g.block_table, state, c, z, bias, lens_t,
+                                        torch.as_tensor(tail.astype(np.int32), device=dev))
+        self.tok_lens.copy_(lens_t)
+        self.host_lens = lens.copy()
+        self.check_status()
+
+    def _fill_entries(self, pool: torch.Tensor, g: _Group, n_ent: np.ndarray, ch: int,
+                      generator: torch.Generator | None) -> None:
+        if pool.dtype == torch.bfloat16:
+            for chunk in pool.split(4096):
+                chunk.normal_(generator=generator)
+            return
+        # fp8 pools: quantize N(0,1) rows so every entry is a valid code/scale set
+        step = 16384
+        done = np.zeros_like(n_ent)
+        tmp_lens = torch.zeros(self.batch, dtype=torch.int32, device=self.device)
+        while (done < n_ent).any():
+            n = np.minimum(n_ent - done, step).astype(np.int32)
+            x = torch.randn(self.batch, int(n.max()), ch, generator=generator,
+                            device=self.device).to(torch.bfloat16)
+            tmp_lens.copy_(torch.as_tensor((done + n).astype(np.int32)))
+            ops.fp8_quant_append(pool, g.block_table, tmp_lens, x, torch.as_tensor(n, device=self.device))
+            done += n
+
+    # -------------------------------------------------- eviction / compaction --
+    def release(self, mask: np.ndarray) -> None:
+        """Finish the sequences with mask[b]: their pages return to the free lists."""
+        mask = np.asarray(mask, dtype=bool)
+        if mask.shape != (self.batch,):
+            raise ValueError("mask must be [batch]")
+        if (mask & (self.host_lens == 0)).any():
+            raise RuntimeError("release of a sequence that holds no tokens (double free)")
+        m_dev = torch.as_tensor(mask.astype(np.uint8), device=self.device)
+        for g in self.groups:
+            ops.release(g.free_stack, g.free_top, g.block_table, g.n_entries, m_dev,
+                        self.block_size, self.status)
+        self.tok_lens.masked_fill_(m_dev.bool(), 0)
+        self.host_lens[mask] = 0
+
+    def compact(self, workspace: torch.Tensor | None = None) -> list[tuple[int, int]]:
+        """Defragment every page group; returns [(n_live, n_moved)] per group."""
+        out = []
+        for gi, g in enumerate(self.groups):
+            pools = []
+            for i, spec in enumerate(self.layers):
+                if spec.kind in ("csa", "hca") and self.group_of_rate[spec.m] == gi:
+                    pools.append(self.pool[i])
+                    if self.idx_pool[i] is not None:
+                        pools.append(self.idx_pool[i])
+            ws = workspace if workspace is not None and workspace.numel() >= 3 * g.n_pages else \
+                torch.empty(3 * g.n_pages, dtype=torch.int32, device=self.device)
+            info = torch.zeros(2, dtype=torch.int32, device=self.device)
+            ops.compact(pools, g.block_table, g.n_entries, self.block_size, g.free_stack,
+                        g.free_top, ws[: 3 * g.n_pages], info)
+            out.append(tuple(int(v) for v in info.cpu()))
+        return out

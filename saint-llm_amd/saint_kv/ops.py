@@ -239,15 +239,15 @@ def _entry_format(pool: torch.Tensor, channels: int) -> int:
     )
 
 
-def compress_append(pool: torch.Tensor, block_table: torch.Tensor, tail_c: torch.Tensor,
-                    tail_z: torch.Tensor, c_new: torch.Tensor, z_new: torch.Tensor,
-                    bias: torch.Tensor, seq_lens: torch.Tensor, n_new: int | torch.Tensor) -> int:
+def compress_append(pool: torch.Tensor, block_table: torch.Tensor, tail_state: torch.Tensor,
+                    c_new: torch.Tensor, z_new: torch.Tensor, bias: torch.Tensor,
+                    seq_lens: torch.Tensor, n_new: int | torch.Tensor) -> int:
     """Pool every block of m tokens completed by this append into the paged cache.
 
     ``pool`` is bf16 [n_pages, bs, C] (bf16 entries) or uint8 [n_pages, bs, E]
-    (fp8 entries); ``tail_c``/``tail_z`` bf16 [B, m, C]; ``c_new``/``z_new``
-    bf16 [B, T, C] with identical strides; ``bias`` fp32 [m, C].  Returns the
-    entry format used.
+    (fp8 entries); ``tail_state`` fp32 [B, 3, C] carries the incomplete block;
+    ``c_new``/``z_new`` bf16 [B, T, C] with identical strides; ``bias`` fp32
+    [m, C] (m = compression rate).  Returns the entry format used.
     """
     n_pages, bs, rb = _check_pool(pool)
     _require_i32(block_table, "block_table")
@@ -255,11 +255,10 @@ def compress_append(pool: torch.Tensor, block_table: torch.Tensor, tail_c: torch
     _require_i32(seq_lens, "seq_lens", (batch,))
     channels = c_new.shape[-1]
     fmt = _entry_format(pool, channels)
-    m = tail_c.shape[1]
-    for name, t in (("tail_c", tail_c), ("tail_z", tail_z)):
-        _require_gpu(t, name)
-        if t.dtype != torch.bfloat16 or tuple(t.shape) != (batch, m, channels) or not t.is_contiguous():
-            raise ValueError(f"{name} must be contiguous bf16 [{batch}, {m}, {channels}]")
+    _require_gpu(tail_state, "tail_state")
+    if (tail_state.dtype != torch.float32 or tuple(tail_state.shape) != (batch, 3, channels)
+            or not tail_state.is_contiguous()):
+        raise ValueError(f"tail_state must be contiguous fp32 [{batch}, 3, {channels}]")
     for name, t in (("c_new", c_new), ("z_new", z_new)):
         _require_gpu(t, name)
         if t.dtype != torch.bfloat16 or t.dim() != 3 or t.shape[0] != batch or t.stride(-1) != 1:
@@ -267,12 +266,14 @@ def compress_append(pool: torch.Tensor, block_table: torch.Tensor, tail_c: torch
     if c_new.shape != z_new.shape or c_new.stride() != z_new.stride():
         raise ValueError("c_new and z_new must have the same shape and strides")
     _require_gpu(bias, "bias")
-    if bias.dtype != torch.float32 or tuple(bias.shape) != (m, channels) or not bias.is_contiguous():
-        raise ValueError(f"bias must be contiguous fp32 [{m}, {channels}]")
+    if bias.dtype != torch.float32 or bias.dim() != 2 or bias.shape[1] != channels \
+            or not bias.is_contiguous():
+        raise ValueError(f"bias must be contiguous fp32 [m, {channels}]")
+    m = bias.shape[0]
     n_ptr, n_uni = _n_new_args(n_new, batch)
     es = c_new.element_size()
     _lib.call("skv_compress_append", pool.data_ptr(), rb, bs, n_pages, block_table.data_ptr(),
-              bt_stride, tail_c.data_ptr(), tail_z.data_ptr(), c_new.data_ptr(), z_new.data_ptr(),
+              bt_stride, tail_state.data_ptr(), c_new.data_ptr(), z_new.data_ptr(),
               c_new.stride(0) * es, c_new.stride(1) * es, c_new.shape[1], bias.data_ptr(),
               seq_lens.data_ptr(), n_ptr, n_uni, m, channels, fmt, batch,
               _lib.stream_handle(pool.device))

@@ -72,7 +72,7 @@ def _compress_case(dev, batch, m, channels, chunks, fp8, seed):
     pool = torch.zeros(n_pages, bs, row, dtype=dt, device=dev)
     pool_bf = torch.zeros(n_pages, bs, channels, dtype=torch.bfloat16, device=dev)
     r_pool = torch.zeros(n_pages, bs, channels, dtype=torch.bfloat16)
-    tail = [torch.zeros(batch, m, channels, dtype=torch.bfloat16, device=dev) for _ in range(4)]
+    state = [torch.zeros(batch, 3, channels, dtype=torch.float32, device=dev) for _ in range(2)]
     r_tc = torch.zeros(batch, m, channels, dtype=torch.bfloat16)
     r_tz = torch.zeros(batch, m, channels, dtype=torch.bfloat16)
     bias = torch.randn(m, channels, generator=g)
@@ -88,15 +88,22 @@ def _compress_case(dev, batch, m, channels, chunks, fp8, seed):
         r_status, r_top = ref.reserve(r_stack, r_top, r_bt, r_ent, new_ent, bs)
         assert r_status == 0
         # same staging, two formats: the fp8 run must quantize the bf16 run's values
-        ops.compress_append(pool_bf, bt, tail[0], tail[1], c.to(dev), z.to(dev), bias.to(dev),
+        ops.compress_append(pool_bf, bt, state[0], c.to(dev), z.to(dev), bias.to(dev),
                             _i32(lens, dev), _i32(n, dev))
-        ops.compress_append(pool, bt, tail[2], tail[3], c.to(dev), z.to(dev), bias.to(dev),
+        ops.compress_append(pool, bt, state[1], c.to(dev), z.to(dev), bias.to(dev),
                             _i32(lens, dev), _i32(n, dev))
         ref.compress_append(r_pool, r_bt, r_tc, r_tz, c, z, bias, lens, n)
     torch.cuda.synchronize()
     assert np.array_equal(_np(bt), r_bt) and np.array_equal(_np(n_ent), r_ent)
-    assert torch.equal(tail[0].cpu(), r_tc) and torch.equal(tail[1].cpu(), r_tz)
-    assert torch.equal(tail[2].cpu(), r_tc)
+    # the carried state of each incomplete block pools (acc / sum) to the
+    # oracle's pooling of that block's buffered tokens
+    assert torch.equal(state[0].cpu(), state[1].cpu())
+    for b in range(batch):
+        r = int(lens[b]) % m
+        if r:
+            part = ref.compress_pool(r_tc[b, :r], r_tz[b, :r], bias[:r])
+            st = state[0][b].cpu()
+            torch.testing.assert_close(st[2] / st[1], part, rtol=1e-4, atol=1e-4)
     got = torch.zeros(batch, int(r_ent.max()), channels, dtype=torch.bfloat16, device=dev)
     ops.paged_gather(pool_bf, bt, n_ent, got)
     exp = ref.paged_gather(r_pool, r_bt, r_ent, torch.zeros(got.shape, dtype=torch.bfloat16))

@@ -1,0 +1,240 @@
+"""GPU parity of the fused decode step (skv_decode_step) against the oracle.
+
+A stack of CSA (bf16 and fp8, m=4), HCA (m=128) and SWA layers is prefilled
+through the kernels, then stepped token by token; after every step the tables,
+rings, top-k indices and gathered outputs are compared with the oracle
+composition of reserve / ring / pooling / top-k / gather.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import reference_cpu as ref
+
+pytestmark = pytest.mark.gpu
+
+
+def _np(t):
+    return t.detach().cpu().numpy()
+
+
+class _Oracle:
+    def __init__(self, cache, specs, order_seed):
+        self.specs = specs
+        self.bs = cache.block_size
+        self.m_groups = [g.m for g in cache.groups]
+        rng = np.random.default_rng(order_seed)
+        self.stack, self.top, self.bt, self.ent = [], [], [], []
+        for g in cache.groups:  # same permutation draws as DecodeCache
+            st, top = ref.free_stack_init(g.n_pages, rng.permutation(g.n_pages).astype(np.int32))
+            self.stack.append(st)
+            self.top.append(top)
+            self.bt.append(np.full(tuple(g.block_table.shape), -1, dtype=np.int32))
+            self.ent.append(np.zeros(cache.batch, dtype=np.int32))
+        B, C, CI, W = cache.batch, cache.latent, cache.c_indexer, cache.window
+        self.ring = [torch.zeros(B, W, C, dtype=torch.bfloat16) for _ in specs]
+        self.pool, self.ipool, self.tails = [], [], []
+        for i, s in enumerate(specs):
+            if s.kind == "swa":
+                self.pool.append(None)
+                self.ipool.append(None)
+                self.tails.append(None)
+                continue
+            n_pages = cache.groups[cache.group_of_rate[s.m]].n_pages
+            self.pool.append(torch.zeros(n_pages, self.bs, C, dtype=torch.bfloat16))
+            self.ipool.append(torch.zeros(n_pages, self.bs, CI, dtype=torch.bfloat16) if s.kind == "csa" else None)
+            self.tails.append([torch.zeros(B, s.m, C, dtype=torch.bfloat16), torch.zeros(B, s.m, C, dtype=torch.bfloat16),
+                               torch.zeros(B, s.m, CI, dtype=torch.bfloat16), torch.zeros(B, s.m, CI, dtype=torch.bfloat16)])
+        self.lens = np.zeros(B, dtype=np.int32)
+
+    def append(self, n, data, bias, ibias):
+        """n new tokens per sequence (data: per layer dict of CPU bf16 [B, T, *])."""
+        n = np.asarray(n, dtype=np.int32)
+        before = self.lens.copy()
+        self.lens = self.lens + n
+        for gi, m in enumerate(self.m_groups):
+            st, self.top[gi] = ref.reserve(self.stack[gi], self.top[gi], self.bt[gi], self.ent[gi],
+                                           self.lens // m - self.ent[gi], self.bs)
+            assert st == 0
+        for i, s in enumerate(self.specs):
+            ref.ring_append(self.ring[i], before, data[i]["kv"], n)
+            if s.kind == "swa":
+                continue
+            gi = self.m_groups.index(s.m)
+            t = self.tails[i]
+            ref.compress_append(self.pool[i], self.bt[gi], t[0], t[1], data[i]["c"], data[i]["z"],
+                                bias[i], self.lens, n)
+            if s.kind == "csa":
+                ref.compress_append(self.ipool[i], self.bt[gi], t[2], t[3], data[i]["ci"],
+                                    data[i]["zi"], ibias[i], self.lens, n)
+
+
+def _rand_data(g, specs, B, T, C, CI):
+    out = []
+    for s in specs:
+        d = {"kv": torch.randn(B, T, C, generator=g).to(torch.bfloat16)}
+        if s.kind != "swa":
+            d["c"] = torch.randn(B, T, C, generator=g).to(torch.bfloat16)
+            d["z"] = torch.randn(B, T, C, generator=g).to(torch.bfloat16)
+        if s.kind == "csa":
+            d["ci"] = torch.randn(B, T, CI, generator=g).to(torch.bfloat16)
+            d["zi"] = torch.randn(B, T, CI, generator=g).to(torch.bfloat16)
+        out.append(d)
+    return out
+
+
+def test_decode_step_matches_oracle(dev) -> None:
+    from saint_kv.decode import DecodeCache, LayerSpec
+
+    specs = [LayerSpec("csa", m=4, top_k=64, fp8=True), LayerSpec("csa", m=4, top_k=64),
+             LayerSpec("hca", m=128), LayerSpec("swa")]
+    B, max_len, bs, W, C, CI = 5, 2048, 16, 32, 576, 128
+    seed = 3
+    cache = DecodeCache(specs, B, max_len, block_size=bs, window=W, device=dev, page_order_seed=seed)
+    orc = _Oracle(cache, specs, seed)
+    g = torch.Generator().manual_seed(seed)
+    bias = [None if s.kind == "swa" else torch.randn(s.m, C, generator=g) for s in specs]
+    ibias = [torch.randn(s.m, CI, generator=g) if s.kind == "csa" else None for s in specs]
+    for i, s in enumerate(specs):
+        if bias[i] is not None:
+            cache.bias[i].copy_(bias[i])
+        if ibias[i] is not None:
+            cache.idx_bias[i].copy_(ibias[i])
+    lens0 = np.array([0, 1, 130, 511, 1300], dtype=np.int64)
+    pre = _rand_data(g, specs, B, int(lens0.max()), C, CI)
+    cache.prefill(lens0, data=[{k: v.to(dev) for k, v in d.items()} for d in pre])
+    orc.append(lens0, pre, bias, ibias)
+    for step in range(40):
+        data = _rand_data(g, specs, B, 1, C, CI)
+        scores = [torch.randn(B, max_len // s.m, generator=g) if s.kind == "csa" else None for s in specs]
+        scores[0][1, :3] = float("nan")
+        if step == 5:
+            scores[1][:, :] = 0.0  # ties everywhere
+        for i, s in enumerate(specs):
+            for k, v in data[i].items():
+                cache.inputs[i][k].copy_(v[:, 0])
+            if scores[i] is not None:
+                cache.scores[i].copy_(scores[i])
+        cache.step()
+        orc.append(np.ones(B, dtype=np.int32), data, bias, ibias)
+        torch.cuda.synchronize()
+        cache.check_status()
+        assert np.array_equal(_np(cache.tok_lens), orc.lens)
+        for gi, grp in enumerate(cache.groups):
+            assert np.array_equal(_np(grp.block_table), orc.bt[gi])
+            assert np.array_equal(_np(grp.n_entries), orc.ent[gi])
+            assert int(grp.free_top.item()) == orc.top[gi]
+        for i, s in enumerate(specs):
+            assert torch.equal(cache.ring[i].cpu(), orc.ring[i]), (step, i)
+            win = ref.ring_read(orc.ring[i], orc.lens, torch.zeros(B, W, C, dtype=torch.bfloat16))
+            ow = cache.out_window[i].cpu()
+            for b in range(B):
+                n = min(W, int(orc.lens[b]))
+                assert torch.equal(ow[b, :n], win[b, :n]), (step, i, b)
+            if s.kind == "swa":
+                continue
+            gi = cache.group_of_rate[s.m]
+            gpu_pool = cache.pool[i].cpu()
+            src = ref.fp8_unpack_entries(gpu_pool.reshape(-1, 656)).reshape(*gpu_pool.shape[:2], C) \
+                if s.fp8 else gpu_pool
+            if s.kind == "csa":
+                q = orc.lens - 1
+                n_valid = np.array([ref.n_valid_blocks(int(x), s.m) for x in q])
+                idx = _np(cache.topk_idx[i])
+                for b in range(B):
+                    n_cols = int(orc.lens[b]) // s.m
+                    exp = ref.topk_select(scores[i][b:b + 1].numpy(), n_valid[b:b + 1], s.top_k, n_cols)[0]
+                    assert np.array_equal(idx[b, : len(exp)], exp), (step, i, b)
+                    assert (idx[b, len(exp):] == -1).all()
+                out = cache.out_entries[i].cpu()
+                exp_out = torch.zeros_like(out)
+                ref.topk_gather(src, orc.bt[gi], np.arange(B), idx, exp_out)
+                for b in range(B):
+                    if orc.ent[gi][b] == 0:
+                        exp_out[b] = 0
+                assert torch.equal(out, exp_out), (step, i)
+            else:
+                out = cache.out_entries[i].cpu()
+                dense = ref.paged_gather(src, orc.bt[gi], orc.ent[gi], torch.zeros_like(out))
+                for b in range(B):
+                    e = int(orc.ent[gi][b])
+                    assert torch.equal(out[b, :e], dense[b, :e]), (step, i, b)
+    # pooled values: GPU entries within the pooling tolerance of the oracle's,
+    # and the fp8 layer's codes equal the quantization of the bf16 layer's
+    # entries (same inputs, same block table)
+    torch.cuda.synchronize()
+    for i, s in enumerate(specs):
+        if s.kind == "swa" or s.fp8:
+            continue
+        gi = cache.group_of_rate[s.m]
+        live = ref.live_pages(orc.bt[gi], orc.ent[gi], bs)
+        for b in range(B):
+            e = int(orc.ent[gi][b])
+            got = ref.paged_gather(cache.pool[i].cpu(), orc.bt[gi][b:b + 1], orc.ent[gi][b:b + 1],
+                                   torch.zeros(1, max(e, 1), C, dtype=torch.bfloat16))
+            exp = ref.paged_gather(orc.pool[i], orc.bt[gi][b:b + 1], orc.ent[gi][b:b + 1],
+                                   torch.zeros(1, max(e, 1), C, dtype=torch.bfloat16))
+            torch.testing.assert_close(got.float(), exp.float(), rtol=1e-2, atol=1e-2)
+        if s.kind == "csa":
+            gi_pool = cache.idx_pool[i].cpu()
+            torch.testing.assert_close(gi_pool[live].float(), orc.ipool[i][live].float(), rtol=1e-2, atol=1e-2)
+        del live
+    # layers 0 (fp8) and 1 (bf16) saw the same data? no: inputs differ per layer,
+    # so fp8 exactness is covered by test_compress_ragged_chunks_fp8.
+
+
+def test_decode_release_and_compact(dev) -> None:
+    from saint_kv.decode import DecodeCache, LayerSpec
+
+    specs = [LayerSpec("csa", m=4, top_k=32, fp8=True), LayerSpec("hca", m=128)]
+    B, max_len = 8, 8192
+    cache = DecodeCache(specs, B, max_len, block_size=16, window=16, device=dev, page_order_seed=9)
+    gen = torch.Generator(device=dev).manual_seed(9)
+    lens0 = np.random.default_rng(9).integers(100, 6000, size=B)
+    cache.prefill(lens0, generator=gen)
+    for i, s in enumerate(specs):
+        for v in cache.inputs[i].values():
+            v.normal_(generator=gen)
+        if cache.scores[i] is not None:
+            cache.scores[i].normal_(generator=gen)
+    for _ in range(3):
+        cache.step()
+    cache.check_status()
+    # dense view of every live sequence before
+    csa_g = cache.groups[cache.group_of_rate[4]]
+    before = []
+    for b in range(B):
+        e = int(csa_g.n_entries[b])
+        out = torch.zeros(1, e, 576, dtype=torch.bfloat16, device=dev)
+        idx = torch.arange(e, dtype=torch.int32, device=dev).view(1, e)
+        from saint_kv import ops
+        ops.topk_gather(cache.pool[0], csa_g.block_table[b:b + 1], csa_g.n_entries[b:b + 1], idx, out, 576)
+        before.append(out)
+    mask = np.zeros(B, dtype=bool)
+    mask[[1, 4, 6]] = True
+    cache.release(mask)
+    with pytest.raises(RuntimeError, match="double free"):
+        cache.release(mask)
+    info = cache.compact()
+    torch.cuda.synchronize()
+    for gi, g in enumerate(cache.groups):
+        n_live, moved = info[gi]
+        bt = _np(g.block_table)
+        ent = _np(g.n_entries)
+        live = ref.live_pages(bt, ent, 16)
+        assert sorted(live.tolist()) == list(range(n_live))
+        assert int(g.free_top.item()) == g.n_pages - n_live
+    from saint_kv import ops
+    for b in range(B):
+        if mask[b]:
+            continue
+        e = int(csa_g.n_entries[b])
+        out = torch.zeros(1, e, 576, dtype=torch.bfloat16, device=dev)
+        idx = torch.arange(e, dtype=torch.int32, device=dev).view(1, e)
+        ops.topk_gather(cache.pool[0], csa_g.block_table[b:b + 1], csa_g.n_entries[b:b + 1], idx, out, 576)
+        assert torch.equal(out, before[b])
+    cache.step()  # decode continues after compaction
+    cache.check_status()
