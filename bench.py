@@ -155,6 +155,178 @@ def cpu_baseline(seconds: float = 10.0, seed: int = 0) -> dict:
     }
 
 
+# ---------------------------------------------------------------------------
+# Decode-step legs: heterogeneous compressed cache (CSA / HCA / SWA layers)
+# ---------------------------------------------------------------------------
+def decode_step_bytes(specs, lens_after: np.ndarray, window: int, latent: int = 576,
+                      c_indexer: int = 128, bs: int = 64) -> int:
+    """Compulsory HBM bytes of one fused decode step, for the sequences'
+    token counts after the step: reads + writes of every row, entry, state,
+    score and index the step touches (the formula is stated in the design notes)."""
+    L = lens_after.astype(np.int64)
+    p = L - 1
+    E = latent * 2
+    total = 0
+    for s in specs:
+        cnt = np.minimum(L, window)
+        total += int((2 * E + 2 * cnt * E).sum())  # token in + ring write; window read + write
+        if s.kind == "swa":
+            continue
+        ent_bytes = (latent - 64) + (latent - 64) // 128 * 4 + 128 if s.fp8 else E
+        streams = [(latent, ent_bytes)]
+        if s.kind == "csa" and s.indexer:
+            streams.append((c_indexer, c_indexer * 2))
+        for ch, eb in streams:
+            st = 3 * ch * 4
+            emit = ((p + 1) % s.m == 0)
+            total += int((2 * ch * 2 + ch * 4  # c, z rows + bias row
+                          + np.where(p % s.m != 0, st, 0)  # state read
+                          + np.where(emit, eb, st)).sum())  # entry or state write
+        n_ent = L // s.m
+        if s.kind == "csa":
+            n_valid = np.maximum(p, 0) // s.m
+            k_eff = np.minimum(s.top_k, n_ent)
+            total += int((n_valid * 4 + s.top_k * 4).sum())  # scores read, indices written
+            total += int((k_eff * (ent_bytes + E + 8) + (s.top_k - k_eff) * E).sum())
+        else:
+            total += int((n_ent * (ent_bytes + E) + (-(-n_ent // bs)) * 4).sum())
+    return total
+
+
+def decode_kv_tokens(specs, lens_after: np.ndarray, window: int) -> int:
+    """KV rows delivered to attention per step: top-k picks + window (CSA),
+    all entries + window (HCA), window (SWA)."""
+    L = lens_after.astype(np.int64)
+    tot = 0
+    for s in specs:
+        tot += int(np.minimum(L, window).sum())
+        if s.kind == "csa":
+            tot += int(np.minimum(s.top_k, L // s.m).sum())
+        elif s.kind == "hca":
+            tot += int((L // s.m).sum())
+    return tot
+
+
+def run_decode_leg(dev, name: str, specs, batch: int, lens0: np.ndarray, steps: int,
+                   per_graph: int = 20, window: int = 128, seed: int = 0,
+                   outlier_frac: float = 0.0, evict_frac: float | None = None) -> dict:
+    from saint_kv.decode import DecodeCache
+
+    max_len = int(lens0.max()) + steps + 2 * per_graph + 8
+    t0 = time.perf_counter()
+    cache = DecodeCache(specs, batch, max_len, window=window, device=dev, page_order_seed=seed,
+                        hca_out_rows=max(1, max_len // 128))
+    gen = torch.Generator(device=dev).manual_seed(seed)
+    for i, s in enumerate(specs):
+        if cache.bias[i] is not None:
+            cache.bias[i].normal_(generator=gen)
+        if cache.idx_bias[i] is not None:
+            cache.idx_bias[i].normal_(generator=gen)
+        for v in cache.inputs[i].values():
+            v.normal_(generator=gen)
+        if cache.scores[i] is not None:
+            cache.scores[i].normal_(generator=gen)
+    cache.prefill(lens0, generator=gen, outlier_frac=outlier_frac)
+    torch.cuda.synchronize()
+    log(f"{name}: prefilled {batch} x mean {int(lens0.mean())} tokens in {time.perf_counter() - t0:.1f} s")
+    graph = cache.capture(per_graph)
+    graph.replay()  # warm-up replay
+    torch.cuda.synchronize()
+    cache.check_status()
+    reps = max(1, steps // per_graph)
+    lens_start = cache.host_lens.copy()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        graph.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    cache.check_status()
+    n_steps = reps * per_graph
+    ms = e0.elapsed_time(e1) / n_steps
+    alg = sum(decode_step_bytes(specs, lens_start + i + 1, window) for i in range(n_steps)) / n_steps
+    toks = sum(decode_kv_tokens(specs, lens_start + i + 1, window) for i in range(n_steps)) / n_steps
+    gbs = alg / (ms * 1e-3) / 1e9
+    rec = {
+        "batch": batch, "layers": [f"{s.kind}{'-fp8' if s.fp8 else ''}(m={s.m},k={s.top_k})" if s.kind != "swa" else "swa" for s in specs],
+        "mean_ctx": int(lens0.mean()), "steps": n_steps, "us_per_step": round(ms * 1e3, 2),
+        "alg_bytes_per_step": int(alg), "gbs": round(gbs, 1), "pct_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 2),
+        "kv_tokens_per_step": int(toks), "kv_tokens_per_s": round(toks / (ms * 1e-3), 1),
+        "launches_per_step": 4, "hip_graph_steps": per_graph,
+    }
+    log(f"{name}: {rec['us_per_step']} us/step, {rec['gbs']} GB/s ({rec['pct_hbm_peak']}%), "
+        f"{rec['kv_tokens_per_s'] / 1e6:.1f} M KV tok/s")
+    if evict_frac is not None:
+        rng = np.random.default_rng(seed + 1)
+        n_fin = int(round(evict_frac * batch))
+        mask = np.zeros(batch, dtype=bool)
+        mask[rng.choice(batch, size=n_fin, replace=False)] = True
+        ws = torch.empty(3 * max(g.n_pages for g in cache.groups), dtype=torch.int32, device=dev)
+        torch.cuda.synchronize()
+        c0, c1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        c0.record()
+        cache.release(mask)
+        info = cache.compact(ws)
+        c1.record()
+        torch.cuda.synchronize()
+        page_bytes = 0
+        for i, s in enumerate(specs):
+            if cache.pool[i] is not None:
+                page_bytes += ops_row_bytes(cache.pool[i]) * cache.block_size
+            if cache.idx_pool[i] is not None:
+                page_bytes += ops_row_bytes(cache.idx_pool[i]) * cache.block_size
+        moved = sum(m for _, m in info)
+        cms = c0.elapsed_time(c1)
+        rec["evict_compact"] = {
+            "finished": n_fin, "pages_live": [n for n, _ in info], "pages_moved": moved,
+            "bytes_moved_rw": 2 * moved * page_bytes, "ms": round(cms, 3),
+            "gbs": round(2 * moved * page_bytes / (cms * 1e-3) / 1e9, 1) if cms > 0 else None,
+        }
+        cache.step()  # decoding continues on the compacted pools
+        torch.cuda.synchronize()
+        cache.check_status()
+        log(f"{name}: release {n_fin} + compaction moved {moved} pages in {cms:.3f} ms")
+    del cache, graph
+    torch.cuda.empty_cache()
+    return rec
+
+
+def ops_row_bytes(pool: torch.Tensor) -> int:
+    from saint_kv import ops
+
+    return ops.row_bytes_of(pool)
+
+
+def cpu_baseline_decode(seconds: float = 5.0, seed: int = 0) -> dict:
+    """The oracle's CSA decode read path (top-k select + block-table gather +
+    window read) on host cores for 2 sequences at 64k context."""
+    from oracle import reference_cpu as ref
+
+    rng = np.random.default_rng(seed)
+    n_seq, m, k, L, bs, w = 2, 4, 512, 65536, 64, 128
+    n_ent = L // m
+    pages = n_seq * (n_ent // bs)
+    pool = torch.randn(pages, bs, ROW).to(torch.bfloat16)
+    bt = rng.permutation(pages).astype(np.int32).reshape(n_seq, n_ent // bs)
+    ring = torch.randn(n_seq, w, ROW).to(torch.bfloat16)
+    scores = rng.standard_normal((n_seq, n_ent)).astype(np.float32)
+    out = torch.empty(n_seq, k, ROW, dtype=torch.bfloat16)
+    win = torch.empty(n_seq, w, ROW, dtype=torch.bfloat16)
+    lens = np.full(n_seq, L, dtype=np.int64)
+    t0, steps = time.perf_counter(), 0
+    while time.perf_counter() - t0 < seconds:
+        idx = ref.topk_select(scores, np.full(n_seq, (L - 1) // m), k, n_ent)
+        ref.topk_gather(pool, bt, np.arange(n_seq), idx, out)
+        ref.ring_read(ring, lens, win)
+        steps += 1
+    dt = time.perf_counter() - t0
+    per_step = n_seq * (n_ent * 4 + k * 4 + k * (2 * ROW * 2 + 8) + w * 2 * ROW * 2)
+    return {"value": round(steps * per_step / dt / 1e9, 3), "unit": "GB/s",
+            "cores": torch.get_num_threads(), "kind": "port",
+            "sample": f"{steps} CSA read steps (top-512 of 16384 scores + gather + 128-row window) "
+                      f"for 2 sequences at 64k context, torch/numpy CPU oracle, {dt:.1f} s"}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -162,6 +334,9 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--legs", default="csa_64k,mixed_8layer,fp8_1m",
+                    help="comma list of decode-step legs to run after the headline ('' for none)")
+    ap.add_argument("--leg-steps", type=int, default=200)
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); the cache shards by "
@@ -214,11 +389,38 @@ def main() -> int:
     log(f"step {ms_per_step * 1e3:.1f} us, kernel {kern_avg_ms * 1e3:.1f} us, "
         f"{value:.0f} GB/s, kernel {achieved:.0f} GB/s")
 
+    del w
+    torch.cuda.empty_cache()
+    legs = {}
+    from saint_kv.decode import LayerSpec
+
+    rng = np.random.default_rng(1)
+    wanted = [x for x in args.legs.split(",") if x]
+    if "csa_64k" in wanted:
+        legs["csa_64k"] = run_decode_leg(
+            dev, "csa_64k", [LayerSpec("csa", m=4, top_k=512)], 16,
+            np.full(16, 65536, dtype=np.int64), args.leg_steps, seed=3)
+    if "mixed_8layer" in wanted:
+        specs = [LayerSpec("csa", m=4, top_k=512) if i % 2 == 0 else LayerSpec("hca", m=128)
+                 for i in range(8)]
+        legs["mixed_8layer"] = run_decode_leg(
+            dev, "mixed_8layer", specs, 32, rng.integers(32768, 131073, size=32), args.leg_steps, seed=4)
+    if "fp8_1m" in wanted:
+        legs["fp8_1m"] = run_decode_leg(
+            dev, "fp8_1m", [LayerSpec("csa", m=4, top_k=1024, fp8=True)], 4,
+            rng.integers(262144, 1048577, size=4), args.leg_steps, seed=5, outlier_frac=0.01,
+            evict_frac=0.3)
+
     cpu = None
+    cpu_dec = None
     if not args.no_cpu_baseline:
         log("timing the CPU oracle baseline")
         cpu = cpu_baseline(args.cpu_seconds)
         log(f"cpu baseline {cpu['value']} GB/s on {cpu['cores']} threads")
+        if "csa_64k" in legs:
+            cpu_dec = cpu_baseline_decode(min(args.cpu_seconds, 5.0))
+            legs["csa_64k"]["cpu_baseline"] = cpu_dec
+            log(f"cpu baseline (64k CSA read path) {cpu_dec['value']} GB/s")
 
     rec = {
         "metric": "KV append+gather GB/s (% of HBM peak) and decode-step KV tokens/s at 64k ctx",
@@ -257,6 +459,8 @@ def main() -> int:
             "avg_launch_us": round(kern_avg_ms * 1e3, 2),
         },
         "cpu_baseline": cpu,
+        "decode_kv_tokens_per_s_64k": legs.get("csa_64k", {}).get("kv_tokens_per_s"),
+        "decode_legs": legs,
     }
     print(json.dumps(rec), flush=True)
     return 0

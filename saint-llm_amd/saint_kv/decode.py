@@ -240,6 +240,10 @@ class DecodeCache:
                   _lib.stream_handle(self.device))
         self.host_lens += 1
 
+    def capture(self, steps: int) -> "CapturedSteps":
+        """Capture ``steps`` decode steps in one HIP graph (see CapturedSteps)."""
+        return CapturedSteps(self, steps)
+
     def check_status(self) -> None:
         """Synchronise and raise if a page reservation was refused."""
         st = int(self.status.item())
@@ -248,14 +252,17 @@ class DecodeCache:
 
     # --------------------------------------------------------------- prefill --
     def prefill(self, lens: np.ndarray, generator: torch.Generator | None = None,
-                data: dict | None = None) -> None:
+                data: dict | None = None, outlier_frac: float = 0.0,
+                outlier_scale: float = 20.0) -> None:
         """Bring every sequence from empty to ``lens[b]`` tokens.
 
         With ``data`` (per layer dicts of bf16 [B, T, ...] tensors "kv", "c", "z",
         "ci", "zi") the caches are built through the kernels exactly as decode
         would build them.  Without it the compressed entries and rings are
-        filled with N(0,1) values (synthetic contexts for benchmarking) and the
-        incomplete blocks' states are folded from N(0,1) tokens.
+        filled with N(0,1) values (synthetic contexts for benchmarking; fp8
+        pools quantize N(0,1) rows in which a fraction ``outlier_frac`` of the
+        values is multiplied by ``outlier_scale``) and the incomplete blocks'
+        states are folded from N(0,1) tokens.
         """
         lens = np.asarray(lens, dtype=np.int64)
         if lens.shape != (self.batch,) or (lens < 0).any() or (lens > self.max_len).any():
@@ -286,7 +293,8 @@ class DecodeCache:
                     ops.compress_append(pool, g.block_table, state, data[i][kc], data[i][kz], bias,
                                         lens_t, lens_t)
                     continue
-                self._fill_entries(pool, g, lens // spec.m, ch, generator)
+                self._fill_entries(pool, g, lens // spec.m, ch, generator, outlier_frac,
+                                   outlier_scale)
                 tail = lens % spec.m
                 if tail.max() > 0:
                     t = int(tail.max())
@@ -299,7 +307,8 @@ class DecodeCache:
         self.check_status()
 
     def _fill_entries(self, pool: torch.Tensor, g: _Group, n_ent: np.ndarray, ch: int,
-                      generator: torch.Generator | None) -> None:
+                      generator: torch.Generator | None, outlier_frac: float,
+                      outlier_scale: float) -> None:
         if pool.dtype == torch.bfloat16:
             for chunk in pool.split(4096):
                 chunk.normal_(generator=generator)
@@ -310,8 +319,11 @@ class DecodeCache:
         tmp_lens = torch.zeros(self.batch, dtype=torch.int32, device=self.device)
         while (done < n_ent).any():
             n = np.minimum(n_ent - done, step).astype(np.int32)
-            x = torch.randn(self.batch, int(n.max()), ch, generator=generator,
-                            device=self.device).to(torch.bfloat16)
+            x = torch.randn(self.batch, int(n.max()), ch, generator=generator, device=self.device)
+            if outlier_frac > 0:
+                hit = torch.rand(x.shape, generator=generator, device=self.device) < outlier_frac
+                x = torch.where(hit, x * outlier_scale, x)
+            x = x.to(torch.bfloat16)
             tmp_lens.copy_(torch.as_tensor((done + n).astype(np.int32)))
             ops.fp8_quant_append(pool, g.block_table, tmp_lens, x, torch.as_tensor(n, device=self.device))
             done += n
@@ -348,3 +360,33 @@ class DecodeCache:
                         g.free_top, ws[: 3 * g.n_pages], info)
             out.append(tuple(int(v) for v in info.cpu()))
         return out
+
+
+class CapturedSteps:
+    """``steps`` decode steps of a DecodeCache recorded in one HIP graph.
+
+    Every replay runs those steps on the device state as it is at replay time
+    (token counts, pages and states live in device memory), with the inputs
+    and scores the buffers hold then.  The host-side token counts advance by
+    ``steps`` per replay; call ``cache.check_status()`` after replays to
+    surface a refused page reservation.
+    """
+
+    def __init__(self, cache: DecodeCache, steps: int) -> None:
+        if steps <= 0:
+            raise ValueError("steps must be positive")
+        self.cache, self.steps = cache, steps
+        self.graph = torch.cuda.CUDAGraph()
+        lens_before = cache.host_lens.copy()
+        with torch.cuda.graph(self.graph):
+            for _ in range(steps):
+                _lib.call("skv_decode_step", ctypes.addressof(cache._desc), cache._desc_dev.data_ptr(),
+                          _lib.stream_handle(cache.device))
+        cache.host_lens = lens_before  # capture records, it does not run
+
+    def replay(self) -> None:
+        if (self.cache.host_lens + self.steps > self.cache.max_len).any():
+            raise RuntimeError(
+                f"DecodeCache overflow: {self.steps} more steps exceed max_len={self.cache.max_len}")
+        self.graph.replay()
+        self.cache.host_lens += self.steps
