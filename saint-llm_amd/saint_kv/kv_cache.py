@@ -1,0 +1,375 @@
+"""Drop-in heterogeneous KV cache layers backed by paged HIP storage.
+
+Same names, constructor signatures, attributes, return values and error
+types/messages as the reference classes in
+packages/inference/src/saint_llm_inference/kv_cache.py:
+
+* ``SWAKVCacheLayer``  (kv_cache.py:32-87)
+* ``HCAKVCacheLayer``  (kv_cache.py:90-207)
+* ``CSAKVCacheLayer``  (kv_cache.py:210-327)
+* ``KVCacheBundle``    (kv_cache.py:333-427)
+
+Differences in mechanism (not in results):
+
+* K/V rows and compressed entries live in fixed-size pages of a per-layer page
+  pool reached through an int32 block table; ``append`` writes the new rows
+  with ``skv_append_gather`` / ``skv_paged_append`` and returns contiguous
+  tensors gathered from the pages (the values the reference's slice views
+  hold).  The returned tensors are views of per-layer gather buffers that the
+  next ``append`` refreshes, as the reference's views alias its storage.
+* Caches live on a ROCm GPU only: ``device=None`` means the current GPU, and a
+  CPU device raises.  There is no CPU code path.
+* ``compressor`` callables are invoked exactly as the reference does (on the
+  m-aligned prefix of ``cat(h_buffer, h_new)``); their output is copied into
+  the paged compressed cache.
+"""
+
+from __future__ import annotations
+
+from collections.abc import Callable
+
+import numpy as np
+import torch
+from torch import Tensor
+
+from saint_kv import ops
+
+DEFAULT_BLOCK_SIZE = 16
+
+
+def _device(device: torch.device | str | None) -> torch.device:
+    if device is None:
+        if not torch.cuda.is_available():
+            raise RuntimeError("saint_kv caches need a ROCm GPU; none is visible (no CPU fallback)")
+        return torch.device("cuda", torch.cuda.current_device())
+    dev = torch.device(device)
+    if dev.type != "cuda":
+        raise RuntimeError(f"saint_kv caches run only on a ROCm GPU, not {dev} (no CPU fallback)")
+    return dev
+
+
+class _PagedRows:
+    """Rows of ``row_shape`` for ``batch`` lock-step sequences in a private page pool.
+
+    The pool holds exactly the pages ``max_rows`` rows need, so it never runs
+    out; page ids are handed out by the device free stack (skv_reserve).  Rows
+    whose size is not a multiple of 16 bytes are stored with the last dim
+    zero-padded (the kernels move 16-byte chunks); views hide the padding.
+    """
+
+    def __init__(self, batch: int, max_rows: int, row_shape: tuple[int, ...], dtype: torch.dtype,
+                 device: torch.device, block_size: int) -> None:
+        es = torch.empty((), dtype=dtype).element_size()
+        lead, d = int(np.prod(row_shape[:-1])), row_shape[-1]
+        d_pad = d
+        while (lead * d_pad * es) % 16:
+            d_pad += 1
+        self.d, self.d_pad = d, d_pad
+        store_shape = (*row_shape[:-1], d_pad)
+        self.batch, self.max_rows, self.block_size = batch, max_rows, block_size
+        self.max_pages = max(1, -(-max_rows // block_size))
+        n_pages = batch * self.max_pages
+        self.pool = torch.zeros(n_pages, block_size, *store_shape, dtype=dtype, device=device)
+        self.free_stack = torch.empty(n_pages, dtype=torch.int32, device=device)
+        self.free_top = torch.empty(1, dtype=torch.int32, device=device)
+        self.block_table = torch.full((batch, self.max_pages), -1, dtype=torch.int32, device=device)
+        self.lens = torch.zeros(batch, dtype=torch.int32, device=device)
+        self.status = torch.zeros(1, dtype=torch.int32, device=device)
+        self._out = torch.zeros(batch, max_rows, *store_shape, dtype=dtype, device=device)
+        ops.free_stack_init(self.free_stack, self.free_top)
+        self.length = 0
+
+    @property
+    def out(self) -> Tensor:
+        """(B, max_rows, *row_shape) gather buffer; rows [0, length) are current."""
+        return self._out if self.d == self.d_pad else self._out[..., : self.d]
+
+    def append(self, rows: Tensor, gather: bool = True) -> Tensor:
+        """Append rows (B, n, *row) and return the gathered (B, length, *row)."""
+        n = rows.shape[1]
+        if n:
+            if self.d_pad != self.d:
+                rows = torch.nn.functional.pad(rows, (0, self.d_pad - self.d))
+            ops.reserve(self.free_stack, self.free_top, self.block_table, self.lens, n,
+                        self.block_size, self.status)
+            if gather:
+                ops.append_gather(self.pool, self.block_table, self.lens, rows, n, self._out)
+            else:
+                ops.paged_append(self.pool, self.block_table, self.lens, rows, n)
+            self.length += n
+        return self.out[:, : self.length]
+
+    def reset(self) -> None:
+        if self.length:
+            mask = torch.ones(self.batch, dtype=torch.uint8, device=self.pool.device)
+            ops.release(self.free_stack, self.free_top, self.block_table, self.lens, mask,
+                        self.block_size, self.status)
+        self.length = 0
+
+
+def _check_3d(what: str, *ts: Tensor) -> None:
+    if any(t.dim() != 3 for t in ts):
+        shapes = ", ".join(str(tuple(t.shape)) for t in ts)
+        raise ValueError(f"{what} must all be 3D (B, T, *); got {shapes}")
+
+
+class SWAKVCacheLayer:
+    """Append-only KV cache for ``SWAttention`` on paged storage (kv_cache.py:32-87).
+
+    K and V of a token share one page row ([K | V]); ``append`` returns the
+    contiguous (B, length, head_dim) K and V.
+    """
+
+    def __init__(self, max_seq_len: int, head_dim: int, *, batch_size: int = 1,
+                 device: torch.device | str | None = None, dtype: torch.dtype = torch.float32,
+                 block_size: int = DEFAULT_BLOCK_SIZE) -> None:
+        if max_seq_len <= 0:
+            raise ValueError(f"max_seq_len must be positive; got {max_seq_len}")
+        self.max_seq_len = max_seq_len
+        self.head_dim = head_dim
+        self.batch_size = batch_size
+        self.dtype = dtype
+        self._rows = _PagedRows(batch_size, max_seq_len, (2, head_dim), dtype, _device(device),
+                                block_size)
+
+    @property
+    def length(self) -> int:
+        return self._rows.length
+
+    @property
+    def k(self) -> Tensor:
+        """(B, max_seq_len, head_dim): rows [0, length) hold the cached keys."""
+        return self._rows.out[:, :, 0]
+
+    @property
+    def v(self) -> Tensor:
+        return self._rows.out[:, :, 1]
+
+    def append(self, k_new: Tensor, v_new: Tensor) -> tuple[Tensor, Tensor]:
+        """Append new K/V entries; return the full cache up to the current length."""
+        if k_new.dim() != 3 or v_new.dim() != 3:
+            raise ValueError(
+                f"k_new/v_new must be 3D (B, T, head_dim); got {tuple(k_new.shape)}, "
+                f"{tuple(v_new.shape)}",
+            )
+        n = k_new.shape[1]
+        if self.length + n > self.max_seq_len:
+            raise RuntimeError(
+                f"SWAKVCacheLayer overflow: tried to append {n} tokens at "
+                f"length {self.length} into max_seq_len={self.max_seq_len}",
+            )
+        rows = torch.stack([k_new.to(self.dtype), v_new.to(self.dtype)], dim=2)
+        full = self._rows.append(rows)
+        return full[:, :, 0], full[:, :, 1]
+
+    def reset(self) -> None:
+        """Drop all cached entries; ready for a fresh prompt."""
+        self._rows.reset()
+
+
+class _CompressedLayer:
+    """Shared HCA/CSA machinery: SW branch rows, h-buffer, compressed streams."""
+
+    kind = "compressed"
+
+    def __init__(self, max_seq_len: int, hidden_dim: int, head_dims: list[int],
+                 compression_rate: int, *, batch_size: int, device, dtype: torch.dtype,
+                 block_size: int) -> None:
+        if max_seq_len <= 0:
+            raise ValueError(f"max_seq_len must be positive; got {max_seq_len}")
+        if compression_rate <= 0:
+            raise ValueError(f"compression_rate must be positive; got {compression_rate}")
+        dev = _device(device)
+        self.max_seq_len = max_seq_len
+        self.hidden_dim = hidden_dim
+        self.head_dim = head_dims[0]
+        self.compression_rate = compression_rate
+        self.batch_size = batch_size
+        self.dtype = dtype
+        max_blocks = max_seq_len // compression_rate
+        self._max_blocks = max_blocks
+        self._sw = _PagedRows(batch_size, max_seq_len, (2, head_dims[0]), dtype, dev, block_size)
+        self._streams = [_PagedRows(batch_size, max(max_blocks, 1), (d,), dtype, dev, block_size)
+                         for d in head_dims]
+        self.h_buffer = torch.zeros(batch_size, compression_rate, hidden_dim, device=dev, dtype=dtype)
+        self.h_buf_count = 0
+
+    @property
+    def length(self) -> int:
+        return self._sw.length
+
+    @property
+    def n_blocks(self) -> int:
+        return self._streams[0].length
+
+    @property
+    def sw_k(self) -> Tensor:
+        return self._sw.out[:, :, 0]
+
+    @property
+    def sw_v(self) -> Tensor:
+        return self._sw.out[:, :, 1]
+
+    def _append(self, name: str, h_new: Tensor, sw_k_new: Tensor, sw_v_new: Tensor,
+                compressors: list[Callable[[Tensor], Tensor]]) -> list[Tensor]:
+        _check_3d("h_new, sw_k_new, sw_v_new", h_new, sw_k_new, sw_v_new)
+        n = sw_k_new.shape[1]
+        if self.length + n > self.max_seq_len:
+            raise RuntimeError(
+                f"{name} overflow: tried to append {n} tokens at "
+                f"length {self.length} into max_seq_len={self.max_seq_len}",
+            )
+        # 1) SW branch K/V (kv_cache.py:167-168)
+        rows = torch.stack([sw_k_new.to(self.dtype), sw_v_new.to(self.dtype)], dim=2)
+        sw = self._sw.append(rows)
+        # 2) combine the buffered h with the new chunk (kv_cache.py:171-179)
+        if self.h_buf_count > 0:
+            combined = torch.cat([self.h_buffer[:, : self.h_buf_count], h_new.to(self.dtype)], dim=1)
+        else:
+            combined = h_new
+        total = self.h_buf_count + n
+        n_complete = total // self.compression_rate
+        n_consumed = n_complete * self.compression_rate
+        # 3) emit complete blocks through the caller's compressors (kv_cache.py:182-189)
+        if n_complete > 0:
+            tail = combined[:, :n_consumed]
+            outs = [c(tail) for c in compressors]
+            if any(o.shape[1] != n_complete for o in outs):
+                got = " / ".join(str(o.shape[1]) for o in outs)
+                raise RuntimeError(f"compressor returned {got} blocks, expected {n_complete}")
+            if self.n_blocks + n_complete > self._max_blocks:
+                raise RuntimeError(
+                    f"{name} overflow: {self.n_blocks + n_complete} compressed blocks exceed "
+                    f"{self._max_blocks}",
+                )
+            for stream, o in zip(self._streams, outs, strict=True):
+                stream.append(o.to(self.dtype).contiguous())
+        # 4) stash the leftover tail (kv_cache.py:192-195)
+        leftover = total - n_consumed
+        if leftover > 0:
+            self.h_buffer[:, :leftover] = combined[:, n_consumed:]
+        self.h_buf_count = leftover
+        compressed = [s.out[:, : s.length] for s in self._streams]
+        return [*compressed, sw[:, :, 0], sw[:, :, 1]]
+
+    def reset(self) -> None:
+        self._sw.reset()
+        for s in self._streams:
+            s.reset()
+        self.h_buf_count = 0
+
+
+class HCAKVCacheLayer(_CompressedLayer):
+    """Append-only KV cache for ``HCA`` on paged storage (kv_cache.py:90-207)."""
+
+    def __init__(self, max_seq_len: int, hidden_dim: int, head_dim: int, compression_rate: int, *,
+                 batch_size: int = 1, device: torch.device | str | None = None,
+                 dtype: torch.dtype = torch.float32, block_size: int = DEFAULT_BLOCK_SIZE) -> None:
+        super().__init__(max_seq_len, hidden_dim, [head_dim], compression_rate,
+                         batch_size=batch_size, device=device, dtype=dtype, block_size=block_size)
+
+    @property
+    def compressed(self) -> Tensor:
+        """(B, max_blocks, head_dim): rows [0, n_blocks) hold the compressed entries."""
+        return self._streams[0].out
+
+    def append(self, h_new: Tensor, sw_k_new: Tensor, sw_v_new: Tensor, *,
+               compressor: Callable[[Tensor], Tensor]) -> tuple[Tensor, Tensor, Tensor]:
+        """Append T_new tokens; return (compressed_view, sw_k_view, sw_v_view)."""
+        out = self._append("HCAKVCacheLayer", h_new, sw_k_new, sw_v_new, [compressor])
+        return out[0], out[1], out[2]
+
+
+class CSAKVCacheLayer(_CompressedLayer):
+    """Append-only KV cache for ``CSA`` on paged storage (kv_cache.py:210-327).
+
+    The main (``compressed_kv``) and indexer (``indexer_kv``) streams advance in
+    lockstep on m-aligned boundaries.
+    """
+
+    def __init__(self, max_seq_len: int, hidden_dim: int, head_dim: int, c_indexer: int,
+                 compression_rate: int, *, batch_size: int = 1,
+                 device: torch.device | str | None = None, dtype: torch.dtype = torch.float32,
+                 block_size: int = DEFAULT_BLOCK_SIZE) -> None:
+        super().__init__(max_seq_len, hidden_dim, [head_dim, c_indexer], compression_rate,
+                         batch_size=batch_size, device=device, dtype=dtype, block_size=block_size)
+        self.c_indexer = c_indexer
+
+    @property
+    def compressed_kv(self) -> Tensor:
+        return self._streams[0].out
+
+    @property
+    def indexer_kv(self) -> Tensor:
+        return self._streams[1].out
+
+    def append(self, h_new: Tensor, sw_k_new: Tensor, sw_v_new: Tensor, *,
+               compressor: Callable[[Tensor], Tensor],
+               indexer_compressor: Callable[[Tensor], Tensor]) -> tuple[Tensor, Tensor, Tensor, Tensor]:
+        """Append T_new tokens. Returns (compressed_kv, indexer_kv, sw_k, sw_v) views."""
+        out = self._append("CSAKVCacheLayer", h_new, sw_k_new, sw_v_new,
+                           [compressor, indexer_compressor])
+        return out[0], out[1], out[2], out[3]
+
+
+_CacheLayer = SWAKVCacheLayer | HCAKVCacheLayer | CSAKVCacheLayer | None
+
+
+class KVCacheBundle:
+    """Per-layer KV cache container indexed by transformer block index (kv_cache.py:333-427)."""
+
+    def __init__(self, layers: list[_CacheLayer]) -> None:
+        self._layers = list(layers)
+
+    def __len__(self) -> int:
+        return len(self._layers)
+
+    def for_layer(self, idx: int) -> _CacheLayer:
+        """Return the cache for block ``idx`` or ``None`` if uncached."""
+        return self._layers[idx]
+
+    @property
+    def length(self) -> int:
+        """Decoded positions cached in the first populated entry (all advance in lockstep)."""
+        for layer in self._layers:
+            if layer is not None:
+                return layer.length
+        return 0
+
+    def reset(self) -> None:
+        for layer in self._layers:
+            if layer is not None:
+                layer.reset()
+
+    @classmethod
+    def for_model(cls, model: object, *, max_seq_len: int, batch_size: int = 1,
+                  device: torch.device | str | None = None,
+                  dtype: torch.dtype = torch.float32) -> KVCacheBundle:
+        """Build a bundle by walking ``model.blocks`` (kv_cache.py:369-427).
+
+        Attention modules are recognised by class name (``SWAttention``, ``HCA``,
+        ``CSA``), so the bundle needs no import of the model package.
+        """
+        cfg = model.cfg  # type: ignore[attr-defined]
+        head_dim = cfg.attention.head_dim
+        hidden_dim = cfg.hidden_dim
+        layers: list[_CacheLayer] = []
+        for block in model.blocks:  # type: ignore[attr-defined]
+            kind = type(block.attention).__name__
+            if kind == "SWAttention":
+                layers.append(SWAKVCacheLayer(max_seq_len=max_seq_len, head_dim=head_dim,
+                                              batch_size=batch_size, device=device, dtype=dtype))
+            elif kind == "HCA":
+                layers.append(HCAKVCacheLayer(max_seq_len=max_seq_len, hidden_dim=hidden_dim,
+                                              head_dim=head_dim,
+                                              compression_rate=cfg.hca.compression_rate,
+                                              batch_size=batch_size, device=device, dtype=dtype))
+            elif kind == "CSA":
+                layers.append(CSAKVCacheLayer(max_seq_len=max_seq_len, hidden_dim=hidden_dim,
+                                              head_dim=head_dim,
+                                              c_indexer=cfg.csa.indexer_head_dim,
+                                              compression_rate=cfg.csa.compression_rate,
+                                              batch_size=batch_size, device=device, dtype=dtype))
+            else:
+                layers.append(None)
+        return cls(layers)
