@@ -176,17 +176,25 @@ int skv_fp8_decode_host(const uint8_t* codes, float* x, int64_t n);
  * min(k, n_cols, n_valid) best valid columns ordered by score descending,
  * ties by ascending index; a pick whose score is not finite is -1, and ranks
  * past that count are -1.  Replaces the mask + topk + isfinite of
- * CSA._indexer_topk_cached (csa.py:411-422).  k <= 2048. */
+ * CSA._indexer_topk_cached (csa.py:411-422).  k <= 2048, rows <= 65535. */
 int skv_topk_select(const float* scores, int64_t score_stride, int64_t rows,
                     const int32_t* n_valid, const int32_t* n_cols, int32_t n_cols_uniform,
-                    int64_t k, int32_t* out_idx, int64_t out_stride, void* stream);
+                    int64_t k, int32_t* out_idx, int64_t out_stride, int32_t* workspace,
+                    void* stream);
 
 /* Decode form: row b is the query at position seq_lens[b]-1 of sequence b,
  * n_cols = seq_lens[b] / m and n_valid = (seq_lens[b]-1) / m (a block s is
  * visible iff s*m + m - 1 < q_pos; kernels/attention.py:53-57). */
 int skv_topk_select_decode(const float* scores, int64_t score_stride, int64_t batch,
                            const int32_t* seq_lens, int64_t m, int64_t k, int32_t* out_idx,
-                           int64_t out_stride, void* stream);
+                           int64_t out_stride, int32_t* workspace, void* stream);
+
+/* Top-k workspace size in int32 words per row.  workspace == NULL selects one
+ * workgroup per row; otherwise each row is cut into 2048-score chunks (one
+ * workgroup each, two launches) using rows * skv_topk_workspace_words() words
+ * that must be zero before the first call and are left zero by every call.
+ * Calls that share a workspace must not overlap. */
+int64_t skv_topk_workspace_words(void);
 
 /* ---- top-k gather -----------------------------------------------------------
  * dst[r, j] = entry max(idx[r*idx_stride + j], 0) of sequence row_seq[r]
@@ -240,7 +248,8 @@ int skv_compact(const skv_pool_ref* pools, int32_t n_pools, int32_t* block_table
  *               layers fold (c, z) into the running pooling state and emit the
  *               entry when the block completes (bf16 or fp8); CSA layers do
  *               the same for the indexer stream (bf16 entries).
- *   3 top-k   : per CSA layer, skv_topk_select_decode over its score row.
+ *   3 top-k   : per CSA layer, skv_topk_select_decode over its score row
+ *               (multi-workgroup form, two launches).
  *   4 gather  : CSA layers gather their top_k picks (fp8 dequantized to bf16;
  *               -1 reads entry 0, picks without an entry give zero rows); HCA
  *               layers copy all their entries (dense read, rows past the
@@ -289,6 +298,7 @@ typedef struct skv_decode_layer {
   const float* scores;    /* CSA: [batch, score_stride] fp32 indexer scores */
   int64_t score_stride;
   int32_t* topk_idx;      /* CSA out: [batch, top_k] */
+  int32_t* topk_ws;       /* CSA: [batch, skv_topk_workspace_words()] int32, zeroed once */
   void* out_entries;      /* CSA: [batch, top_k, latent]; HCA: [batch, out_rows, latent] bf16 */
   int64_t out_rows;       /* HCA: rows per sequence of out_entries */
   void* out_window;       /* [batch, window, latent] bf16 */

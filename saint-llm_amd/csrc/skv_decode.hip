@@ -143,23 +143,39 @@ __global__ __launch_bounds__(kPoolWave) void k_decode_append(const skv_decode_de
 }
 
 // ---------------------------------------------------------------------------
-// 3. top-k: grid (batch, CSA layers)
+// 3. top-k: two launches over grid (chunks, batch, CSA layers): chunk
+//    histograms, then filter + last-chunk ordering (skv_topk.h).
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(kTopkThreads) void k_decode_topk(const skv_decode_desc* __restrict__ d) {
-  __shared__ TopkSmem sm;
-  const int b = blockIdx.x;
-  int want = blockIdx.y, li = 0;
-  for (; li < d->n_layers; ++li) {
-    if (d->layers[li].kind == SKV_LAYER_CSA && want-- == 0) break;
+__device__ __forceinline__ const skv_decode_layer* csa_layer(const skv_decode_desc* d, int want) {
+  for (int li = 0; li < d->n_layers; ++li) {
+    if (d->layers[li].kind == SKV_LAYER_CSA && want-- == 0) return &d->layers[li];
   }
-  if (li >= d->n_layers) return;  // uniform over the workgroup
-  const skv_decode_layer& Ly = d->layers[li];
-  const skv_page_group& G = d->groups[Ly.group];
+  return nullptr;
+}
+
+__global__ __launch_bounds__(kTopkThreads) void k_decode_topk_hist(const skv_decode_desc* __restrict__ d) {
+  __shared__ TopkHistSmem sm;
+  const skv_decode_layer* Ly = csa_layer(d, blockIdx.z);
+  if (!Ly) return;  // uniform over the workgroup
+  const int b = blockIdx.y;
+  const int m = d->groups[Ly->group].m;
   const int L = d->tok_lens[b];
-  const int n_cols = L / G.m;
-  const int n_valid = L > 0 ? (L - 1) / G.m : 0;
-  topk_row(sm, Ly.scores + static_cast<int64_t>(b) * Ly.score_stride, n_cols, n_valid, Ly.top_k,
-           Ly.topk_idx + static_cast<int64_t>(b) * Ly.top_k);
+  topk_hist_chunk(sm, Ly->scores + static_cast<int64_t>(b) * Ly->score_stride, L / m,
+                  L > 0 ? (L - 1) / m : 0, Ly->top_k, blockIdx.x, gridDim.x,
+                  Ly->topk_ws + static_cast<int64_t>(b) * kTkWsWords);
+}
+
+__global__ __launch_bounds__(kTopkThreads) void k_decode_topk_select(const skv_decode_desc* __restrict__ d) {
+  __shared__ TopkSelectSmem sm;
+  const skv_decode_layer* Ly = csa_layer(d, blockIdx.z);
+  if (!Ly) return;
+  const int b = blockIdx.y;
+  const int m = d->groups[Ly->group].m;
+  const int L = d->tok_lens[b];
+  topk_select_chunk(sm, Ly->scores + static_cast<int64_t>(b) * Ly->score_stride, L / m,
+                    L > 0 ? (L - 1) / m : 0, Ly->top_k, blockIdx.x, gridDim.x,
+                    Ly->topk_ws + static_cast<int64_t>(b) * kTkWsWords,
+                    Ly->topk_idx + static_cast<int64_t>(b) * Ly->top_k);
 }
 
 // ---------------------------------------------------------------------------
@@ -315,6 +331,7 @@ extern "C" int skv_decode_step(const skv_decode_desc* h, const skv_decode_desc* 
     }
   }
   int n_csa = 0, max_rows = 0;
+  int64_t max_score_cols = 1;
   for (int l = 0; l < h->n_layers; ++l) {
     const skv_decode_layer& Ly = h->layers[l];
     if (!Ly.ring || !Ly.kv_new || !Ly.out_window) return set_error(SKV_EINVAL, "%s: layer %d lacks ring/kv_new/out_window", what, l);
@@ -329,9 +346,12 @@ extern "C" int skv_decode_step(const skv_decode_desc* h, const skv_decode_desc* 
                          (long long)Ly.entry_bytes, Ly.format);
       }
       if (Ly.kind == SKV_LAYER_CSA) {
-        if (Ly.top_k <= 0 || Ly.top_k > kMaxTopK || !Ly.scores || !Ly.topk_idx) {
-          return set_error(SKV_EINVAL, "%s: CSA layer %d needs 0 < top_k <= %d, scores and topk_idx", what, l, kMaxTopK);
+        if (Ly.top_k <= 0 || Ly.top_k > kMaxTopK || !Ly.scores || !Ly.topk_idx || !Ly.topk_ws ||
+            Ly.score_stride <= 0) {
+          return set_error(SKV_EINVAL, "%s: CSA layer %d needs 0 < top_k <= %d, scores, topk_idx and topk_ws",
+                           what, l, kMaxTopK);
         }
+        max_score_cols = max(max_score_cols, Ly.score_stride);
         if (Ly.idx_pool && (!Ly.idx_state || !Ly.idx_bias || !Ly.ci_new || !Ly.zi_new || h->c_indexer <= 0)) {
           return set_error(SKV_EINVAL, "%s: CSA layer %d indexer stream incomplete", what, l);
         }
@@ -354,7 +374,10 @@ extern "C" int skv_decode_step(const skv_decode_desc* h, const skv_decode_desc* 
   hipLaunchKernelGGL(k_decode_append, dim3(h->batch, h->n_layers), dim3(kPoolWave), 0, s, dd);
   if ((rc = check_launch(what))) return rc;
   if (n_csa > 0) {
-    hipLaunchKernelGGL(k_decode_topk, dim3(h->batch, n_csa), dim3(kTopkThreads), 0, s, dd);
+    const dim3 tgrid(static_cast<unsigned>(ceil_div(max_score_cols, kTkChunk)), h->batch, n_csa);
+    hipLaunchKernelGGL(k_decode_topk_hist, tgrid, dim3(kTopkThreads), 0, s, dd);
+    if ((rc = check_launch(what))) return rc;
+    hipLaunchKernelGGL(k_decode_topk_select, tgrid, dim3(kTopkThreads), 0, s, dd);
     if ((rc = check_launch(what))) return rc;
   }
   const dim3 ggrid(static_cast<unsigned>(ceil_div(max_rows, kGatherRowsD)), h->batch, h->n_layers);

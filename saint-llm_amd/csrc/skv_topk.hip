@@ -30,6 +30,7 @@ struct TopkArgs {
 
 __global__ __launch_bounds__(kTopkThreads) void k_topk_select(TopkArgs a) {
   __shared__ TopkSmem sm;
+  __shared__ uint32_t keys[kLdsKeys];
   const int r = blockIdx.x;
   int n_cols, n_valid;
   if (a.lens) {
@@ -40,7 +41,43 @@ __global__ __launch_bounds__(kTopkThreads) void k_topk_select(TopkArgs a) {
     n_cols = a.n_cols ? a.n_cols[r] : a.n_cols_uni;
     n_valid = a.n_valid[r];
   }
-  topk_row(sm, a.scores + r * a.stride, n_cols, n_valid, a.k, a.out + r * a.out_stride);
+  topk_row(sm, keys, a.scores + r * a.stride, n_cols, n_valid, a.k, a.out + r * a.out_stride);
+}
+
+// Multi-workgroup form: grid (chunks, rows), workspace kTkWsWords int32 per row.
+struct TopkMultiArgs {
+  TopkArgs a;
+  int32_t* ws;
+  int n_chunks;
+};
+
+__device__ __forceinline__ void topk_row_dims(const TopkArgs& a, int r, int& n_cols, int& n_valid) {
+  if (a.lens) {
+    const int L = max(a.lens[r], 0);
+    n_cols = L / a.m;
+    n_valid = L > 0 ? (L - 1) / a.m : 0;
+  } else {
+    n_cols = a.n_cols ? a.n_cols[r] : a.n_cols_uni;
+    n_valid = a.n_valid[r];
+  }
+}
+
+__global__ __launch_bounds__(kTopkThreads) void k_topk_hist(TopkMultiArgs m) {
+  __shared__ TopkHistSmem sm;
+  const int r = blockIdx.y;
+  int n_cols, n_valid;
+  topk_row_dims(m.a, r, n_cols, n_valid);
+  topk_hist_chunk(sm, m.a.scores + r * m.a.stride, n_cols, n_valid, m.a.k, blockIdx.x, m.n_chunks,
+                  m.ws + static_cast<int64_t>(r) * kTkWsWords);
+}
+
+__global__ __launch_bounds__(kTopkThreads) void k_topk_select_multi(TopkMultiArgs m) {
+  __shared__ TopkSelectSmem sm;
+  const int r = blockIdx.y;
+  int n_cols, n_valid;
+  topk_row_dims(m.a, r, n_cols, n_valid);
+  topk_select_chunk(sm, m.a.scores + r * m.a.stride, n_cols, n_valid, m.a.k, blockIdx.x, m.n_chunks,
+                    m.ws + static_cast<int64_t>(r) * kTkWsWords, m.a.out + r * m.a.out_stride);
 }
 
 // ---------------------------------------------------------------------------
@@ -146,22 +183,35 @@ __global__ __launch_bounds__(kGatherThreads) void k_topk_gather(TopkGatherArgs a
 
 using namespace skv;
 
-static int launch_topk(const TopkArgs& a, int64_t rows, void* stream, const char* what) {
+static int launch_topk(const TopkArgs& a, int64_t rows, int32_t* workspace, void* stream,
+                       const char* what) {
   if (a.k < 0 || a.k > kMaxTopK) {
     return set_error(SKV_EINVAL, "%s: k must be in [0, %d]; got %d", what, kMaxTopK, a.k);
   }
-  if (rows < 0 || rows > INT32_MAX) return set_error(SKV_EINVAL, "%s: bad rows", what);
+  if (rows < 0 || rows > 65535) return set_error(SKV_EINVAL, "%s: rows must be in [0, 65535]", what);
   if (!a.out || a.out_stride < a.k) return set_error(SKV_EINVAL, "%s: out_stride must be >= k", what);
+  if (a.stride <= 0) return set_error(SKV_EINVAL, "%s: score_stride must be positive", what);
   if (rows == 0 || a.k == 0) return SKV_OK;
-  hipLaunchKernelGGL(k_topk_select, dim3(static_cast<unsigned>(rows)), dim3(kTopkThreads), 0,
-                     static_cast<hipStream_t>(stream), a);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (!workspace) {
+    hipLaunchKernelGGL(k_topk_select, dim3(static_cast<unsigned>(rows)), dim3(kTopkThreads), 0, s, a);
+    return check_launch(what);
+  }
+  TopkMultiArgs m{a, workspace, static_cast<int>(ceil_div(a.stride, kTkChunk))};
+  const dim3 grid(static_cast<unsigned>(m.n_chunks), static_cast<unsigned>(rows));
+  hipLaunchKernelGGL(k_topk_hist, grid, dim3(kTopkThreads), 0, s, m);
+  int rc = check_launch(what);
+  if (rc) return rc;
+  hipLaunchKernelGGL(k_topk_select_multi, grid, dim3(kTopkThreads), 0, s, m);
   return check_launch(what);
 }
+
+extern "C" int64_t skv_topk_workspace_words(void) { return kTkWsWords; }
 
 extern "C" int skv_topk_select(const float* scores, int64_t score_stride, int64_t rows,
                                const int32_t* n_valid, const int32_t* n_cols,
                                int32_t n_cols_uniform, int64_t k, int32_t* out_idx,
-                               int64_t out_stride, void* stream) {
+                               int64_t out_stride, int32_t* workspace, void* stream) {
   if (!n_valid) return set_error(SKV_EINVAL, "skv_topk_select: n_valid is NULL");
   TopkArgs a{};
   a.scores = scores;
@@ -172,12 +222,13 @@ extern "C" int skv_topk_select(const float* scores, int64_t score_stride, int64_
   a.k = static_cast<int>(k);
   a.out = out_idx;
   a.out_stride = out_stride;
-  return launch_topk(a, rows, stream, "skv_topk_select");
+  return launch_topk(a, rows, workspace, stream, "skv_topk_select");
 }
 
 extern "C" int skv_topk_select_decode(const float* scores, int64_t score_stride, int64_t batch,
                                       const int32_t* seq_lens, int64_t m, int64_t k,
-                                      int32_t* out_idx, int64_t out_stride, void* stream) {
+                                      int32_t* out_idx, int64_t out_stride, int32_t* workspace,
+                                      void* stream) {
   if (m <= 0) return set_error(SKV_EINVAL, "skv_topk_select_decode: compression_rate must be positive; got %lld", (long long)m);
   if (!seq_lens) return set_error(SKV_EINVAL, "skv_topk_select_decode: seq_lens is NULL");
   TopkArgs a{};
@@ -188,7 +239,7 @@ extern "C" int skv_topk_select_decode(const float* scores, int64_t score_stride,
   a.k = static_cast<int>(k);
   a.out = out_idx;
   a.out_stride = out_stride;
-  return launch_topk(a, batch, stream, "skv_topk_select_decode");
+  return launch_topk(a, batch, workspace, stream, "skv_topk_select_decode");
 }
 
 extern "C" int skv_topk_gather(void* dst, const void* pool, int64_t entry_bytes, int64_t block_size,

@@ -58,8 +58,9 @@ SIGNATURES: dict[str, list] = {
     ],
     "skv_fp8_encode_host": [_P, _P, _I64],
     "skv_fp8_decode_host": [_P, _P, _I64],
-    "skv_topk_select": [_P, _I64, _I64, _P, _P, _I32, _I64, _P, _I64, _P],
-    "skv_topk_select_decode": [_P, _I64, _I64, _P, _I64, _I64, _P, _I64, _P],
+    "skv_topk_select": [_P, _I64, _I64, _P, _P, _I32, _I64, _P, _I64, _P, _P],
+    "skv_topk_select_decode": [_P, _I64, _I64, _P, _I64, _I64, _P, _I64, _P, _P],
+    "skv_topk_workspace_words": [],
     "skv_topk_gather": [
         _P, _P, _I64, _I64, _I64, _P, _I64, _P, _P, _I64, _I64, _I64, _P, _I64, _I32, _P,
     ],
@@ -85,6 +86,9 @@ class PoolRef(ctypes.Structure):
 
     _fields_ = [("base", ctypes.c_void_p), ("page_bytes", ctypes.c_int64)]
 
+# entry points returning a size rather than a status code
+INT64_RESULTS = {"skv_topk_workspace_words"}
+
 _lib: ctypes.CDLL | None = None
 
 
@@ -106,7 +110,7 @@ def load() -> ctypes.CDLL:
     for name, argtypes in SIGNATURES.items():
         fn = getattr(lib, name)
         fn.argtypes = argtypes
-        fn.restype = ctypes.c_int
+        fn.restype = ctypes.c_int64 if name in INT64_RESULTS else ctypes.c_int
     lib.skv_last_error.argtypes = []
     lib.skv_last_error.restype = ctypes.c_char_p
     abi = lib.skv_abi_version()
@@ -143,3 +147,7 @@ def stream_handle(device: torch.device | None = None) -> int:
 
 def ptr(t: torch.Tensor | None) -> int | None:
     return None if t is None else t.data_ptr()
+
+
+def topk_workspace_words() -> int:
+    return int(load().skv_topk_workspace_words())

@@ -11,7 +11,7 @@
 * per CSA layer the indexer stream (bf16 entries, same pages).
 
 ``step()`` runs one decode step for every sequence through the fused C-ABI
-entry point ``skv_decode_step`` (four launches).  The per-step inputs live in
+entry point ``skv_decode_step`` (five launches).  The per-step inputs live in
 fixed device buffers (``inputs``), so a sequence of steps can be captured in a
 HIP graph and replayed.
 
@@ -52,7 +52,7 @@ class DecodeLayerC(ctypes.Structure):
         ("top_k", ctypes.c_int32), ("ring", _P), ("pool", _P), ("entry_bytes", ctypes.c_int64),
         ("state", _P), ("bias", _P), ("idx_pool", _P), ("idx_state", _P), ("idx_bias", _P),
         ("kv_new", _P), ("c_new", _P), ("z_new", _P), ("ci_new", _P), ("zi_new", _P),
-        ("scores", _P), ("score_stride", ctypes.c_int64), ("topk_idx", _P),
+        ("scores", _P), ("score_stride", ctypes.c_int64), ("topk_idx", _P), ("topk_ws", _P),
         ("out_entries", _P), ("out_rows", ctypes.c_int64), ("out_window", _P),
     ]
 
@@ -150,13 +150,14 @@ class DecodeCache:
         self.idx_pool, self.idx_state, self.idx_bias = [], [], []
         self.inputs: list[dict[str, torch.Tensor]] = []
         self.scores, self.topk_idx, self.out_entries, self.out_window = [], [], [], []
+        self.topk_ws = []
         for spec in layers:
             if spec.kind not in KIND:
                 raise ValueError(f"unknown layer kind {spec.kind!r}")
             self.ring.append(torch.zeros(batch, window, latent, dtype=bf, device=dev))
             self.out_window.append(torch.zeros(batch, window, latent, dtype=bf, device=dev))
             inp = {"kv": torch.zeros(batch, latent, dtype=bf, device=dev)}
-            pool = state = bias = ipool = istate = ibias = sc = tk = oe = None
+            pool = state = bias = ipool = istate = ibias = sc = tk = oe = ws = None
             if spec.kind in ("csa", "hca"):
                 g = self.groups[self.group_of_rate[spec.m]]
                 if spec.fp8:
@@ -177,6 +178,7 @@ class DecodeCache:
                         inp["zi"] = torch.zeros(batch, c_indexer, dtype=bf, device=dev)
                     sc = torch.zeros(batch, max(1, max_len // spec.m), dtype=torch.float32, device=dev)
                     tk = torch.full((batch, spec.top_k), -1, dtype=torch.int32, device=dev)
+                    ws = ops.topk_workspace(batch, dev)
                     oe = torch.zeros(batch, spec.top_k, latent, dtype=bf, device=dev)
                 else:
                     rows = hca_out_rows or max(1, max_len // spec.m)
@@ -190,6 +192,7 @@ class DecodeCache:
             self.inputs.append(inp)
             self.scores.append(sc)
             self.topk_idx.append(tk)
+            self.topk_ws.append(ws)
             self.out_entries.append(oe)
         self._build_desc()
 
@@ -221,6 +224,7 @@ class DecodeCache:
                     Ly.top_k = spec.top_k
                     Ly.scores, Ly.score_stride = p(self.scores[i]), self.scores[i].shape[1]
                     Ly.topk_idx = p(self.topk_idx[i])
+                    Ly.topk_ws = p(self.topk_ws[i])
                     if spec.indexer:
                         Ly.idx_pool, Ly.idx_state = p(self.idx_pool[i]), p(self.idx_state[i])
                         Ly.idx_bias = p(self.idx_bias[i])

@@ -338,9 +338,27 @@ def _check_idx_out(out: torch.Tensor, rows: int, k: int) -> None:
         raise ValueError("out must have unit column stride")
 
 
+def topk_workspace(rows: int, device: torch.device) -> torch.Tensor:
+    """Zeroed workspace for the multi-workgroup top-k of ``rows`` rows."""
+    return torch.zeros(rows * _lib.topk_workspace_words(), dtype=torch.int32, device=device)
+
+
+def _ws_ptr(workspace: torch.Tensor | None, rows: int) -> int | None:
+    if workspace is None:
+        return None
+    _require_i32(workspace, "workspace")
+    if workspace.numel() < rows * _lib.topk_workspace_words():
+        raise ValueError("top-k workspace too small: need rows * skv_topk_workspace_words() int32")
+    return workspace.data_ptr()
+
+
 def topk_select(scores: torch.Tensor, n_valid: torch.Tensor, n_cols: int | torch.Tensor, k: int,
-                out: torch.Tensor) -> torch.Tensor:
-    """Per row: the min(k, n_cols, n_valid) best valid columns, -1 padded to k."""
+                out: torch.Tensor, workspace: torch.Tensor | None = None) -> torch.Tensor:
+    """Per row: the min(k, n_cols, n_valid) best valid columns, -1 padded to k.
+
+    With ``workspace`` (see topk_workspace) each row is spread over several
+    workgroups; without it one workgroup handles a row.
+    """
     rows = n_valid.shape[0]
     _require_i32(n_valid, "n_valid", (rows,))
     _check_scores(scores, rows)
@@ -353,19 +371,20 @@ def topk_select(scores: torch.Tensor, n_valid: torch.Tensor, n_cols: int | torch
         if nc_uni > scores.shape[1]:
             raise ValueError(f"n_cols={nc_uni} exceeds the score row length {scores.shape[1]}")
     _lib.call("skv_topk_select", scores.data_ptr(), scores.stride(0), rows, n_valid.data_ptr(),
-              nc_ptr, nc_uni, k, out.data_ptr(), out.stride(0), _lib.stream_handle(scores.device))
+              nc_ptr, nc_uni, k, out.data_ptr(), out.stride(0), _ws_ptr(workspace, rows),
+              _lib.stream_handle(scores.device))
     return out
 
 
 def topk_select_decode(scores: torch.Tensor, seq_lens: torch.Tensor, m: int, k: int,
-                       out: torch.Tensor) -> torch.Tensor:
+                       out: torch.Tensor, workspace: torch.Tensor | None = None) -> torch.Tensor:
     """Decode query at position L-1 of each sequence: causal block mask from seq_lens."""
     batch = seq_lens.shape[0]
     _require_i32(seq_lens, "seq_lens", (batch,))
     _check_scores(scores, batch)
     _check_idx_out(out, batch, k)
     _lib.call("skv_topk_select_decode", scores.data_ptr(), scores.stride(0), batch,
-              seq_lens.data_ptr(), m, k, out.data_ptr(), out.stride(0),
+              seq_lens.data_ptr(), m, k, out.data_ptr(), out.stride(0), _ws_ptr(workspace, batch),
               _lib.stream_handle(scores.device))
     return out
 

@@ -168,19 +168,29 @@ def test_fp8_quant_append_bit_exact(dev) -> None:
 
 
 # ------------------------------------------------------------------ top-k ----
+@pytest.mark.parametrize("multi", [False, True])
 @pytest.mark.parametrize("n,k", [(64, 16), (16384, 512), (20000, 1024), (100_000, 1024), (5000, 2048)])
-def test_topk_select_distinct(dev, n, k) -> None:
+def test_topk_select_distinct(dev, n, k, multi) -> None:
     from saint_kv import ops
 
     rng = np.random.default_rng(n + k)
     rows = 6
+    ws = ops.topk_workspace(rows, dev) if multi else None
+    if multi:  # a first call on other data: the workspace must come back clean
+        warm = torch.randn(rows, n, device=dev)
+        ops.topk_select(warm, _i32(np.full(rows, n), dev), n, k,
+                        torch.empty(rows, k, dtype=torch.int32, device=dev), ws)
     s = rng.standard_normal((rows, n)).astype(np.float32)
     n_valid = rng.integers(0, n + 1, size=rows).astype(np.int32)
     n_valid[0], n_valid[1] = n, min(k // 2, n)
     out = torch.full((rows, k), -7, dtype=torch.int32, device=dev)
-    ops.topk_select(torch.from_numpy(s).to(dev), _i32(n_valid, dev), n, k, out)
+    ops.topk_select(torch.from_numpy(s).to(dev), _i32(n_valid, dev), n, k, out, ws)
     exp = ref.topk_select(s, n_valid, k, n)
     torch.cuda.synchronize()
+    if multi:
+        # histograms and counters are back to zero (the meta words may persist)
+        wsv = ws.view(rows, -1).cpu()
+        assert (wsv[:, :2048] == 0).all() and (wsv[:, 2052:2056] == 0).all()
     got = _np(out)[:, : exp.shape[1]]
     assert np.array_equal(got, exp)
     assert (_np(out)[:, exp.shape[1]:] == -1).all()
@@ -193,7 +203,8 @@ def test_topk_select_distinct(dev, n, k) -> None:
                           np.where(exp_t >= 0, s[rows_i, np.maximum(exp_t, 0)], 0))
 
 
-def test_topk_select_ties_nonfinite_ragged_cols(dev) -> None:
+@pytest.mark.parametrize("multi", [False, True])
+def test_topk_select_ties_nonfinite_ragged_cols(dev, multi) -> None:
     from saint_kv import ops
 
     rng = np.random.default_rng(13)
@@ -206,7 +217,8 @@ def test_topk_select_ties_nonfinite_ragged_cols(dev) -> None:
     n_cols = np.array([n, n, 30000, 20000, 100], dtype=np.int32)
     n_valid = np.array([n, 39000, 30000, 20000, 50], dtype=np.int32)
     out = torch.full((rows, k), -7, dtype=torch.int32, device=dev)
-    ops.topk_select(torch.from_numpy(s).to(dev), _i32(n_valid, dev), _i32(n_cols, dev), k, out)
+    ws = ops.topk_workspace(rows, dev) if multi else None
+    ops.topk_select(torch.from_numpy(s).to(dev), _i32(n_valid, dev), _i32(n_cols, dev), k, out, ws)
     torch.cuda.synchronize()
     for r in range(rows):
         exp = ref.topk_select(s[r:r + 1], n_valid[r:r + 1], k, int(n_cols[r]))[0]
@@ -214,7 +226,25 @@ def test_topk_select_ties_nonfinite_ragged_cols(dev) -> None:
         assert (_np(out)[r, len(exp):] == -1).all()
 
 
-def test_topk_select_decode_masks(dev) -> None:
+def test_topk_select_multi_threshold_ties(dev) -> None:
+    """Duplicates straddling the threshold, few enough for the multi path's tie list."""
+    from saint_kv import ops
+
+    rng = np.random.default_rng(21)
+    rows, n, k = 4, 30000, 700
+    s = rng.standard_normal((rows, n)).astype(np.float32)
+    s = np.round(s * 2048) / 2048  # ~1e-3 resolution: many equal keys near the threshold
+    ws = ops.topk_workspace(rows, dev)
+    out = torch.full((rows, k), -7, dtype=torch.int32, device=dev)
+    n_valid = np.array([n, n - 5, 12345, 701], dtype=np.int32)
+    ops.topk_select(torch.from_numpy(s).to(dev), _i32(n_valid, dev), n, k, out, ws)
+    torch.cuda.synchronize()
+    exp = ref.topk_select(s, n_valid, k, n)
+    assert np.array_equal(_np(out), exp)
+
+
+@pytest.mark.parametrize("multi", [False, True])
+def test_topk_select_decode_masks(dev, multi) -> None:
     from saint_kv import ops
 
     rng = np.random.default_rng(14)
@@ -223,7 +253,8 @@ def test_topk_select_decode_masks(dev) -> None:
     n = int(lens.max() // m)
     s = rng.standard_normal((len(lens), n)).astype(np.float32)
     out = torch.full((len(lens), k), -7, dtype=torch.int32, device=dev)
-    ops.topk_select_decode(torch.from_numpy(s).to(dev), _i32(lens, dev), m, k, out)
+    ws = ops.topk_workspace(len(lens), dev) if multi else None
+    ops.topk_select_decode(torch.from_numpy(s).to(dev), _i32(lens, dev), m, k, out, ws)
     torch.cuda.synchronize()
     for b, L in enumerate(lens):
         n_cols = int(L) // m
