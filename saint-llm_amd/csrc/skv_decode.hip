@@ -88,64 +88,14 @@ __global__ __launch_bounds__(kPlanThreads) void k_decode_plan(const skv_decode_d
 }
 
 // ---------------------------------------------------------------------------
-// 2. append: ring row, pooling state fold / entry emission.  grid (batch, layers)
+// 2. append + top-k histograms, one launch, 256-thread workgroups:
+//    blocks [0, batch*layers)        : (sequence, layer) appends — wave 0-1 fold
+//                                      the main stream, wave 2 the indexer stream,
+//                                      wave 3 copies the ring row;
+//    blocks [batch*layers, + chunks*batch*csa) : top-k histogram chunks.
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ void decode_fold(const skv_page_group& G, int b, int64_t p, void* pool,
-                                            int64_t entry_bytes, float* state, const float* bias,
-                                            const void* c_all, const void* z_all, int channels,
-                                            int format, int fp8_main, int lane) {
-  const int groups = channels >> 3;
-  float* sbase = state + static_cast<int64_t>(b) * 3 * channels;
-  const uint16_t* crow = static_cast<const uint16_t*>(c_all) + static_cast<int64_t>(b) * channels;
-  const uint16_t* zrow = static_cast<const uint16_t*>(z_all) + static_cast<int64_t>(b) * channels;
-  PoolState st;
-  if (p % G.m != 0) {
-    state_load(st, sbase, channels, lane, groups);
-  } else {
-    state_reset(st);
-  }
-  state_update(st, crow, zrow, bias + (p % G.m) * channels, lane, groups);
-  if ((p + 1) % G.m == 0) {
-    const int64_t e = (p + 1) / G.m - 1;
-    const int64_t pi = e / G.block_size;
-    const int32_t page = (pi < G.bt_stride) ? G.block_table[b * G.bt_stride + pi] : -1;
-    if (page >= 0 && page < G.n_pages) {
-      uint8_t* entry = static_cast<uint8_t*>(pool) +
-                       (static_cast<int64_t>(page) * G.block_size + e % G.block_size) * entry_bytes;
-      state_emit_entry(st, entry, lane, groups, format, fp8_main);
-    }
-  } else {
-    state_store(st, sbase, channels, lane, groups);
-  }
-}
+constexpr int kAppendThreads = 256;
 
-__global__ __launch_bounds__(kPoolWave) void k_decode_append(const skv_decode_desc* __restrict__ d) {
-  const int b = blockIdx.x;
-  const skv_decode_layer& Ly = d->layers[blockIdx.y];
-  const int lane = threadIdx.x;
-  const int L = d->tok_lens[b];
-  if (L <= 0) return;
-  const int64_t p = L - 1;
-  // ring row of the token
-  const int row_chunks = d->latent >> 3;  // 16-byte chunks of a bf16 row
-  const u32x4* src = static_cast<const u32x4*>(Ly.kv_new) + static_cast<int64_t>(b) * row_chunks;
-  u32x4* dst = static_cast<u32x4*>(Ly.ring) + (static_cast<int64_t>(b) * d->window + p % d->window) * row_chunks;
-  for (int c = lane; c < row_chunks; c += kPoolWave) dst[c] = src[c];
-  if (Ly.kind == SKV_LAYER_SWA) return;
-  const skv_page_group& G = d->groups[Ly.group];
-  const int fp8_main = (Ly.format == SKV_FMT_FP8) ? d->latent - SKV_FP8_ROPE_DIMS : 0;
-  decode_fold(G, b, p, Ly.pool, Ly.entry_bytes, Ly.state, Ly.bias, Ly.c_new, Ly.z_new, d->latent,
-              Ly.format, fp8_main, lane);
-  if (Ly.kind == SKV_LAYER_CSA && Ly.idx_pool) {
-    decode_fold(G, b, p, Ly.idx_pool, static_cast<int64_t>(d->c_indexer) * 2, Ly.idx_state, Ly.idx_bias,
-                Ly.ci_new, Ly.zi_new, d->c_indexer, SKV_FMT_BF16, 0, lane);
-  }
-}
-
-// ---------------------------------------------------------------------------
-// 3. top-k: two launches over grid (chunks, batch, CSA layers): chunk
-//    histograms, then filter + last-chunk ordering (skv_topk.h).
-// ---------------------------------------------------------------------------
 __device__ __forceinline__ const skv_decode_layer* csa_layer(const skv_decode_desc* d, int want) {
   for (int li = 0; li < d->n_layers; ++li) {
     if (d->layers[li].kind == SKV_LAYER_CSA && want-- == 0) return &d->layers[li];
@@ -153,29 +103,170 @@ __device__ __forceinline__ const skv_decode_layer* csa_layer(const skv_decode_de
   return nullptr;
 }
 
-__global__ __launch_bounds__(kTopkThreads) void k_decode_topk_hist(const skv_decode_desc* __restrict__ d) {
-  __shared__ TopkHistSmem sm;
+// Fold the token into the running state of channel groups t, t + nt (8
+// channels each) of one stream and emit the entry when the block completes.
+// All threads t in [0, nt) of a stream must call it (fp8 amax shuffles span
+// the 16 lanes of a 128-channel block, which nt = 128 keeps inside a wave).
+__device__ __forceinline__ void decode_fold_part(const skv_page_group& G, int b, int64_t p, void* pool,
+                                                 int64_t entry_bytes, float* state, const float* bias,
+                                                 const void* c_all, const void* z_all, int channels,
+                                                 int format, int fp8_main, int t, int nt) {
+  const int groups = channels >> 3;
+  float* sbase = state + static_cast<int64_t>(b) * 3 * channels;
+  const uint16_t* crow = static_cast<const uint16_t*>(c_all) + static_cast<int64_t>(b) * channels;
+  const uint16_t* zrow = static_cast<const uint16_t*>(z_all) + static_cast<int64_t>(b) * channels;
+  const float* brow = bias + (p % G.m) * channels;
+  const bool fresh = (p % G.m) == 0;
+  const bool emit = ((p + 1) % G.m) == 0;
+  uint8_t* entry = nullptr;
+  if (emit) {
+    const int64_t e = (p + 1) / G.m - 1;
+    const int64_t pi = e / G.block_size;
+    const int32_t page = (pi < G.bt_stride) ? G.block_table[b * G.bt_stride + pi] : -1;
+    if (page >= 0 && page < G.n_pages) {
+      entry = static_cast<uint8_t*>(pool) +
+              (static_cast<int64_t>(page) * G.block_size + e % G.block_size) * entry_bytes;
+    }
+  }
+  for (int grp = t; grp < ((groups + nt - 1) / nt) * nt; grp += nt) {
+    const bool mine = grp < groups;
+    float mx[8], sum[8], acc[8];
+    if (mine && !fresh) {
+      const u32x4* sp = reinterpret_cast<const u32x4*>(sbase + grp * 8);
+      const u32x4 m0 = sp[0], m1 = sp[1];
+      const u32x4 s0 = *reinterpret_cast<const u32x4*>(sbase + channels + grp * 8);
+      const u32x4 s1 = *(reinterpret_cast<const u32x4*>(sbase + channels + grp * 8) + 1);
+      const u32x4 a0 = *reinterpret_cast<const u32x4*>(sbase + 2 * channels + grp * 8);
+      const u32x4 a1 = *(reinterpret_cast<const u32x4*>(sbase + 2 * channels + grp * 8) + 1);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        mx[j] = __uint_as_float(m0[j]);
+        mx[j + 4] = __uint_as_float(m1[j]);
+        sum[j] = __uint_as_float(s0[j]);
+        sum[j + 4] = __uint_as_float(s1[j]);
+        acc[j] = __uint_as_float(a0[j]);
+        acc[j + 4] = __uint_as_float(a1[j]);
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        mx[j] = -INFINITY;
+        sum[j] = 0.f;
+        acc[j] = 0.f;
+      }
+    }
+    float out[8];
+    if (mine) {
+      float c[8], z[8];
+      unpack8_bf16(*reinterpret_cast<const u32x4*>(crow + grp * 8), c);
+      unpack8_bf16(*reinterpret_cast<const u32x4*>(zrow + grp * 8), z);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float v = z[j] + brow[grp * 8 + j];
+        if (v > mx[j]) {
+          const float sc = expf(mx[j] - v);
+          sum[j] = sum[j] * sc + 1.f;
+          acc[j] = acc[j] * sc + c[j];
+          mx[j] = v;
+        } else {
+          const float w = expf(v - mx[j]);
+          sum[j] += w;
+          acc[j] += w * c[j];
+        }
+        out[j] = bf16_to_f32(f32_to_bf16(acc[j] / sum[j]));
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) out[j] = 0.f;
+    }
+    if (emit) {
+      if (entry) store_entry_group(entry, out, grp, groups, format, fp8_main);
+    } else if (mine) {
+      u32x4* sp = reinterpret_cast<u32x4*>(sbase + grp * 8);
+      sp[0] = u32x4{__float_as_uint(mx[0]), __float_as_uint(mx[1]), __float_as_uint(mx[2]), __float_as_uint(mx[3])};
+      sp[1] = u32x4{__float_as_uint(mx[4]), __float_as_uint(mx[5]), __float_as_uint(mx[6]), __float_as_uint(mx[7])};
+      u32x4* ss = reinterpret_cast<u32x4*>(sbase + channels + grp * 8);
+      ss[0] = u32x4{__float_as_uint(sum[0]), __float_as_uint(sum[1]), __float_as_uint(sum[2]), __float_as_uint(sum[3])};
+      ss[1] = u32x4{__float_as_uint(sum[4]), __float_as_uint(sum[5]), __float_as_uint(sum[6]), __float_as_uint(sum[7])};
+      u32x4* sa = reinterpret_cast<u32x4*>(sbase + 2 * channels + grp * 8);
+      sa[0] = u32x4{__float_as_uint(acc[0]), __float_as_uint(acc[1]), __float_as_uint(acc[2]), __float_as_uint(acc[3])};
+      sa[1] = u32x4{__float_as_uint(acc[4]), __float_as_uint(acc[5]), __float_as_uint(acc[6]), __float_as_uint(acc[7])};
+    }
+  }
+}
+
+__global__ __launch_bounds__(kAppendThreads) void k_decode_append(const skv_decode_desc* __restrict__ d,
+                                                                  int n_chunks) {
+  __shared__ TopkHistSmem hsm;
+  const int n_append = d->batch * d->n_layers;
+  if (static_cast<int>(blockIdx.x) >= n_append) {
+    // top-k histogram chunk (chunk, b, csa layer)
+    int u = blockIdx.x - n_append;
+    const int chunk = u % n_chunks;
+    u /= n_chunks;
+    const int b = u % d->batch;
+    const skv_decode_layer* Ly = csa_layer(d, u / d->batch);
+    if (!Ly) return;
+    const int m = d->groups[Ly->group].m;
+    const int L = d->tok_lens[b];
+    topk_hist_chunk(hsm, Ly->scores + static_cast<int64_t>(b) * Ly->score_stride, L / m,
+                    L > 0 ? (L - 1) / m : 0, Ly->top_k, chunk,
+                    Ly->topk_ws + static_cast<int64_t>(b) * kTkWsWords);
+    return;
+  }
+  const int b = blockIdx.x % d->batch;
+  const skv_decode_layer& Ly = d->layers[blockIdx.x / d->batch];
+  const int L = d->tok_lens[b];
+  if (L <= 0) return;
+  const int64_t p = L - 1;
+  const int tid = threadIdx.x;
+  const int wave = tid / kWave;
+  if (wave == 3) {
+    const int row_chunks = d->latent >> 3;  // 16-byte chunks of a bf16 row
+    const u32x4* src = static_cast<const u32x4*>(Ly.kv_new) + static_cast<int64_t>(b) * row_chunks;
+    u32x4* dst = static_cast<u32x4*>(Ly.ring) + (static_cast<int64_t>(b) * d->window + p % d->window) * row_chunks;
+    for (int c = tid - 3 * kWave; c < row_chunks; c += kWave) dst[c] = src[c];
+    return;
+  }
+  if (Ly.kind == SKV_LAYER_SWA) return;
+  const skv_page_group& G = d->groups[Ly.group];
+  if (wave < 2) {
+    const int fp8_main = (Ly.format == SKV_FMT_FP8) ? d->latent - SKV_FP8_ROPE_DIMS : 0;
+    decode_fold_part(G, b, p, Ly.pool, Ly.entry_bytes, Ly.state, Ly.bias, Ly.c_new, Ly.z_new, d->latent,
+                     Ly.format, fp8_main, tid, 2 * kWave);
+  } else if (Ly.kind == SKV_LAYER_CSA && Ly.idx_pool) {
+    decode_fold_part(G, b, p, Ly.idx_pool, static_cast<int64_t>(d->c_indexer) * 2, Ly.idx_state,
+                     Ly.idx_bias, Ly.ci_new, Ly.zi_new, d->c_indexer, SKV_FMT_BF16, 0, tid - 2 * kWave,
+                     kWave);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// 3. top-k filter (grid chunks, batch, CSA layers) and final (grid batch, CSA
+//    layers); see skv_topk.h.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(kTkPartThreads) void k_decode_topk_filter(const skv_decode_desc* __restrict__ d) {
+  __shared__ TopkFilterSmem sm;
   const skv_decode_layer* Ly = csa_layer(d, blockIdx.z);
   if (!Ly) return;  // uniform over the workgroup
   const int b = blockIdx.y;
   const int m = d->groups[Ly->group].m;
   const int L = d->tok_lens[b];
-  topk_hist_chunk(sm, Ly->scores + static_cast<int64_t>(b) * Ly->score_stride, L / m,
-                  L > 0 ? (L - 1) / m : 0, Ly->top_k, blockIdx.x, gridDim.x,
-                  Ly->topk_ws + static_cast<int64_t>(b) * kTkWsWords);
+  topk_filter_chunk(sm, Ly->scores + static_cast<int64_t>(b) * Ly->score_stride, L / m,
+                    L > 0 ? (L - 1) / m : 0, Ly->top_k, blockIdx.x,
+                    Ly->topk_ws + static_cast<int64_t>(b) * kTkWsWords);
 }
 
-__global__ __launch_bounds__(kTopkThreads) void k_decode_topk_select(const skv_decode_desc* __restrict__ d) {
-  __shared__ TopkSelectSmem sm;
-  const skv_decode_layer* Ly = csa_layer(d, blockIdx.z);
+__global__ __launch_bounds__(kTopkThreads) void k_decode_topk_final(const skv_decode_desc* __restrict__ d) {
+  __shared__ TopkFinalSmem sm;
+  const skv_decode_layer* Ly = csa_layer(d, blockIdx.y);
   if (!Ly) return;
-  const int b = blockIdx.y;
+  const int b = blockIdx.x;
   const int m = d->groups[Ly->group].m;
   const int L = d->tok_lens[b];
-  topk_select_chunk(sm, Ly->scores + static_cast<int64_t>(b) * Ly->score_stride, L / m,
-                    L > 0 ? (L - 1) / m : 0, Ly->top_k, blockIdx.x, gridDim.x,
-                    Ly->topk_ws + static_cast<int64_t>(b) * kTkWsWords,
-                    Ly->topk_idx + static_cast<int64_t>(b) * Ly->top_k);
+  topk_final_row(sm, Ly->scores + static_cast<int64_t>(b) * Ly->score_stride, L / m,
+                 L > 0 ? (L - 1) / m : 0, Ly->top_k, Ly->topk_ws + static_cast<int64_t>(b) * kTkWsWords,
+                 Ly->topk_idx + static_cast<int64_t>(b) * Ly->top_k);
 }
 
 // ---------------------------------------------------------------------------
@@ -371,13 +462,16 @@ extern "C" int skv_decode_step(const skv_decode_desc* h, const skv_decode_desc* 
   hipLaunchKernelGGL(k_decode_plan, dim3(1), dim3(kPlanThreads), 0, s, dd);
   int rc = check_launch(what);
   if (rc) return rc;
-  hipLaunchKernelGGL(k_decode_append, dim3(h->batch, h->n_layers), dim3(kPoolWave), 0, s, dd);
+  const int n_chunks = static_cast<int>(ceil_div(max_score_cols, kTkChunk));
+  const int64_t n_blocks = static_cast<int64_t>(h->batch) * h->n_layers +
+                           static_cast<int64_t>(n_chunks) * h->batch * n_csa;
+  hipLaunchKernelGGL(k_decode_append, dim3(static_cast<unsigned>(n_blocks)), dim3(kAppendThreads), 0, s,
+                     dd, n_chunks);
   if ((rc = check_launch(what))) return rc;
   if (n_csa > 0) {
-    const dim3 tgrid(static_cast<unsigned>(ceil_div(max_score_cols, kTkChunk)), h->batch, n_csa);
-    hipLaunchKernelGGL(k_decode_topk_hist, tgrid, dim3(kTopkThreads), 0, s, dd);
+    hipLaunchKernelGGL(k_decode_topk_filter, dim3(n_chunks, h->batch, n_csa), dim3(kTkPartThreads), 0, s, dd);
     if ((rc = check_launch(what))) return rc;
-    hipLaunchKernelGGL(k_decode_topk_select, tgrid, dim3(kTopkThreads), 0, s, dd);
+    hipLaunchKernelGGL(k_decode_topk_final, dim3(h->batch, n_csa), dim3(kTopkThreads), 0, s, dd);
     if ((rc = check_launch(what))) return rc;
   }
   const dim3 ggrid(static_cast<unsigned>(ceil_div(max_rows, kGatherRowsD)), h->batch, h->n_layers);

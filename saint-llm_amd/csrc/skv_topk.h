@@ -151,30 +151,29 @@ __device__ __forceinline__ void topk_row(TopkSmem& sm, uint32_t* keys, const flo
 }
 
 // ===========================================================================
-// Multi-workgroup selection: a row is cut into kTkChunk-score chunks, one
-// workgroup each, over two launches:
-//   hist   : every chunk adds its 11-bit key histogram (top bits of the key)
-//            to the row's global histogram; the last chunk to finish finds
-//            the threshold bin t (the bin holding rank `sel`) and stores
-//            {t, above = #keys in bins > t, need = sel - above, ties = hist[t]}.
-//   select : every chunk appends its keys in bins > t ("sure") and == t
-//            ("ties") to the row's lists (one atomic per wave); the last
-//            chunk to finish orders the winners: each candidate's rank among
-//            the candidates of its own bin gives its output position, and in
-//            bin t only the first `need` by (key desc, index asc) survive.
-//            It then clears the row's workspace for the next call.
-// No workgroup waits for another; "last" is decided by an atomic counter.
-// A tie bin larger than kTkTieCap falls back to the single-workgroup select.
+// Multi-workgroup selection in three launches (kernel boundaries order the
+// phases; no workgroup waits for or fences against another):
+//   hist   : every kTkChunk-score chunk of a row adds its 11-bit key histogram
+//            (top bits of the order key) to the row's global histogram.
+//   filter : every chunk finds the threshold bin t (the bin holding rank sel)
+//            from the histogram and appends its keys in bins > t ("sure") and
+//            == t ("ties") to the row's lists, one atomic per wave.
+//   final  : one workgroup per row orders the winners: a candidate's rank
+//            among the candidates of its own bin gives its output position;
+//            in bin t only the first `need` by (key desc, index asc) survive.
+//            It then zeroes the row's histogram and counters for the next call.
+// A tie bin larger than kTkTieCap makes final fall back to the single-
+// workgroup select over the row.
 // ===========================================================================
 constexpr int kTkChunk = 2048;
+constexpr int kTkPartThreads = 256;  // hist / filter workgroups
 constexpr int kTkBins = 2048;
 constexpr int kTkShift = 21;
 constexpr int kTkTieCap = 4096;
 // per-row workspace layout, int32 words
 constexpr int kTkWsHist = 0;
-constexpr int kTkWsMeta = kTkBins;          // t, above, need, ties
-constexpr int kTkWsCnt = kTkWsMeta + 4;     // done_hist, done_select, n_sure, n_tie
-constexpr int kTkWsSure = kTkWsCnt + 4;     // (key, idx) pairs, kMaxTopK of them
+constexpr int kTkWsCnt = kTkBins;       // n_sure, n_tie, (2 spare)
+constexpr int kTkWsSure = kTkWsCnt + 4; // (key, idx) pairs, kMaxTopK of them
 constexpr int kTkWsTie = kTkWsSure + 2 * kMaxTopK;
 constexpr int kTkWsWords = kTkWsTie + 2 * kTkTieCap;
 
@@ -186,82 +185,129 @@ __device__ __forceinline__ int topk_sel(int k, int n_cols, int n_valid) {
 
 struct TopkHistSmem {
   int hist[kTkBins];
-  int scan_lds[17];
-  int last;
 };
 
 __device__ __forceinline__ void topk_hist_chunk(TopkHistSmem& sm, const float* row, int n_cols,
-                                                int n_valid, int k, int chunk, int n_chunks,
-                                                int32_t* ws) {
+                                                int n_valid, int k, int chunk, int32_t* ws) {
   const int tid = threadIdx.x;
-  const int sel = topk_sel(k, n_cols, n_valid);
-  n_valid = max(0, min(n_valid, max(n_cols, 0)));
+  if (topk_sel(k, n_cols, n_valid) == 0) return;  // uniform
+  n_valid = max(0, min(n_valid, n_cols));
   const int i0 = chunk * kTkChunk;
   const int i1 = min(n_valid, i0 + kTkChunk);
-  if (sel > 0 && i0 < i1) {
-    for (int b = tid; b < kTkBins; b += kTopkThreads) sm.hist[b] = 0;
-    __syncthreads();
-    for (int i = i0 + tid; i < i1; i += kTopkThreads) {
-      atomicAdd(&sm.hist[score_key(row[i]) >> kTkShift], 1);
-    }
-    __syncthreads();
-    for (int b = tid; b < kTkBins; b += kTopkThreads) {
-      if (sm.hist[b]) atomicAdd(&ws[kTkWsHist + b], sm.hist[b]);
-    }
-  }
-  __threadfence();
+  if (i0 >= i1) return;
+  for (int b = tid; b < kTkBins; b += kTkPartThreads) sm.hist[b] = 0;
   __syncthreads();
-  if (tid == 0) sm.last = (atomicAdd(&ws[kTkWsCnt + 0], 1) == n_chunks - 1);
+  for (int i = i0 + tid; i < i1; i += kTkPartThreads) {
+    atomicAdd(&sm.hist[score_key(row[i]) >> kTkShift], 1);
+  }
   __syncthreads();
-  if (!sm.last) return;
-  __threadfence();
-  // the whole row's histogram is in: find the bin of rank `sel`
-  if (tid == 0) ws[kTkWsCnt + 0] = 0;
-  if (sel == 0) {
-    if (tid == 0) {
-      ws[kTkWsMeta + 0] = -1;
-      ws[kTkWsMeta + 1] = 0;
-      ws[kTkWsMeta + 2] = 0;
-      ws[kTkWsMeta + 3] = 0;
-    }
-    return;
-  }
-  // exactly one thread owns the bin of rank sel (the histogram totals n_valid >= sel)
-  const int b0 = kTkBins - 1 - 2 * tid;  // this thread's bins, descending: b0, b0 - 1
-  const int v0 = __atomic_load_n(&ws[kTkWsHist + b0], __ATOMIC_RELAXED);
-  const int v1 = __atomic_load_n(&ws[kTkWsHist + b0 - 1], __ATOMIC_RELAXED);
-  int tot;
-  const int ex = block_exclusive_scan(v0 + v1, sm.scan_lds, &tot);  // keys in bins > b0
-  int t = -1, above = 0, ties = 0;
-  if (ex < sel && sel <= ex + v0) {
-    t = b0;
-    above = ex;
-    ties = v0;
-  } else if (ex + v0 < sel && sel <= ex + v0 + v1) {
-    t = b0 - 1;
-    above = ex + v0;
-    ties = v1;
-  }
-  if (t >= 0) {
-    ws[kTkWsMeta + 0] = t;
-    ws[kTkWsMeta + 1] = above;
-    ws[kTkWsMeta + 2] = sel - above;
-    ws[kTkWsMeta + 3] = ties;
+  for (int b = tid; b < kTkBins; b += kTkPartThreads) {
+    if (sm.hist[b]) atomicAdd(&ws[kTkWsHist + b], sm.hist[b]);
   }
 }
 
-struct TopkSelectSmem {
+// Threshold bin of rank sel from the row histogram (every thread gets it).
+// hist[] is the histogram staged in LDS; nthreads * per == kTkBins.
+template <int kThreads>
+__device__ __forceinline__ void topk_threshold(const int* hist, int sel, int* scan_lds, int* sh,
+                                               int& t, int& above, int& ties) {
+  constexpr int per = kTkBins / kThreads;
+  const int tid = threadIdx.x;
+  const int hi = kTkBins - 1 - tid * per;  // this thread's bins: hi, hi-1, ..., hi-per+1
+  int v[per];
+  int sum = 0;
+#pragma unroll
+  for (int q = 0; q < per; ++q) {
+    v[q] = hist[hi - q];
+    sum += v[q];
+  }
+  int tot;
+  int ex = block_exclusive_scan(sum, scan_lds, &tot);  // keys in bins > hi
+#pragma unroll
+  for (int q = 0; q < per; ++q) {
+    if (ex < sel && sel <= ex + v[q]) {
+      sh[0] = hi - q;
+      sh[1] = ex;
+      sh[2] = v[q];
+    }
+    ex += v[q];
+  }
+  __syncthreads();
+  t = sh[0];
+  above = sh[1];
+  ties = sh[2];
+  __syncthreads();
+}
+
+struct TopkFilterSmem {
+  int hist[kTkBins];
   int scan_lds[17];
+  int sh[3];
+};
+
+__device__ __forceinline__ void topk_filter_chunk(TopkFilterSmem& sm, const float* row, int n_cols,
+                                                  int n_valid, int k, int chunk, int32_t* ws) {
+  const int tid = threadIdx.x;
+  const int lane = tid & (kWave - 1);
+  const int sel = topk_sel(k, n_cols, n_valid);
+  if (sel == 0) return;  // uniform
+  n_valid = max(0, min(n_valid, n_cols));
+  const int i0 = chunk * kTkChunk;
+  const int i1 = min(n_valid, i0 + kTkChunk);
+  if (i0 >= i1) return;
+  for (int b = tid; b < kTkBins; b += kTkPartThreads) sm.hist[b] = ws[kTkWsHist + b];
+  __syncthreads();
+  int t, above, ties;
+  topk_threshold<kTkPartThreads>(sm.hist, sel, sm.scan_lds, sm.sh, t, above, ties);
+  if (ties > kTkTieCap) return;  // final falls back to the single-workgroup select
+  for (int base = i0; base < i0 + kTkChunk; base += kTkPartThreads) {
+    const int i = base + tid;
+    const bool valid = i < i1;
+    const uint32_t key = valid ? score_key(row[i]) : 0u;
+    const int b = static_cast<int>(key >> kTkShift);
+    const bool sure = valid && b > t;
+    const bool tie = valid && b == t;
+    const uint64_t ms = __ballot(sure);
+    const uint64_t mt = __ballot(tie);
+    const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+    int bs = 0, bt = 0;
+    if (lane == 0) {
+      if (ms) bs = atomicAdd(&ws[kTkWsCnt + 0], __popcll(ms));
+      if (mt) bt = atomicAdd(&ws[kTkWsCnt + 1], __popcll(mt));
+    }
+    bs = __shfl(bs, 0);
+    bt = __shfl(bt, 0);
+    if (sure) {
+      const int s = bs + __popcll(ms & below);
+      ws[kTkWsSure + 2 * s] = static_cast<int32_t>(key);
+      ws[kTkWsSure + 2 * s + 1] = i;
+    }
+    if (tie) {
+      const int s = bt + __popcll(mt & below);
+      ws[kTkWsTie + 2 * s] = static_cast<int32_t>(key);
+      ws[kTkWsTie + 2 * s + 1] = i;
+    }
+  }
+}
+
+constexpr int kTkBuckets = 4096;  // final ordering: buckets of the top 15 key bits
+constexpr int kTkCand = kMaxTopK + kTkTieCap;
+
+struct TopkFinalSmem {
+  int scan_lds[17];
+  int sh[3];
   union {
     TopkSmem full;  // single-workgroup fallback (global-memory passes)
     struct {
       int hist[kTkBins];
-      int cursor[kTkBins];
-      uint32_t key[kMaxTopK + kTkTieCap];
-      int idx[kMaxTopK + kTkTieCap];
+      int cursor[kTkBuckets];  // counts, then running cursors (bucket ends after the scatter)
+      int start[kTkBuckets];   // first slot of each bucket (descending key order)
+      uint32_t key[kTkCand];   // candidates as read from the lists
+      int idx[kTkCand];
+      uint32_t skey[kTkCand];  // candidates in bucket order
+      int sidx[kTkCand];
     } fin;
   } u;
-  int last;
 };
 
 __device__ __forceinline__ void topk_clear_ws(int32_t* ws) {
@@ -269,107 +315,85 @@ __device__ __forceinline__ void topk_clear_ws(int32_t* ws) {
   if (threadIdx.x < 4) ws[kTkWsCnt + threadIdx.x] = 0;
 }
 
-__device__ __forceinline__ void topk_select_chunk(TopkSelectSmem& sm, const float* row, int n_cols,
-                                                  int n_valid, int k, int chunk, int n_chunks,
-                                                  int32_t* ws, int32_t* out) {
+// One 1024-thread workgroup per row.  The candidates (every key in bins > t
+// and every tie in bin t) are counting-sorted by bucket = (key >> 17) - (t << 4)
+// (clamped to the last bucket: a monotone map of the key), ranked by
+// (key desc, index asc) inside their bucket, and the first sel are written.
+__device__ __forceinline__ void topk_final_row(TopkFinalSmem& sm, const float* row, int n_cols,
+                                               int n_valid, int k, int32_t* ws, int32_t* out) {
   const int tid = threadIdx.x;
-  const int lane = tid & (kWave - 1);
   const int sel = topk_sel(k, n_cols, n_valid);
   n_valid = max(0, min(n_valid, max(n_cols, 0)));
-  const int t = ws[kTkWsMeta + 0];
-  const int above = ws[kTkWsMeta + 1];
-  const int need = ws[kTkWsMeta + 2];
-  const int ties = ws[kTkWsMeta + 3];
-  const bool fallback = ties > kTkTieCap;
-  if (sel > 0 && !fallback) {
-    const int i0 = chunk * kTkChunk;
-    const int i1 = min(n_valid, i0 + kTkChunk);
-    for (int base = i0; base < i0 + kTkChunk; base += kTopkThreads) {
-      const int i = base + tid;
-      const bool valid = i < i1;
-      const uint32_t key = valid ? score_key(row[i]) : 0u;
-      const int b = static_cast<int>(key >> kTkShift);
-      const bool sure = valid && b > t;
-      const bool tie = valid && b == t;
-      const uint64_t ms = __ballot(sure);
-      const uint64_t mt = __ballot(tie);
-      const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-      int bs = 0, bt = 0;
-      if (lane == 0) {
-        if (ms) bs = atomicAdd(&ws[kTkWsCnt + 2], __popcll(ms));
-        if (mt) bt = atomicAdd(&ws[kTkWsCnt + 3], __popcll(mt));
-      }
-      bs = __shfl(bs, 0);
-      bt = __shfl(bt, 0);
-      if (sure) {
-        const int s = bs + __popcll(ms & below);
-        ws[kTkWsSure + 2 * s] = static_cast<int32_t>(key);
-        ws[kTkWsSure + 2 * s + 1] = i;
-      }
-      if (tie) {
-        const int s = bt + __popcll(mt & below);
-        ws[kTkWsTie + 2 * s] = static_cast<int32_t>(key);
-        ws[kTkWsTie + 2 * s + 1] = i;
-      }
-    }
-  }
-  __threadfence();
-  __syncthreads();
-  if (tid == 0) sm.last = (atomicAdd(&ws[kTkWsCnt + 1], 1) == n_chunks - 1);
-  __syncthreads();
-  if (!sm.last) return;
-  __threadfence();
   for (int j = sel + tid; j < k; j += kTopkThreads) out[j] = -1;
   if (sel == 0) {
     topk_clear_ws(ws);
     return;
   }
-  if (fallback) {
-    __syncthreads();
+  auto& F = sm.u.fin;
+  for (int b = tid; b < kTkBins; b += kTopkThreads) F.hist[b] = ws[kTkWsHist + b];
+  for (int b = tid; b < kTkBuckets; b += kTopkThreads) F.cursor[b] = 0;
+  __syncthreads();
+  int t, above, ties;
+  topk_threshold<kTopkThreads>(F.hist, sel, sm.scan_lds, sm.sh, t, above, ties);
+  if (ties > kTkTieCap) {
     topk_row(sm.u.full, nullptr, row, n_cols, n_valid, k, out);
     __syncthreads();
     topk_clear_ws(ws);
     return;
   }
-  // bin segments: bins > t hold every key of theirs, bin t holds all ties
-  auto& F = sm.u.fin;
-  for (int b = tid; b < kTkBins; b += kTopkThreads) {
-    F.hist[b] = (b >= t) ? __atomic_load_n(&ws[kTkWsHist + b], __ATOMIC_RELAXED) : 0;
-  }
-  __syncthreads();
-  {
-    // exclusive suffix sums = segment starts, bins descending
-    const int b0 = kTkBins - 1 - 2 * tid;
-    const int v0 = F.hist[b0], v1 = F.hist[b0 - 1];
-    int tot;
-    const int ex = block_exclusive_scan(v0 + v1, sm.scan_lds, &tot);
-    F.cursor[b0] = ex;
-    F.cursor[b0 - 1] = ex + v0;
-  }
-  __syncthreads();
+  const uint32_t base = static_cast<uint32_t>(t) << 4;
+  auto bucket_of = [&](uint32_t key) -> int {
+    return static_cast<int>(min((key >> 17) - base, static_cast<uint32_t>(kTkBuckets - 1)));
+  };
   const int total = above + ties;
   for (int c = tid; c < total; c += kTopkThreads) {
     const int32_t* src = (c < above) ? &ws[kTkWsSure + 2 * c] : &ws[kTkWsTie + 2 * (c - above)];
-    const uint32_t key = static_cast<uint32_t>(__atomic_load_n(src, __ATOMIC_RELAXED));
-    const int idx = __atomic_load_n(src + 1, __ATOMIC_RELAXED);
-    const int slot = atomicAdd(&F.cursor[key >> kTkShift], 1);
-    F.key[slot] = key;
-    F.idx[slot] = idx;
+    const uint32_t key = static_cast<uint32_t>(src[0]);
+    F.key[c] = key;
+    F.idx[c] = src[1];
+    atomicAdd(&F.cursor[bucket_of(key)], 1);
+  }
+  __syncthreads();
+  {
+    constexpr int per = kTkBuckets / kTopkThreads;  // buckets per thread, descending
+    const int hi = kTkBuckets - 1 - tid * per;
+    int v[per];
+    int sum = 0;
+#pragma unroll
+    for (int q = 0; q < per; ++q) {
+      v[q] = F.cursor[hi - q];
+      sum += v[q];
+    }
+    int tot;
+    int ex = block_exclusive_scan(sum, sm.scan_lds, &tot);  // candidates in higher buckets
+#pragma unroll
+    for (int q = 0; q < per; ++q) {
+      F.start[hi - q] = ex;
+      F.cursor[hi - q] = ex;
+      ex += v[q];
+    }
   }
   __syncthreads();
   for (int c = tid; c < total; c += kTopkThreads) {
-    const uint32_t kc = F.key[c];
-    const int ic = F.idx[c];
-    const int b = static_cast<int>(kc >> kTkShift);
-    const int s1 = F.cursor[b];  // end of this bin's segment after the scatter
-    const int s0 = s1 - F.hist[b];
+    const uint32_t key = F.key[c];
+    const int slot = atomicAdd(&F.cursor[bucket_of(key)], 1);
+    F.skey[slot] = key;
+    F.sidx[slot] = F.idx[c];
+  }
+  __syncthreads();
+  for (int c = tid; c < total; c += kTopkThreads) {
+    const uint32_t kc = F.skey[c];
+    const int ic = F.sidx[c];
+    const int bkt = bucket_of(kc);
+    const int s0 = F.start[bkt];
+    if (s0 >= sel) continue;  // the whole bucket ranks past the winners
+    const int s1 = F.cursor[bkt];
     int rank = 0;
     for (int j = s0; j < s1; ++j) {
-      const uint32_t kj = F.key[j];
-      rank += (kj > kc) || (kj == kc && F.idx[j] < ic);
+      const uint32_t kj = F.skey[j];
+      rank += (kj > kc) || (kj == kc && F.sidx[j] < ic);
     }
-    if (b == t && rank >= need) continue;
-    out[s0 + rank] = key_finite(kc) ? ic : -1;
+    if (s0 + rank < sel) out[s0 + rank] = key_finite(kc) ? ic : -1;
   }
   __syncthreads();
   topk_clear_ws(ws);

@@ -44,11 +44,11 @@ __global__ __launch_bounds__(kTopkThreads) void k_topk_select(TopkArgs a) {
   topk_row(sm, keys, a.scores + r * a.stride, n_cols, n_valid, a.k, a.out + r * a.out_stride);
 }
 
-// Multi-workgroup form: grid (chunks, rows), workspace kTkWsWords int32 per row.
+// Multi-workgroup form: hist and filter over grid (chunks, rows), final over
+// grid (rows); workspace kTkWsWords int32 per row.
 struct TopkMultiArgs {
   TopkArgs a;
   int32_t* ws;
-  int n_chunks;
 };
 
 __device__ __forceinline__ void topk_row_dims(const TopkArgs& a, int r, int& n_cols, int& n_valid) {
@@ -62,22 +62,31 @@ __device__ __forceinline__ void topk_row_dims(const TopkArgs& a, int r, int& n_c
   }
 }
 
-__global__ __launch_bounds__(kTopkThreads) void k_topk_hist(TopkMultiArgs m) {
+__global__ __launch_bounds__(kTkPartThreads) void k_topk_hist(TopkMultiArgs m) {
   __shared__ TopkHistSmem sm;
   const int r = blockIdx.y;
   int n_cols, n_valid;
   topk_row_dims(m.a, r, n_cols, n_valid);
-  topk_hist_chunk(sm, m.a.scores + r * m.a.stride, n_cols, n_valid, m.a.k, blockIdx.x, m.n_chunks,
+  topk_hist_chunk(sm, m.a.scores + r * m.a.stride, n_cols, n_valid, m.a.k, blockIdx.x,
                   m.ws + static_cast<int64_t>(r) * kTkWsWords);
 }
 
-__global__ __launch_bounds__(kTopkThreads) void k_topk_select_multi(TopkMultiArgs m) {
-  __shared__ TopkSelectSmem sm;
+__global__ __launch_bounds__(kTkPartThreads) void k_topk_filter(TopkMultiArgs m) {
+  __shared__ TopkFilterSmem sm;
   const int r = blockIdx.y;
   int n_cols, n_valid;
   topk_row_dims(m.a, r, n_cols, n_valid);
-  topk_select_chunk(sm, m.a.scores + r * m.a.stride, n_cols, n_valid, m.a.k, blockIdx.x, m.n_chunks,
-                    m.ws + static_cast<int64_t>(r) * kTkWsWords, m.a.out + r * m.a.out_stride);
+  topk_filter_chunk(sm, m.a.scores + r * m.a.stride, n_cols, n_valid, m.a.k, blockIdx.x,
+                    m.ws + static_cast<int64_t>(r) * kTkWsWords);
+}
+
+__global__ __launch_bounds__(kTopkThreads) void k_topk_final(TopkMultiArgs m) {
+  __shared__ TopkFinalSmem sm;
+  const int r = blockIdx.x;
+  int n_cols, n_valid;
+  topk_row_dims(m.a, r, n_cols, n_valid);
+  topk_final_row(sm, m.a.scores + r * m.a.stride, n_cols, n_valid, m.a.k,
+                 m.ws + static_cast<int64_t>(r) * kTkWsWords, m.a.out + r * m.a.out_stride);
 }
 
 // ---------------------------------------------------------------------------
@@ -197,12 +206,14 @@ static int launch_topk(const TopkArgs& a, int64_t rows, int32_t* workspace, void
     hipLaunchKernelGGL(k_topk_select, dim3(static_cast<unsigned>(rows)), dim3(kTopkThreads), 0, s, a);
     return check_launch(what);
   }
-  TopkMultiArgs m{a, workspace, static_cast<int>(ceil_div(a.stride, kTkChunk))};
-  const dim3 grid(static_cast<unsigned>(m.n_chunks), static_cast<unsigned>(rows));
-  hipLaunchKernelGGL(k_topk_hist, grid, dim3(kTopkThreads), 0, s, m);
+  TopkMultiArgs m{a, workspace};
+  const dim3 grid(static_cast<unsigned>(ceil_div(a.stride, kTkChunk)), static_cast<unsigned>(rows));
+  hipLaunchKernelGGL(k_topk_hist, grid, dim3(kTkPartThreads), 0, s, m);
   int rc = check_launch(what);
   if (rc) return rc;
-  hipLaunchKernelGGL(k_topk_select_multi, grid, dim3(kTopkThreads), 0, s, m);
+  hipLaunchKernelGGL(k_topk_filter, grid, dim3(kTkPartThreads), 0, s, m);
+  if ((rc = check_launch(what))) return rc;
+  hipLaunchKernelGGL(k_topk_final, dim3(static_cast<unsigned>(rows)), dim3(kTopkThreads), 0, s, m);
   return check_launch(what);
 }
 
