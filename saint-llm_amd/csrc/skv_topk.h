@@ -243,12 +243,19 @@ struct TopkFilterSmem {
   int hist[kTkBins];
   int scan_lds[17];
   int sh[3];
+  int wcnt[2][kTkPartThreads / kWave];  // per-wave candidate counts of this chunk
+  int base[2];                          // this chunk's slots in the row's lists
+  uint32_t key[2][kTkChunk];            // chunk-local compaction (sure, ties)
+  int idx[2][kTkChunk];
 };
 
+// Chunk-local compaction first, then one global atomic per list per chunk.
 __device__ __forceinline__ void topk_filter_chunk(TopkFilterSmem& sm, const float* row, int n_cols,
                                                   int n_valid, int k, int chunk, int32_t* ws) {
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
+  const int wid = tid / kWave;
+  constexpr int kWaves = kTkPartThreads / kWave;
   const int sel = topk_sel(k, n_cols, n_valid);
   if (sel == 0) return;  // uniform
   n_valid = max(0, min(n_valid, n_cols));
@@ -260,8 +267,13 @@ __device__ __forceinline__ void topk_filter_chunk(TopkFilterSmem& sm, const floa
   int t, above, ties;
   topk_threshold<kTkPartThreads>(sm.hist, sel, sm.scan_lds, sm.sh, t, above, ties);
   if (ties > kTkTieCap) return;  // final falls back to the single-workgroup select
-  for (int base = i0; base < i0 + kTkChunk; base += kTkPartThreads) {
-    const int i = base + tid;
+  // each wave owns a contiguous run of kTkChunk / kWaves scores
+  constexpr int kRun = kTkChunk / kWaves;
+  const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+  int ns = 0, nt = 0;  // wave-uniform running counts
+  const int r0 = i0 + wid * kRun;
+  for (int off = 0; off < kRun; off += kWave) {
+    const int i = r0 + off + lane;
     const bool valid = i < i1;
     const uint32_t key = valid ? score_key(row[i]) : 0u;
     const int b = static_cast<int>(key >> kTkShift);
@@ -269,23 +281,41 @@ __device__ __forceinline__ void topk_filter_chunk(TopkFilterSmem& sm, const floa
     const bool tie = valid && b == t;
     const uint64_t ms = __ballot(sure);
     const uint64_t mt = __ballot(tie);
-    const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-    int bs = 0, bt = 0;
-    if (lane == 0) {
-      if (ms) bs = atomicAdd(&ws[kTkWsCnt + 0], __popcll(ms));
-      if (mt) bt = atomicAdd(&ws[kTkWsCnt + 1], __popcll(mt));
-    }
-    bs = __shfl(bs, 0);
-    bt = __shfl(bt, 0);
     if (sure) {
-      const int s = bs + __popcll(ms & below);
-      ws[kTkWsSure + 2 * s] = static_cast<int32_t>(key);
-      ws[kTkWsSure + 2 * s + 1] = i;
+      const int s = wid * kRun + ns + __popcll(ms & below);
+      sm.key[0][s] = key;
+      sm.idx[0][s] = i;
     }
     if (tie) {
-      const int s = bt + __popcll(mt & below);
-      ws[kTkWsTie + 2 * s] = static_cast<int32_t>(key);
-      ws[kTkWsTie + 2 * s + 1] = i;
+      const int s = wid * kRun + nt + __popcll(mt & below);
+      sm.key[1][s] = key;
+      sm.idx[1][s] = i;
+    }
+    ns += __popcll(ms);
+    nt += __popcll(mt);
+  }
+  if (lane == 0) {
+    sm.wcnt[0][wid] = ns;
+    sm.wcnt[1][wid] = nt;
+  }
+  __syncthreads();
+  if (tid < 2) {
+    int tot = 0;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) tot += sm.wcnt[tid][w];
+    sm.base[tid] = tot ? atomicAdd(&ws[kTkWsCnt + tid], tot) : 0;
+  }
+  __syncthreads();
+  // copy each wave's run to the row lists, waves in order
+#pragma unroll
+  for (int l = 0; l < 2; ++l) {
+    int pre = sm.base[l];
+    for (int w = 0; w < wid; ++w) pre += sm.wcnt[l][w];
+    const int cnt = sm.wcnt[l][wid];
+    int32_t* dst = ws + (l == 0 ? kTkWsSure : kTkWsTie);
+    for (int q = lane; q < cnt; q += kWave) {
+      dst[2 * (pre + q)] = static_cast<int32_t>(sm.key[l][wid * kRun + q]);
+      dst[2 * (pre + q) + 1] = sm.idx[l][wid * kRun + q];
     }
   }
 }
