@@ -9,6 +9,9 @@ allocation) + fused append+gather of every sequence into a packed buffer.
 
 Prints one JSON line (see the keys below).  Progress goes to stderr.
 
+A step is one skv_decode_append_gather call: a one-workgroup planner (page
+reservation + page-unit table) and the fused append + gather over 4 KB slices.
+
 Algorithmic bytes per step (read + write of every gathered row, the appended
 row read + written, one int32 block-table entry per page):
     2 * sum(L) * 1152 + B * 2 * 1152 + sum(ceil(L / 64)) * 4
@@ -95,6 +98,7 @@ class PagedDecode:
         self.out = torch.empty(int(cap.sum()), ROW, dtype=torch.bfloat16, device=dev)
         self.tokens = torch.empty(steps_total, batch, 1, ROW, dtype=torch.bfloat16, device=dev)
         self.tokens.normal_(generator=gen)
+        self.units = ops.unit_table(batch * max_pages, dev)
         self.step_idx = 0
         torch.cuda.synchronize()
         if int(self.status.item()) != 0:
@@ -104,11 +108,13 @@ class PagedDecode:
         return self.lens0 + self.step_idx
 
     def step(self, ev: tuple | None = None) -> None:
-        self.ops.reserve(self.stack, self.top, self.bt, self.lens, 1, self.bs, self.status)
+        """skv_decode_append_gather: planner (reserve + page-unit table) + 4 KB-slice copy."""
+        max_units = int((-(-(self.host_lens() + 1) // self.bs)).sum())
+        self.ops.plan_units(self.stack, self.top, self.bt, self.lens, 1, self.bs, self.out,
+                            ROW_BYTES, self.units, max_units, self.offsets, self.status)
         if ev is not None:
             ev[0].record()
-        self.ops.append_gather(self.pool, self.bt, self.lens, self.tokens[self.step_idx], 1,
-                               self.out, self.offsets)
+        self.ops.copy_slices(self.pool, self.tokens[self.step_idx], self.out, self.units, max_units)
         if ev is not None:
             ev[1].record()
         self.step_idx += 1
@@ -252,7 +258,7 @@ def run_decode_leg(dev, name: str, specs, batch: int, lens0: np.ndarray, steps: 
         "mean_ctx": int(lens0.mean()), "steps": n_steps, "us_per_step": round(ms * 1e3, 2),
         "alg_bytes_per_step": int(alg), "gbs": round(gbs, 1), "pct_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 2),
         "kv_tokens_per_step": int(toks), "kv_tokens_per_s": round(toks / (ms * 1e-3), 1),
-        "launches_per_step": 4, "hip_graph_steps": per_graph,
+        "launches_per_step": 5, "hip_graph_steps": per_graph,
     }
     log(f"{name}: {rec['us_per_step']} us/step, {rec['gbs']} GB/s ({rec['pct_hbm_peak']}%), "
         f"{rec['kv_tokens_per_s'] / 1e6:.1f} M KV tok/s")
@@ -449,7 +455,7 @@ def main() -> int:
         "copy_yardstick_gbs": round(copy_gbs, 1),
         "roofline": {
             "bound": "hbm",
-            "kernel": "k_paged_copy<2> (skv_append_gather)",
+            "kernel": "k_copy_slices (fused append + gather of skv_decode_append_gather)",
             "achieved": round(achieved, 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",

@@ -58,6 +58,7 @@ extern "C" {
 #define SKV_STATUS_NOSPC 2     /* not enough free pages                     */
 #define SKV_STATUS_BADARG 4    /* negative count                            */
 #define SKV_STATUS_STACK 8     /* release would overfill the free stack     */
+#define SKV_STATUS_UNITS 16    /* page-unit table too small                 */
 
 /* ABI version tag (SKV_ABI_VERSION) and the last error on this thread. */
 int skv_abi_version(void);
@@ -115,6 +116,38 @@ int skv_append_gather(void* dst, const int64_t* dst_row_offsets, int64_t dst_seq
                       int64_t bt_stride, const int32_t* seq_lens, const int32_t* n_new,
                       int32_t n_new_uniform, const void* src, int64_t src_seq_stride,
                       int64_t src_row_stride, int64_t src_len, int64_t batch, void* stream);
+
+/* skv_decode_append_gather: skv_reserve + skv_append_gather as one decode
+ * step in two launches, the copy cut into 4 KB slices of page units (one
+ * 256-thread workgroup per slice).  units: int32 workspace of
+ * 8 + 8*max_units words where max_units >= sum over b of
+ * ceil((seq_lens[b] + n_new[b]) / block_size); the launch covers max_units
+ * units (pass the exact count when the host knows it).  On a refusal
+ * (SKV_STATUS_* in *status, including SKV_STATUS_UNITS) nothing changes and
+ * nothing is copied.  Same results as skv_reserve followed by
+ * skv_append_gather (kv_cache.py:63-83 on paged storage). */
+int skv_decode_append_gather(int32_t* free_stack, int32_t* free_top, int64_t n_pages,
+                             int32_t* block_table, int64_t bt_stride, int32_t* seq_lens,
+                             const int32_t* n_new, int32_t n_new_uniform, int32_t* status, void* dst,
+                             const int64_t* dst_row_offsets, int64_t dst_seq_stride_rows,
+                             int64_t dst_capacity_rows, void* pool, int64_t row_bytes,
+                             int64_t block_size, const void* src, int64_t src_seq_stride,
+                             int64_t src_row_stride, int64_t src_len, int32_t* units,
+                             int64_t max_units, int64_t batch, void* stream);
+
+/* The two launches of skv_decode_append_gather as separate calls:
+ * skv_plan_units reserves the pages, advances seq_lens and writes the unit
+ * table; skv_copy_slices performs the copy the table describes (new rows
+ * [seq_lens-n_new, seq_lens) of each unit from src, the rest from the pool). */
+int skv_plan_units(int32_t* free_stack, int32_t* free_top, int64_t n_pages, int32_t* block_table,
+                   int64_t bt_stride, int32_t* seq_lens, const int32_t* n_new,
+                   int32_t n_new_uniform, int32_t* status, const int64_t* dst_row_offsets,
+                   int64_t dst_seq_stride_rows, int64_t block_size, int32_t* units,
+                   int64_t max_units, int64_t batch, void* stream);
+int skv_copy_slices(void* dst, int64_t dst_capacity_rows, void* pool, int64_t row_bytes,
+                    int64_t block_size, int64_t n_pages, const void* src, int64_t src_seq_stride,
+                    int64_t src_row_stride, int64_t src_len, const int32_t* units,
+                    int64_t max_units, void* stream);
 
 /* ---- SWA ring -------------------------------------------------------------
  * ring: [batch, window, row_bytes]; token at position p of sequence b lives

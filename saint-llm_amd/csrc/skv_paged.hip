@@ -289,6 +289,161 @@ static int launch_copy(const CopyArgs& a, hipStream_t stream, const char* what) 
   return check_launch(what);
 }
 
+// ---------------------------------------------------------------------------
+// Decode step of a paged raw-token cache in two launches: a one-workgroup
+// planner (reserve + page-unit table) and a copy over 4 KB slices of the page
+// units, one 256-thread workgroup per slice (one 16-byte load per lane).
+// Unit table: word 0 = unit count; unit u at words 8 + 8u:
+//   page, sequence, rows, first new row (relative to the unit), dst row (int64)
+// ---------------------------------------------------------------------------
+constexpr int kUnitWords = 8;
+constexpr int kUnitHeader = 8;
+constexpr int kSliceThreads = 256;
+
+__global__ __launch_bounds__(kReserveThreads) void k_plan_units(
+    int32_t* __restrict__ stack, int32_t* __restrict__ top_ptr, int64_t n_pages,
+    int32_t* __restrict__ bt, int64_t bt_stride, int32_t* __restrict__ lens,
+    const int32_t* __restrict__ n_new, int32_t n_uni, int batch, int bs,
+    const int64_t* __restrict__ dst_off, int64_t dst_seq_stride_rows, int32_t* __restrict__ units,
+    int64_t max_units, int32_t* __restrict__ status) {
+  __shared__ int off[kMaxBatch + 1];
+  __shared__ int first[kMaxBatch];
+  __shared__ int uoff[kMaxBatch + 1];
+  __shared__ int scan_lds[17];
+  __shared__ int bad_all;
+  const int tid = threadIdx.x;
+  if (tid == 0) bad_all = 0;
+  int bad = 0;
+  int carry = 0, ucarry = 0;
+  for (int base = 0; base < batch; base += kReserveThreads) {
+    const int b = base + tid;
+    int need = 0, nu = 0;
+    if (b < batch) {
+      const int L = lens[b];
+      const int n = n_new ? n_new[b] : n_uni;
+      if (n < 0 || L < 0) {
+        bad |= SKV_STATUS_BADARG;
+      } else {
+        const int64_t p0 = ceil_div(L, bs);
+        const int64_t p1 = ceil_div(static_cast<int64_t>(L) + n, bs);
+        if (p1 > bt_stride) bad |= SKV_STATUS_MAX_PAGES;
+        need = static_cast<int>(p1 - p0);
+        nu = static_cast<int>(p1);
+        first[b] = static_cast<int>(p0);
+      }
+    }
+    int tot, utot;
+    const int ex = block_exclusive_scan(need, scan_lds, &tot);
+    const int uex = block_exclusive_scan(nu, scan_lds, &utot);
+    if (b < batch) {
+      off[b] = carry + ex;
+      uoff[b] = ucarry + uex;
+    }
+    carry += tot;
+    ucarry += utot;
+  }
+  const int top = *top_ptr;
+  if (top < 0 || top > n_pages) bad |= SKV_STATUS_BADARG;
+  else if (carry > top) bad |= SKV_STATUS_NOSPC;
+  if (ucarry > max_units) bad |= SKV_STATUS_UNITS;
+  if (bad) atomicOr(&bad_all, bad);
+  __syncthreads();
+  if (bad_all) {
+    if (tid == 0) {
+      units[0] = 0;  // the copy launch finds no work
+      if (status) *status = bad_all;
+    }
+    return;
+  }
+  if (tid == 0) {
+    off[batch] = carry;
+    uoff[batch] = ucarry;
+  }
+  __syncthreads();
+  for (int t = tid; t < carry; t += kReserveThreads) {
+    int lo = 0, hi = batch;
+    while (hi - lo > 1) {
+      const int mid = (lo + hi) >> 1;
+      if (off[mid] <= t) lo = mid; else hi = mid;
+    }
+    bt[static_cast<int64_t>(lo) * bt_stride + first[lo] + (t - off[lo])] = stack[top - 1 - t];
+  }
+  // unit table (pages popped above are taken from the stack, not re-read from bt)
+  for (int t = tid; t < ucarry; t += kReserveThreads) {
+    int lo = 0, hi = batch;
+    while (hi - lo > 1) {
+      const int mid = (lo + hi) >> 1;
+      if (uoff[mid] <= t) lo = mid; else hi = mid;
+    }
+    const int b = lo;
+    const int k = t - uoff[b];
+    const int L0 = lens[b];
+    const int n = n_new ? n_new[b] : n_uni;
+    const int L = L0 + n;
+    const int32_t page = (k >= first[b]) ? stack[top - 1 - (off[b] + k - first[b])]
+                                         : bt[static_cast<int64_t>(b) * bt_stride + k];
+    const int64_t drow = (dst_off ? dst_off[b] : static_cast<int64_t>(b) * dst_seq_stride_rows) +
+                         static_cast<int64_t>(k) * bs;
+    int32_t* e = units + kUnitHeader + static_cast<int64_t>(t) * kUnitWords;
+    e[0] = page;
+    e[1] = b;
+    e[2] = min(bs, L - k * bs);
+    e[3] = L0 - k * bs;  // rows at or after this index of the unit are new
+    e[4] = static_cast<int32_t>(drow & 0xffffffffll);
+    e[5] = static_cast<int32_t>(drow >> 32);
+  }
+  __syncthreads();  // every thread read lens[] before it advances
+  for (int b = tid; b < batch; b += kReserveThreads) lens[b] += n_new ? n_new[b] : n_uni;
+  if (tid == 0) {
+    *top_ptr = top - carry;
+    units[0] = ucarry;
+    if (status) *status = 0;
+  }
+}
+
+struct SliceArgs {
+  uint8_t* dst;
+  int64_t dst_cap;
+  uint8_t* pool;
+  int64_t row_bytes;
+  int bs;
+  int64_t n_pages;
+  const uint8_t* src;
+  int64_t src_seq_stride;
+  int64_t src_row_stride;
+  int64_t src_len;
+  const int32_t* units;
+  int slices;  // 4 KB slices per page
+};
+
+__global__ __launch_bounds__(kSliceThreads) void k_copy_slices(SliceArgs a) {
+  const int u = blockIdx.x / a.slices;
+  const int s = blockIdx.x - u * a.slices;
+  if (u >= a.units[0]) return;
+  const int32_t* e = a.units + kUnitHeader + static_cast<int64_t>(u) * kUnitWords;
+  const int32_t page = e[0];
+  const int b = e[1];
+  const int rows = e[2];
+  const int new_row0 = e[3];
+  const int64_t drow = (static_cast<int64_t>(static_cast<uint32_t>(e[4]))) | (static_cast<int64_t>(e[5]) << 32);
+  const int row_chunks = static_cast<int>(a.row_bytes >> 4);
+  const int c = s * kSliceThreads + threadIdx.x;
+  if (c >= rows * row_chunks || page < 0 || page >= a.n_pages || drow < 0 || drow + rows > a.dst_cap) return;
+  u32x4* pslot = reinterpret_cast<u32x4*>(a.pool + static_cast<int64_t>(page) * a.bs * a.row_bytes) + c;
+  u32x4* dslot = reinterpret_cast<u32x4*>(a.dst + drow * a.row_bytes) + c;
+  if (c >= max(new_row0, 0) * row_chunks) {
+    const int r = c / row_chunks;
+    const int i = r - new_row0;  // index among this call's new rows
+    if (i >= a.src_len) return;
+    const u32x4 v = *(reinterpret_cast<const u32x4*>(a.src + b * a.src_seq_stride + i * a.src_row_stride) +
+                      (c - r * row_chunks));
+    *pslot = v;
+    st_stream(dslot, v);
+  } else {
+    st_stream(dslot, ld_stream(pslot));
+  }
+}
+
 }  // namespace skv
 
 using namespace skv;
@@ -411,4 +566,83 @@ extern "C" int skv_append_gather(void* dst, const int64_t* dst_row_offsets,
   a.src_len = src_len;
   a.batch = static_cast<int>(batch);
   return launch_copy<2>(a, static_cast<hipStream_t>(stream), "skv_append_gather");
+}
+
+extern "C" int skv_plan_units(int32_t* free_stack, int32_t* free_top, int64_t n_pages,
+                              int32_t* block_table, int64_t bt_stride, int32_t* seq_lens,
+                              const int32_t* n_new, int32_t n_new_uniform, int32_t* status,
+                              const int64_t* dst_row_offsets, int64_t dst_seq_stride_rows,
+                              int64_t block_size, int32_t* units, int64_t max_units, int64_t batch,
+                              void* stream) {
+  const char* what = "skv_plan_units";
+  if (batch < 0 || batch > kMaxBatch) {
+    return set_error(SKV_EINVAL, "%s: batch must be in [0, %d]; got %lld", what, kMaxBatch, (long long)batch);
+  }
+  if (block_size <= 0 || bt_stride <= 0 || n_pages <= 0 || n_pages > INT32_MAX) {
+    return set_error(SKV_EINVAL, "%s: bad block_size/bt_stride/n_pages", what);
+  }
+  if (!n_new && n_new_uniform < 0) return set_error(SKV_EINVAL, "%s: n_new_uniform must be >= 0", what);
+  if (!units || max_units < 0 || max_units > INT32_MAX / kUnitWords) {
+    return set_error(SKV_EINVAL, "%s: need a unit table and 0 <= max_units < 2^28", what);
+  }
+  if (batch == 0) return SKV_OK;
+  hipLaunchKernelGGL(k_plan_units, dim3(1), dim3(kReserveThreads), 0, static_cast<hipStream_t>(stream),
+                     free_stack, free_top, n_pages, block_table, bt_stride, seq_lens, n_new, n_new_uniform,
+                     static_cast<int>(batch), static_cast<int>(block_size), dst_row_offsets,
+                     dst_seq_stride_rows, units, max_units, status);
+  return check_launch(what);
+}
+
+extern "C" int skv_copy_slices(void* dst, int64_t dst_capacity_rows, void* pool, int64_t row_bytes,
+                               int64_t block_size, int64_t n_pages, const void* src,
+                               int64_t src_seq_stride, int64_t src_row_stride, int64_t src_len,
+                               const int32_t* units, int64_t max_units, void* stream) {
+  const char* what = "skv_copy_slices";
+  int rc = validate_copy(what, row_bytes, block_size, 0, 1, pool, dst);
+  if (rc) return rc;
+  if ((rc = validate_src(what, src, src_seq_stride, src_row_stride))) return rc;
+  if (!units || max_units < 0 || max_units > INT32_MAX / kUnitWords) {
+    return set_error(SKV_EINVAL, "%s: need a unit table and 0 <= max_units < 2^28", what);
+  }
+  SliceArgs a{};
+  a.dst = static_cast<uint8_t*>(dst);
+  a.dst_cap = dst_capacity_rows;
+  a.pool = static_cast<uint8_t*>(pool);
+  a.row_bytes = row_bytes;
+  a.bs = static_cast<int>(block_size);
+  a.n_pages = n_pages;
+  a.src = static_cast<const uint8_t*>(src);
+  a.src_seq_stride = src_seq_stride;
+  a.src_row_stride = src_row_stride;
+  a.src_len = src_len;
+  a.units = units;
+  a.slices = static_cast<int>(ceil_div(block_size * (row_bytes >> 4), kSliceThreads));
+  const int64_t grid = max_units * a.slices;
+  if (grid == 0) return SKV_OK;
+  if (grid > INT32_MAX) return set_error(SKV_EINVAL, "%s: too many slices", what);
+  hipLaunchKernelGGL(k_copy_slices, dim3(static_cast<unsigned>(grid)), dim3(kSliceThreads), 0,
+                     static_cast<hipStream_t>(stream), a);
+  return check_launch(what);
+}
+
+extern "C" int skv_decode_append_gather(int32_t* free_stack, int32_t* free_top, int64_t n_pages,
+                                        int32_t* block_table, int64_t bt_stride, int32_t* seq_lens,
+                                        const int32_t* n_new, int32_t n_new_uniform, int32_t* status,
+                                        void* dst, const int64_t* dst_row_offsets,
+                                        int64_t dst_seq_stride_rows, int64_t dst_capacity_rows,
+                                        void* pool, int64_t row_bytes, int64_t block_size,
+                                        const void* src, int64_t src_seq_stride,
+                                        int64_t src_row_stride, int64_t src_len, int32_t* units,
+                                        int64_t max_units, int64_t batch, void* stream) {
+  const char* what = "skv_decode_append_gather";
+  int rc = validate_copy(what, row_bytes, block_size, batch, bt_stride, pool, dst);
+  if (rc) return rc;
+  if ((rc = validate_src(what, src, src_seq_stride, src_row_stride))) return rc;
+  if (batch == 0) return SKV_OK;
+  rc = skv_plan_units(free_stack, free_top, n_pages, block_table, bt_stride, seq_lens, n_new,
+                      n_new_uniform, status, dst_row_offsets, dst_seq_stride_rows, block_size, units,
+                      max_units, batch, stream);
+  if (rc) return rc;
+  return skv_copy_slices(dst, dst_capacity_rows, pool, row_bytes, block_size, n_pages, src,
+                         src_seq_stride, src_row_stride, src_len, units, max_units, stream);
 }

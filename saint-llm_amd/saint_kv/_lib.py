@@ -28,6 +28,7 @@ SKV_STATUS_MAX_PAGES = 1
 SKV_STATUS_NOSPC = 2
 SKV_STATUS_BADARG = 4
 SKV_STATUS_STACK = 8
+SKV_STATUS_UNITS = 16
 
 _P = ctypes.c_void_p
 _I64 = ctypes.c_int64
@@ -47,6 +48,12 @@ SIGNATURES: dict[str, list] = {
         _P, _P, _I64, _I64, _P, _I64, _I64, _I64, _P, _I64, _P, _P, _I32, _P, _I64, _I64, _I64,
         _I64, _P,
     ],
+    "skv_decode_append_gather": [
+        _P, _P, _I64, _P, _I64, _P, _P, _I32, _P, _P, _P, _I64, _I64, _P, _I64, _I64, _P, _I64,
+        _I64, _I64, _P, _I64, _I64, _P,
+    ],
+    "skv_plan_units": [_P, _P, _I64, _P, _I64, _P, _P, _I32, _P, _P, _I64, _I64, _P, _I64, _I64, _P],
+    "skv_copy_slices": [_P, _I64, _P, _I64, _I64, _I64, _P, _I64, _I64, _I64, _P, _I64, _P],
     "skv_ring_append": [_P, _I64, _I64, _P, _P, _I32, _P, _I64, _I64, _I64, _I64, _P],
     "skv_ring_read": [_P, _I64, _I64, _P, _I64, _I64, _P, _I64, _P],
     "skv_compress_append": [

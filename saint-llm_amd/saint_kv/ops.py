@@ -189,6 +189,79 @@ def append_gather(pool: torch.Tensor, block_table: torch.Tensor, seq_lens: torch
     return out
 
 
+def unit_table(max_units: int, device: torch.device) -> torch.Tensor:
+    """Workspace of skv_decode_append_gather for up to ``max_units`` page units."""
+    return torch.zeros(8 + 8 * max_units, dtype=torch.int32, device=device)
+
+
+def plan_units(free_stack: torch.Tensor, free_top: torch.Tensor, block_table: torch.Tensor,
+               seq_lens: torch.Tensor, n_new: int | torch.Tensor, block_size: int,
+               out: torch.Tensor, row_bytes: int, units: torch.Tensor, max_units: int,
+               row_offsets: torch.Tensor | None = None, status: torch.Tensor | None = None) -> None:
+    """First launch of decode_append_gather: reserve pages + page-unit table."""
+    _require_i32(free_stack, "free_stack")
+    _require_i32(free_top, "free_top", (1,))
+    _require_i32(block_table, "block_table")
+    batch, bt_stride = block_table.shape
+    _require_i32(seq_lens, "seq_lens", (batch,))
+    n_ptr, n_uni = _n_new_args(n_new, batch)
+    off_ptr, seq_rows, _ = _dst_args(out, row_bytes, batch, row_offsets)
+    _require_i32(units, "units")
+    if units.numel() < 8 + 8 * max_units:
+        raise ValueError(f"unit table of {units.numel()} words is smaller than 8 + 8*{max_units}")
+    _lib.call("skv_plan_units", free_stack.data_ptr(), free_top.data_ptr(), free_stack.numel(),
+              block_table.data_ptr(), bt_stride, seq_lens.data_ptr(), n_ptr, n_uni,
+              _lib.ptr(status), off_ptr, seq_rows, block_size, units.data_ptr(), max_units, batch,
+              _lib.stream_handle(block_table.device))
+
+
+def copy_slices(pool: torch.Tensor, src: torch.Tensor, out: torch.Tensor, units: torch.Tensor,
+                max_units: int) -> None:
+    """Second launch of decode_append_gather: the copy over 4 KB page-unit slices."""
+    n_pages, bs, rb = _check_pool(pool)
+    _require_gpu(src, "src")
+    s_seq, s_row = _row_view_strides(src, rb, "src")
+    _require_gpu(out, "out")
+    _require_i32(units, "units")
+    if units.numel() < 8 + 8 * max_units:
+        raise ValueError(f"unit table of {units.numel()} words is smaller than 8 + 8*{max_units}")
+    _lib.call("skv_copy_slices", out.data_ptr(), _capacity_rows(out, rb), pool.data_ptr(), rb, bs,
+              n_pages, src.data_ptr(), s_seq, s_row, src.shape[1], units.data_ptr(), max_units,
+              _lib.stream_handle(pool.device))
+
+
+def decode_append_gather(free_stack: torch.Tensor, free_top: torch.Tensor, block_table: torch.Tensor,
+                         seq_lens: torch.Tensor, pool: torch.Tensor, src: torch.Tensor,
+                         n_new: int | torch.Tensor, out: torch.Tensor, units: torch.Tensor,
+                         max_units: int, row_offsets: torch.Tensor | None = None,
+                         status: torch.Tensor | None = None) -> torch.Tensor:
+    """Reserve pages for ``n_new`` rows per sequence, append ``src`` and gather
+    every sequence into ``out`` (two launches; see skv_decode_append_gather)."""
+    n_pages, bs, rb = _check_pool(pool)
+    _require_i32(free_stack, "free_stack", (n_pages,))
+    _require_i32(free_top, "free_top", (1,))
+    _require_i32(block_table, "block_table")
+    batch, bt_stride = block_table.shape
+    _require_i32(seq_lens, "seq_lens", (batch,))
+    _require_gpu(src, "src")
+    if src.shape[0] != batch:
+        raise ValueError(f"src batch {src.shape[0]} != block_table batch {batch}")
+    s_seq, s_row = _row_view_strides(src, rb, "src")
+    n_ptr, n_uni = _n_new_args(n_new, batch)
+    off_ptr, seq_rows, cap = _dst_args(out, rb, batch, row_offsets)
+    _require_i32(units, "units")
+    if units.numel() < 8 + 8 * max_units:
+        raise ValueError(f"unit table of {units.numel()} words is smaller than 8 + 8*{max_units}")
+    if status is not None:
+        _require_i32(status, "status", (1,))
+    _lib.call("skv_decode_append_gather", free_stack.data_ptr(), free_top.data_ptr(), n_pages,
+              block_table.data_ptr(), bt_stride, seq_lens.data_ptr(), n_ptr, n_uni,
+              _lib.ptr(status), out.data_ptr(), off_ptr, seq_rows, cap, pool.data_ptr(), rb, bs,
+              src.data_ptr(), s_seq, s_row, src.shape[1], units.data_ptr(), max_units, batch,
+              _lib.stream_handle(pool.device))
+    return out
+
+
 # ---------------------------------------------------------------------------
 # SWA ring
 # ---------------------------------------------------------------------------

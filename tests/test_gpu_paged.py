@@ -217,3 +217,49 @@ def test_full_size_decode_gather_config(dev) -> None:
         o = int(offs[b]) + b
         assert torch.equal(out[o: o + lens0[b]], src[offs[b]: offs[b] + lens0[b]])
         assert torch.equal(out[o + lens0[b]], tok[b, 0])
+
+
+def test_decode_append_gather_matches_two_call_path(dev) -> None:
+    """skv_decode_append_gather (planner + 4 KB slices) == skv_reserve + skv_append_gather."""
+    from saint_kv import ops
+
+    rng = np.random.default_rng(7)
+    g = torch.Generator().manual_seed(7)
+    batch, bs, n_pages, d = 9, 64, 3000, 576
+    order = rng.permutation(n_pages).astype(np.int32)
+    a = _State(dev, batch, n_pages, 80, bs, (d,), torch.bfloat16, order)
+    b = _State(dev, batch, n_pages, 80, bs, (d,), torch.bfloat16, order)
+    lens0 = rng.integers(0, 4000, size=batch).astype(np.int32)
+    lens0[3] = 0
+    pre = torch.randn(batch, int(lens0.max()), d, generator=g).to(torch.bfloat16).to(dev)
+    for s in (a, b):
+        s.reserve(lens0)
+        s.ops.paged_append(s.pool, s.bt, s.lens, pre, torch.as_tensor(lens0, device=dev))
+    cap = lens0.astype(np.int64) + 2 * 20  # up to 2 new tokens per step
+    offs = torch.as_tensor(np.concatenate([[0], np.cumsum(cap)[:-1]]), device=dev)
+    out_a = torch.zeros(int(cap.sum()), d, dtype=torch.bfloat16, device=dev)
+    out_b = torch.zeros_like(out_a)
+    units = ops.unit_table(batch * 80, dev)
+    lens = lens0.astype(np.int64)
+    for step in range(20):
+        n = 1 if step % 3 else int(rng.integers(0, 3))
+        tok = torch.randn(batch, max(n, 1), d, generator=g).to(torch.bfloat16).to(dev)
+        max_units = int((-(-(lens + n) // bs)).sum())
+        ops.decode_append_gather(a.stack, a.top, a.bt, a.lens, a.pool, tok, n, out_a, units,
+                                 max_units, offs, a.status)
+        b.reserve(n)
+        ops.append_gather(b.pool, b.bt, b.lens, tok, n, out_b, offs)
+        lens += n
+        torch.cuda.synchronize()
+        assert int(a.status.item()) == 0
+        assert torch.equal(a.bt, b.bt) and torch.equal(a.lens, b.lens) and torch.equal(a.top, b.top)
+        assert torch.equal(out_a, out_b), step
+    assert torch.equal(a.pool, b.pool)
+    # a unit table that is too small is refused: nothing changes, nothing copied
+    before = (a.bt.clone(), a.lens.clone(), a.top.clone(), out_a.clone())
+    ops.decode_append_gather(a.stack, a.top, a.bt, a.lens, a.pool, tok, 1, out_a, units, 3, offs,
+                             a.status)
+    torch.cuda.synchronize()
+    assert int(a.status.item()) == 16  # SKV_STATUS_UNITS
+    assert torch.equal(a.bt, before[0]) and torch.equal(a.lens, before[1])
+    assert torch.equal(a.top, before[2]) and torch.equal(out_a, before[3])
