@@ -35,6 +35,17 @@ import numpy as np  # noqa: E402
 import torch  # noqa: E402
 
 HBM_PEAK_GBS = 8000.0  # MI355X HBM3E peak, 8 TB/s
+TRAFFIC_FILE = ROOT / "profiles" / "hbm_traffic_k_copy_slices_b64_L1k-32k.json"
+
+
+def measured_traffic(alg_bytes: float) -> int | None:
+    """HBM bytes per launch of k_copy_slices from the committed FETCH_SIZE/WRITE_SIZE
+    passes (counted traffic / algorithmic bytes, applied to this run's launch)."""
+    try:
+        ratio = json.loads(TRAFFIC_FILE.read_text())["traffic_over_alg"]
+    except (OSError, KeyError, ValueError):
+        return None
+    return int(round(ratio * alg_bytes))
 ROW = 576  # 512 latent + 64 rope, bf16
 ROW_BYTES = ROW * 2
 
@@ -460,7 +471,7 @@ def main() -> int:
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": measured_traffic(alg_per_launch),
             "alg_bytes_per_launch": int(alg_per_launch),
             "avg_launch_us": round(kern_avg_ms * 1e3, 2),
         },
