@@ -269,7 +269,7 @@ def run_decode_leg(dev, name: str, specs, batch: int, lens0: np.ndarray, steps: 
         "mean_ctx": int(lens0.mean()), "steps": n_steps, "us_per_step": round(ms * 1e3, 2),
         "alg_bytes_per_step": int(alg), "gbs": round(gbs, 1), "pct_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 2),
         "kv_tokens_per_step": int(toks), "kv_tokens_per_s": round(toks / (ms * 1e-3), 1),
-        "launches_per_step": 5, "hip_graph_steps": per_graph,
+        "launches_per_step": 4, "hip_graph_steps": per_graph,
     }
     log(f"{name}: {rec['us_per_step']} us/step, {rec['gbs']} GB/s ({rec['pct_hbm_peak']}%), "
         f"{rec['kv_tokens_per_s'] / 1e6:.1f} M KV tok/s")

@@ -1,5 +1,6 @@
 // Fused decode step over a stack of heterogeneous layers: four launches per
-// step whatever the number of layers (plan, append/compress, top-k, gather).
+// step whatever the number of layers (plan; append/compress + top-k
+// histograms; top-k filter + dense gathers; top-k rank + sparse gather).
 //
 // Reference: one cached decode call of SaintLLM.forward walks the blocks and
 // hands each attention its cache layer (model.py:294-315); the per-layer cache
@@ -15,7 +16,10 @@ namespace skv {
 constexpr int kDecodeMaxBatch = 1024;
 constexpr int kPlanThreads = 1024;
 constexpr int kGatherThreadsD = 256;
-constexpr int kGatherRowsD = 8;
+#ifndef SKV_GATHER_ROWS
+#define SKV_GATHER_ROWS 8
+#endif
+constexpr int kGatherRowsD = SKV_GATHER_ROWS;  // output rows per gather workgroup
 
 // ---------------------------------------------------------------------------
 // 1. plan: token counts +1 and page reservation of every group.
@@ -198,20 +202,23 @@ __device__ __forceinline__ void decode_fold_part(const skv_page_group& G, int b,
 __global__ __launch_bounds__(kAppendThreads) void k_decode_append(const skv_decode_desc* __restrict__ d,
                                                                   int n_chunks) {
   __shared__ TopkHistSmem hsm;
+  if (*d->status) return;  // refused step: no state changes
   const int n_append = d->batch * d->n_layers;
   if (static_cast<int>(blockIdx.x) >= n_append) {
-    // top-k histogram chunk (chunk, b, csa layer)
+    // top-k histogram chunk (chunk, b, csa layer); chunk 0 also zeroes the
+    // row's list counters, which the previous step's rank launch still read
     int u = blockIdx.x - n_append;
     const int chunk = u % n_chunks;
     u /= n_chunks;
     const int b = u % d->batch;
     const skv_decode_layer* Ly = csa_layer(d, u / d->batch);
     if (!Ly) return;
+    int32_t* ws = Ly->topk_ws + static_cast<int64_t>(b) * kTkWsWords;
+    if (chunk == 0 && threadIdx.x < 3) ws[kTkWsCnt + threadIdx.x] = 0;
     const int m = d->groups[Ly->group].m;
     const int L = d->tok_lens[b];
     topk_hist_chunk(hsm, Ly->scores + static_cast<int64_t>(b) * Ly->score_stride, L / m,
-                    L > 0 ? (L - 1) / m : 0, Ly->top_k, chunk,
-                    Ly->topk_ws + static_cast<int64_t>(b) * kTkWsWords);
+                    L > 0 ? (L - 1) / m : 0, Ly->top_k, chunk, ws);
     return;
   }
   const int b = blockIdx.x % d->batch;
@@ -242,40 +249,11 @@ __global__ __launch_bounds__(kAppendThreads) void k_decode_append(const skv_deco
 }
 
 // ---------------------------------------------------------------------------
-// 3. top-k filter (grid chunks, batch, CSA layers) and final (grid batch, CSA
-//    layers); see skv_topk.h.
+// Row copies shared by the gather tiles and the top-k rank step.  Row kinds:
+// 0 skip, 1 copy a bf16 row, 2 dequantize an fp8 entry to bf16, 3 zero row.
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(kTkPartThreads) void k_decode_topk_filter(const skv_decode_desc* __restrict__ d) {
-  __shared__ TopkFilterSmem sm;
-  const skv_decode_layer* Ly = csa_layer(d, blockIdx.z);
-  if (!Ly) return;  // uniform over the workgroup
-  const int b = blockIdx.y;
-  const int m = d->groups[Ly->group].m;
-  const int L = d->tok_lens[b];
-  topk_filter_chunk(sm, Ly->scores + static_cast<int64_t>(b) * Ly->score_stride, L / m,
-                    L > 0 ? (L - 1) / m : 0, Ly->top_k, blockIdx.x,
-                    Ly->topk_ws + static_cast<int64_t>(b) * kTkWsWords);
-}
-
-__global__ __launch_bounds__(kTopkThreads) void k_decode_topk_final(const skv_decode_desc* __restrict__ d) {
-  __shared__ TopkFinalSmem sm;
-  const skv_decode_layer* Ly = csa_layer(d, blockIdx.y);
-  if (!Ly) return;
-  const int b = blockIdx.x;
-  const int m = d->groups[Ly->group].m;
-  const int L = d->tok_lens[b];
-  topk_final_row(sm, Ly->scores + static_cast<int64_t>(b) * Ly->score_stride, L / m,
-                 L > 0 ? (L - 1) / m : 0, Ly->top_k, Ly->topk_ws + static_cast<int64_t>(b) * kTkWsWords,
-                 Ly->topk_idx + static_cast<int64_t>(b) * Ly->top_k);
-}
-
-// ---------------------------------------------------------------------------
-// 4. gather: grid (tiles, batch, layers); a tile is 8 output rows of the
-//    layer's row space [entries (top_k or out_rows) | window].
-// ---------------------------------------------------------------------------
-__device__ __forceinline__ void dequant_chunk(const uint8_t* entry, int fp8_main, int c, u32x4& o0, u32x4& o1) {
-  const u32x4 codes = *(reinterpret_cast<const u32x4*>(entry) + c);
-  const float scale = *reinterpret_cast<const float*>(entry + fp8_main + (c >> 3) * 4);
+// 16 fp8 e4m3fn codes times their block scale -> 16 bf16 (two 16-byte chunks).
+__device__ __forceinline__ void dequant_codes(const u32x4 codes, float scale, u32x4& o0, u32x4& o1) {
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
     float f[4];
@@ -293,51 +271,140 @@ __device__ __forceinline__ void dequant_chunk(const uint8_t* entry, int fp8_main
   }
 }
 
-__global__ __launch_bounds__(kGatherThreadsD) void k_decode_gather(const skv_decode_desc* __restrict__ d) {
-  __shared__ const uint8_t* src_row[kGatherRowsD];
-  __shared__ uint8_t* dst_row[kGatherRowsD];
-  __shared__ int row_kind[kGatherRowsD];  // 0 skip, 1 copy bf16 row, 2 dequant fp8 entry, 3 zero row
-  const int b = blockIdx.y;
-  const skv_decode_layer& Ly = d->layers[blockIdx.z];
+struct RowRef {
+  const uint8_t* src;
+  uint8_t* dst;
+  int kind;
+};
+
+// Copies rows [0, n) with all kThreads threads; row(r) gives row r's RowRef.
+// Each thread issues kUnroll loads before its stores.  The loads are
+// unconditional (a lane with nothing to load reads 16 bytes at `safe`, any
+// readable device address, and drops them): a load under a branch is waited
+// for before the branch joins, which would serialize the memory round trips.
+// `fp8` says whether any row may be of kind 2 (uniform over the workgroup).
+template <int kThreads, int kUnroll, class RowFn>
+__device__ __forceinline__ void copy_rows(int n, RowFn row, int latent, bool fp8, const void* safe) {
+  const u32x4* safe4 = static_cast<const u32x4*>(safe);
+  const int bf_chunks = latent >> 3;  // 16-byte chunks of an output row
+  const int total = n * bf_chunks;
+  for (int t0 = threadIdx.x; t0 < total; t0 += kThreads * kUnroll) {
+    u32x4 v[kUnroll];
+    RowRef rf[kUnroll];
+    int c[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const int t = t0 + u * kThreads;
+      const int tt = (t < total) ? t : 0;
+      const int rr = tt / bf_chunks;
+      c[u] = tt - rr * bf_chunks;
+      rf[u] = row(rr);
+      if (t >= total) rf[u].kind = 0;
+      const u32x4* p = (rf[u].kind == 1) ? reinterpret_cast<const u32x4*>(rf[u].src) + c[u] : safe4;
+      v[u] = ld_stream(p);
+    }
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      if (rf[u].kind == 1) st_stream(reinterpret_cast<u32x4*>(rf[u].dst) + c[u], v[u]);
+      if (rf[u].kind == 3) st_stream(reinterpret_cast<u32x4*>(rf[u].dst) + c[u], u32x4{0u, 0u, 0u, 0u});
+    }
+  }
+  if (!fp8) return;
+  const int fp8_main = latent - SKV_FP8_ROPE_DIMS;
+  const int code_chunks = fp8_main >> 4;  // 16 codes -> 2 output chunks
+  const int fp8_tasks = code_chunks + (SKV_FP8_ROPE_DIMS >> 3);
+  const int ftotal = n * fp8_tasks;
+  for (int t0 = threadIdx.x; t0 < ftotal; t0 += kThreads * kUnroll) {
+    u32x4 v[kUnroll];
+    float scale[kUnroll];
+    RowRef rf[kUnroll];
+    int c[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const int t = t0 + u * kThreads;
+      const int tt = (t < ftotal) ? t : 0;
+      const int rr = tt / fp8_tasks;
+      c[u] = tt - rr * fp8_tasks;
+      rf[u] = row(rr);
+      if (t >= ftotal) rf[u].kind = 0;
+      const bool is_code = c[u] < code_chunks;
+      const uint8_t* codes = is_code ? rf[u].src + c[u] * 16
+                                     : rf[u].src + fp8_main + (fp8_main >> 7) * 4 + (c[u] - code_chunks) * 16;
+      const uint8_t* sc = rf[u].src + fp8_main + (c[u] >> 3) * 4;
+      const bool live = rf[u].kind == 2;
+      v[u] = *(live ? reinterpret_cast<const u32x4*>(codes) : safe4);
+      scale[u] = *(live && is_code ? reinterpret_cast<const float*>(sc) : reinterpret_cast<const float*>(safe4));
+    }
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      if (rf[u].kind != 2) continue;
+      u32x4* o = reinterpret_cast<u32x4*>(rf[u].dst);
+      if (c[u] < code_chunks) {
+        u32x4 o0, o1;
+        dequant_codes(v[u], scale[u], o0, o1);
+        st_stream(o + 2 * c[u], o0);
+        st_stream(o + 2 * c[u] + 1, o1);
+      } else {
+        st_stream(o + (fp8_main >> 3) + (c[u] - code_chunks), v[u]);
+      }
+    }
+  }
+}
+
+// Source of compressed entry e of sequence b: the row kind (1 bf16, 2 fp8)
+// and its address, or 0 when e is past n_ent or its page is not mapped.
+__device__ __forceinline__ int entry_source(const skv_page_group& G, const skv_decode_layer& Ly, int b, int e,
+                                            int n_ent, const uint8_t** src) {
+  if (e < 0 || e >= n_ent) return 0;
+  const int64_t pi = e / G.block_size;
+  const int32_t page = (pi < G.bt_stride) ? G.block_table[b * G.bt_stride + pi] : -1;
+  if (page < 0 || page >= G.n_pages) return 0;
+  *src = static_cast<const uint8_t*>(Ly.pool) +
+         (static_cast<int64_t>(page) * G.block_size + e % G.block_size) * Ly.entry_bytes;
+  return (Ly.format == SKV_FMT_FP8) ? 2 : 1;
+}
+
+// ---------------------------------------------------------------------------
+// 3. filter launch, 256-thread workgroups:
+//    blocks [0, chunks*batch*csa)  : top-k filter chunks (skv_topk.h);
+//    then gather tiles             : kGatherRowsD rows of a layer's dense rows
+//                                    [HCA entries (out_rows) | window].
+// ---------------------------------------------------------------------------
+struct GatherTileSmem {
+  const uint8_t* src_row[kGatherRowsD];
+  uint8_t* dst_row[kGatherRowsD];
+  int row_kind[kGatherRowsD];
+};
+
+union FilterLaunchSmem {
+  TopkFilterSmem filter;
+  GatherTileSmem tile;
+};
+
+__device__ __forceinline__ int dense_rows(const skv_decode_desc* d, const skv_decode_layer& Ly) {
+  return d->window + (Ly.kind == SKV_LAYER_HCA ? static_cast<int>(Ly.out_rows) : 0);
+}
+
+__device__ __forceinline__ void gather_tile(GatherTileSmem& sm, const skv_decode_desc* d,
+                                            const skv_decode_layer& Ly, int b, int tile) {
   const int latent = d->latent;
   const int64_t out_row = static_cast<int64_t>(latent) * 2;
   const int L = d->tok_lens[b];
-  int n_entry_rows = 0;
-  if (Ly.kind == SKV_LAYER_CSA) n_entry_rows = Ly.top_k;
-  else if (Ly.kind == SKV_LAYER_HCA) n_entry_rows = static_cast<int>(Ly.out_rows);
-  const int n_rows = n_entry_rows + d->window;
-  const int r0 = blockIdx.x * kGatherRowsD;
-  if (r0 >= n_rows) return;
+  const int n_dense = (Ly.kind == SKV_LAYER_HCA) ? static_cast<int>(Ly.out_rows) : 0;
+  const int n_rows = n_dense + d->window;
+  const int r0 = tile * kGatherRowsD;
   if (threadIdx.x < kGatherRowsD) {
     const int r = r0 + threadIdx.x;
     int kind = 0;
     const uint8_t* s = nullptr;
     uint8_t* o = nullptr;
-    if (r < n_entry_rows) {
+    if (r < n_dense) {
+      // dense HCA rows past the entries stay untouched
       const skv_page_group& G = d->groups[Ly.group];
-      const int n_ent = G.n_entries[b];
-      int e;
-      if (Ly.kind == SKV_LAYER_CSA) {
-        e = Ly.topk_idx[static_cast<int64_t>(b) * Ly.top_k + r];
-        if (e < 0) e = 0;  // clamp(min=0): a -1 pick reads entry 0
-        o = static_cast<uint8_t*>(Ly.out_entries) + (static_cast<int64_t>(b) * Ly.top_k + r) * out_row;
-        kind = 3;
-      } else {
-        e = r;
-        o = static_cast<uint8_t*>(Ly.out_entries) + (static_cast<int64_t>(b) * Ly.out_rows + r) * out_row;
-        kind = 0;  // dense rows past the entries stay untouched
-      }
-      if (e < n_ent) {
-        const int64_t pi = e / G.block_size;
-        const int32_t page = (pi < G.bt_stride) ? G.block_table[b * G.bt_stride + pi] : -1;
-        if (page >= 0 && page < G.n_pages) {
-          s = static_cast<const uint8_t*>(Ly.pool) +
-              (static_cast<int64_t>(page) * G.block_size + e % G.block_size) * Ly.entry_bytes;
-          kind = (Ly.format == SKV_FMT_FP8) ? 2 : 1;
-        }
-      }
+      kind = entry_source(G, Ly, b, r, G.n_entries[b], &s);
+      o = static_cast<uint8_t*>(Ly.out_entries) + (static_cast<int64_t>(b) * Ly.out_rows + r) * out_row;
     } else if (r < n_rows) {
-      const int w = r - n_entry_rows;
+      const int w = r - n_dense;
       const int cnt = min(max(L, 0), d->window);
       if (w < cnt) {
         const int64_t slot = (static_cast<int64_t>(L) - cnt + w) % d->window;
@@ -346,45 +413,214 @@ __global__ __launch_bounds__(kGatherThreadsD) void k_decode_gather(const skv_dec
         kind = 1;
       }
     }
-    src_row[threadIdx.x] = s;
-    dst_row[threadIdx.x] = o;
-    row_kind[threadIdx.x] = kind;
+    sm.src_row[threadIdx.x] = s;
+    sm.dst_row[threadIdx.x] = o;
+    sm.row_kind[threadIdx.x] = kind;
   }
   __syncthreads();
-  const int bf_chunks = latent >> 3;                 // 16-byte chunks of an output row
-  const int fp8_main = latent - SKV_FP8_ROPE_DIMS;
-  const int code_chunks = fp8_main >> 4;             // 16 codes -> 2 output chunks
-  const int rope_chunks = SKV_FP8_ROPE_DIMS >> 3;
-  const int fp8_tasks = code_chunks + rope_chunks;
-  // bf16 copies and zero rows: one task per output chunk
-  for (int t = threadIdx.x; t < kGatherRowsD * bf_chunks; t += kGatherThreadsD) {
-    const int rr = t / bf_chunks;
-    const int c = t - rr * bf_chunks;
-    const int kind = row_kind[rr];
-    if (kind == 1) {
-      st_stream(reinterpret_cast<u32x4*>(dst_row[rr]) + c, *(reinterpret_cast<const u32x4*>(src_row[rr]) + c));
-    } else if (kind == 3) {
-      st_stream(reinterpret_cast<u32x4*>(dst_row[rr]) + c, u32x4{0u, 0u, 0u, 0u});
+  copy_rows<kGatherThreadsD, 4>(
+      kGatherRowsD, [&](int r) { return RowRef{sm.src_row[r], sm.dst_row[r], sm.row_kind[r]}; }, latent,
+      Ly.format == SKV_FMT_FP8 && Ly.kind == SKV_LAYER_HCA, d);
+}
+
+__global__ __launch_bounds__(kTkPartThreads) void k_decode_filter(const skv_decode_desc* __restrict__ d,
+                                                                  int n_chunks, int n_csa) {
+  static_assert(kTkPartThreads == kGatherThreadsD, "filter and gather tiles share the launch");
+  __shared__ FilterLaunchSmem sm;
+  if (*d->status) return;  // refused step
+  const int batch = d->batch;
+  int u = blockIdx.x;
+  const int n_filter = n_chunks * batch * n_csa;
+  if (u < n_filter) {
+    const int chunk = u % n_chunks;
+    u /= n_chunks;
+    const int b = u % batch;
+    const skv_decode_layer* Ly = csa_layer(d, u / batch);
+    if (!Ly) return;  // uniform over the workgroup
+    const int m = d->groups[Ly->group].m;
+    const int L = d->tok_lens[b];
+    topk_filter_chunk(sm.filter, Ly->scores + static_cast<int64_t>(b) * Ly->score_stride, L / m,
+                      L > 0 ? (L - 1) / m : 0, Ly->top_k, chunk,
+                      Ly->topk_ws + static_cast<int64_t>(b) * kTkWsWords);
+    return;
+  }
+  u -= n_filter;
+  for (int l = 0; l < d->n_layers; ++l) {
+    const skv_decode_layer& Ly = d->layers[l];
+    const int tiles = static_cast<int>(ceil_div(dense_rows(d, Ly), kGatherRowsD));
+    if (u < tiles * batch) {
+      gather_tile(sm.tile, d, Ly, u / tiles, u % tiles);
+      return;
+    }
+    u -= tiles * batch;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// 4. top-k rank + sparse gather: grid (parts, batch, CSA layers), part p of a
+//    row owns output positions [p*rank_out, (p+1)*rank_out), rank_out 16 or
+//    32 (the host picks 16 when the rows alone give few workgroups).
+//    Every part loads the row's candidate lists as 64-bit order keys
+//    (key << 32 | ~index: larger means earlier in the output), ranks the sure
+//    candidates p, p + parts, ... among the sure list and the tie candidates
+//    p, p + parts, ... among the tie list (kRankSub lanes per candidate, each
+//    counting a strided share of the list), and writes each winner's index
+//    and entry at its output position; positions in [sel, top_k) it owns get
+//    index -1 and entry 0 (the reference's clamp(min=0) before its gather).
+//    On a tie bin too large for the lists every part runs the full select.
+//    Part 0 zeroes the row's histogram for the next step; the counters are
+//    zeroed by the next step's histogram launch.
+// ---------------------------------------------------------------------------
+constexpr int kRankThreads = 256;
+constexpr int kRankOutMin = 16;  // output positions per part: 16 or 32, chosen per launch
+constexpr int kRankOut = 32;
+constexpr int kRankSub = 8;
+constexpr int kRankCands = kRankThreads / kRankSub;  // candidates ranked per round
+constexpr int kRankMaxRows = 512;  // rows one part can collect (checked below)
+
+struct RankSmem {
+  int cnt[3];  // n_sure, n_tie, tie-overflow flag
+  int n_rows;
+  int2 win[kRankMaxRows];         // (output position, pick)
+  uintptr_t src_kind[kRankMaxRows];  // entry address | row kind (entries are 4-byte aligned)
+  union {
+    uint64_t ck[kTkCand];
+    struct {
+      TopkSmemT<kRankThreads> full;
+      int32_t order[kMaxTopK];
+    } f;
+  } u;
+};
+
+// Rows a part collects, worst case over top_k and the part size: its sure
+// winners (at most ceil(top_k/parts) <= part size), its tie winners (at most
+// ceil(kTkTieCap/parts) and at most top_k in all) and its fills (< part size).
+constexpr int rank_rows_max() {
+  int worst = 0;
+  for (int out = kRankOutMin; out <= kRankOut; out *= 2) {
+    for (int k = 1; k <= kMaxTopK; ++k) {
+      const int parts = (k + out - 1) / out;
+      int win = out + (kTkTieCap + parts - 1) / parts;
+      if (win > k) win = k;
+      if (win + out > worst) worst = win + out;
     }
   }
-  // fp8 entries: one task per 16 codes (two output chunks) or per rope chunk
-  for (int t = threadIdx.x; t < kGatherRowsD * fp8_tasks; t += kGatherThreadsD) {
-    const int rr = t / fp8_tasks;
-    if (row_kind[rr] != 2) continue;
-    const int c = t - rr * fp8_tasks;
-    const uint8_t* s = src_row[rr];
-    u32x4* o = reinterpret_cast<u32x4*>(dst_row[rr]);
-    if (c < code_chunks) {
-      u32x4 o0, o1;
-      dequant_chunk(s, fp8_main, c, o0, o1);
-      st_stream(o + 2 * c, o0);
-      st_stream(o + 2 * c + 1, o1);
-    } else {
-      const int rc = c - code_chunks;
-      st_stream(o + (fp8_main >> 3) + rc,
-                *reinterpret_cast<const u32x4*>(s + fp8_main + (fp8_main >> 7) * 4 + rc * 16));
-    }
+  return worst;
+}
+static_assert(rank_rows_max() <= kRankMaxRows, "rank row lists too small");
+
+__global__ __launch_bounds__(kRankThreads) void k_decode_topk_rank(const skv_decode_desc* __restrict__ d,
+                                                                    int rank_out) {
+  __shared__ RankSmem sm;
+  if (*d->status) return;  // refused step
+  const skv_decode_layer* Lp = csa_layer(d, blockIdx.z);
+  if (!Lp) return;
+  const skv_decode_layer& Ly = *Lp;
+  const int k = Ly.top_k;
+  const int parts = static_cast<int>(ceil_div(k, rank_out));
+  const int part = blockIdx.x;
+  if (part >= parts) return;  // the grid is sized for the largest top_k
+  const int b = blockIdx.y;
+  const int tid = threadIdx.x;
+  const skv_page_group& G = d->groups[Ly.group];
+  const int L = d->tok_lens[b];
+  const int n_cols = L / G.m;
+  const int n_valid = L > 0 ? (L - 1) / G.m : 0;
+  const int sel = topk_sel(k, n_cols, n_valid);
+  int32_t* ws = Ly.topk_ws + static_cast<int64_t>(b) * kTkWsWords;
+  if (part == 0) {
+    for (int i = tid; i < kTkBins; i += kRankThreads) ws[kTkWsHist + i] = 0;
   }
+  if (tid < 3) sm.cnt[tid] = ws[kTkWsCnt + tid];
+  if (tid == 0) sm.n_rows = 0;
+  __syncthreads();
+  const int o0 = part * rank_out;
+  const int o1 = min(k, o0 + rank_out);
+  const int f0 = max(o0, sel);  // positions [f0, o1) are fills
+  int n_rows;
+  if (sel > 0 && sm.cnt[2]) {
+    // tie bin over the list capacity: full select of the row, then this part's positions
+    topk_row<kRankThreads>(sm.u.f.full, nullptr, Ly.scores + static_cast<int64_t>(b) * Ly.score_stride,
+                           n_cols, n_valid, k, sm.u.f.order);
+    __syncthreads();
+    if (tid < o1 - o0) sm.win[tid] = make_int2(o0 + tid, sm.u.f.order[o0 + tid]);
+    n_rows = o1 - o0;
+  } else {
+    if (sel > 0) {
+      const int S = min(sm.cnt[0], kMaxTopK);
+      const int C = S + min(sm.cnt[1], kTkTieCap);
+      const int2* sure_list = reinterpret_cast<const int2*>(ws + kTkWsSure);
+      const int2* tie_list = reinterpret_cast<const int2*>(ws + kTkWsTie);
+      constexpr int kLoad = 8;  // list loads in flight per thread
+      for (int c0 = tid; c0 < C; c0 += kRankThreads * kLoad) {
+        int2 v[kLoad];
+#pragma unroll
+        for (int u = 0; u < kLoad; ++u) {
+          const int c = min(c0 + u * kRankThreads, C - 1);  // unconditional: C >= sel > 0
+          v[u] = (c < S ? sure_list : tie_list - S)[c];
+        }
+#pragma unroll
+        for (int u = 0; u < kLoad; ++u) {
+          const int c = c0 + u * kRankThreads;
+          if (c < C) {
+            sm.u.ck[c] = (static_cast<uint64_t>(static_cast<uint32_t>(v[u].x)) << 32) |
+                         static_cast<uint32_t>(~v[u].y);
+          }
+        }
+      }
+      __syncthreads();
+      const int sub = tid % kRankSub;
+#pragma unroll 1
+      for (int cls = 0; cls < 2; ++cls) {
+        const int lo = cls ? S : 0;
+        const int hi = cls ? C : S;
+        const int n_mine = (part < hi - lo) ? static_cast<int>(ceil_div(hi - lo - part, parts)) : 0;
+        for (int j0 = 0; j0 < n_mine; j0 += kRankCands) {
+          const int j = j0 + tid / kRankSub;
+          const bool valid = j < n_mine;
+          const uint64_t mine = valid ? sm.u.ck[lo + part + j * parts] : ~0ull;
+          int rank = 0;
+#pragma unroll 8
+          for (int q = lo + sub; q < hi; q += kRankSub) rank += sm.u.ck[q] > mine;
+          rank += __shfl_xor(rank, 1);
+          rank += __shfl_xor(rank, 2);
+          rank += __shfl_xor(rank, 4);
+          const int pos = lo + rank;
+          if (valid && sub == 0 && pos < sel) {
+            const uint32_t key = static_cast<uint32_t>(mine >> 32);
+            const int idx = static_cast<int>(~static_cast<uint32_t>(mine));
+            sm.win[atomicAdd(&sm.n_rows, 1)] = make_int2(pos, key_finite(key) ? idx : -1);
+          }
+        }
+      }
+    }
+    __syncthreads();
+    n_rows = sm.n_rows;
+    if (tid < o1 - f0) sm.win[n_rows + tid] = make_int2(f0 + tid, -1);
+    n_rows += max(0, o1 - f0);
+  }
+  __syncthreads();
+  // indices out, entry sources, then one copy pass over every row
+  const int n_ent = G.n_entries[b];
+  const int64_t out_row = static_cast<int64_t>(d->latent) * 2;
+  int32_t* out_idx = Ly.topk_idx + static_cast<int64_t>(b) * k;
+  uint8_t* out_base = static_cast<uint8_t*>(Ly.out_entries) + static_cast<int64_t>(b) * k * out_row;
+  for (int w = tid; w < n_rows; w += kRankThreads) {
+    const int2 pw = sm.win[w];
+    out_idx[pw.x] = pw.y;
+    const uint8_t* s = nullptr;
+    int kind = entry_source(G, Ly, b, pw.y < 0 ? 0 : pw.y, n_ent, &s);
+    sm.src_kind[w] = reinterpret_cast<uintptr_t>(s) | static_cast<uintptr_t>(kind ? kind : 3);
+  }
+  __syncthreads();
+  copy_rows<kRankThreads, 16>(
+      n_rows,
+      [&](int r) {
+        const uintptr_t sk = sm.src_kind[r];
+        return RowRef{reinterpret_cast<const uint8_t*>(sk & ~static_cast<uintptr_t>(3)),
+                      out_base + sm.win[r].x * out_row, static_cast<int>(sk & 3)};
+      },
+      d->latent, Ly.format == SKV_FMT_FP8, d);
 }
 
 }  // namespace skv
@@ -421,12 +657,12 @@ extern "C" int skv_decode_step(const skv_decode_desc* h, const skv_decode_desc* 
       return set_error(SKV_EINVAL, "%s: page group %d is incomplete", what, g);
     }
   }
-  int n_csa = 0, max_rows = 0;
-  int64_t max_score_cols = 1;
+  int n_csa = 0, max_top_k = 0;
+  int64_t max_score_cols = 1, n_tiles = 0;
   for (int l = 0; l < h->n_layers; ++l) {
     const skv_decode_layer& Ly = h->layers[l];
     if (!Ly.ring || !Ly.kv_new || !Ly.out_window) return set_error(SKV_EINVAL, "%s: layer %d lacks ring/kv_new/out_window", what, l);
-    int rows = h->window;
+    int64_t dense = h->window;
     if (Ly.kind == SKV_LAYER_HCA || Ly.kind == SKV_LAYER_CSA) {
       if (Ly.group < 0 || Ly.group >= h->n_groups) return set_error(SKV_EINVAL, "%s: layer %d group out of range", what, l);
       if (!Ly.pool || !Ly.state || !Ly.bias || !Ly.c_new || !Ly.z_new || !Ly.out_entries) {
@@ -447,34 +683,42 @@ extern "C" int skv_decode_step(const skv_decode_desc* h, const skv_decode_desc* 
           return set_error(SKV_EINVAL, "%s: CSA layer %d indexer stream incomplete", what, l);
         }
         ++n_csa;
-        rows += Ly.top_k;
+        max_top_k = max(max_top_k, Ly.top_k);
       } else {
-        if (Ly.out_rows <= 0) return set_error(SKV_EINVAL, "%s: HCA layer %d needs out_rows > 0", what, l);
-        rows += static_cast<int>(Ly.out_rows);
+        if (Ly.out_rows <= 0 || Ly.out_rows > (1 << 24)) {
+          return set_error(SKV_EINVAL, "%s: HCA layer %d needs 0 < out_rows <= 2^24", what, l);
+        }
+        dense += Ly.out_rows;
       }
     } else if (Ly.kind != SKV_LAYER_SWA) {
       return set_error(SKV_EINVAL, "%s: layer %d has unknown kind %d", what, l, Ly.kind);
     }
-    max_rows = max(max_rows, rows);
+    n_tiles += ceil_div(dense, kGatherRowsD) * h->batch;
   }
   if (h->batch == 0 || h->n_layers == 0) return SKV_OK;
+  const int n_chunks = static_cast<int>(ceil_div(max_score_cols, kTkChunk));
+  const int64_t n_append = static_cast<int64_t>(h->batch) * h->n_layers +
+                           static_cast<int64_t>(n_chunks) * h->batch * n_csa;
+  const int64_t n_filter = static_cast<int64_t>(n_chunks) * h->batch * n_csa + n_tiles;
+  if (n_append > INT32_MAX || n_filter > INT32_MAX) {
+    return set_error(SKV_EINVAL, "%s: score_stride/out_rows give a grid over 2^31 workgroups", what);
+  }
   hipStream_t s = static_cast<hipStream_t>(stream);
   hipLaunchKernelGGL(k_decode_plan, dim3(1), dim3(kPlanThreads), 0, s, dd);
   int rc = check_launch(what);
   if (rc) return rc;
-  const int n_chunks = static_cast<int>(ceil_div(max_score_cols, kTkChunk));
-  const int64_t n_blocks = static_cast<int64_t>(h->batch) * h->n_layers +
-                           static_cast<int64_t>(n_chunks) * h->batch * n_csa;
-  hipLaunchKernelGGL(k_decode_append, dim3(static_cast<unsigned>(n_blocks)), dim3(kAppendThreads), 0, s,
+  hipLaunchKernelGGL(k_decode_append, dim3(static_cast<unsigned>(n_append)), dim3(kAppendThreads), 0, s,
                      dd, n_chunks);
   if ((rc = check_launch(what))) return rc;
+  hipLaunchKernelGGL(k_decode_filter, dim3(static_cast<unsigned>(n_filter)), dim3(kTkPartThreads), 0, s,
+                     dd, n_chunks, n_csa);
+  if ((rc = check_launch(what))) return rc;
   if (n_csa > 0) {
-    hipLaunchKernelGGL(k_decode_topk_filter, dim3(n_chunks, h->batch, n_csa), dim3(kTkPartThreads), 0, s, dd);
-    if ((rc = check_launch(what))) return rc;
-    hipLaunchKernelGGL(k_decode_topk_final, dim3(h->batch, n_csa), dim3(kTopkThreads), 0, s, dd);
-    if ((rc = check_launch(what))) return rc;
+    // smaller parts when the rows alone would leave most CUs idle
+    const int rank_out = (static_cast<int64_t>(h->batch) * n_csa * ceil_div(max_top_k, kRankOut) < 512)
+                             ? kRankOutMin : kRankOut;
+    const dim3 rgrid(static_cast<unsigned>(ceil_div(max_top_k, rank_out)), h->batch, n_csa);
+    hipLaunchKernelGGL(k_decode_topk_rank, rgrid, dim3(kRankThreads), 0, s, dd, rank_out);
   }
-  const dim3 ggrid(static_cast<unsigned>(ceil_div(max_rows, kGatherRowsD)), h->batch, h->n_layers);
-  hipLaunchKernelGGL(k_decode_gather, ggrid, dim3(kGatherThreadsD), 0, s, dd);
   return check_launch(what);
 }

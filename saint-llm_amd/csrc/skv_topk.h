@@ -34,32 +34,38 @@ __device__ __forceinline__ bool key_finite(uint32_t k) {
   return k != kKeyNaN && k != kKeyPosInf && k != kKeyNegInf;
 }
 
-struct TopkSmem {
-  int whist[kTopkWaves][256];
+template <int kThreads>
+struct TopkSmemT {
+  int whist[kThreads / kWave][256];
   int hist[256];
   uint32_t cand_key[kMaxTopK];
   int cand_idx[kMaxTopK];
   int scan_lds[17];
   int digit, above, cnt;
 };
+using TopkSmem = TopkSmemT<kTopkThreads>;
 
 // out[0, k): the sel = min(k, n_cols, n_valid) best of row[0, n_valid) in
 // (score desc, index asc) order, -1 for non-finite picks and ranks >= sel.
 // `keys` (kLdsKeys words of LDS) stages short rows; nullptr reads global
-// memory on every pass.  Every thread of the workgroup must call it.
-__device__ __forceinline__ void topk_row(TopkSmem& sm, uint32_t* keys, const float* row, int n_cols,
-                                         int n_valid, int k, int32_t* out) {
+// memory on every pass.  Every thread of the kThreads-thread workgroup
+// (kThreads >= 256) must call it.
+template <int kThreads = kTopkThreads>
+__device__ __forceinline__ void topk_row(TopkSmemT<kThreads>& sm, uint32_t* keys, const float* row,
+                                         int n_cols, int n_valid, int k, int32_t* out) {
+  static_assert(kThreads >= 256 && kThreads % kWave == 0, "topk_row needs >= 256 threads");
+  constexpr int kWaves = kThreads / kWave;
   const int tid = threadIdx.x;
   const int wid = tid / kWave;
   n_cols = max(n_cols, 0);
   n_valid = max(0, min(n_valid, n_cols));
   const int k_eff = min(k, n_cols);
   const int sel = min(k_eff, n_valid);
-  for (int j = sel + tid; j < k; j += kTopkThreads) out[j] = -1;
+  for (int j = sel + tid; j < k; j += kThreads) out[j] = -1;
   if (sel == 0) return;
   const bool in_lds = keys != nullptr && n_valid <= kLdsKeys;
   if (in_lds) {
-    for (int i = tid; i < n_valid; i += kTopkThreads) keys[i] = score_key(row[i]);
+    for (int i = tid; i < n_valid; i += kThreads) keys[i] = score_key(row[i]);
     __syncthreads();
   }
   auto key_at = [&](int i) -> uint32_t { return in_lds ? keys[i] : score_key(row[i]); };
@@ -70,9 +76,9 @@ __device__ __forceinline__ void topk_row(TopkSmem& sm, uint32_t* keys, const flo
   int eq_total = 0;
   for (int pass = 0; pass < 4; ++pass) {
     const int shift = 24 - 8 * pass;
-    for (int i = tid; i < kTopkWaves * 256; i += kTopkThreads) (&sm.whist[0][0])[i] = 0;
+    for (int i = tid; i < kWaves * 256; i += kThreads) (&sm.whist[0][0])[i] = 0;
     __syncthreads();
-    for (int i = tid; i < n_valid; i += kTopkThreads) {
+    for (int i = tid; i < n_valid; i += kThreads) {
       const uint32_t key = key_at(i);
       if ((key & pmask) == prefix) atomicAdd(&sm.whist[wid][(key >> shift) & 255u], 1);
     }
@@ -80,7 +86,7 @@ __device__ __forceinline__ void topk_row(TopkSmem& sm, uint32_t* keys, const flo
     if (tid < 256) {
       int s = 0;
 #pragma unroll
-      for (int w = 0; w < kTopkWaves; ++w) s += sm.whist[w][tid];
+      for (int w = 0; w < kWaves; ++w) s += sm.whist[w][tid];
       sm.hist[tid] = s;
     }
     __syncthreads();
@@ -110,7 +116,7 @@ __device__ __forceinline__ void topk_row(TopkSmem& sm, uint32_t* keys, const flo
   // ---- collect the sel winners ------------------------------------------------
   if (tid == 0) sm.cnt = 0;
   __syncthreads();
-  for (int i = tid; i < n_valid; i += kTopkThreads) {
+  for (int i = tid; i < n_valid; i += kThreads) {
     const uint32_t key = key_at(i);
     if (key > T || (key == T && eq_total == need_eq)) {
       const int slot = atomicAdd(&sm.cnt, 1);
@@ -122,7 +128,7 @@ __device__ __forceinline__ void topk_row(TopkSmem& sm, uint32_t* keys, const flo
   if (eq_total != need_eq) {
     // ties at the threshold: take the need_eq smallest indices, in index order
     int carry = 0;
-    for (int base = 0; base < n_valid; base += kTopkThreads) {
+    for (int base = 0; base < n_valid; base += kThreads) {
       const int i = base + tid;
       const int is_eq = (i < n_valid && key_at(i) == T) ? 1 : 0;
       int tot;
@@ -138,7 +144,7 @@ __device__ __forceinline__ void topk_row(TopkSmem& sm, uint32_t* keys, const flo
   }
 
   // ---- order the winners: key descending, index ascending ------------------
-  for (int c = tid; c < sel; c += kTopkThreads) {
+  for (int c = tid; c < sel; c += kThreads) {
     const uint32_t kc = sm.cand_key[c];
     const int ic = sm.cand_idx[c];
     int rank = 0;
@@ -157,11 +163,13 @@ __device__ __forceinline__ void topk_row(TopkSmem& sm, uint32_t* keys, const flo
 //            (top bits of the order key) to the row's global histogram.
 //   filter : every chunk finds the threshold bin t (the bin holding rank sel)
 //            from the histogram and appends its keys in bins > t ("sure") and
-//            == t ("ties") to the row's lists, one atomic per wave.
-//   final  : one workgroup per row orders the winners: a candidate's rank
-//            among the candidates of its own bin gives its output position;
-//            in bin t only the first `need` by (key desc, index asc) survive.
-//            It then zeroes the row's histogram and counters for the next call.
+//            == t ("ties") to the row's lists, one atomic per list per chunk.
+//   final  : orders the winners by (key desc, index asc).  Every sure key
+//            wins; in bin t only the first `need` = sel - n_sure survive.
+//            Standalone select: one workgroup per row (topk_final_row), which
+//            then zeroes the row's histogram and counters.  Decode step:
+//            several workgroups per row each rank a share of the candidates
+//            and gather their entries (k_decode_topk_rank).
 // A tie bin larger than kTkTieCap makes final fall back to the single-
 // workgroup select over the row.
 // ===========================================================================
@@ -172,7 +180,8 @@ constexpr int kTkShift = 21;
 constexpr int kTkTieCap = 4096;
 // per-row workspace layout, int32 words
 constexpr int kTkWsHist = 0;
-constexpr int kTkWsCnt = kTkBins;       // n_sure, n_tie, (2 spare)
+constexpr int kTkWsCnt = kTkBins;       // n_sure, n_tie, tie-overflow flag, (spare)
+constexpr int kTkWsFlag = kTkWsCnt + 2;
 constexpr int kTkWsSure = kTkWsCnt + 4; // (key, idx) pairs, kMaxTopK of them
 constexpr int kTkWsTie = kTkWsSure + 2 * kMaxTopK;
 constexpr int kTkWsWords = kTkWsTie + 2 * kTkTieCap;
@@ -195,10 +204,15 @@ __device__ __forceinline__ void topk_hist_chunk(TopkHistSmem& sm, const float* r
   const int i0 = chunk * kTkChunk;
   const int i1 = min(n_valid, i0 + kTkChunk);
   if (i0 >= i1) return;
+  constexpr int kPer = kTkChunk / kTkPartThreads;
+  float f[kPer];  // unconditional loads (clamped index), all in flight together
+#pragma unroll
+  for (int q = 0; q < kPer; ++q) f[q] = row[min(i0 + q * kTkPartThreads + tid, i1 - 1)];
   for (int b = tid; b < kTkBins; b += kTkPartThreads) sm.hist[b] = 0;
   __syncthreads();
-  for (int i = i0 + tid; i < i1; i += kTkPartThreads) {
-    atomicAdd(&sm.hist[score_key(row[i]) >> kTkShift], 1);
+#pragma unroll
+  for (int q = 0; q < kPer; ++q) {
+    if (i0 + q * kTkPartThreads + tid < i1) atomicAdd(&sm.hist[score_key(f[q]) >> kTkShift], 1);
   }
   __syncthreads();
   for (int b = tid; b < kTkBins; b += kTkPartThreads) {
@@ -239,60 +253,73 @@ __device__ __forceinline__ void topk_threshold(const int* hist, int sel, int* sc
   __syncthreads();
 }
 
+// Stages the kTkBins-word row histogram in LDS (16-byte aligned).  Each of
+// the first kTkBins/8 threads copies two 16-byte pieces, both loads issued
+// before either LDS store.
+__device__ __forceinline__ void load_hist(int* lds, const int32_t* g) {
+  constexpr int kHalf = kTkBins / 8;  // threads taking part; each moves 2 x int4
+  if (threadIdx.x < kHalf) {
+    const int4 a = reinterpret_cast<const int4*>(g)[threadIdx.x];
+    const int4 b = reinterpret_cast<const int4*>(g)[threadIdx.x + kHalf];
+    reinterpret_cast<int4*>(lds)[threadIdx.x] = a;
+    reinterpret_cast<int4*>(lds)[threadIdx.x + kHalf] = b;
+  }
+}
+
 struct TopkFilterSmem {
-  int hist[kTkBins];
+  alignas(16) int hist[kTkBins];
   int scan_lds[17];
   int sh[3];
   int wcnt[2][kTkPartThreads / kWave];  // per-wave candidate counts of this chunk
-  int base[2];                          // this chunk's slots in the row's lists
-  uint32_t key[2][kTkChunk];            // chunk-local compaction (sure, ties)
-  int idx[2][kTkChunk];
+  int base[2];                          // this chunk's first slots in the row's lists
 };
 
-// Chunk-local compaction first, then one global atomic per list per chunk.
+// The chunk's keys stay in registers: a first ballot pass counts each wave's
+// sure and tie candidates, one global atomic per list reserves the chunk's
+// slots, and a second ballot pass writes every candidate to its slot (waves in
+// order, lanes in order, so each list is index-sorted within a chunk).  The
+// scores are loaded before the histogram is read, so the two memory
+// latencies overlap.  A tie bin above kTkTieCap is flagged in ws[kTkWsFlag]
+// by chunk 0 and no list is written.
 __device__ __forceinline__ void topk_filter_chunk(TopkFilterSmem& sm, const float* row, int n_cols,
                                                   int n_valid, int k, int chunk, int32_t* ws) {
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
   const int wid = tid / kWave;
   constexpr int kWaves = kTkPartThreads / kWave;
+  constexpr int kRun = kTkChunk / kWaves;  // each wave owns a contiguous run of scores
+  constexpr int kPer = kRun / kWave;
   const int sel = topk_sel(k, n_cols, n_valid);
   if (sel == 0) return;  // uniform
   n_valid = max(0, min(n_valid, n_cols));
   const int i0 = chunk * kTkChunk;
   const int i1 = min(n_valid, i0 + kTkChunk);
   if (i0 >= i1) return;
-  for (int b = tid; b < kTkBins; b += kTkPartThreads) sm.hist[b] = ws[kTkWsHist + b];
+  const int r0 = i0 + wid * kRun;
+  // unconditional loads (index clamped into the chunk) so that all of them
+  // are in flight together; lanes past the chunk drop the value
+  float f[kPer];
+#pragma unroll
+  for (int q = 0; q < kPer; ++q) f[q] = row[min(r0 + q * kWave + lane, i1 - 1)];
+  uint32_t keys[kPer];
+#pragma unroll
+  for (int q = 0; q < kPer; ++q) keys[q] = (r0 + q * kWave + lane < i1) ? score_key(f[q]) : 0u;
+  load_hist(sm.hist, ws + kTkWsHist);
   __syncthreads();
   int t, above, ties;
   topk_threshold<kTkPartThreads>(sm.hist, sel, sm.scan_lds, sm.sh, t, above, ties);
-  if (ties > kTkTieCap) return;  // final falls back to the single-workgroup select
-  // each wave owns a contiguous run of kTkChunk / kWaves scores
-  constexpr int kRun = kTkChunk / kWaves;
+  if (ties > kTkTieCap) {  // the final step falls back to a full single-workgroup select
+    if (chunk == 0 && tid == 0) ws[kTkWsFlag] = 1;
+    return;
+  }
   const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-  int ns = 0, nt = 0;  // wave-uniform running counts
-  const int r0 = i0 + wid * kRun;
-  for (int off = 0; off < kRun; off += kWave) {
-    const int i = r0 + off + lane;
-    const bool valid = i < i1;
-    const uint32_t key = valid ? score_key(row[i]) : 0u;
-    const int b = static_cast<int>(key >> kTkShift);
-    const bool sure = valid && b > t;
-    const bool tie = valid && b == t;
-    const uint64_t ms = __ballot(sure);
-    const uint64_t mt = __ballot(tie);
-    if (sure) {
-      const int s = wid * kRun + ns + __popcll(ms & below);
-      sm.key[0][s] = key;
-      sm.idx[0][s] = i;
-    }
-    if (tie) {
-      const int s = wid * kRun + nt + __popcll(mt & below);
-      sm.key[1][s] = key;
-      sm.idx[1][s] = i;
-    }
-    ns += __popcll(ms);
-    nt += __popcll(mt);
+  int ns = 0, nt = 0;  // wave-uniform counts
+#pragma unroll
+  for (int q = 0; q < kPer; ++q) {
+    const bool valid = r0 + q * kWave + lane < i1;
+    const int b = static_cast<int>(keys[q] >> kTkShift);
+    ns += __popcll(__ballot(valid && b > t));
+    nt += __popcll(__ballot(valid && b == t));
   }
   if (lane == 0) {
     sm.wcnt[0][wid] = ns;
@@ -306,17 +333,26 @@ __device__ __forceinline__ void topk_filter_chunk(TopkFilterSmem& sm, const floa
     sm.base[tid] = tot ? atomicAdd(&ws[kTkWsCnt + tid], tot) : 0;
   }
   __syncthreads();
-  // copy each wave's run to the row lists, waves in order
+  int ps = sm.base[0], pt = sm.base[1];
+  for (int w = 0; w < wid; ++w) {
+    ps += sm.wcnt[0][w];
+    pt += sm.wcnt[1][w];
+  }
+  int2* sure_list = reinterpret_cast<int2*>(ws + kTkWsSure);
+  int2* tie_list = reinterpret_cast<int2*>(ws + kTkWsTie);
 #pragma unroll
-  for (int l = 0; l < 2; ++l) {
-    int pre = sm.base[l];
-    for (int w = 0; w < wid; ++w) pre += sm.wcnt[l][w];
-    const int cnt = sm.wcnt[l][wid];
-    int32_t* dst = ws + (l == 0 ? kTkWsSure : kTkWsTie);
-    for (int q = lane; q < cnt; q += kWave) {
-      dst[2 * (pre + q)] = static_cast<int32_t>(sm.key[l][wid * kRun + q]);
-      dst[2 * (pre + q) + 1] = sm.idx[l][wid * kRun + q];
-    }
+  for (int q = 0; q < kPer; ++q) {
+    const int i = r0 + q * kWave + lane;
+    const bool valid = i < i1;
+    const int b = static_cast<int>(keys[q] >> kTkShift);
+    const bool sure = valid && b > t;
+    const bool tie = valid && b == t;
+    const uint64_t ms = __ballot(sure);
+    const uint64_t mt = __ballot(tie);
+    if (sure) sure_list[ps + __popcll(ms & below)] = make_int2(static_cast<int32_t>(keys[q]), i);
+    if (tie) tie_list[pt + __popcll(mt & below)] = make_int2(static_cast<int32_t>(keys[q]), i);
+    ps += __popcll(ms);
+    pt += __popcll(mt);
   }
 }
 
@@ -329,7 +365,7 @@ struct TopkFinalSmem {
   union {
     TopkSmem full;  // single-workgroup fallback (global-memory passes)
     struct {
-      int hist[kTkBins];
+      alignas(16) int hist[kTkBins];
       int cursor[kTkBuckets];  // counts, then running cursors (bucket ends after the scatter)
       int start[kTkBuckets];   // first slot of each bucket (descending key order)
       uint32_t key[kTkCand];   // candidates as read from the lists
@@ -360,7 +396,7 @@ __device__ __forceinline__ void topk_final_row(TopkFinalSmem& sm, const float* r
     return;
   }
   auto& F = sm.u.fin;
-  for (int b = tid; b < kTkBins; b += kTopkThreads) F.hist[b] = ws[kTkWsHist + b];
+  load_hist(F.hist, ws + kTkWsHist);
   for (int b = tid; b < kTkBuckets; b += kTopkThreads) F.cursor[b] = 0;
   __syncthreads();
   int t, above, ties;
@@ -376,12 +412,24 @@ __device__ __forceinline__ void topk_final_row(TopkFinalSmem& sm, const float* r
     return static_cast<int>(min((key >> 17) - base, static_cast<uint32_t>(kTkBuckets - 1)));
   };
   const int total = above + ties;
-  for (int c = tid; c < total; c += kTopkThreads) {
-    const int32_t* src = (c < above) ? &ws[kTkWsSure + 2 * c] : &ws[kTkWsTie + 2 * (c - above)];
-    const uint32_t key = static_cast<uint32_t>(src[0]);
-    F.key[c] = key;
-    F.idx[c] = src[1];
-    atomicAdd(&F.cursor[bucket_of(key)], 1);
+  constexpr int kLoad = (kTkCand + kTopkThreads - 1) / kTopkThreads;  // every list load in flight at once
+  {
+    int2 v[kLoad];
+#pragma unroll
+    for (int u = 0; u < kLoad; ++u) {
+      const int c = min(tid + u * kTopkThreads, total - 1);  // total >= sel > 0
+      v[u] = reinterpret_cast<const int2*>(ws + (c < above ? kTkWsSure : kTkWsTie))[c < above ? c : c - above];
+    }
+#pragma unroll
+    for (int u = 0; u < kLoad; ++u) {
+      const int c = tid + u * kTopkThreads;
+      if (c < total) {
+        const uint32_t key = static_cast<uint32_t>(v[u].x);
+        F.key[c] = key;
+        F.idx[c] = v[u].y;
+        atomicAdd(&F.cursor[bucket_of(key)], 1);
+      }
+    }
   }
   __syncthreads();
   {

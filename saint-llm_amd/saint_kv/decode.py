@@ -11,7 +11,7 @@
 * per CSA layer the indexer stream (bf16 entries, same pages).
 
 ``step()`` runs one decode step for every sequence through the fused C-ABI
-entry point ``skv_decode_step`` (five launches).  The per-step inputs live in
+entry point ``skv_decode_step`` (four launches).  The per-step inputs live in
 fixed device buffers (``inputs``), so a sequence of steps can be captured in a
 HIP graph and replayed.
 
@@ -249,9 +249,14 @@ class DecodeCache:
         return CapturedSteps(self, steps)
 
     def check_status(self) -> None:
-        """Synchronise and raise if a page reservation was refused."""
+        """Synchronise and raise if a page reservation was refused.
+
+        A refused step changes nothing on the device (every later step of a
+        captured sequence is refused the same way), so the host-side lengths
+        are re-read from ``tok_lens`` before raising."""
         st = int(self.status.item())
         if st:
+            self.host_lens = self.tok_lens.cpu().numpy().astype(np.int64)
             raise RuntimeError(f"DecodeCache page reservation refused (status bits {st})")
 
     # --------------------------------------------------------------- prefill --

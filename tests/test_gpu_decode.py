@@ -238,3 +238,121 @@ def test_decode_release_and_compact(dev) -> None:
         assert torch.equal(out, before[b])
     cache.step()  # decode continues after compaction
     cache.check_status()
+
+
+def _check_csa_outputs(cache, i, scores, ctx):
+    """topk_idx and out_entries of CSA layer i against the oracle select and
+    gather over the cache's own pool and block table."""
+    s = cache.layers[i]
+    g = cache.groups[cache.group_of_rate[s.m]]
+    lens = _np(cache.tok_lens).astype(np.int64)
+    bt, ent = _np(g.block_table), _np(g.n_entries)
+    idx = _np(cache.topk_idx[i])
+    exp_idx = np.full_like(idx, -1)
+    for b in range(cache.batch):
+        n_cols = int(lens[b]) // s.m
+        nv = np.array([ref.n_valid_blocks(int(lens[b]) - 1, s.m)])
+        e = ref.topk_select(scores[b:b + 1].numpy(), nv, s.top_k, n_cols)[0]
+        exp_idx[b, :len(e)] = e
+    assert np.array_equal(idx, exp_idx), ctx
+    pool = cache.pool[i].cpu()
+    src = ref.fp8_unpack_entries(pool.reshape(-1, pool.shape[-1])).reshape(*pool.shape[:2], -1) \
+        if s.fp8 else pool
+    exp_out = torch.zeros(cache.batch, s.top_k, cache.latent, dtype=torch.bfloat16)
+    ref.topk_gather(src, bt, np.arange(cache.batch), exp_idx, exp_out)
+    exp_out[ent == 0] = 0
+    assert torch.equal(cache.out_entries[i].cpu(), exp_out), ctx
+
+
+def test_decode_topk_rank_cases(dev) -> None:
+    """Sparse selection of the decode step over score patterns that exercise
+    every path of the rank step: sure and tie candidates, exact duplicates,
+    sel < top_k fills across several parts, an empty row, non-finite scores,
+    and tie bins over the list capacity (the full-select fallback)."""
+    from saint_kv.decode import DecodeCache, LayerSpec
+
+    specs = [LayerSpec("csa", m=4, top_k=300), LayerSpec("csa", m=4, top_k=50, fp8=True)]
+    B, max_len = 4, 20480
+    cache = DecodeCache(specs, B, max_len, block_size=64, window=16, device=dev, page_order_seed=5)
+    gen = torch.Generator(device=dev).manual_seed(5)
+    cache.prefill(np.array([2, 900, 17000, 20000]), generator=gen)
+    g = torch.Generator().manual_seed(5)
+    patterns = ["normal", "const", "dup", "sparse", "nonfinite", "const_neg", "normal"]
+    for step, pat in enumerate(patterns):
+        for i in range(len(specs)):
+            for v in cache.inputs[i].values():
+                v.normal_(generator=gen)
+        scores = []
+        for s in specs:
+            shape = (B, max_len // s.m)
+            if pat == "normal":
+                sc = torch.randn(*shape, generator=g)
+            elif pat == "const":
+                sc = torch.full(shape, 0.5)  # one tie bin holding every score
+            elif pat == "const_neg":
+                sc = torch.full(shape, -3.0)
+                sc[:, ::97] = 1.0
+            elif pat == "dup":
+                sc = torch.randint(0, 8, shape, generator=g).float()
+            elif pat == "sparse":
+                sc = torch.relu(torch.randn(*shape, generator=g) - 1.3)
+            else:
+                sc = torch.randn(*shape, generator=g)
+                sc[:, 5:40:3] = float("nan")
+                sc[:, 7:60:5] = float("inf")
+                sc[:, 9:90:4] = float("-inf")
+                sc[2, :] = float("-inf")
+            scores.append(sc)
+            cache.scores[len(scores) - 1].copy_(sc)
+        cache.step()
+        torch.cuda.synchronize()
+        cache.check_status()
+        for i in range(len(specs)):
+            _check_csa_outputs(cache, i, scores[i], (step, pat, i))
+
+
+def test_decode_refused_step_changes_nothing(dev) -> None:
+    """A step whose page reservation is refused (pool exhausted) sets the
+    status bit and leaves every buffer of the cache as it was."""
+    from saint_kv.decode import DecodeCache, LayerSpec
+
+    specs = [LayerSpec("csa", m=4, top_k=8), LayerSpec("hca", m=128), LayerSpec("swa")]
+    B, bs = 2, 16
+    cache = DecodeCache(specs, B, 1024, block_size=bs, window=8, device=dev, page_order_seed=1,
+                        pages_per_group={4: 2})
+    gen = torch.Generator(device=dev).manual_seed(1)
+    cache.prefill(np.array([64, 10]), generator=gen)  # 16 + 2 CSA entries: both pages taken
+
+    def fill():
+        for i in range(len(specs)):
+            for v in cache.inputs[i].values():
+                v.normal_(generator=gen)
+            if cache.scores[i] is not None:
+                cache.scores[i].normal_(generator=gen)
+
+    for _ in range(3):  # lens 65..67: still 16 entries in one page
+        fill()
+        cache.step()
+    cache.check_status()
+
+    def snapshot():
+        bufs = [cache.tok_lens]
+        for grp in cache.groups:
+            bufs += [grp.block_table, grp.n_entries, grp.free_top, grp.free_stack]
+        for lst in (cache.ring, cache.pool, cache.state, cache.idx_pool, cache.idx_state,
+                    cache.topk_idx, cache.out_entries, cache.out_window, cache.topk_ws):
+            bufs += [t for t in lst if t is not None]
+        return [t.clone() for t in bufs]
+
+    fill()
+    torch.cuda.synchronize()
+    before = snapshot()
+    cache.step()  # length 68 of sequence 0 needs a 17th entry, i.e. a second page
+    torch.cuda.synchronize()
+    assert int(cache.status.item()) == 2  # SKV_STATUS_NOSPC
+    after = snapshot()
+    for j, (x, y) in enumerate(zip(before, after)):
+        assert torch.equal(x, y), j
+    with pytest.raises(RuntimeError, match="refused"):
+        cache.check_status()
+    assert cache.host_lens.tolist() == [67, 13]
