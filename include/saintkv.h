@@ -272,22 +272,25 @@ int skv_compact(const skv_pool_ref* pools, int32_t n_pools, int32_t* block_table
 
 /* ---- fused decode step ----------------------------------------------------
  * One decode step (one new token per sequence) of a stack of heterogeneous
- * layers in four launches, whatever the layer count:
- *   1 plan    : every sequence's token count +1; for each page group, reserve
- *               the page of any compressed entry this token completes
- *               (skv_reserve policy, groups in order; all-or-nothing: on a
- *               refusal nothing changes and *status gets SKV_STATUS_* bits).
- *   2 append  : per layer, the token's latent row into its SWA ring; HCA/CSA
- *               layers fold (c, z) into the running pooling state and emit the
- *               entry when the block completes (bf16 or fp8); CSA layers do
- *               the same for the indexer stream (bf16 entries).
- *   3 top-k   : per CSA layer, skv_topk_select_decode over its score row
- *               (multi-workgroup form, two launches).
- *   4 gather  : CSA layers gather their top_k picks (fp8 dequantized to bf16;
- *               -1 reads entry 0, picks without an entry give zero rows); HCA
- *               layers copy all their entries (dense read, rows past the
- *               sequence's entries are left untouched); every layer copies the
- *               last min(window, L) tokens of its ring in position order.
+ * layers in three launches, whatever the layer count:
+ *   append : every workgroup computes the step's page plan (for each page
+ *            group, the page of any compressed entry this token completes,
+ *            popped in skv_reserve order: groups in order, ascending
+ *            sequence; all-or-nothing: on a refusal nothing changes and
+ *            *status gets SKV_STATUS_* bits); per layer, the token's latent
+ *            row goes into its SWA ring; HCA/CSA layers fold (c, z) into the
+ *            running pooling state and emit the entry when the block
+ *            completes (bf16 or fp8); CSA layers do the same for the indexer
+ *            stream (bf16 entries) and histogram their score rows.  New
+ *            lengths and free-stack tops go to step_lens / step_top.
+ *   filter : per CSA layer the top-k candidate lists (skv_topk_select_decode
+ *            semantics); HCA layers copy all their entries (dense read, rows
+ *            past the sequence's entries are left untouched); every layer
+ *            copies the last min(window, L) tokens of its ring in position
+ *            order; the step's lengths and tops are committed.
+ *   rank   : per CSA layer the ordered top_k picks and their gather (fp8
+ *            dequantized to bf16; -1 reads entry 0, picks without an entry
+ *            give zero rows).
  * Mirrors one cached step of CSA/HCA/SWAttention.forward over a
  * KVCacheBundle (model.py:294-315; csa.py:299-331; hca.py:110-141;
  * swa.py:107-125).  The kernels read the descriptor from device memory:
@@ -346,6 +349,8 @@ typedef struct skv_decode_desc {
   int32_t window;         /* SWA ring rows */
   int32_t* tok_lens;      /* [batch] tokens per sequence */
   int32_t* status;        /* [1] */
+  int32_t* step_lens;     /* [batch] scratch: lengths after the step in flight */
+  int32_t* step_top;      /* [SKV_MAX_GROUPS] scratch: free-stack tops after the step */
   skv_page_group groups[SKV_MAX_GROUPS];
   skv_decode_layer layers[SKV_MAX_LAYERS];
 } skv_decode_desc;

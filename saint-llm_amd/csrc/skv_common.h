@@ -105,6 +105,49 @@ __host__ __device__ __forceinline__ float e4m3fn_to_f32(uint8_t c) {
   return f;
 }
 
+// gfx950's conversion instructions use the OCP e4m3fn format.  They give
+// bit-identical results to e4m3fn_to_f32 for all 256 codes and to
+// f32_to_e4m3fn for every fp32 value of magnitude <= 448 (checked
+// exhaustively on MI355X), i.e. over the quantizer's clamped domain.
+
+// Two fp32 -> two bf16 in one word (a in the low half) with the native
+// conversion: round to nearest even, NaN quieted with its payload truncated,
+// bit-identical to f32_to_bf16 for every fp32 (checked exhaustively on
+// MI355X).
+__device__ __forceinline__ uint32_t bf16_pack2(float a, float b) {
+  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+  typedef float f32x2_t __attribute__((ext_vector_type(2)));
+  const f32x2_t v = {a, b};
+  const bf16x2_t r = __builtin_convertvector(v, bf16x2_t);
+  uint32_t u;
+  __builtin_memcpy(&u, &r, 4);
+  return u;
+}
+
+// x rounded to bf16 and back, for two values at once.
+__device__ __forceinline__ void bf16_round2(float& a, float& b) {
+  const uint32_t u = bf16_pack2(a, b);
+  a = __uint_as_float(u << 16);
+  b = __uint_as_float(u & 0xffff0000u);
+}
+
+// The four codes of w (byte 0 first) -> fp32.
+__device__ __forceinline__ void e4m3fn_x4_to_f32(uint32_t w, float* f) {
+  const auto lo = __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(w), false);
+  const auto hi = __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(w), true);
+  f[0] = lo[0];
+  f[1] = lo[1];
+  f[2] = hi[0];
+  f[3] = hi[1];
+}
+
+// a, b (|x| <= 448, not NaN) -> their codes in half kHi of `old` (a in the
+// lower byte); the other half of `old` is kept.
+template <bool kHi>
+__device__ __forceinline__ uint32_t e4m3fn_pack2(float a, float b, uint32_t old) {
+  return static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_fp8_f32(a, b, static_cast<int>(old), kHi));
+}
+
 constexpr float kE4M3Max = 448.0f;
 constexpr float kF32Tiny = 1.17549435082228750797e-38f;  // FLT_MIN
 
@@ -150,6 +193,22 @@ __device__ __forceinline__ int block_reduce_sum(int v, int* lds16) {
 }
 
 __host__ __device__ __forceinline__ int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+// a / b for 0 <= a < 2^24 and 1 <= b < 2^24: an fp32 reciprocal estimate is
+// within one of the quotient, and one integer correction makes it exact
+// (about 8 instructions instead of a full 32-bit division sequence).
+__device__ __forceinline__ uint32_t udiv24(uint32_t a, uint32_t b) {
+  uint32_t q = static_cast<uint32_t>(static_cast<float>(a) * __builtin_amdgcn_rcpf(static_cast<float>(b)));
+  const int r = static_cast<int>(a - q * b);
+  if (r < 0) --q;
+  else if (r >= static_cast<int>(b)) ++q;
+  return q;
+}
+
+__device__ __forceinline__ uint32_t umod24(uint32_t a, uint32_t b) { return a - udiv24(a, b) * b; }
+
+// ceil(a / b) for a + b - 1 < 2^24.
+__device__ __forceinline__ uint32_t ceil_div24(uint32_t a, uint32_t b) { return udiv24(a + b - 1, b); }
 
 // Grid size for persistent grid-stride kernels: enough workgroups to cover
 // all 256 CUs several times over.

@@ -1,6 +1,13 @@
-// Fused decode step over a stack of heterogeneous layers: four launches per
-// step whatever the number of layers (plan; append/compress + top-k
-// histograms; top-k filter + dense gathers; top-k rank + sparse gather).
+// Fused decode step over a stack of heterogeneous layers in three launches,
+// whatever the number of layers:
+//   append : step page plan (computed by every workgroup) + SWA ring rows +
+//            pooling fold / entry emission + top-k histogram chunks
+//   filter : top-k candidate lists + dense HCA / window copies + commit of
+//            the step's lengths
+//   rank   : per (CSA layer, sequence, part) ordering of the candidates and
+//            the sparse gather of the winners' entries
+// Every kernel boundary orders a producer before its consumers; no workgroup
+// waits for or fences against another.
 //
 // Reference: one cached decode call of SaintLLM.forward walks the blocks and
 // hands each attention its cache layer (model.py:294-315); the per-layer cache
@@ -14,91 +21,13 @@
 namespace skv {
 
 constexpr int kDecodeMaxBatch = 1024;
-constexpr int kPlanThreads = 1024;
-constexpr int kGatherThreadsD = 256;
-#ifndef SKV_GATHER_ROWS
-#define SKV_GATHER_ROWS 8
-#endif
-constexpr int kGatherRowsD = SKV_GATHER_ROWS;  // output rows per gather workgroup
-
-// ---------------------------------------------------------------------------
-// 1. plan: token counts +1 and page reservation of every group.
-// ---------------------------------------------------------------------------
-__global__ __launch_bounds__(kPlanThreads) void k_decode_plan(const skv_decode_desc* __restrict__ d) {
-  __shared__ int off[SKV_MAX_GROUPS][kDecodeMaxBatch + 1];
-  __shared__ int first[SKV_MAX_GROUPS][kDecodeMaxBatch];
-  __shared__ int total[SKV_MAX_GROUPS];
-  __shared__ int scan_lds[17];
-  __shared__ int bad_all;
-  const int tid = threadIdx.x;
-  const int batch = d->batch;
-  if (tid == 0) bad_all = 0;
-  __syncthreads();
-  int bad = 0;
-  for (int g = 0; g < d->n_groups; ++g) {
-    const skv_page_group& G = d->groups[g];
-    int need = 0;
-    if (tid < batch) {
-      const int L1 = d->tok_lens[tid] + 1;
-      const int cur = G.n_entries[tid];
-      const int target = L1 / G.m;
-      if (target < cur) {
-        bad |= SKV_STATUS_BADARG;
-      } else {
-        const int64_t p0 = ceil_div(cur, G.block_size);
-        const int64_t p1 = ceil_div(target, G.block_size);
-        if (p1 > G.bt_stride) bad |= SKV_STATUS_MAX_PAGES;
-        need = static_cast<int>(p1 - p0);
-        first[g][tid] = static_cast<int>(p0);
-      }
-    }
-    int tot;
-    const int ex = block_exclusive_scan(need, scan_lds, &tot);
-    if (tid < batch) off[g][tid] = ex;
-    if (tid == 0) {
-      off[g][batch] = tot;
-      total[g] = tot;
-    }
-    const int top = *G.free_top;
-    if (top < 0 || top > G.n_pages) bad |= SKV_STATUS_BADARG;
-    else if (tot > top) bad |= SKV_STATUS_NOSPC;
-  }
-  if (bad) atomicOr(&bad_all, bad);
-  __syncthreads();
-  if (bad_all) {
-    if (tid == 0) *d->status = bad_all;
-    return;
-  }
-  for (int g = 0; g < d->n_groups; ++g) {
-    const skv_page_group& G = d->groups[g];
-    const int top = *G.free_top;
-    const int tot = total[g];
-    for (int t = tid; t < tot; t += kPlanThreads) {
-      int lo = 0, hi = batch;
-      while (hi - lo > 1) {
-        const int mid = (lo + hi) >> 1;
-        if (off[g][mid] <= t) lo = mid; else hi = mid;
-      }
-      G.block_table[static_cast<int64_t>(lo) * G.bt_stride + first[g][lo] + (t - off[g][lo])] =
-          G.free_stack[top - 1 - t];
-    }
-    __syncthreads();  // every thread has read free_top before it moves
-    if (tid < batch) G.n_entries[tid] = (d->tok_lens[tid] + 1) / G.m;
-    if (tid == 0) *G.free_top = top - tot;
-  }
-  __syncthreads();  // n_entries used the old token count
-  if (tid < batch) d->tok_lens[tid] += 1;
-  if (tid == 0) *d->status = 0;
-}
-
-// ---------------------------------------------------------------------------
-// 2. append + top-k histograms, one launch, 256-thread workgroups:
-//    blocks [0, batch*layers)        : (sequence, layer) appends — wave 0-1 fold
-//                                      the main stream, wave 2 the indexer stream,
-//                                      wave 3 copies the ring row;
-//    blocks [batch*layers, + chunks*batch*csa) : top-k histogram chunks.
-// ---------------------------------------------------------------------------
-constexpr int kAppendThreads = 256;
+constexpr int kStepThreads = 256;  // every workgroup of the decode step
+constexpr int kGatherRowsD = 8;    // output rows per dense gather tile
+// Longest sequence the step accepts (longer ones are refused with
+// SKV_STATUS_BADARG): lengths, entry counts, page indices and grid indices
+// stay below 2^24, so the kernels divide with udiv24.
+constexpr int kMaxTokLen = (1 << 24) - (1 << 16);
+static_assert(kTkPartThreads == kStepThreads, "top-k chunk workgroups are step workgroups");
 
 __device__ __forceinline__ const skv_decode_layer* csa_layer(const skv_decode_desc* d, int want) {
   for (int li = 0; li < d->n_layers; ++li) {
@@ -107,160 +36,351 @@ __device__ __forceinline__ const skv_decode_layer* csa_layer(const skv_decode_de
   return nullptr;
 }
 
+// Score columns of a CSA query at length L (entries L/m; the causal mask
+// keeps (L-1)/m of them), clamped to the row's width so that no length can
+// send a read past the row.
+__device__ __forceinline__ void score_cols(const skv_decode_layer& Ly, int m, int L, int& n_cols, int& n_valid) {
+  const uint32_t Lc = static_cast<uint32_t>(min(max(L, 0), kMaxTokLen));
+  n_cols = static_cast<int>(min<int64_t>(udiv24(Lc, m), Ly.score_stride));
+  n_valid = Lc > 0 ? static_cast<int>(min<int64_t>(udiv24(Lc - 1, m), Ly.score_stride)) : 0;
+}
+
+// ---------------------------------------------------------------------------
+// 1. step plan.  skv_reserve policy over the page groups: a sequence whose
+//    entry count (L+1)/m needs more pages takes them from the group's free
+//    stack, pops in ascending sequence order; all-or-nothing over every
+//    group and sequence.  Every workgroup of the append launch computes it
+//    from the same inputs with the same arithmetic, so each knows the
+//    outcome and its own sequence's pops without waiting for another.
+// ---------------------------------------------------------------------------
+struct PlanSmem {
+  int red[kStepThreads / kWave][2 * SKV_MAX_GROUPS + 1];
+};
+
+struct OwnPlan {
+  int bad;   // SKV_STATUS_* bits, 0 when the step goes ahead
+  int top;   // free-stack top of group g_own before the step
+  int off;   // pops of the sequences before b in group g_own
+  int p0;    // pages sequence b held before the step
+  int need;  // pages sequence b takes
+};
+
+__device__ __forceinline__ int wave_sum(int v) {
+#pragma unroll
+  for (int s = 1; s < kWave; s <<= 1) v += __shfl_xor(v, s);
+  return v;
+}
+
+__device__ __forceinline__ int wave_or(int v) {
+#pragma unroll
+  for (int s = 1; s < kWave; s <<= 1) v |= __shfl_xor(v, s);
+  return v;
+}
+
+// g_own < 0: no group (SWA layer).  write_tops: this workgroup also writes
+// the groups' tops after the step to step_top.
+__device__ __forceinline__ OwnPlan step_plan(PlanSmem& sm, const skv_decode_desc* d, int b, int g_own,
+                                             bool write_tops) {
+  constexpr int kPerT = kDecodeMaxBatch / kStepThreads;
+  const int tid = threadIdx.x;
+  const int lane = tid & (kWave - 1);
+  const int wid = tid / kWave;
+  const int batch = d->batch;
+  const int ng = d->n_groups;
+  OwnPlan P{0, 0, 0, 0, 0};
+  if (ng == 0) return P;  // uniform: no page group, nothing to plan
+  // every load first (clamped indices), so they are all in flight together
+  int len1[kPerT];
+  int cur[kPerT][SKV_MAX_GROUPS];
+#pragma unroll
+  for (int j = 0; j < kPerT; ++j) {
+    const int s = min(tid + j * kStepThreads, batch - 1);
+    len1[j] = d->tok_lens[s] + 1;
+#pragma unroll
+    for (int g = 0; g < SKV_MAX_GROUPS; ++g) cur[j][g] = d->groups[min(g, ng - 1)].n_entries[s];
+  }
+  int top[SKV_MAX_GROUPS];
+#pragma unroll
+  for (int g = 0; g < SKV_MAX_GROUPS; ++g) top[g] = *d->groups[min(g, ng - 1)].free_top;
+  int bad = 0;
+  int tot[SKV_MAX_GROUPS], pre[SKV_MAX_GROUPS];
+#pragma unroll
+  for (int g = 0; g < SKV_MAX_GROUPS; ++g) {
+    tot[g] = 0;
+    pre[g] = 0;
+    if (g >= ng) continue;
+    const skv_page_group& G = d->groups[g];
+    const uint32_t m = static_cast<uint32_t>(G.m);
+    const uint32_t bs = static_cast<uint32_t>(G.block_size);
+#pragma unroll
+    for (int j = 0; j < kPerT; ++j) {
+      const int s = tid + j * kStepThreads;
+      if (s >= batch) continue;
+      if (len1[j] <= 0 || len1[j] > kMaxTokLen || cur[j][g] < 0 || cur[j][g] > kMaxTokLen) {
+        bad |= SKV_STATUS_BADARG;
+        continue;
+      }
+      const uint32_t target = udiv24(static_cast<uint32_t>(len1[j]), m);
+      const uint32_t c = static_cast<uint32_t>(cur[j][g]);
+      if (target < c) {
+        bad |= SKV_STATUS_BADARG;
+        continue;
+      }
+      const uint32_t p0 = ceil_div24(c, bs);
+      const uint32_t p1 = ceil_div24(target, bs);
+      if (p1 > G.bt_stride) bad |= SKV_STATUS_MAX_PAGES;
+      const int need = static_cast<int>(p1 - p0);
+      tot[g] += need;
+      if (s < b) pre[g] += need;
+    }
+  }
+  bad = wave_or(bad);
+#pragma unroll
+  for (int g = 0; g < SKV_MAX_GROUPS; ++g) {
+    tot[g] = wave_sum(tot[g]);
+    pre[g] = wave_sum(pre[g]);
+  }
+  if (lane == 0) {
+    sm.red[wid][0] = bad;
+#pragma unroll
+    for (int g = 0; g < SKV_MAX_GROUPS; ++g) {
+      sm.red[wid][1 + g] = tot[g];
+      sm.red[wid][1 + SKV_MAX_GROUPS + g] = pre[g];
+    }
+  }
+  __syncthreads();
+  bad = 0;
+#pragma unroll
+  for (int g = 0; g < SKV_MAX_GROUPS; ++g) {
+    tot[g] = 0;
+    pre[g] = 0;
+  }
+#pragma unroll
+  for (int w = 0; w < kStepThreads / kWave; ++w) {
+    bad |= sm.red[w][0];
+#pragma unroll
+    for (int g = 0; g < SKV_MAX_GROUPS; ++g) {
+      tot[g] += sm.red[w][1 + g];
+      pre[g] += sm.red[w][1 + SKV_MAX_GROUPS + g];
+    }
+  }
+  __syncthreads();  // sm.red is reused by the caller's union
+#pragma unroll
+  for (int g = 0; g < SKV_MAX_GROUPS; ++g) {
+    if (g >= ng) continue;
+    if (top[g] < 0 || top[g] > d->groups[g].n_pages) bad |= SKV_STATUS_BADARG;
+    else if (tot[g] > top[g]) bad |= SKV_STATUS_NOSPC;
+  }
+  P.bad = bad;
+  if (bad) return P;
+  if (write_tops && tid == 0) {
+#pragma unroll
+    for (int g = 0; g < SKV_MAX_GROUPS; ++g) {
+      if (g < ng) d->step_top[g] = top[g] - tot[g];
+    }
+  }
+#pragma unroll
+  for (int g = 0; g < SKV_MAX_GROUPS; ++g) {
+    if (g == g_own) {
+      const skv_page_group& G = d->groups[g];
+      const uint32_t c0 = static_cast<uint32_t>(G.n_entries[b]);
+      const uint32_t target = udiv24(static_cast<uint32_t>(d->tok_lens[b] + 1), G.m);
+      P.top = top[g];
+      P.off = pre[g];
+      P.p0 = static_cast<int>(ceil_div24(c0, G.block_size));
+      P.need = static_cast<int>(ceil_div24(target, G.block_size)) - P.p0;
+    }
+  }
+  return P;
+}
+
+// ---------------------------------------------------------------------------
+// 2. append launch, 256-thread workgroups:
+//    blocks [0, batch*layers)        : (sequence, layer) appends — waves 0-1
+//                                      fold the main stream, wave 2 the
+//                                      indexer stream, wave 3 copies the ring
+//                                      row;
+//    then                            : top-k histogram chunks.
+// ---------------------------------------------------------------------------
+
 // Fold the token into the running state of channel groups t, t + nt (8
-// channels each) of one stream and emit the entry when the block completes.
-// All threads t in [0, nt) of a stream must call it (fp8 amax shuffles span
-// the 16 lanes of a 128-channel block, which nt = 128 keeps inside a wave).
-__device__ __forceinline__ void decode_fold_part(const skv_page_group& G, int b, int64_t p, void* pool,
-                                                 int64_t entry_bytes, float* state, const float* bias,
-                                                 const void* c_all, const void* z_all, int channels,
-                                                 int format, int fp8_main, int t, int nt) {
+// channels each) of one stream and write the entry at `entry` (when not
+// null) if the token completes the block.  All threads t in [0, nt) of a
+// stream must call it (fp8 amax shuffles span the 16 lanes of a 128-channel
+// block, which nt = 128 keeps inside a wave).  Every load is issued before
+// the arithmetic.
+__device__ __forceinline__ void decode_fold_part(int m, int b, int64_t p, uint8_t* entry, float* state,
+                                                 const float* bias, const void* c_all, const void* z_all,
+                                                 int channels, int format, int fp8_main, int t, int nt) {
   const int groups = channels >> 3;
   float* sbase = state + static_cast<int64_t>(b) * 3 * channels;
   const uint16_t* crow = static_cast<const uint16_t*>(c_all) + static_cast<int64_t>(b) * channels;
   const uint16_t* zrow = static_cast<const uint16_t*>(z_all) + static_cast<int64_t>(b) * channels;
-  const float* brow = bias + (p % G.m) * channels;
-  const bool fresh = (p % G.m) == 0;
-  const bool emit = ((p + 1) % G.m) == 0;
-  uint8_t* entry = nullptr;
-  if (emit) {
-    const int64_t e = (p + 1) / G.m - 1;
-    const int64_t pi = e / G.block_size;
-    const int32_t page = (pi < G.bt_stride) ? G.block_table[b * G.bt_stride + pi] : -1;
-    if (page >= 0 && page < G.n_pages) {
-      entry = static_cast<uint8_t*>(pool) +
-              (static_cast<int64_t>(page) * G.block_size + e % G.block_size) * entry_bytes;
-    }
-  }
-  for (int grp = t; grp < ((groups + nt - 1) / nt) * nt; grp += nt) {
-    const bool mine = grp < groups;
-    float mx[8], sum[8], acc[8];
-    if (mine && !fresh) {
-      const u32x4* sp = reinterpret_cast<const u32x4*>(sbase + grp * 8);
-      const u32x4 m0 = sp[0], m1 = sp[1];
-      const u32x4 s0 = *reinterpret_cast<const u32x4*>(sbase + channels + grp * 8);
-      const u32x4 s1 = *(reinterpret_cast<const u32x4*>(sbase + channels + grp * 8) + 1);
-      const u32x4 a0 = *reinterpret_cast<const u32x4*>(sbase + 2 * channels + grp * 8);
-      const u32x4 a1 = *(reinterpret_cast<const u32x4*>(sbase + 2 * channels + grp * 8) + 1);
+  const uint32_t pm = umod24(static_cast<uint32_t>(p), m);  // p < 2^24
+  const float* brow = bias + pm * channels;
+  const bool fresh = pm == 0;
+  const bool emit = pm + 1 == static_cast<uint32_t>(m);
+  for (int grp0 = t; grp0 < ((groups + nt - 1) / nt) * nt; grp0 += nt) {
+    const bool mine = grp0 < groups;
+    const int grp = mine ? grp0 : groups - 1;  // in-range address for every lane
+    const u32x4* sp = reinterpret_cast<const u32x4*>(sbase + grp * 8);
+    const u32x4* ss = reinterpret_cast<const u32x4*>(sbase + channels + grp * 8);
+    const u32x4* sa = reinterpret_cast<const u32x4*>(sbase + 2 * channels + grp * 8);
+    const u32x4 m0 = sp[0], m1 = sp[1], s0 = ss[0], s1 = ss[1], a0 = sa[0], a1 = sa[1];
+    const u32x4 cv = *reinterpret_cast<const u32x4*>(crow + grp * 8);
+    const u32x4 zv = *reinterpret_cast<const u32x4*>(zrow + grp * 8);
+    const u32x4 b0 = *reinterpret_cast<const u32x4*>(brow + grp * 8);
+    const u32x4 b1 = *(reinterpret_cast<const u32x4*>(brow + grp * 8) + 1);
+    float mx[8], sum[8], acc[8], c[8], z[8], bb[8];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        mx[j] = __uint_as_float(m0[j]);
-        mx[j + 4] = __uint_as_float(m1[j]);
-        sum[j] = __uint_as_float(s0[j]);
-        sum[j + 4] = __uint_as_float(s1[j]);
-        acc[j] = __uint_as_float(a0[j]);
-        acc[j + 4] = __uint_as_float(a1[j]);
-      }
-    } else {
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        mx[j] = -INFINITY;
-        sum[j] = 0.f;
-        acc[j] = 0.f;
-      }
+    for (int j = 0; j < 4; ++j) {
+      mx[j] = fresh ? -INFINITY : __uint_as_float(m0[j]);
+      mx[j + 4] = fresh ? -INFINITY : __uint_as_float(m1[j]);
+      sum[j] = fresh ? 0.f : __uint_as_float(s0[j]);
+      sum[j + 4] = fresh ? 0.f : __uint_as_float(s1[j]);
+      acc[j] = fresh ? 0.f : __uint_as_float(a0[j]);
+      acc[j + 4] = fresh ? 0.f : __uint_as_float(a1[j]);
+      bb[j] = __uint_as_float(b0[j]);
+      bb[j + 4] = __uint_as_float(b1[j]);
     }
+    unpack8_bf16(cv, c);
+    unpack8_bf16(zv, z);
     float out[8];
-    if (mine) {
-      float c[8], z[8];
-      unpack8_bf16(*reinterpret_cast<const u32x4*>(crow + grp * 8), c);
-      unpack8_bf16(*reinterpret_cast<const u32x4*>(zrow + grp * 8), z);
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const float v = z[j] + brow[grp * 8 + j];
-        if (v > mx[j]) {
-          const float sc = expf(mx[j] - v);
-          sum[j] = sum[j] * sc + 1.f;
-          acc[j] = acc[j] * sc + c[j];
-          mx[j] = v;
-        } else {
-          const float w = expf(v - mx[j]);
-          sum[j] += w;
-          acc[j] += w * c[j];
-        }
-        out[j] = bf16_to_f32(f32_to_bf16(acc[j] / sum[j]));
+    for (int j = 0; j < 8; ++j) {
+      const float v = z[j] + bb[j];
+      if (v > mx[j]) {
+        const float sc = expf(mx[j] - v);
+        sum[j] = sum[j] * sc + 1.f;
+        acc[j] = acc[j] * sc + c[j];
+        mx[j] = v;
+      } else {
+        const float w = expf(v - mx[j]);
+        sum[j] += w;
+        acc[j] += w * c[j];
       }
-    } else {
-#pragma unroll
-      for (int j = 0; j < 8; ++j) out[j] = 0.f;
+      out[j] = mine ? acc[j] / sum[j] : 0.f;
     }
+#pragma unroll
+    for (int j = 0; j < 8; j += 2) bf16_round2(out[j], out[j + 1]);  // the compressor emits bf16 entries
     if (emit) {
-      if (entry) store_entry_group(entry, out, grp, groups, format, fp8_main);
+      if (entry) store_entry_group(entry, out, grp0, groups, format, fp8_main);
     } else if (mine) {
-      u32x4* sp = reinterpret_cast<u32x4*>(sbase + grp * 8);
-      sp[0] = u32x4{__float_as_uint(mx[0]), __float_as_uint(mx[1]), __float_as_uint(mx[2]), __float_as_uint(mx[3])};
-      sp[1] = u32x4{__float_as_uint(mx[4]), __float_as_uint(mx[5]), __float_as_uint(mx[6]), __float_as_uint(mx[7])};
-      u32x4* ss = reinterpret_cast<u32x4*>(sbase + channels + grp * 8);
-      ss[0] = u32x4{__float_as_uint(sum[0]), __float_as_uint(sum[1]), __float_as_uint(sum[2]), __float_as_uint(sum[3])};
-      ss[1] = u32x4{__float_as_uint(sum[4]), __float_as_uint(sum[5]), __float_as_uint(sum[6]), __float_as_uint(sum[7])};
-      u32x4* sa = reinterpret_cast<u32x4*>(sbase + 2 * channels + grp * 8);
-      sa[0] = u32x4{__float_as_uint(acc[0]), __float_as_uint(acc[1]), __float_as_uint(acc[2]), __float_as_uint(acc[3])};
-      sa[1] = u32x4{__float_as_uint(acc[4]), __float_as_uint(acc[5]), __float_as_uint(acc[6]), __float_as_uint(acc[7])};
+      u32x4* wp = reinterpret_cast<u32x4*>(sbase + grp * 8);
+      wp[0] = u32x4{__float_as_uint(mx[0]), __float_as_uint(mx[1]), __float_as_uint(mx[2]), __float_as_uint(mx[3])};
+      wp[1] = u32x4{__float_as_uint(mx[4]), __float_as_uint(mx[5]), __float_as_uint(mx[6]), __float_as_uint(mx[7])};
+      u32x4* ws = reinterpret_cast<u32x4*>(sbase + channels + grp * 8);
+      ws[0] = u32x4{__float_as_uint(sum[0]), __float_as_uint(sum[1]), __float_as_uint(sum[2]), __float_as_uint(sum[3])};
+      ws[1] = u32x4{__float_as_uint(sum[4]), __float_as_uint(sum[5]), __float_as_uint(sum[6]), __float_as_uint(sum[7])};
+      u32x4* wa = reinterpret_cast<u32x4*>(sbase + 2 * channels + grp * 8);
+      wa[0] = u32x4{__float_as_uint(acc[0]), __float_as_uint(acc[1]), __float_as_uint(acc[2]), __float_as_uint(acc[3])};
+      wa[1] = u32x4{__float_as_uint(acc[4]), __float_as_uint(acc[5]), __float_as_uint(acc[6]), __float_as_uint(acc[7])};
     }
   }
 }
 
-__global__ __launch_bounds__(kAppendThreads) void k_decode_append(const skv_decode_desc* __restrict__ d,
-                                                                  int n_chunks) {
-  __shared__ TopkHistSmem hsm;
-  if (*d->status) return;  // refused step: no state changes
+union AppendSmem {
+  PlanSmem plan;
+  TopkHistSmem hist;
+};
+
+__global__ __launch_bounds__(kStepThreads) void k_decode_append(const skv_decode_desc* __restrict__ d,
+                                                                int n_chunks) {
+  __shared__ AppendSmem sm;
   const int n_append = d->batch * d->n_layers;
+  const int tid = threadIdx.x;
   if (static_cast<int>(blockIdx.x) >= n_append) {
-    // top-k histogram chunk (chunk, b, csa layer); chunk 0 also zeroes the
-    // row's list counters, which the previous step's rank launch still read
-    int u = blockIdx.x - n_append;
-    const int chunk = u % n_chunks;
-    u /= n_chunks;
-    const int b = u % d->batch;
-    const skv_decode_layer* Ly = csa_layer(d, u / d->batch);
+    // top-k histogram chunk (chunk, b, csa layer).  It assumes the step
+    // goes ahead; on a refusal the rank launch still clears
+    // the histogram.  Chunk 0 zeroes the row's list counters, which the
+    // previous step's rank launch read.
+    const uint32_t u = blockIdx.x - n_append;  // grids stay below 2^24 workgroups
+    const uint32_t ub = udiv24(u, n_chunks);
+    const int chunk = static_cast<int>(u - ub * n_chunks);
+    const uint32_t uc = udiv24(ub, d->batch);
+    const int b = static_cast<int>(ub - uc * d->batch);
+    const skv_decode_layer* Ly = csa_layer(d, static_cast<int>(uc));
     if (!Ly) return;
     int32_t* ws = Ly->topk_ws + static_cast<int64_t>(b) * kTkWsWords;
-    if (chunk == 0 && threadIdx.x < 3) ws[kTkWsCnt + threadIdx.x] = 0;
-    const int m = d->groups[Ly->group].m;
-    const int L = d->tok_lens[b];
-    topk_hist_chunk(hsm, Ly->scores + static_cast<int64_t>(b) * Ly->score_stride, L / m,
-                    L > 0 ? (L - 1) / m : 0, Ly->top_k, chunk, ws);
+    if (chunk == 0 && tid < 3) ws[kTkWsCnt + tid] = 0;
+    int n_cols, n_valid;
+    score_cols(*Ly, d->groups[Ly->group].m, d->tok_lens[b] + 1, n_cols, n_valid);
+    topk_hist_chunk(sm.hist, Ly->scores + static_cast<int64_t>(b) * Ly->score_stride, n_cols, n_valid,
+                    Ly->top_k, chunk, ws);
     return;
   }
-  const int b = blockIdx.x % d->batch;
-  const skv_decode_layer& Ly = d->layers[blockIdx.x / d->batch];
-  const int L = d->tok_lens[b];
-  if (L <= 0) return;
-  const int64_t p = L - 1;
-  const int tid = threadIdx.x;
+  const int l = static_cast<int>(udiv24(blockIdx.x, d->batch));
+  const int b = static_cast<int>(blockIdx.x) - l * d->batch;
+  const skv_decode_layer& Ly = d->layers[l];
+  const bool paged = Ly.kind != SKV_LAYER_SWA;
+  const OwnPlan P = step_plan(sm.plan, d, b, paged ? Ly.group : -1, blockIdx.x == 0);
+  if (P.bad) {
+    if (blockIdx.x == 0 && tid == 0) *d->status = P.bad;
+    return;  // refused: nothing changes
+  }
+  if (blockIdx.x == 0 && tid == 0) *d->status = 0;
+  const int L0 = d->tok_lens[b];
+  const int64_t p = L0;  // position of the new token
+  if (l == 0 && tid == 0) d->step_lens[b] = L0 + 1;
   const int wave = tid / kWave;
   if (wave == 3) {
     const int row_chunks = d->latent >> 3;  // 16-byte chunks of a bf16 row
     const u32x4* src = static_cast<const u32x4*>(Ly.kv_new) + static_cast<int64_t>(b) * row_chunks;
-    u32x4* dst = static_cast<u32x4*>(Ly.ring) + (static_cast<int64_t>(b) * d->window + p % d->window) * row_chunks;
+    u32x4* dst = static_cast<u32x4*>(Ly.ring) + (static_cast<int64_t>(b) * d->window + umod24(static_cast<uint32_t>(p), d->window)) * row_chunks;
     for (int c = tid - 3 * kWave; c < row_chunks; c += kWave) dst[c] = src[c];
     return;
   }
-  if (Ly.kind == SKV_LAYER_SWA) return;
+  if (!paged) return;
   const skv_page_group& G = d->groups[Ly.group];
+  // the group's first layer records the sequence's new pages in the table
+  bool first = true;
+  for (int li = 0; li < l; ++li) {
+    if (d->layers[li].kind != SKV_LAYER_SWA && d->layers[li].group == Ly.group) first = false;
+  }
+  if (first && tid < P.need) {
+    G.block_table[b * G.bt_stride + P.p0 + tid] = G.free_stack[P.top - 1 - P.off - tid];
+  }
+  // the page of the entry this token completes, if any
+  uint8_t* entry = nullptr;
+  uint8_t* ientry = nullptr;
+  const uint32_t e1 = udiv24(static_cast<uint32_t>(p + 1), G.m);  // entries after the token
+  if (e1 * G.m == static_cast<uint32_t>(p + 1)) {
+    const uint32_t e = e1 - 1;
+    const int pi = static_cast<int>(udiv24(e, G.block_size));
+    int32_t page = -1;
+    if (pi < P.p0) page = G.block_table[b * G.bt_stride + pi];
+    else if (pi - P.p0 < P.need) page = G.free_stack[P.top - 1 - P.off - (pi - P.p0)];
+    if (page >= 0 && page < G.n_pages) {
+      const int64_t slot = static_cast<int64_t>(page) * G.block_size + (e - pi * G.block_size);
+      entry = static_cast<uint8_t*>(Ly.pool) + slot * Ly.entry_bytes;
+      if (Ly.idx_pool) ientry = static_cast<uint8_t*>(Ly.idx_pool) + slot * static_cast<int64_t>(d->c_indexer) * 2;
+    }
+  }
   if (wave < 2) {
     const int fp8_main = (Ly.format == SKV_FMT_FP8) ? d->latent - SKV_FP8_ROPE_DIMS : 0;
-    decode_fold_part(G, b, p, Ly.pool, Ly.entry_bytes, Ly.state, Ly.bias, Ly.c_new, Ly.z_new, d->latent,
-                     Ly.format, fp8_main, tid, 2 * kWave);
+    decode_fold_part(G.m, b, p, entry, Ly.state, Ly.bias, Ly.c_new, Ly.z_new, d->latent, Ly.format, fp8_main,
+                     tid, 2 * kWave);
   } else if (Ly.kind == SKV_LAYER_CSA && Ly.idx_pool) {
-    decode_fold_part(G, b, p, Ly.idx_pool, static_cast<int64_t>(d->c_indexer) * 2, Ly.idx_state,
-                     Ly.idx_bias, Ly.ci_new, Ly.zi_new, d->c_indexer, SKV_FMT_BF16, 0, tid - 2 * kWave,
-                     kWave);
+    decode_fold_part(G.m, b, p, ientry, Ly.idx_state, Ly.idx_bias, Ly.ci_new, Ly.zi_new, d->c_indexer,
+                     SKV_FMT_BF16, 0, tid - 2 * kWave, kWave);
   }
 }
 
 // ---------------------------------------------------------------------------
-// Row copies shared by the gather tiles and the top-k rank step.  Row kinds:
+// Row copies shared by the gather tiles and the sparse gather.  Row kinds:
 // 0 skip, 1 copy a bf16 row, 2 dequantize an fp8 entry to bf16, 3 zero row.
 // ---------------------------------------------------------------------------
+
 // 16 fp8 e4m3fn codes times their block scale -> 16 bf16 (two 16-byte chunks).
 __device__ __forceinline__ void dequant_codes(const u32x4 codes, float scale, u32x4& o0, u32x4& o1) {
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
     float f[4];
+    e4m3fn_x4_to_f32(codes[q], f);
 #pragma unroll
-    for (int h = 0; h < 4; ++h) f[h] = e4m3fn_to_f32(static_cast<uint8_t>(codes[q] >> (8 * h))) * scale;
-    const uint32_t lo = f32_to_bf16(f[0]) | (static_cast<uint32_t>(f32_to_bf16(f[1])) << 16);
-    const uint32_t hi = f32_to_bf16(f[2]) | (static_cast<uint32_t>(f32_to_bf16(f[3])) << 16);
+    for (int h = 0; h < 4; ++h) f[h] *= scale;
+    const uint32_t lo = bf16_pack2(f[0], f[1]);
+    const uint32_t hi = bf16_pack2(f[2], f[3]);
     if (q < 2) {
       o0[2 * q] = lo;
       o0[2 * q + 1] = hi;
@@ -277,75 +397,70 @@ struct RowRef {
   int kind;
 };
 
-// Copies rows [0, n) with all kThreads threads; row(r) gives row r's RowRef.
-// Each thread issues kUnroll loads before its stores.  The loads are
-// unconditional (a lane with nothing to load reads 16 bytes at `safe`, any
-// readable device address, and drops them): a load under a branch is waited
-// for before the branch joins, which would serialize the memory round trips.
-// `fp8` says whether any row may be of kind 2 (uniform over the workgroup).
-template <int kThreads, int kUnroll, class RowFn>
+// Copies rows [0, n) with all kStepThreads threads, kTPR threads per row
+// (kStepThreads / kTPR rows at a time); row(r) gives row r's RowRef.  A
+// thread copies chunks sub, sub + kTPR, ... of its row, issuing kU 16-byte
+// loads before their stores.  The loads are unconditional (a lane with
+// nothing to load reads 16 bytes at `safe`, any readable device address,
+// and drops them): a load under a divergent branch is waited for before the
+// branch joins, which would serialize the memory round trips.  `fp8` says
+// whether any row may be of kind 2 (uniform over the workgroup).
+template <int kTPR, int kU, class RowFn>
 __device__ __forceinline__ void copy_rows(int n, RowFn row, int latent, bool fp8, const void* safe) {
+  constexpr int kRowsAtOnce = kStepThreads / kTPR;
   const u32x4* safe4 = static_cast<const u32x4*>(safe);
+  const int sub = threadIdx.x % kTPR;
   const int bf_chunks = latent >> 3;  // 16-byte chunks of an output row
-  const int total = n * bf_chunks;
-  for (int t0 = threadIdx.x; t0 < total; t0 += kThreads * kUnroll) {
-    u32x4 v[kUnroll];
-    RowRef rf[kUnroll];
-    int c[kUnroll];
-#pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-      const int t = t0 + u * kThreads;
-      const int tt = (t < total) ? t : 0;
-      const int rr = tt / bf_chunks;
-      c[u] = tt - rr * bf_chunks;
-      rf[u] = row(rr);
-      if (t >= total) rf[u].kind = 0;
-      const u32x4* p = (rf[u].kind == 1) ? reinterpret_cast<const u32x4*>(rf[u].src) + c[u] : safe4;
-      v[u] = ld_stream(p);
-    }
-#pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-      if (rf[u].kind == 1) st_stream(reinterpret_cast<u32x4*>(rf[u].dst) + c[u], v[u]);
-      if (rf[u].kind == 3) st_stream(reinterpret_cast<u32x4*>(rf[u].dst) + c[u], u32x4{0u, 0u, 0u, 0u});
-    }
-  }
-  if (!fp8) return;
   const int fp8_main = latent - SKV_FP8_ROPE_DIMS;
   const int code_chunks = fp8_main >> 4;  // 16 codes -> 2 output chunks
   const int fp8_tasks = code_chunks + (SKV_FP8_ROPE_DIMS >> 3);
-  const int ftotal = n * fp8_tasks;
-  for (int t0 = threadIdx.x; t0 < ftotal; t0 += kThreads * kUnroll) {
-    u32x4 v[kUnroll];
-    float scale[kUnroll];
-    RowRef rf[kUnroll];
-    int c[kUnroll];
+  for (int r0 = 0; r0 < n; r0 += kRowsAtOnce) {
+    const int r = r0 + static_cast<int>(threadIdx.x) / kTPR;
+    RowRef rf = row(min(r, n - 1));
+    if (r >= n) rf.kind = 0;
+    for (int c0 = sub; c0 < bf_chunks; c0 += kTPR * kU) {
+      u32x4 v[kU];
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-      const int t = t0 + u * kThreads;
-      const int tt = (t < ftotal) ? t : 0;
-      const int rr = tt / fp8_tasks;
-      c[u] = tt - rr * fp8_tasks;
-      rf[u] = row(rr);
-      if (t >= ftotal) rf[u].kind = 0;
-      const bool is_code = c[u] < code_chunks;
-      const uint8_t* codes = is_code ? rf[u].src + c[u] * 16
-                                     : rf[u].src + fp8_main + (fp8_main >> 7) * 4 + (c[u] - code_chunks) * 16;
-      const uint8_t* sc = rf[u].src + fp8_main + (c[u] >> 3) * 4;
-      const bool live = rf[u].kind == 2;
-      v[u] = *(live ? reinterpret_cast<const u32x4*>(codes) : safe4);
-      scale[u] = *(live && is_code ? reinterpret_cast<const float*>(sc) : reinterpret_cast<const float*>(safe4));
+      for (int u = 0; u < kU; ++u) {
+        const int c = min(c0 + u * kTPR, bf_chunks - 1);
+        v[u] = ld_stream(rf.kind == 1 ? reinterpret_cast<const u32x4*>(rf.src) + c : safe4);
+      }
+#pragma unroll
+      for (int u = 0; u < kU; ++u) {
+        const int c = c0 + u * kTPR;
+        if (c < bf_chunks && (rf.kind == 1 || rf.kind == 3)) {
+          st_stream(reinterpret_cast<u32x4*>(rf.dst) + c, rf.kind == 1 ? v[u] : u32x4{0u, 0u, 0u, 0u});
+        }
+      }
     }
+    if (!fp8) continue;
+    for (int c0 = sub; c0 < fp8_tasks; c0 += kTPR * kU) {
+      u32x4 v[kU];
+      float scale[kU];
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-      if (rf[u].kind != 2) continue;
-      u32x4* o = reinterpret_cast<u32x4*>(rf[u].dst);
-      if (c[u] < code_chunks) {
-        u32x4 o0, o1;
-        dequant_codes(v[u], scale[u], o0, o1);
-        st_stream(o + 2 * c[u], o0);
-        st_stream(o + 2 * c[u] + 1, o1);
-      } else {
-        st_stream(o + (fp8_main >> 3) + (c[u] - code_chunks), v[u]);
+      for (int u = 0; u < kU; ++u) {
+        const int c = min(c0 + u * kTPR, fp8_tasks - 1);
+        const bool live = rf.kind == 2;
+        const bool is_code = c < code_chunks;
+        const uint8_t* src = is_code ? rf.src + c * 16
+                                     : rf.src + fp8_main + (fp8_main >> 7) * 4 + (c - code_chunks) * 16;
+        v[u] = *(live ? reinterpret_cast<const u32x4*>(src) : safe4);
+        scale[u] = *(live && is_code ? reinterpret_cast<const float*>(rf.src + fp8_main + (c >> 3) * 4)
+                                     : reinterpret_cast<const float*>(safe4));
+      }
+#pragma unroll
+      for (int u = 0; u < kU; ++u) {
+        const int c = c0 + u * kTPR;
+        if (c >= fp8_tasks || rf.kind != 2) continue;
+        u32x4* o = reinterpret_cast<u32x4*>(rf.dst);
+        if (c < code_chunks) {
+          u32x4 o0, o1;
+          dequant_codes(v[u], scale[u], o0, o1);
+          st_stream(o + 2 * c, o0);
+          st_stream(o + 2 * c + 1, o1);
+        } else {
+          st_stream(o + (fp8_main >> 3) + (c - code_chunks), v[u]);
+        }
       }
     }
   }
@@ -356,19 +471,21 @@ __device__ __forceinline__ void copy_rows(int n, RowFn row, int latent, bool fp8
 __device__ __forceinline__ int entry_source(const skv_page_group& G, const skv_decode_layer& Ly, int b, int e,
                                             int n_ent, const uint8_t** src) {
   if (e < 0 || e >= n_ent) return 0;
-  const int64_t pi = e / G.block_size;
+  const int pi = static_cast<int>(udiv24(e, G.block_size));  // e < 2^24
   const int32_t page = (pi < G.bt_stride) ? G.block_table[b * G.bt_stride + pi] : -1;
   if (page < 0 || page >= G.n_pages) return 0;
   *src = static_cast<const uint8_t*>(Ly.pool) +
-         (static_cast<int64_t>(page) * G.block_size + e % G.block_size) * Ly.entry_bytes;
+         (static_cast<int64_t>(page) * G.block_size + (e - pi * G.block_size)) * Ly.entry_bytes;
   return (Ly.format == SKV_FMT_FP8) ? 2 : 1;
 }
 
 // ---------------------------------------------------------------------------
-// 3. filter launch, 256-thread workgroups:
-//    blocks [0, chunks*batch*csa)  : top-k filter chunks (skv_topk.h);
-//    then gather tiles             : kGatherRowsD rows of a layer's dense rows
-//                                    [HCA entries (out_rows) | window].
+// 3. dense gather tiles (HCA entries and SWA windows) and the commit of the
+//    step: the filter launch ends its grid with these blocks.
+//    Tile t of (layer, sequence) copies rows [8t, 8t+8) of the layer's dense
+//    row space [HCA entries (out_rows) | window].  Tile 0 of (layer 0, b)
+//    commits the step's length of b (tokens and entry counts), tile 0 of
+//    (layer 0, 0) the free-stack tops; nothing in these launches reads them.
 // ---------------------------------------------------------------------------
 struct GatherTileSmem {
   const uint8_t* src_row[kGatherRowsD];
@@ -376,20 +493,14 @@ struct GatherTileSmem {
   int row_kind[kGatherRowsD];
 };
 
-union FilterLaunchSmem {
-  TopkFilterSmem filter;
-  GatherTileSmem tile;
-};
-
 __device__ __forceinline__ int dense_rows(const skv_decode_desc* d, const skv_decode_layer& Ly) {
   return d->window + (Ly.kind == SKV_LAYER_HCA ? static_cast<int>(Ly.out_rows) : 0);
 }
 
 __device__ __forceinline__ void gather_tile(GatherTileSmem& sm, const skv_decode_desc* d,
-                                            const skv_decode_layer& Ly, int b, int tile) {
+                                            const skv_decode_layer& Ly, int b, int tile, int L) {
   const int latent = d->latent;
   const int64_t out_row = static_cast<int64_t>(latent) * 2;
-  const int L = d->tok_lens[b];
   const int n_dense = (Ly.kind == SKV_LAYER_HCA) ? static_cast<int>(Ly.out_rows) : 0;
   const int n_rows = n_dense + d->window;
   const int r0 = tile * kGatherRowsD;
@@ -401,13 +512,13 @@ __device__ __forceinline__ void gather_tile(GatherTileSmem& sm, const skv_decode
     if (r < n_dense) {
       // dense HCA rows past the entries stay untouched
       const skv_page_group& G = d->groups[Ly.group];
-      kind = entry_source(G, Ly, b, r, G.n_entries[b], &s);
+      kind = entry_source(G, Ly, b, r, static_cast<int>(udiv24(L, G.m)), &s);
       o = static_cast<uint8_t*>(Ly.out_entries) + (static_cast<int64_t>(b) * Ly.out_rows + r) * out_row;
     } else if (r < n_rows) {
       const int w = r - n_dense;
       const int cnt = min(max(L, 0), d->window);
       if (w < cnt) {
-        const int64_t slot = (static_cast<int64_t>(L) - cnt + w) % d->window;
+        const int64_t slot = umod24(static_cast<uint32_t>(L - cnt + w), d->window);
         s = static_cast<const uint8_t*>(Ly.ring) + (static_cast<int64_t>(b) * d->window + slot) * out_row;
         o = static_cast<uint8_t*>(Ly.out_window) + (static_cast<int64_t>(b) * d->window + w) * out_row;
         kind = 1;
@@ -418,38 +529,30 @@ __device__ __forceinline__ void gather_tile(GatherTileSmem& sm, const skv_decode
     sm.row_kind[threadIdx.x] = kind;
   }
   __syncthreads();
-  copy_rows<kGatherThreadsD, 4>(
+  copy_rows<kStepThreads / kGatherRowsD, 3>(
       kGatherRowsD, [&](int r) { return RowRef{sm.src_row[r], sm.dst_row[r], sm.row_kind[r]}; }, latent,
       Ly.format == SKV_FMT_FP8 && Ly.kind == SKV_LAYER_HCA, d);
 }
 
-__global__ __launch_bounds__(kTkPartThreads) void k_decode_filter(const skv_decode_desc* __restrict__ d,
-                                                                  int n_chunks, int n_csa) {
-  static_assert(kTkPartThreads == kGatherThreadsD, "filter and gather tiles share the launch");
-  __shared__ FilterLaunchSmem sm;
+// Block u of the dense part of the filter launch.
+__device__ __forceinline__ void dense_block(GatherTileSmem& sm, const skv_decode_desc* d, int u) {
   if (*d->status) return;  // refused step
   const int batch = d->batch;
-  int u = blockIdx.x;
-  const int n_filter = n_chunks * batch * n_csa;
-  if (u < n_filter) {
-    const int chunk = u % n_chunks;
-    u /= n_chunks;
-    const int b = u % batch;
-    const skv_decode_layer* Ly = csa_layer(d, u / batch);
-    if (!Ly) return;  // uniform over the workgroup
-    const int m = d->groups[Ly->group].m;
-    const int L = d->tok_lens[b];
-    topk_filter_chunk(sm.filter, Ly->scores + static_cast<int64_t>(b) * Ly->score_stride, L / m,
-                      L > 0 ? (L - 1) / m : 0, Ly->top_k, chunk,
-                      Ly->topk_ws + static_cast<int64_t>(b) * kTkWsWords);
-    return;
-  }
-  u -= n_filter;
   for (int l = 0; l < d->n_layers; ++l) {
     const skv_decode_layer& Ly = d->layers[l];
-    const int tiles = static_cast<int>(ceil_div(dense_rows(d, Ly), kGatherRowsD));
+    const int tiles = (dense_rows(d, Ly) + kGatherRowsD - 1) / kGatherRowsD;
     if (u < tiles * batch) {
-      gather_tile(sm.tile, d, Ly, u / tiles, u % tiles);
+      const int b = static_cast<int>(udiv24(u, tiles));
+      const int tile = u - b * tiles;
+      const int L = d->step_lens[b];
+      if (l == 0 && tile == 0 && threadIdx.x == 0) {
+        d->tok_lens[b] = L;
+        for (int g = 0; g < d->n_groups; ++g) d->groups[g].n_entries[b] = udiv24(L, d->groups[g].m);
+        if (b == 0) {
+          for (int g = 0; g < d->n_groups; ++g) *d->groups[g].free_top = d->step_top[g];
+        }
+      }
+      gather_tile(sm, d, Ly, b, tile, L);
       return;
     }
     u -= tiles * batch;
@@ -457,40 +560,22 @@ __global__ __launch_bounds__(kTkPartThreads) void k_decode_filter(const skv_deco
 }
 
 // ---------------------------------------------------------------------------
-// 4. top-k rank + sparse gather: grid (parts, batch, CSA layers), part p of a
-//    row owns output positions [p*rank_out, (p+1)*rank_out), rank_out 16 or
-//    32 (the host picks 16 when the rows alone give few workgroups).
-//    Every part loads the row's candidate lists as 64-bit order keys
-//    (key << 32 | ~index: larger means earlier in the output), ranks the sure
-//    candidates p, p + parts, ... among the sure list and the tie candidates
-//    p, p + parts, ... among the tie list (kRankSub lanes per candidate, each
-//    counting a strided share of the list), and writes each winner's index
-//    and entry at its output position; positions in [sel, top_k) it owns get
-//    index -1 and entry 0 (the reference's clamp(min=0) before its gather).
-//    On a tie bin too large for the lists every part runs the full select.
-//    Part 0 zeroes the row's histogram for the next step; the counters are
-//    zeroed by the next step's histogram launch.
+// 4. top-k ordering + sparse gather of one part of a row.  Part p of a row
+//    owns output positions [p*rank_out, (p+1)*rank_out), rank_out 16 or 32.
+//    The row's candidates sit in LDS as 64-bit order keys (key << 32 | ~idx:
+//    larger means earlier in the output), the sure list [0, S) then the tie
+//    list [S, C), each in the same order in every part.  A part ranks its
+//    candidates p, p + parts, ... of each list within that list (kRankSub
+//    lanes per candidate, each counting a strided share), writes every
+//    winner's index and entry at its output position, and gives the
+//    positions in [sel, top_k) it owns index -1 and entry 0 (the reference's
+//    clamp(min=0) before its gather).
 // ---------------------------------------------------------------------------
-constexpr int kRankThreads = 256;
-constexpr int kRankOutMin = 16;  // output positions per part: 16 or 32, chosen per launch
+constexpr int kRankOutMin = 16;
 constexpr int kRankOut = 32;
 constexpr int kRankSub = 8;
-constexpr int kRankCands = kRankThreads / kRankSub;  // candidates ranked per round
-constexpr int kRankMaxRows = 512;  // rows one part can collect (checked below)
-
-struct RankSmem {
-  int cnt[3];  // n_sure, n_tie, tie-overflow flag
-  int n_rows;
-  int2 win[kRankMaxRows];         // (output position, pick)
-  uintptr_t src_kind[kRankMaxRows];  // entry address | row kind (entries are 4-byte aligned)
-  union {
-    uint64_t ck[kTkCand];
-    struct {
-      TopkSmemT<kRankThreads> full;
-      int32_t order[kMaxTopK];
-    } f;
-  } u;
-};
+constexpr int kRankCands = kStepThreads / kRankSub;  // candidates ranked per round
+constexpr int kRankMaxRows = 512;                    // rows one part can collect (checked below)
 
 // Rows a part collects, worst case over top_k and the part size: its sure
 // winners (at most ceil(top_k/parts) <= part size), its tie winners (at most
@@ -509,118 +594,182 @@ constexpr int rank_rows_max() {
 }
 static_assert(rank_rows_max() <= kRankMaxRows, "rank row lists too small");
 
-__global__ __launch_bounds__(kRankThreads) void k_decode_topk_rank(const skv_decode_desc* __restrict__ d,
-                                                                    int rank_out) {
+struct RankRows {
+  int n_rows;
+  int2 win[kRankMaxRows];            // (output position, pick)
+  uintptr_t src_kind[kRankMaxRows];  // entry address | row kind (entries are 4-byte aligned)
+};
+
+__device__ __forceinline__ void rank_candidates(RankRows& rr, const uint64_t* ck, int S, int C, int sel,
+                                                int part, int parts) {
+  const int tid = threadIdx.x;
+  const int sub = tid % kRankSub;
+#pragma unroll 1
+  for (int cls = 0; cls < 2; ++cls) {
+    const int lo = cls ? S : 0;
+    const int hi = cls ? C : S;
+    const int n_mine = (part < hi - lo) ? static_cast<int>(ceil_div24(hi - lo - part, parts)) : 0;
+    for (int j0 = 0; j0 < n_mine; j0 += kRankCands) {
+      const int j = j0 + tid / kRankSub;
+      const bool valid = j < n_mine;
+      const uint64_t mine = valid ? ck[lo + part + j * parts] : ~0ull;
+      int rank = 0;
+#pragma unroll 8
+      for (int q = lo + sub; q < hi; q += kRankSub) rank += ck[q] > mine;
+      rank += __shfl_xor(rank, 1);
+      rank += __shfl_xor(rank, 2);
+      rank += __shfl_xor(rank, 4);
+      const int pos = lo + rank;
+      if (valid && sub == 0 && pos < sel) {
+        const uint32_t key = static_cast<uint32_t>(mine >> 32);
+        const int idx = static_cast<int>(~static_cast<uint32_t>(mine));
+        rr.win[atomicAdd(&rr.n_rows, 1)] = make_int2(pos, key_finite(key) ? idx : -1);
+      }
+    }
+  }
+}
+
+// Adds the fills [f0, o1), writes the indices and copies every collected row.
+// n_rows: rows collected so far (read after a barrier by the caller).
+__device__ __forceinline__ void finish_rows(RankRows& rr, int n_rows, int f0, int o1,
+                                            const skv_decode_desc* d, const skv_decode_layer& Ly, int b, int L) {
+  const int tid = threadIdx.x;
+  if (tid < o1 - f0) rr.win[n_rows + tid] = make_int2(f0 + tid, -1);
+  n_rows += max(0, o1 - f0);
+  __syncthreads();
+  const skv_page_group& G = d->groups[Ly.group];
+  const int n_ent = static_cast<int>(udiv24(L, G.m));
+  const int k = Ly.top_k;
+  const int64_t out_row = static_cast<int64_t>(d->latent) * 2;
+  int32_t* out_idx = Ly.topk_idx + static_cast<int64_t>(b) * k;
+  uint8_t* out_base = static_cast<uint8_t*>(Ly.out_entries) + static_cast<int64_t>(b) * k * out_row;
+  for (int w = tid; w < n_rows; w += kStepThreads) {
+    const int2 pw = rr.win[w];
+    out_idx[pw.x] = pw.y;
+    const uint8_t* s = nullptr;
+    const int kind = entry_source(G, Ly, b, pw.y < 0 ? 0 : pw.y, n_ent, &s);
+    rr.src_kind[w] = reinterpret_cast<uintptr_t>(s) | static_cast<uintptr_t>(kind ? kind : 3);
+  }
+  __syncthreads();
+  copy_rows<8, 9>(
+      n_rows,
+      [&](int r) {
+        const uintptr_t sk = rr.src_kind[r];
+        return RowRef{reinterpret_cast<const uint8_t*>(sk & ~static_cast<uintptr_t>(3)),
+                      out_base + rr.win[r].x * out_row, static_cast<int>(sk & 3)};
+      },
+      d->latent, Ly.format == SKV_FMT_FP8, d);
+}
+
+// ---------------------------------------------------------------------------
+// 5. filter launch (top-k filter chunks, see skv_topk.h, then the dense
+//    blocks) and rank launch (every part loads the row's candidate lists,
+//    ranks and gathers).  Part 0 of the rank launch zeroes the row's
+//    histogram for the next step, also after a refusal.
+// ---------------------------------------------------------------------------
+union FilterLaunchSmem {
+  TopkFilterSmem filter;
+  GatherTileSmem tile;
+};
+
+__global__ __launch_bounds__(kStepThreads) void k_decode_filter(const skv_decode_desc* __restrict__ d,
+                                                                int n_chunks, int n_csa) {
+  __shared__ FilterLaunchSmem sm;
+  int u = blockIdx.x;
+  const int n_filter = n_chunks * d->batch * n_csa;
+  if (u < n_filter) {
+    if (*d->status) return;  // refused step
+    const uint32_t ub = udiv24(u, n_chunks);
+    const int chunk = static_cast<int>(u - ub * n_chunks);
+    const uint32_t uc = udiv24(ub, d->batch);
+    const int b = static_cast<int>(ub - uc * d->batch);
+    const skv_decode_layer* Ly = csa_layer(d, static_cast<int>(uc));
+    if (!Ly) return;  // uniform over the workgroup
+    int n_cols, n_valid;
+    score_cols(*Ly, d->groups[Ly->group].m, d->step_lens[b], n_cols, n_valid);
+    topk_filter_chunk(sm.filter, Ly->scores + static_cast<int64_t>(b) * Ly->score_stride, n_cols, n_valid,
+                      Ly->top_k, chunk, Ly->topk_ws + static_cast<int64_t>(b) * kTkWsWords);
+    return;
+  }
+  dense_block(sm.tile, d, u - n_filter);
+}
+
+struct RankSmem {
+  RankRows rr;
+  int cnt[3];  // n_sure, n_tie, tie-overflow flag
+  union {
+    uint64_t ck[kTkCand];
+    struct {
+      TopkSmemT<kStepThreads> full;
+      int32_t order[kMaxTopK];
+    } f;
+  } u;
+};
+
+__global__ __launch_bounds__(kStepThreads) void k_decode_topk_rank(const skv_decode_desc* __restrict__ d,
+                                                                   int rank_out) {
   __shared__ RankSmem sm;
-  if (*d->status) return;  // refused step
   const skv_decode_layer* Lp = csa_layer(d, blockIdx.z);
   if (!Lp) return;
   const skv_decode_layer& Ly = *Lp;
   const int k = Ly.top_k;
-  const int parts = static_cast<int>(ceil_div(k, rank_out));
+  const int parts = static_cast<int>(ceil_div24(k, rank_out));
   const int part = blockIdx.x;
   if (part >= parts) return;  // the grid is sized for the largest top_k
   const int b = blockIdx.y;
   const int tid = threadIdx.x;
-  const skv_page_group& G = d->groups[Ly.group];
-  const int L = d->tok_lens[b];
-  const int n_cols = L / G.m;
-  const int n_valid = L > 0 ? (L - 1) / G.m : 0;
-  const int sel = topk_sel(k, n_cols, n_valid);
   int32_t* ws = Ly.topk_ws + static_cast<int64_t>(b) * kTkWsWords;
   if (part == 0) {
-    for (int i = tid; i < kTkBins; i += kRankThreads) ws[kTkWsHist + i] = 0;
+    for (int i = tid; i < kTkBins; i += kStepThreads) ws[kTkWsHist + i] = 0;
   }
+  if (*d->status) return;  // refused step
+  const skv_page_group& G = d->groups[Ly.group];
+  const int L = d->step_lens[b];
+  int n_cols, n_valid;
+  score_cols(Ly, G.m, L, n_cols, n_valid);
+  const int sel = topk_sel(k, n_cols, n_valid);
   if (tid < 3) sm.cnt[tid] = ws[kTkWsCnt + tid];
-  if (tid == 0) sm.n_rows = 0;
+  if (tid == 0) sm.rr.n_rows = 0;
   __syncthreads();
   const int o0 = part * rank_out;
   const int o1 = min(k, o0 + rank_out);
-  const int f0 = max(o0, sel);  // positions [f0, o1) are fills
-  int n_rows;
   if (sel > 0 && sm.cnt[2]) {
     // tie bin over the list capacity: full select of the row, then this part's positions
-    topk_row<kRankThreads>(sm.u.f.full, nullptr, Ly.scores + static_cast<int64_t>(b) * Ly.score_stride,
+    topk_row<kStepThreads>(sm.u.f.full, nullptr, Ly.scores + static_cast<int64_t>(b) * Ly.score_stride,
                            n_cols, n_valid, k, sm.u.f.order);
     __syncthreads();
-    if (tid < o1 - o0) sm.win[tid] = make_int2(o0 + tid, sm.u.f.order[o0 + tid]);
-    n_rows = o1 - o0;
-  } else {
-    if (sel > 0) {
-      const int S = min(sm.cnt[0], kMaxTopK);
-      const int C = S + min(sm.cnt[1], kTkTieCap);
-      const int2* sure_list = reinterpret_cast<const int2*>(ws + kTkWsSure);
-      const int2* tie_list = reinterpret_cast<const int2*>(ws + kTkWsTie);
-      constexpr int kLoad = 8;  // list loads in flight per thread
-      for (int c0 = tid; c0 < C; c0 += kRankThreads * kLoad) {
-        int2 v[kLoad];
+    if (tid < o1 - o0) sm.rr.win[tid] = make_int2(o0 + tid, sm.u.f.order[o0 + tid]);
+    __syncthreads();
+    finish_rows(sm.rr, o1 - o0, o1, o1, d, Ly, b, L);
+    return;
+  }
+  if (sel > 0) {
+    const int S = min(sm.cnt[0], kMaxTopK);
+    const int C = S + min(sm.cnt[1], kTkTieCap);
+    const int2* sure_list = reinterpret_cast<const int2*>(ws + kTkWsSure);
+    const int2* tie_list = reinterpret_cast<const int2*>(ws + kTkWsTie);
+    constexpr int kLoad = 8;  // list loads in flight per thread
+    for (int c0 = tid; c0 < C; c0 += kStepThreads * kLoad) {
+      int2 v[kLoad];
 #pragma unroll
-        for (int u = 0; u < kLoad; ++u) {
-          const int c = min(c0 + u * kRankThreads, C - 1);  // unconditional: C >= sel > 0
-          v[u] = (c < S ? sure_list : tie_list - S)[c];
-        }
-#pragma unroll
-        for (int u = 0; u < kLoad; ++u) {
-          const int c = c0 + u * kRankThreads;
-          if (c < C) {
-            sm.u.ck[c] = (static_cast<uint64_t>(static_cast<uint32_t>(v[u].x)) << 32) |
-                         static_cast<uint32_t>(~v[u].y);
-          }
-        }
+      for (int u = 0; u < kLoad; ++u) {
+        const int c = min(c0 + u * kStepThreads, C - 1);  // unconditional: C >= sel > 0
+        v[u] = (c < S ? sure_list : tie_list - S)[c];
       }
-      __syncthreads();
-      const int sub = tid % kRankSub;
-#pragma unroll 1
-      for (int cls = 0; cls < 2; ++cls) {
-        const int lo = cls ? S : 0;
-        const int hi = cls ? C : S;
-        const int n_mine = (part < hi - lo) ? static_cast<int>(ceil_div(hi - lo - part, parts)) : 0;
-        for (int j0 = 0; j0 < n_mine; j0 += kRankCands) {
-          const int j = j0 + tid / kRankSub;
-          const bool valid = j < n_mine;
-          const uint64_t mine = valid ? sm.u.ck[lo + part + j * parts] : ~0ull;
-          int rank = 0;
-#pragma unroll 8
-          for (int q = lo + sub; q < hi; q += kRankSub) rank += sm.u.ck[q] > mine;
-          rank += __shfl_xor(rank, 1);
-          rank += __shfl_xor(rank, 2);
-          rank += __shfl_xor(rank, 4);
-          const int pos = lo + rank;
-          if (valid && sub == 0 && pos < sel) {
-            const uint32_t key = static_cast<uint32_t>(mine >> 32);
-            const int idx = static_cast<int>(~static_cast<uint32_t>(mine));
-            sm.win[atomicAdd(&sm.n_rows, 1)] = make_int2(pos, key_finite(key) ? idx : -1);
-          }
+#pragma unroll
+      for (int u = 0; u < kLoad; ++u) {
+        const int c = c0 + u * kStepThreads;
+        if (c < C) {
+          sm.u.ck[c] = (static_cast<uint64_t>(static_cast<uint32_t>(v[u].x)) << 32) |
+                       static_cast<uint32_t>(~v[u].y);
         }
       }
     }
     __syncthreads();
-    n_rows = sm.n_rows;
-    if (tid < o1 - f0) sm.win[n_rows + tid] = make_int2(f0 + tid, -1);
-    n_rows += max(0, o1 - f0);
+    rank_candidates(sm.rr, sm.u.ck, S, C, sel, part, parts);
   }
   __syncthreads();
-  // indices out, entry sources, then one copy pass over every row
-  const int n_ent = G.n_entries[b];
-  const int64_t out_row = static_cast<int64_t>(d->latent) * 2;
-  int32_t* out_idx = Ly.topk_idx + static_cast<int64_t>(b) * k;
-  uint8_t* out_base = static_cast<uint8_t*>(Ly.out_entries) + static_cast<int64_t>(b) * k * out_row;
-  for (int w = tid; w < n_rows; w += kRankThreads) {
-    const int2 pw = sm.win[w];
-    out_idx[pw.x] = pw.y;
-    const uint8_t* s = nullptr;
-    int kind = entry_source(G, Ly, b, pw.y < 0 ? 0 : pw.y, n_ent, &s);
-    sm.src_kind[w] = reinterpret_cast<uintptr_t>(s) | static_cast<uintptr_t>(kind ? kind : 3);
-  }
-  __syncthreads();
-  copy_rows<kRankThreads, 16>(
-      n_rows,
-      [&](int r) {
-        const uintptr_t sk = sm.src_kind[r];
-        return RowRef{reinterpret_cast<const uint8_t*>(sk & ~static_cast<uintptr_t>(3)),
-                      out_base + sm.win[r].x * out_row, static_cast<int>(sk & 3)};
-      },
-      d->latent, Ly.format == SKV_FMT_FP8, d);
+  finish_rows(sm.rr, sm.rr.n_rows, max(o0, sel), o1, d, Ly, b, L);
 }
 
 }  // namespace skv
@@ -649,7 +798,9 @@ extern "C" int skv_decode_step(const skv_decode_desc* h, const skv_decode_desc* 
       h->window <= 0) {
     return set_error(SKV_EINVAL, "%s: latent/c_indexer must be multiples of 8 in range and window > 0", what);
   }
-  if (!h->tok_lens || !h->status) return set_error(SKV_EINVAL, "%s: NULL tok_lens/status", what);
+  if (!h->tok_lens || !h->status || !h->step_lens || !h->step_top) {
+    return set_error(SKV_EINVAL, "%s: NULL tok_lens/status/step_lens/step_top", what);
+  }
   for (int g = 0; g < h->n_groups; ++g) {
     const skv_page_group& G = h->groups[g];
     if (!G.free_stack || !G.free_top || !G.block_table || !G.n_entries || G.m <= 0 ||
@@ -700,25 +851,23 @@ extern "C" int skv_decode_step(const skv_decode_desc* h, const skv_decode_desc* 
   const int64_t n_append = static_cast<int64_t>(h->batch) * h->n_layers +
                            static_cast<int64_t>(n_chunks) * h->batch * n_csa;
   const int64_t n_filter = static_cast<int64_t>(n_chunks) * h->batch * n_csa + n_tiles;
-  if (n_append > INT32_MAX || n_filter > INT32_MAX) {
-    return set_error(SKV_EINVAL, "%s: score_stride/out_rows give a grid over 2^31 workgroups", what);
+  if (n_append >= (1 << 24) || n_filter >= (1 << 24)) {
+    return set_error(SKV_EINVAL, "%s: score_stride/out_rows give a grid of 2^24 workgroups or more", what);
   }
   hipStream_t s = static_cast<hipStream_t>(stream);
-  hipLaunchKernelGGL(k_decode_plan, dim3(1), dim3(kPlanThreads), 0, s, dd);
+  hipLaunchKernelGGL(k_decode_append, dim3(static_cast<unsigned>(n_append)), dim3(kStepThreads), 0, s, dd,
+                     n_chunks);
   int rc = check_launch(what);
   if (rc) return rc;
-  hipLaunchKernelGGL(k_decode_append, dim3(static_cast<unsigned>(n_append)), dim3(kAppendThreads), 0, s,
-                     dd, n_chunks);
-  if ((rc = check_launch(what))) return rc;
-  hipLaunchKernelGGL(k_decode_filter, dim3(static_cast<unsigned>(n_filter)), dim3(kTkPartThreads), 0, s,
-                     dd, n_chunks, n_csa);
+  hipLaunchKernelGGL(k_decode_filter, dim3(static_cast<unsigned>(n_filter)), dim3(kStepThreads), 0, s, dd,
+                     n_chunks, n_csa);
   if ((rc = check_launch(what))) return rc;
   if (n_csa > 0) {
     // smaller parts when the rows alone would leave most CUs idle
     const int rank_out = (static_cast<int64_t>(h->batch) * n_csa * ceil_div(max_top_k, kRankOut) < 512)
                              ? kRankOutMin : kRankOut;
     const dim3 rgrid(static_cast<unsigned>(ceil_div(max_top_k, rank_out)), h->batch, n_csa);
-    hipLaunchKernelGGL(k_decode_topk_rank, rgrid, dim3(kRankThreads), 0, s, dd, rank_out);
+    hipLaunchKernelGGL(k_decode_topk_rank, rgrid, dim3(kStepThreads), 0, s, dd, rank_out);
   }
   return check_launch(what);
 }

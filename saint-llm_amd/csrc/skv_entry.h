@@ -16,10 +16,7 @@ namespace skv {
 __device__ __forceinline__ u32x4 pack8_bf16(const float* f) {
   u32x4 v;
 #pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    v[q] = static_cast<uint32_t>(f32_to_bf16(f[2 * q])) |
-           (static_cast<uint32_t>(f32_to_bf16(f[2 * q + 1])) << 16);
-  }
+  for (int q = 0; q < 4; ++q) v[q] = bf16_pack2(f[2 * q], f[2 * q + 1]);
   return v;
 }
 
@@ -48,14 +45,12 @@ __device__ __forceinline__ void store_entry_group(uint8_t* entry, const float* v
 #pragma unroll
     for (int d = 1; d < 16; d <<= 1) amax = fmaxf(amax, __shfl_xor(amax, d, 16));
     const float scale = fmaxf(amax / kE4M3Max, kF32Tiny);
-    u32x2 codes;
-    codes[0] = 0u;
-    codes[1] = 0u;
+    float q[8];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const float q = fminf(fmaxf(v[j] / scale, -kE4M3Max), kE4M3Max);
-      codes[j >> 2] |= static_cast<uint32_t>(f32_to_e4m3fn(q)) << (8 * (j & 3));
-    }
+    for (int j = 0; j < 8; ++j) q[j] = fminf(fmaxf(v[j] / scale, -kE4M3Max), kE4M3Max);
+    u32x2 codes;
+    codes[0] = e4m3fn_pack2<true>(q[2], q[3], e4m3fn_pack2<false>(q[0], q[1], 0u));
+    codes[1] = e4m3fn_pack2<true>(q[6], q[7], e4m3fn_pack2<false>(q[4], q[5], 0u));
     *reinterpret_cast<u32x2*>(entry + grp * 8) = codes;
     if ((grp & 15) == 0) *reinterpret_cast<float*>(entry + fp8_main + (grp >> 4) * 4) = scale;
   } else if (grp < groups) {

@@ -96,10 +96,9 @@ __device__ __forceinline__ void state_emit_entry(const PoolState& st, uint8_t* e
     // every lane takes part in the fp8 shuffles; only lanes with a group store
     float out[8];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const float r = (grp < groups) ? st.acc[g][j] / st.sum[g][j] : 0.f;
-      out[j] = bf16_to_f32(f32_to_bf16(r));  // the compressor emits bf16 entries
-    }
+    for (int j = 0; j < 8; ++j) out[j] = (grp < groups) ? st.acc[g][j] / st.sum[g][j] : 0.f;
+#pragma unroll
+    for (int j = 0; j < 8; j += 2) bf16_round2(out[j], out[j + 1]);  // the compressor emits bf16 entries
     store_entry_group(entry, out, grp, groups, format, fp8_main);
   }
 }

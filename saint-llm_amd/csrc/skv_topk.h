@@ -222,9 +222,11 @@ __device__ __forceinline__ void topk_hist_chunk(TopkHistSmem& sm, const float* r
 
 // Threshold bin of rank sel from the row histogram (every thread gets it).
 // hist[] is the histogram staged in LDS; nthreads * per == kTkBins.
+// total (optional): the histogram's sum; when it is below sel no bin holds
+// rank sel and t / above / ties are undefined.
 template <int kThreads>
 __device__ __forceinline__ void topk_threshold(const int* hist, int sel, int* scan_lds, int* sh,
-                                               int& t, int& above, int& ties) {
+                                               int& t, int& above, int& ties, int* total = nullptr) {
   constexpr int per = kTkBins / kThreads;
   const int tid = threadIdx.x;
   const int hi = kTkBins - 1 - tid * per;  // this thread's bins: hi, hi-1, ..., hi-per+1
@@ -237,6 +239,7 @@ __device__ __forceinline__ void topk_threshold(const int* hist, int sel, int* sc
   }
   int tot;
   int ex = block_exclusive_scan(sum, scan_lds, &tot);  // keys in bins > hi
+  if (total) *total = tot;
 #pragma unroll
   for (int q = 0; q < per; ++q) {
     if (ex < sel && sel <= ex + v[q]) {

@@ -165,14 +165,13 @@ __global__ __launch_bounds__(kGatherThreads) void k_topk_gather(TopkGatherArgs a
         const float scale = *reinterpret_cast<const float*>(src + a.fp8_main + (c >> 3) * 4);
         float f[16];
 #pragma unroll
-        for (int q = 0; q < 16; ++q) {
-          const uint8_t code = static_cast<uint8_t>(codes[q >> 2] >> (8 * (q & 3)));
-          f[q] = e4m3fn_to_f32(code) * scale;
-        }
+        for (int q = 0; q < 4; ++q) e4m3fn_x4_to_f32(codes[q], f + 4 * q);
+#pragma unroll
+        for (int q = 0; q < 16; ++q) f[q] *= scale;
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-          o0[q] = f32_to_bf16(f[2 * q]) | (static_cast<uint32_t>(f32_to_bf16(f[2 * q + 1])) << 16);
-          o1[q] = f32_to_bf16(f[8 + 2 * q]) | (static_cast<uint32_t>(f32_to_bf16(f[8 + 2 * q + 1])) << 16);
+          o0[q] = bf16_pack2(f[2 * q], f[2 * q + 1]);
+          o1[q] = bf16_pack2(f[8 + 2 * q], f[8 + 2 * q + 1]);
         }
       }
       st_stream(reinterpret_cast<u32x4*>(orow) + 2 * c, o0);

@@ -11,7 +11,7 @@
 * per CSA layer the indexer stream (bf16 entries, same pages).
 
 ``step()`` runs one decode step for every sequence through the fused C-ABI
-entry point ``skv_decode_step`` (four launches).  The per-step inputs live in
+entry point ``skv_decode_step`` (three launches).  The per-step inputs live in
 fixed device buffers (``inputs``), so a sequence of steps can be captured in a
 HIP graph and replayed.
 
@@ -61,7 +61,7 @@ class DecodeDescC(ctypes.Structure):
     _fields_ = [
         ("batch", ctypes.c_int32), ("n_layers", ctypes.c_int32), ("n_groups", ctypes.c_int32),
         ("latent", ctypes.c_int32), ("c_indexer", ctypes.c_int32), ("window", ctypes.c_int32),
-        ("tok_lens", _P), ("status", _P),
+        ("tok_lens", _P), ("status", _P), ("step_lens", _P), ("step_top", _P),
         ("groups", PageGroupC * MAX_GROUPS), ("layers", DecodeLayerC * MAX_LAYERS),
     ]
 
@@ -97,13 +97,18 @@ class _Group:
 
 
 class DecodeCache:
-    """Paged heterogeneous cache of ``batch`` ragged sequences on one GPU."""
+    """Paged heterogeneous cache of ``batch`` ragged sequences on one GPU.
+
+    ``score_cols`` sets the width of each CSA layer's indexer-score buffer
+    (default ``max_len // m`` rounded up to a multiple of 4); the step reads
+    only the first ``L // m`` columns of a row.
+    """
 
     def __init__(self, layers: list[LayerSpec], batch: int, max_len: int, *,
                  latent: int = 576, c_indexer: int = 128, window: int = 128,
                  block_size: int = 64, device: torch.device | str | None = None,
                  page_order_seed: int | None = 0, pages_per_group: dict[int, int] | None = None,
-                 hca_out_rows: int | None = None) -> None:
+                 hca_out_rows: int | None = None, score_cols: int | None = None) -> None:
         if not 0 < len(layers) <= MAX_LAYERS:
             raise ValueError(f"1..{MAX_LAYERS} layers supported; got {len(layers)}")
         if not 0 < batch <= MAX_BATCH:
@@ -121,6 +126,8 @@ class DecodeCache:
         self.latent, self.c_indexer, self.window, self.block_size = latent, c_indexer, window, block_size
         self.tok_lens = torch.zeros(batch, dtype=torch.int32, device=dev)
         self.status = torch.zeros(1, dtype=torch.int32, device=dev)
+        self.step_lens = torch.zeros(batch, dtype=torch.int32, device=dev)
+        self.step_top = torch.zeros(MAX_GROUPS, dtype=torch.int32, device=dev)
         self.host_lens = np.zeros(batch, dtype=np.int64)
 
         # page groups: one per compression rate
@@ -176,7 +183,11 @@ class DecodeCache:
                         ibias = torch.zeros(spec.m, c_indexer, dtype=torch.float32, device=dev)
                         inp["ci"] = torch.zeros(batch, c_indexer, dtype=bf, device=dev)
                         inp["zi"] = torch.zeros(batch, c_indexer, dtype=bf, device=dev)
-                    sc = torch.zeros(batch, max(1, max_len // spec.m), dtype=torch.float32, device=dev)
+                    # default width rounded up to 4 columns (16-byte rows)
+                    cols = -(-max(1, max_len // spec.m) // 4) * 4 if score_cols is None else int(score_cols)
+                    if cols < max_len // spec.m:
+                        raise ValueError(f"score_cols must be >= max_len // m = {max_len // spec.m}")
+                    sc = torch.zeros(batch, cols, dtype=torch.float32, device=dev)
                     tk = torch.full((batch, spec.top_k), -1, dtype=torch.int32, device=dev)
                     ws = ops.topk_workspace(batch, dev)
                     oe = torch.zeros(batch, spec.top_k, latent, dtype=bf, device=dev)
@@ -202,6 +213,7 @@ class DecodeCache:
         d.batch, d.n_layers, d.n_groups = self.batch, len(self.layers), len(self.groups)
         d.latent, d.c_indexer, d.window = self.latent, self.c_indexer, self.window
         d.tok_lens, d.status = self.tok_lens.data_ptr(), self.status.data_ptr()
+        d.step_lens, d.step_top = self.step_lens.data_ptr(), self.step_top.data_ptr()
         for i, g in enumerate(self.groups):
             G = d.groups[i]
             G.free_stack, G.free_top, G.n_pages = g.free_stack.data_ptr(), g.free_top.data_ptr(), g.n_pages

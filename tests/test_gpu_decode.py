@@ -86,14 +86,21 @@ def _rand_data(g, specs, B, T, C, CI):
     return out
 
 
-def test_decode_step_matches_oracle(dev) -> None:
+# score_cols: default width, or a wider buffer whose extra columns are NaN
+# (the step must read only the first L // m columns of a row)
+@pytest.mark.parametrize("score_cols", [None, 17412])
+def test_decode_step_matches_oracle(dev, score_cols) -> None:
     from saint_kv.decode import DecodeCache, LayerSpec
 
     specs = [LayerSpec("csa", m=4, top_k=64, fp8=True), LayerSpec("csa", m=4, top_k=64),
              LayerSpec("hca", m=128), LayerSpec("swa")]
     B, max_len, bs, W, C, CI = 5, 2048, 16, 32, 576, 128
     seed = 3
-    cache = DecodeCache(specs, B, max_len, block_size=bs, window=W, device=dev, page_order_seed=seed)
+    cache = DecodeCache(specs, B, max_len, block_size=bs, window=W, device=dev, page_order_seed=seed,
+                        score_cols=score_cols)
+    for sc in cache.scores:
+        if sc is not None:
+            sc.fill_(float("nan"))  # columns past max_len // m must never be read
     orc = _Oracle(cache, specs, seed)
     g = torch.Generator().manual_seed(seed)
     bias = [None if s.kind == "swa" else torch.randn(s.m, C, generator=g) for s in specs]
@@ -117,7 +124,7 @@ def test_decode_step_matches_oracle(dev) -> None:
             for k, v in data[i].items():
                 cache.inputs[i][k].copy_(v[:, 0])
             if scores[i] is not None:
-                cache.scores[i].copy_(scores[i])
+                cache.scores[i][:, :scores[i].shape[1]].copy_(scores[i])
         cache.step()
         orc.append(np.ones(B, dtype=np.int32), data, bias, ibias)
         torch.cuda.synchronize()
@@ -264,18 +271,20 @@ def _check_csa_outputs(cache, i, scores, ctx):
     assert torch.equal(cache.out_entries[i].cpu(), exp_out), ctx
 
 
-def test_decode_topk_rank_cases(dev) -> None:
+@pytest.mark.parametrize("max_len", [20480, 70000])
+def test_decode_topk_rank_cases(dev, max_len) -> None:
     """Sparse selection of the decode step over score patterns that exercise
     every path of the rank step: sure and tie candidates, exact duplicates,
     sel < top_k fills across several parts, an empty row, non-finite scores,
-    and tie bins over the list capacity (the full-select fallback)."""
+    and tie bins over the list capacity (the full-select fallback), at score
+    rows of 5120 and 17500 columns."""
     from saint_kv.decode import DecodeCache, LayerSpec
 
     specs = [LayerSpec("csa", m=4, top_k=300), LayerSpec("csa", m=4, top_k=50, fp8=True)]
-    B, max_len = 4, 20480
+    B = 4
     cache = DecodeCache(specs, B, max_len, block_size=64, window=16, device=dev, page_order_seed=5)
     gen = torch.Generator(device=dev).manual_seed(5)
-    cache.prefill(np.array([2, 900, 17000, 20000]), generator=gen)
+    cache.prefill(np.array([2, 900, 17000, max_len - 480]), generator=gen)
     g = torch.Generator().manual_seed(5)
     patterns = ["normal", "const", "dup", "sparse", "nonfinite", "const_neg", "normal"]
     for step, pat in enumerate(patterns):
@@ -303,7 +312,7 @@ def test_decode_topk_rank_cases(dev) -> None:
                 sc[:, 9:90:4] = float("-inf")
                 sc[2, :] = float("-inf")
             scores.append(sc)
-            cache.scores[len(scores) - 1].copy_(sc)
+            cache.scores[len(scores) - 1][:, :sc.shape[1]].copy_(sc)
         cache.step()
         torch.cuda.synchronize()
         cache.check_status()
@@ -339,8 +348,10 @@ def test_decode_refused_step_changes_nothing(dev) -> None:
         bufs = [cache.tok_lens]
         for grp in cache.groups:
             bufs += [grp.block_table, grp.n_entries, grp.free_top, grp.free_stack]
+        # (topk_ws is scratch: the step leaves its histogram and counters ready
+        # for the next step, whatever they held before)
         for lst in (cache.ring, cache.pool, cache.state, cache.idx_pool, cache.idx_state,
-                    cache.topk_idx, cache.out_entries, cache.out_window, cache.topk_ws):
+                    cache.topk_idx, cache.out_entries, cache.out_window):
             bufs += [t for t in lst if t is not None]
         return [t.clone() for t in bufs]
 
@@ -356,3 +367,9 @@ def test_decode_refused_step_changes_nothing(dev) -> None:
     with pytest.raises(RuntimeError, match="refused"):
         cache.check_status()
     assert cache.host_lens.tolist() == [67, 13]
+    # a sequence that needs no page can still step once the other one finishes
+    cache.release(np.array([True, False]))
+    fill()
+    cache.step()
+    cache.check_status()
+    assert cache.tok_lens.tolist() == [1, 14]
