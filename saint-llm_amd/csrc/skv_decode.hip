@@ -203,19 +203,52 @@ __device__ __forceinline__ OwnPlan step_plan(PlanSmem& sm, const skv_decode_desc
 //    then                            : top-k histogram chunks.
 // ---------------------------------------------------------------------------
 
+// Raw inputs of one 8-channel group of a stream: running state (max, sum,
+// acc) and the token's c and z.  They depend on the sequence only, so the
+// append launch issues them before the step plan.
+struct FoldIn {
+  u32x4 m0, m1, s0, s1, a0, a1, cv, zv;
+};
+
+__device__ __forceinline__ void fold_load(FoldIn& in, const float* state, const void* c_all, const void* z_all,
+                                          int b, int channels, int grp) {
+  const float* sbase = state + static_cast<int64_t>(b) * 3 * channels;
+  const u32x4* sp = reinterpret_cast<const u32x4*>(sbase + grp * 8);
+  const u32x4* ss = reinterpret_cast<const u32x4*>(sbase + channels + grp * 8);
+  const u32x4* sa = reinterpret_cast<const u32x4*>(sbase + 2 * channels + grp * 8);
+  in.m0 = sp[0];
+  in.m1 = sp[1];
+  in.s0 = ss[0];
+  in.s1 = ss[1];
+  in.a0 = sa[0];
+  in.a1 = sa[1];
+  in.cv = *reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(c_all) + static_cast<int64_t>(b) * channels + grp * 8);
+  in.zv = *reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(z_all) + static_cast<int64_t>(b) * channels + grp * 8);
+}
+
+// Where an emitted entry goes: slot `in_page` of page `page` (checked against
+// n_pages only when the entry is stored, so that the page's load overlaps
+// the fold).
+struct EmitSlot {
+  uint8_t* pool;
+  int64_t row_bytes;
+  int32_t page;
+  int32_t n_pages;
+  int32_t block_size;
+  int32_t in_page;
+};
+
 // Fold the token into the running state of channel groups t, t + nt (8
-// channels each) of one stream and write the entry at `entry` (when not
-// null) if the token completes the block.  All threads t in [0, nt) of a
-// stream must call it (fp8 amax shuffles span the 16 lanes of a 128-channel
-// block, which nt = 128 keeps inside a wave).  Every load is issued before
-// the arithmetic.
-__device__ __forceinline__ void decode_fold_part(int m, int b, int64_t p, uint8_t* entry, float* state,
+// channels each) of one stream and store the entry at `slot` if the token
+// completes the block.  All threads t in [0, nt) of a stream must call it
+// (fp8 amax shuffles span the 16 lanes of a 128-channel block, which
+// nt = 128 keeps inside a wave).  `first` holds the inputs of group t.
+__device__ __forceinline__ void decode_fold_part(int m, int b, int64_t p, const EmitSlot& slot, float* state,
                                                  const float* bias, const void* c_all, const void* z_all,
-                                                 int channels, int format, int fp8_main, int t, int nt) {
+                                                 int channels, int format, int fp8_main, int t, int nt,
+                                                 const FoldIn& first) {
   const int groups = channels >> 3;
   float* sbase = state + static_cast<int64_t>(b) * 3 * channels;
-  const uint16_t* crow = static_cast<const uint16_t*>(c_all) + static_cast<int64_t>(b) * channels;
-  const uint16_t* zrow = static_cast<const uint16_t*>(z_all) + static_cast<int64_t>(b) * channels;
   const uint32_t pm = umod24(static_cast<uint32_t>(p), m);  // p < 2^24
   const float* brow = bias + pm * channels;
   const bool fresh = pm == 0;
@@ -223,28 +256,24 @@ __device__ __forceinline__ void decode_fold_part(int m, int b, int64_t p, uint8_
   for (int grp0 = t; grp0 < ((groups + nt - 1) / nt) * nt; grp0 += nt) {
     const bool mine = grp0 < groups;
     const int grp = mine ? grp0 : groups - 1;  // in-range address for every lane
-    const u32x4* sp = reinterpret_cast<const u32x4*>(sbase + grp * 8);
-    const u32x4* ss = reinterpret_cast<const u32x4*>(sbase + channels + grp * 8);
-    const u32x4* sa = reinterpret_cast<const u32x4*>(sbase + 2 * channels + grp * 8);
-    const u32x4 m0 = sp[0], m1 = sp[1], s0 = ss[0], s1 = ss[1], a0 = sa[0], a1 = sa[1];
-    const u32x4 cv = *reinterpret_cast<const u32x4*>(crow + grp * 8);
-    const u32x4 zv = *reinterpret_cast<const u32x4*>(zrow + grp * 8);
+    FoldIn in = first;
+    if (grp0 != t) fold_load(in, state, c_all, z_all, b, channels, grp);
     const u32x4 b0 = *reinterpret_cast<const u32x4*>(brow + grp * 8);
     const u32x4 b1 = *(reinterpret_cast<const u32x4*>(brow + grp * 8) + 1);
     float mx[8], sum[8], acc[8], c[8], z[8], bb[8];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      mx[j] = fresh ? -INFINITY : __uint_as_float(m0[j]);
-      mx[j + 4] = fresh ? -INFINITY : __uint_as_float(m1[j]);
-      sum[j] = fresh ? 0.f : __uint_as_float(s0[j]);
-      sum[j + 4] = fresh ? 0.f : __uint_as_float(s1[j]);
-      acc[j] = fresh ? 0.f : __uint_as_float(a0[j]);
-      acc[j + 4] = fresh ? 0.f : __uint_as_float(a1[j]);
+      mx[j] = fresh ? -INFINITY : __uint_as_float(in.m0[j]);
+      mx[j + 4] = fresh ? -INFINITY : __uint_as_float(in.m1[j]);
+      sum[j] = fresh ? 0.f : __uint_as_float(in.s0[j]);
+      sum[j + 4] = fresh ? 0.f : __uint_as_float(in.s1[j]);
+      acc[j] = fresh ? 0.f : __uint_as_float(in.a0[j]);
+      acc[j + 4] = fresh ? 0.f : __uint_as_float(in.a1[j]);
       bb[j] = __uint_as_float(b0[j]);
       bb[j + 4] = __uint_as_float(b1[j]);
     }
-    unpack8_bf16(cv, c);
-    unpack8_bf16(zv, z);
+    unpack8_bf16(in.cv, c);
+    unpack8_bf16(in.zv, z);
     float out[8];
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
@@ -264,7 +293,10 @@ __device__ __forceinline__ void decode_fold_part(int m, int b, int64_t p, uint8_
 #pragma unroll
     for (int j = 0; j < 8; j += 2) bf16_round2(out[j], out[j + 1]);  // the compressor emits bf16 entries
     if (emit) {
-      if (entry) store_entry_group(entry, out, grp0, groups, format, fp8_main);
+      if (slot.page >= 0 && slot.page < slot.n_pages) {
+        uint8_t* entry = slot.pool + (static_cast<int64_t>(slot.page) * slot.block_size + slot.in_page) * slot.row_bytes;
+        store_entry_group(entry, out, grp0, groups, format, fp8_main);
+      }
     } else if (mine) {
       u32x4* wp = reinterpret_cast<u32x4*>(sbase + grp * 8);
       wp[0] = u32x4{__float_as_uint(mx[0]), __float_as_uint(mx[1]), __float_as_uint(mx[2]), __float_as_uint(mx[3])};
@@ -313,6 +345,17 @@ __global__ __launch_bounds__(kStepThreads) void k_decode_append(const skv_decode
   const int b = static_cast<int>(blockIdx.x) - l * d->batch;
   const skv_decode_layer& Ly = d->layers[l];
   const bool paged = Ly.kind != SKV_LAYER_SWA;
+  const int wave = tid / kWave;
+  // the fold's state and token inputs go out before the plan's loads
+  const bool main_stream = wave < 2;
+  const bool idx_stream = wave == 2 && Ly.kind == SKV_LAYER_CSA && Ly.idx_pool;
+  FoldIn first{};
+  if (paged && (main_stream || idx_stream)) {
+    const int channels = main_stream ? d->latent : d->c_indexer;
+    const int t = main_stream ? tid : tid - 2 * kWave;
+    fold_load(first, main_stream ? Ly.state : Ly.idx_state, main_stream ? Ly.c_new : Ly.ci_new,
+              main_stream ? Ly.z_new : Ly.zi_new, b, channels, min(t, (channels >> 3) - 1));
+  }
   const OwnPlan P = step_plan(sm.plan, d, b, paged ? Ly.group : -1, blockIdx.x == 0);
   if (P.bad) {
     if (blockIdx.x == 0 && tid == 0) *d->status = P.bad;
@@ -322,7 +365,6 @@ __global__ __launch_bounds__(kStepThreads) void k_decode_append(const skv_decode
   const int L0 = d->tok_lens[b];
   const int64_t p = L0;  // position of the new token
   if (l == 0 && tid == 0) d->step_lens[b] = L0 + 1;
-  const int wave = tid / kWave;
   if (wave == 3) {
     const int row_chunks = d->latent >> 3;  // 16-byte chunks of a bf16 row
     const u32x4* src = static_cast<const u32x4*>(Ly.kv_new) + static_cast<int64_t>(b) * row_chunks;
@@ -333,36 +375,34 @@ __global__ __launch_bounds__(kStepThreads) void k_decode_append(const skv_decode
   if (!paged) return;
   const skv_page_group& G = d->groups[Ly.group];
   // the group's first layer records the sequence's new pages in the table
-  bool first = true;
+  bool first_layer = true;
   for (int li = 0; li < l; ++li) {
-    if (d->layers[li].kind != SKV_LAYER_SWA && d->layers[li].group == Ly.group) first = false;
+    if (d->layers[li].kind != SKV_LAYER_SWA && d->layers[li].group == Ly.group) first_layer = false;
   }
-  if (first && tid < P.need) {
+  if (first_layer && tid < P.need) {
     G.block_table[b * G.bt_stride + P.p0 + tid] = G.free_stack[P.top - 1 - P.off - tid];
   }
-  // the page of the entry this token completes, if any
-  uint8_t* entry = nullptr;
-  uint8_t* ientry = nullptr;
+  // the page of the entry this token completes, if any (its load overlaps the fold)
   const uint32_t e1 = udiv24(static_cast<uint32_t>(p + 1), G.m);  // entries after the token
-  if (e1 * G.m == static_cast<uint32_t>(p + 1)) {
-    const uint32_t e = e1 - 1;
-    const int pi = static_cast<int>(udiv24(e, G.block_size));
-    int32_t page = -1;
+  const uint32_t e = e1 > 0 ? e1 - 1 : 0;
+  const int pi = static_cast<int>(udiv24(e, G.block_size));
+  int32_t page = -1;
+  if (e1 * G.m == static_cast<uint32_t>(p + 1)) {  // uniform
     if (pi < P.p0) page = G.block_table[b * G.bt_stride + pi];
     else if (pi - P.p0 < P.need) page = G.free_stack[P.top - 1 - P.off - (pi - P.p0)];
-    if (page >= 0 && page < G.n_pages) {
-      const int64_t slot = static_cast<int64_t>(page) * G.block_size + (e - pi * G.block_size);
-      entry = static_cast<uint8_t*>(Ly.pool) + slot * Ly.entry_bytes;
-      if (Ly.idx_pool) ientry = static_cast<uint8_t*>(Ly.idx_pool) + slot * static_cast<int64_t>(d->c_indexer) * 2;
-    }
   }
-  if (wave < 2) {
+  const int in_page = static_cast<int>(e) - pi * G.block_size;
+  if (main_stream) {
     const int fp8_main = (Ly.format == SKV_FMT_FP8) ? d->latent - SKV_FP8_ROPE_DIMS : 0;
-    decode_fold_part(G.m, b, p, entry, Ly.state, Ly.bias, Ly.c_new, Ly.z_new, d->latent, Ly.format, fp8_main,
-                     tid, 2 * kWave);
-  } else if (Ly.kind == SKV_LAYER_CSA && Ly.idx_pool) {
-    decode_fold_part(G.m, b, p, ientry, Ly.idx_state, Ly.idx_bias, Ly.ci_new, Ly.zi_new, d->c_indexer,
-                     SKV_FMT_BF16, 0, tid - 2 * kWave, kWave);
+    const EmitSlot slot{static_cast<uint8_t*>(Ly.pool), Ly.entry_bytes, page, static_cast<int32_t>(G.n_pages),
+                        G.block_size, in_page};
+    decode_fold_part(G.m, b, p, slot, Ly.state, Ly.bias, Ly.c_new, Ly.z_new, d->latent, Ly.format, fp8_main,
+                     tid, 2 * kWave, first);
+  } else if (idx_stream) {
+    const EmitSlot slot{static_cast<uint8_t*>(Ly.idx_pool), static_cast<int64_t>(d->c_indexer) * 2, page,
+                        static_cast<int32_t>(G.n_pages), G.block_size, in_page};
+    decode_fold_part(G.m, b, p, slot, Ly.idx_state, Ly.idx_bias, Ly.ci_new, Ly.zi_new, d->c_indexer,
+                     SKV_FMT_BF16, 0, tid - 2 * kWave, kWave, first);
   }
 }
 
@@ -468,15 +508,81 @@ __device__ __forceinline__ void copy_rows(int n, RowFn row, int latent, bool fp8
 
 // Source of compressed entry e of sequence b: the row kind (1 bf16, 2 fp8)
 // and its address, or 0 when e is past n_ent or its page is not mapped.
+// The first n_lds entries of the sequence's block-table row may be staged
+// in LDS (bt_lds).
 __device__ __forceinline__ int entry_source(const skv_page_group& G, const skv_decode_layer& Ly, int b, int e,
-                                            int n_ent, const uint8_t** src) {
+                                            int n_ent, const uint8_t** src, const int32_t* bt_lds = nullptr,
+                                            int n_lds = 0) {
   if (e < 0 || e >= n_ent) return 0;
   const int pi = static_cast<int>(udiv24(e, G.block_size));  // e < 2^24
-  const int32_t page = (pi < G.bt_stride) ? G.block_table[b * G.bt_stride + pi] : -1;
+  const int32_t page = (pi < n_lds) ? bt_lds[pi]
+                       : (pi < G.bt_stride) ? G.block_table[b * G.bt_stride + pi] : -1;
   if (page < 0 || page >= G.n_pages) return 0;
   *src = static_cast<const uint8_t*>(Ly.pool) +
          (static_cast<int64_t>(page) * G.block_size + (e - pi * G.block_size)) * Ly.entry_bytes;
   return (Ly.format == SKV_FMT_FP8) ? 2 : 1;
+}
+
+// One compressed-entry output row split over kTPR threads: thread `sub`
+// takes tasks sub, sub + kTPR, ... (a bf16 layer: the row's 16-byte chunks;
+// an fp8 layer: 16-code chunks, each giving two output chunks, then the
+// rope chunks).  Kind 3 rows are written as zeros.  The loads of a share can
+// be issued long before its stores (see the rank launch).
+template <int kU>
+struct EntryShare {
+  u32x4 v[kU];
+  float sc[kU];
+};
+
+template <int kTPR, int kU>
+__device__ __forceinline__ int entry_tasks(int latent, bool fp8) {
+  return fp8 ? ((latent - SKV_FP8_ROPE_DIMS) >> 4) + (SKV_FP8_ROPE_DIMS >> 3) : (latent >> 3);
+}
+
+template <int kTPR, int kU>
+__device__ __forceinline__ void entry_share_load(EntryShare<kU>& sh, const uint8_t* src, int kind, int latent,
+                                                 bool fp8, const u32x4* safe4) {
+  const int sub = threadIdx.x % kTPR;
+  const int n = entry_tasks<kTPR, kU>(latent, fp8);
+  const int fp8_main = latent - SKV_FP8_ROPE_DIMS;
+  const int code_chunks = fp8_main >> 4;
+  const bool live = fp8 ? kind == 2 : kind == 1;
+#pragma unroll
+  for (int u = 0; u < kU; ++u) {
+    const int c = min(sub + u * kTPR, n - 1);
+    const bool is_code = fp8 && c < code_chunks;
+    const uint8_t* p = !fp8 ? src + c * 16
+                            : is_code ? src + c * 16 : src + fp8_main + (fp8_main >> 7) * 4 + (c - code_chunks) * 16;
+    sh.v[u] = ld_stream(live ? reinterpret_cast<const u32x4*>(p) : safe4);
+    sh.sc[u] = *(live && is_code ? reinterpret_cast<const float*>(src + fp8_main + (c >> 3) * 4)
+                                 : reinterpret_cast<const float*>(safe4));
+  }
+}
+
+template <int kTPR, int kU>
+__device__ __forceinline__ void entry_share_store(const EntryShare<kU>& sh, uint8_t* dst, int kind, int latent,
+                                                  bool fp8) {
+  const int sub = threadIdx.x % kTPR;
+  const int n = entry_tasks<kTPR, kU>(latent, fp8);
+  const int fp8_main = latent - SKV_FP8_ROPE_DIMS;
+  const int code_chunks = fp8_main >> 4;
+  u32x4* o = reinterpret_cast<u32x4*>(dst);
+  const u32x4 zero = {0u, 0u, 0u, 0u};
+#pragma unroll
+  for (int u = 0; u < kU; ++u) {
+    const int c = sub + u * kTPR;
+    if (c >= n || kind == 0) continue;
+    if (!fp8) {
+      st_stream(o + c, kind == 1 ? sh.v[u] : zero);
+    } else if (c < code_chunks) {
+      u32x4 o0 = zero, o1 = zero;
+      if (kind == 2) dequant_codes(sh.v[u], sh.sc[u], o0, o1);
+      st_stream(o + 2 * c, o0);
+      st_stream(o + 2 * c + 1, o1);
+    } else {
+      st_stream(o + (fp8_main >> 3) + (c - code_chunks), kind == 2 ? sh.v[u] : zero);
+    }
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -536,7 +642,6 @@ __device__ __forceinline__ void gather_tile(GatherTileSmem& sm, const skv_decode
 
 // Block u of the dense part of the filter launch.
 __device__ __forceinline__ void dense_block(GatherTileSmem& sm, const skv_decode_desc* d, int u) {
-  if (*d->status) return;  // refused step
   const int batch = d->batch;
   for (int l = 0; l < d->n_layers; ++l) {
     const skv_decode_layer& Ly = d->layers[l];
@@ -544,7 +649,8 @@ __device__ __forceinline__ void dense_block(GatherTileSmem& sm, const skv_decode
     if (u < tiles * batch) {
       const int b = static_cast<int>(udiv24(u, tiles));
       const int tile = u - b * tiles;
-      const int L = d->step_lens[b];
+      const int L = d->step_lens[b];  // loaded with the status: one round trip
+      if (*d->status) return;         // refused step
       if (l == 0 && tile == 0 && threadIdx.x == 0) {
         d->tok_lens[b] = L;
         for (int g = 0; g < d->n_groups; ++g) d->groups[g].n_entries[b] = udiv24(L, d->groups[g].m);
@@ -573,8 +679,7 @@ __device__ __forceinline__ void dense_block(GatherTileSmem& sm, const skv_decode
 // ---------------------------------------------------------------------------
 constexpr int kRankOutMin = 16;
 constexpr int kRankOut = 32;
-constexpr int kRankSub = 8;
-constexpr int kRankCands = kStepThreads / kRankSub;  // candidates ranked per round
+constexpr int kRankSub = 8;  // fewest lanes that rank one candidate together
 constexpr int kRankMaxRows = 512;                    // rows one part can collect (checked below)
 
 // Rows a part collects, worst case over top_k and the part size: its sure
@@ -600,30 +705,45 @@ struct RankRows {
   uintptr_t src_kind[kRankMaxRows];  // entry address | row kind (entries are 4-byte aligned)
 };
 
+// Lanes that rank one candidate together: the largest power of two in
+// [8, 64] that still gives every candidate of the round a lane group.
+__device__ __forceinline__ int rank_lanes(int n_mine) {
+  int sub_n = kWave;
+  while (sub_n > kRankSub && sub_n * n_mine > kStepThreads) sub_n >>= 1;
+  return sub_n;
+}
+
+// own_pos (optional): instead of collecting the winners, record for the
+// part's j-th candidate (its sure ones first, then its ties) the output
+// position, or -1 for a tie past the winners.
 __device__ __forceinline__ void rank_candidates(RankRows& rr, const uint64_t* ck, int S, int C, int sel,
-                                                int part, int parts) {
+                                                int part, int parts, int* own_pos = nullptr) {
+  const int n_sure_mine = (part < S) ? static_cast<int>(ceil_div24(S - part, parts)) : 0;
   const int tid = threadIdx.x;
-  const int sub = tid % kRankSub;
 #pragma unroll 1
   for (int cls = 0; cls < 2; ++cls) {
     const int lo = cls ? S : 0;
     const int hi = cls ? C : S;
     const int n_mine = (part < hi - lo) ? static_cast<int>(ceil_div24(hi - lo - part, parts)) : 0;
-    for (int j0 = 0; j0 < n_mine; j0 += kRankCands) {
-      const int j = j0 + tid / kRankSub;
+    const int sub_n = rank_lanes(n_mine);  // uniform
+    const int sub = tid & (sub_n - 1);
+    for (int j0 = 0; j0 < n_mine; j0 += kStepThreads / sub_n) {
+      const int j = j0 + tid / sub_n;
       const bool valid = j < n_mine;
       const uint64_t mine = valid ? ck[lo + part + j * parts] : ~0ull;
       int rank = 0;
 #pragma unroll 8
-      for (int q = lo + sub; q < hi; q += kRankSub) rank += ck[q] > mine;
-      rank += __shfl_xor(rank, 1);
-      rank += __shfl_xor(rank, 2);
-      rank += __shfl_xor(rank, 4);
+      for (int q = lo + sub; q < hi; q += sub_n) rank += ck[q] > mine;
+      for (int o = 1; o < sub_n; o <<= 1) rank += __shfl_xor(rank, o);  // within the lane group
       const int pos = lo + rank;
-      if (valid && sub == 0 && pos < sel) {
-        const uint32_t key = static_cast<uint32_t>(mine >> 32);
-        const int idx = static_cast<int>(~static_cast<uint32_t>(mine));
-        rr.win[atomicAdd(&rr.n_rows, 1)] = make_int2(pos, key_finite(key) ? idx : -1);
+      if (valid && sub == 0) {
+        if (own_pos) {
+          own_pos[(cls ? n_sure_mine : 0) + j] = (pos < sel) ? pos : -1;
+        } else if (pos < sel) {
+          const uint32_t key = static_cast<uint32_t>(mine >> 32);
+          const int idx = static_cast<int>(~static_cast<uint32_t>(mine));
+          rr.win[atomicAdd(&rr.n_rows, 1)] = make_int2(pos, key_finite(key) ? idx : -1);
+        }
       }
     }
   }
@@ -632,7 +752,8 @@ __device__ __forceinline__ void rank_candidates(RankRows& rr, const uint64_t* ck
 // Adds the fills [f0, o1), writes the indices and copies every collected row.
 // n_rows: rows collected so far (read after a barrier by the caller).
 __device__ __forceinline__ void finish_rows(RankRows& rr, int n_rows, int f0, int o1,
-                                            const skv_decode_desc* d, const skv_decode_layer& Ly, int b, int L) {
+                                            const skv_decode_desc* d, const skv_decode_layer& Ly, int b, int L,
+                                            const int32_t* bt_lds, int n_lds) {
   const int tid = threadIdx.x;
   if (tid < o1 - f0) rr.win[n_rows + tid] = make_int2(f0 + tid, -1);
   n_rows += max(0, o1 - f0);
@@ -647,7 +768,7 @@ __device__ __forceinline__ void finish_rows(RankRows& rr, int n_rows, int f0, in
     const int2 pw = rr.win[w];
     out_idx[pw.x] = pw.y;
     const uint8_t* s = nullptr;
-    const int kind = entry_source(G, Ly, b, pw.y < 0 ? 0 : pw.y, n_ent, &s);
+    const int kind = entry_source(G, Ly, b, pw.y < 0 ? 0 : pw.y, n_ent, &s, bt_lds, n_lds);
     rr.src_kind[w] = reinterpret_cast<uintptr_t>(s) | static_cast<uintptr_t>(kind ? kind : 3);
   }
   __syncthreads();
@@ -678,15 +799,16 @@ __global__ __launch_bounds__(kStepThreads) void k_decode_filter(const skv_decode
   int u = blockIdx.x;
   const int n_filter = n_chunks * d->batch * n_csa;
   if (u < n_filter) {
-    if (*d->status) return;  // refused step
     const uint32_t ub = udiv24(u, n_chunks);
     const int chunk = static_cast<int>(u - ub * n_chunks);
     const uint32_t uc = udiv24(ub, d->batch);
     const int b = static_cast<int>(ub - uc * d->batch);
     const skv_decode_layer* Ly = csa_layer(d, static_cast<int>(uc));
     if (!Ly) return;  // uniform over the workgroup
+    const int L = d->step_lens[b];  // loaded with the status: one round trip
+    if (*d->status) return;         // refused step
     int n_cols, n_valid;
-    score_cols(*Ly, d->groups[Ly->group].m, d->step_lens[b], n_cols, n_valid);
+    score_cols(*Ly, d->groups[Ly->group].m, L, n_cols, n_valid);
     topk_filter_chunk(sm.filter, Ly->scores + static_cast<int64_t>(b) * Ly->score_stride, n_cols, n_valid,
                       Ly->top_k, chunk, Ly->topk_ws + static_cast<int64_t>(b) * kTkWsWords);
     return;
@@ -694,9 +816,16 @@ __global__ __launch_bounds__(kStepThreads) void k_decode_filter(const skv_decode
   dense_block(sm.tile, d, u - n_filter);
 }
 
+constexpr int kRankHead = 2 * kStepThreads;  // entries of each candidate list fetched with the counters
+constexpr int kRankBt = 16 * kStepThreads;   // block-table entries of the sequence staged in LDS
+
+constexpr int kRankPf = kStepThreads / 8;  // own candidates whose entries are loaded before ranking
+
 struct RankSmem {
   RankRows rr;
   int cnt[3];  // n_sure, n_tie, tie-overflow flag
+  int own_pos[kRankPf];
+  int32_t bt[kRankBt];
   union {
     uint64_t ck[kTkCand];
     struct {
@@ -706,6 +835,14 @@ struct RankSmem {
   } u;
 };
 
+__device__ __forceinline__ uint64_t order_key(int2 v) {
+  return (static_cast<uint64_t>(static_cast<uint32_t>(v.x)) << 32) | static_cast<uint32_t>(~v.y);
+}
+
+// One memory round trip brings the status, the length, the list counters,
+// the heads of both candidate lists and the sequence's block-table row;
+// longer lists take a second one.  Ranking then runs on LDS, page lookups
+// read the LDS table, and the entry copy is the last round trip.
 __global__ __launch_bounds__(kStepThreads) void k_decode_topk_rank(const skv_decode_desc* __restrict__ d,
                                                                    int rank_out) {
   __shared__ RankSmem sm;
@@ -718,58 +855,114 @@ __global__ __launch_bounds__(kStepThreads) void k_decode_topk_rank(const skv_dec
   if (part >= parts) return;  // the grid is sized for the largest top_k
   const int b = blockIdx.y;
   const int tid = threadIdx.x;
+  const skv_page_group& G = d->groups[Ly.group];
   int32_t* ws = Ly.topk_ws + static_cast<int64_t>(b) * kTkWsWords;
+  const int2* sure_list = reinterpret_cast<const int2*>(ws + kTkWsSure);
+  const int2* tie_list = reinterpret_cast<const int2*>(ws + kTkWsTie);
+  const int32_t* bt_row = G.block_table + static_cast<int64_t>(b) * G.bt_stride;
+  const int n_bt = static_cast<int>(min<int64_t>(G.bt_stride, kRankBt));
+  // every load of the first round trip, unconditional (clamped indices)
+  const int status = *d->status;
+  const int L = d->step_lens[b];
+  const int cnt0 = ws[kTkWsCnt], cnt1 = ws[kTkWsCnt + 1], flag = ws[kTkWsCnt + 2];
+  int2 sh[kRankHead / kStepThreads], th[kRankHead / kStepThreads];
+#pragma unroll
+  for (int u = 0; u < kRankHead / kStepThreads; ++u) {
+    sh[u] = sure_list[tid + u * kStepThreads];
+    th[u] = tie_list[tid + u * kStepThreads];
+  }
+  int32_t btv[kRankBt / kStepThreads];
+#pragma unroll
+  for (int u = 0; u < kRankBt / kStepThreads; ++u) btv[u] = bt_row[min(tid + u * kStepThreads, n_bt - 1)];
   if (part == 0) {
     for (int i = tid; i < kTkBins; i += kStepThreads) ws[kTkWsHist + i] = 0;
   }
-  if (*d->status) return;  // refused step
-  const skv_page_group& G = d->groups[Ly.group];
-  const int L = d->step_lens[b];
+  if (status) return;  // refused step
   int n_cols, n_valid;
   score_cols(Ly, G.m, L, n_cols, n_valid);
   const int sel = topk_sel(k, n_cols, n_valid);
-  if (tid < 3) sm.cnt[tid] = ws[kTkWsCnt + tid];
+#pragma unroll
+  for (int u = 0; u < kRankBt / kStepThreads; ++u) {
+    if (tid + u * kStepThreads < n_bt) sm.bt[tid + u * kStepThreads] = btv[u];
+  }
   if (tid == 0) sm.rr.n_rows = 0;
-  __syncthreads();
   const int o0 = part * rank_out;
   const int o1 = min(k, o0 + rank_out);
-  if (sel > 0 && sm.cnt[2]) {
+  if (sel > 0 && flag) {
     // tie bin over the list capacity: full select of the row, then this part's positions
     topk_row<kStepThreads>(sm.u.f.full, nullptr, Ly.scores + static_cast<int64_t>(b) * Ly.score_stride,
                            n_cols, n_valid, k, sm.u.f.order);
     __syncthreads();
     if (tid < o1 - o0) sm.rr.win[tid] = make_int2(o0 + tid, sm.u.f.order[o0 + tid]);
     __syncthreads();
-    finish_rows(sm.rr, o1 - o0, o1, o1, d, Ly, b, L);
+    finish_rows(sm.rr, o1 - o0, o1, o1, d, Ly, b, L, sm.bt, n_bt);
     return;
   }
   if (sel > 0) {
-    const int S = min(sm.cnt[0], kMaxTopK);
-    const int C = S + min(sm.cnt[1], kTkTieCap);
-    const int2* sure_list = reinterpret_cast<const int2*>(ws + kTkWsSure);
-    const int2* tie_list = reinterpret_cast<const int2*>(ws + kTkWsTie);
-    constexpr int kLoad = 8;  // list loads in flight per thread
-    for (int c0 = tid; c0 < C; c0 += kStepThreads * kLoad) {
-      int2 v[kLoad];
+    const int S = min(cnt0, kMaxTopK);
+    const int T = min(cnt1, kTkTieCap);
+    const int C = S + T;
 #pragma unroll
-      for (int u = 0; u < kLoad; ++u) {
-        const int c = min(c0 + u * kStepThreads, C - 1);  // unconditional: C >= sel > 0
-        v[u] = (c < S ? sure_list : tie_list - S)[c];
-      }
+    for (int u = 0; u < kRankHead / kStepThreads; ++u) {
+      const int c = tid + u * kStepThreads;
+      if (c < S) sm.u.ck[c] = order_key(sh[u]);
+      if (c < T) sm.u.ck[S + c] = order_key(th[u]);
+    }
+    if (S > kRankHead || T > kRankHead) {  // uniform: the rest of the lists
+      constexpr int kLoad = 8;  // list loads in flight per thread
+      for (int c0 = tid; c0 < C; c0 += kStepThreads * kLoad) {
+        int2 v[kLoad];
 #pragma unroll
-      for (int u = 0; u < kLoad; ++u) {
-        const int c = c0 + u * kStepThreads;
-        if (c < C) {
-          sm.u.ck[c] = (static_cast<uint64_t>(static_cast<uint32_t>(v[u].x)) << 32) |
-                       static_cast<uint32_t>(~v[u].y);
+        for (int u = 0; u < kLoad; ++u) {
+          const int c = min(c0 + u * kStepThreads, C - 1);  // unconditional: C >= sel > 0
+          v[u] = (c < S ? sure_list : tie_list - S)[c];
+        }
+#pragma unroll
+        for (int u = 0; u < kLoad; ++u) {
+          const int c = c0 + u * kStepThreads;
+          const bool head = c < S ? c < kRankHead : c - S < kRankHead;
+          if (c < C && !head) sm.u.ck[c] = order_key(v[u]);
         }
       }
     }
     __syncthreads();
+    // a part with at most kRankPf candidates loads their entries first, so
+    // that the loads overlap the ranking; the winners are stored after it
+    const int n_own = ((part < S) ? static_cast<int>(ceil_div24(S - part, parts)) : 0) +
+                      ((part < T) ? static_cast<int>(ceil_div24(T - part, parts)) : 0);
+    constexpr int kPfU = 9;  // 8 threads x 9 tasks cover a 576-channel row (bf16 72 chunks, fp8 40 tasks)
+    const bool fp8 = Ly.format == SKV_FMT_FP8;
+    if (n_own <= kRankPf && entry_tasks<8, kPfU>(d->latent, fp8) <= 8 * kPfU) {  // uniform
+      const int n_sure_mine = (part < S) ? static_cast<int>(ceil_div24(S - part, parts)) : 0;
+      const int r = tid / 8;
+      int pick = -1, kind = 0;
+      const uint8_t* src = nullptr;
+      if (r < n_own) {
+        const int c = (r < n_sure_mine) ? part + r * parts : S + part + (r - n_sure_mine) * parts;
+        const uint64_t v = sm.u.ck[c];
+        pick = key_finite(static_cast<uint32_t>(v >> 32)) ? static_cast<int>(~static_cast<uint32_t>(v)) : -1;
+        kind = entry_source(G, Ly, b, pick < 0 ? 0 : pick, static_cast<int>(udiv24(L, G.m)), &src, sm.bt, n_bt);
+        if (kind == 0) kind = 3;
+      }
+      EntryShare<kPfU> share;
+      entry_share_load<8, kPfU>(share, src, kind, d->latent, fp8, reinterpret_cast<const u32x4*>(d));
+      rank_candidates(sm.rr, sm.u.ck, S, C, sel, part, parts, sm.own_pos);
+      __syncthreads();
+      const int pos = (r < n_own) ? sm.own_pos[r] : -1;
+      if (pos >= 0) {
+        const int64_t out_row = static_cast<int64_t>(d->latent) * 2;
+        if ((tid & 7) == 0) Ly.topk_idx[static_cast<int64_t>(b) * k + pos] = pick;
+        entry_share_store<8, kPfU>(share, static_cast<uint8_t*>(Ly.out_entries) +
+                                              (static_cast<int64_t>(b) * k + pos) * out_row,
+                                   kind, d->latent, fp8);
+      }
+      finish_rows(sm.rr, 0, max(o0, sel), o1, d, Ly, b, L, sm.bt, n_bt);  // the fills
+      return;
+    }
     rank_candidates(sm.rr, sm.u.ck, S, C, sel, part, parts);
   }
   __syncthreads();
-  finish_rows(sm.rr, sm.rr.n_rows, max(o0, sel), o1, d, Ly, b, L);
+  finish_rows(sm.rr, sm.rr.n_rows, max(o0, sel), o1, d, Ly, b, L, sm.bt, n_bt);
 }
 
 }  // namespace skv
