@@ -54,7 +54,9 @@ __device__ __forceinline__ void score_cols(const skv_decode_layer& Ly, int m, in
 //    outcome and its own sequence's pops without waiting for another.
 // ---------------------------------------------------------------------------
 struct PlanSmem {
-  int red[kStepThreads / kWave][2 * SKV_MAX_GROUPS + 1];
+  int bad;
+  int tot[SKV_MAX_GROUPS];  // pages the step pops from each group
+  int pre[SKV_MAX_GROUPS];  // of which for the sequences before this workgroup's
 };
 
 struct OwnPlan {
@@ -65,26 +67,12 @@ struct OwnPlan {
   int need;  // pages sequence b takes
 };
 
-__device__ __forceinline__ int wave_sum(int v) {
-#pragma unroll
-  for (int s = 1; s < kWave; s <<= 1) v += __shfl_xor(v, s);
-  return v;
-}
-
-__device__ __forceinline__ int wave_or(int v) {
-#pragma unroll
-  for (int s = 1; s < kWave; s <<= 1) v |= __shfl_xor(v, s);
-  return v;
-}
-
 // g_own < 0: no group (SWA layer).  write_tops: this workgroup also writes
 // the groups' tops after the step to step_top.
 __device__ __forceinline__ OwnPlan step_plan(PlanSmem& sm, const skv_decode_desc* d, int b, int g_own,
                                              bool write_tops) {
   constexpr int kPerT = kDecodeMaxBatch / kStepThreads;
   const int tid = threadIdx.x;
-  const int lane = tid & (kWave - 1);
-  const int wid = tid / kWave;
   const int batch = d->batch;
   const int ng = d->n_groups;
   OwnPlan P{0, 0, 0, 0, 0};
@@ -102,12 +90,19 @@ __device__ __forceinline__ OwnPlan step_plan(PlanSmem& sm, const skv_decode_desc
   int top[SKV_MAX_GROUPS];
 #pragma unroll
   for (int g = 0; g < SKV_MAX_GROUPS; ++g) top[g] = *d->groups[min(g, ng - 1)].free_top;
+  if (tid == 0) {
+    sm.bad = 0;
+#pragma unroll
+    for (int g = 0; g < SKV_MAX_GROUPS; ++g) {
+      sm.tot[g] = 0;
+      sm.pre[g] = 0;
+    }
+  }
+  __syncthreads();
+  // only sequences that take pages (or are refused) touch the LDS counters
   int bad = 0;
-  int tot[SKV_MAX_GROUPS], pre[SKV_MAX_GROUPS];
 #pragma unroll
   for (int g = 0; g < SKV_MAX_GROUPS; ++g) {
-    tot[g] = 0;
-    pre[g] = 0;
     if (g >= ng) continue;
     const skv_page_group& G = d->groups[g];
     const uint32_t m = static_cast<uint32_t>(G.m);
@@ -130,41 +125,22 @@ __device__ __forceinline__ OwnPlan step_plan(PlanSmem& sm, const skv_decode_desc
       const uint32_t p1 = ceil_div24(target, bs);
       if (p1 > G.bt_stride) bad |= SKV_STATUS_MAX_PAGES;
       const int need = static_cast<int>(p1 - p0);
-      tot[g] += need;
-      if (s < b) pre[g] += need;
+      if (need) {
+        atomicAdd(&sm.tot[g], need);
+        if (s < b) atomicAdd(&sm.pre[g], need);
+      }
     }
   }
-  bad = wave_or(bad);
-#pragma unroll
-  for (int g = 0; g < SKV_MAX_GROUPS; ++g) {
-    tot[g] = wave_sum(tot[g]);
-    pre[g] = wave_sum(pre[g]);
-  }
-  if (lane == 0) {
-    sm.red[wid][0] = bad;
-#pragma unroll
-    for (int g = 0; g < SKV_MAX_GROUPS; ++g) {
-      sm.red[wid][1 + g] = tot[g];
-      sm.red[wid][1 + SKV_MAX_GROUPS + g] = pre[g];
-    }
-  }
+  if (bad) atomicOr(&sm.bad, bad);
   __syncthreads();
-  bad = 0;
+  bad = sm.bad;
+  int tot[SKV_MAX_GROUPS], pre[SKV_MAX_GROUPS];
 #pragma unroll
   for (int g = 0; g < SKV_MAX_GROUPS; ++g) {
-    tot[g] = 0;
-    pre[g] = 0;
+    tot[g] = sm.tot[g];
+    pre[g] = sm.pre[g];
   }
-#pragma unroll
-  for (int w = 0; w < kStepThreads / kWave; ++w) {
-    bad |= sm.red[w][0];
-#pragma unroll
-    for (int g = 0; g < SKV_MAX_GROUPS; ++g) {
-      tot[g] += sm.red[w][1 + g];
-      pre[g] += sm.red[w][1 + SKV_MAX_GROUPS + g];
-    }
-  }
-  __syncthreads();  // sm.red is reused by the caller's union
+  __syncthreads();  // the counters share the caller's LDS union
 #pragma unroll
   for (int g = 0; g < SKV_MAX_GROUPS; ++g) {
     if (g >= ng) continue;
