@@ -350,23 +350,29 @@ class DecodeCache:
             done += n
 
     # -------------------------------------------------- eviction / compaction --
-    def release(self, mask: np.ndarray) -> None:
-        """Finish the sequences with mask[b]: their pages return to the free lists."""
+    def release(self, mask: np.ndarray, mask_dev: torch.Tensor | None = None) -> None:
+        """Finish the sequences with mask[b]: their pages return to the free lists.
+
+        ``mask_dev`` (optional): the same mask already on the device as uint8,
+        so that the call issues no host-to-device copy."""
         mask = np.asarray(mask, dtype=bool)
         if mask.shape != (self.batch,):
             raise ValueError("mask must be [batch]")
         if (mask & (self.host_lens == 0)).any():
             raise RuntimeError("release of a sequence that holds no tokens (double free)")
-        m_dev = torch.as_tensor(mask.astype(np.uint8), device=self.device)
+        m_dev = torch.as_tensor(mask.astype(np.uint8), device=self.device) if mask_dev is None else mask_dev
         for g in self.groups:
             ops.release(g.free_stack, g.free_top, g.block_table, g.n_entries, m_dev,
                         self.block_size, self.status)
         self.tok_lens.masked_fill_(m_dev.bool(), 0)
         self.host_lens[mask] = 0
 
-    def compact(self, workspace: torch.Tensor | None = None) -> list[tuple[int, int]]:
-        """Defragment every page group; returns [(n_live, n_moved)] per group."""
-        out = []
+    def compact(self, workspace: torch.Tensor | None = None, sync: bool = True):
+        """Defragment every page group; returns [(n_live, n_moved)] per group.
+
+        With ``sync=False`` nothing waits for the device: the result is an
+        int32 device tensor [n_groups, 2] holding the same pairs."""
+        info = torch.zeros(len(self.groups), 2, dtype=torch.int32, device=self.device)
         for gi, g in enumerate(self.groups):
             pools = []
             for i, spec in enumerate(self.layers):
@@ -376,11 +382,11 @@ class DecodeCache:
                         pools.append(self.idx_pool[i])
             ws = workspace if workspace is not None and workspace.numel() >= 3 * g.n_pages else \
                 torch.empty(3 * g.n_pages, dtype=torch.int32, device=self.device)
-            info = torch.zeros(2, dtype=torch.int32, device=self.device)
             ops.compact(pools, g.block_table, g.n_entries, self.block_size, g.free_stack,
-                        g.free_top, ws[: 3 * g.n_pages], info)
-            out.append(tuple(int(v) for v in info.cpu()))
-        return out
+                        g.free_top, ws[: 3 * g.n_pages], info[gi])
+        if not sync:
+            return info
+        return [tuple(int(v) for v in row) for row in info.cpu()]
 
 
 class CapturedSteps:
