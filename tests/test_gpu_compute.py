@@ -167,6 +167,71 @@ def test_fp8_quant_append_bit_exact(dev) -> None:
     assert torch.equal(got.cpu(), exp)
 
 
+def _bf16_in_range(lim: float = 448.0) -> torch.Tensor:
+    """Every finite bf16 value x with |x| <= lim (both zeros included)."""
+    bits = torch.arange(0, 1 << 16, dtype=torch.int32).to(torch.int16).view(torch.bfloat16)
+    f = bits.float()
+    return bits[torch.isfinite(f) & (f.abs() <= lim)]
+
+
+def test_fp8_encode_all_bf16_inputs(dev) -> None:
+    """The GPU quantizer over every bf16 value in [-448, 448]: each 128-dim
+    block holds a 448 anchor, so its scale is exactly 1 and every other code
+    is the encoder's direct output (compared with torch's e4m3fn cast)."""
+    from saint_kv import ops
+
+    vals = _bf16_in_range()
+    per_block = 127
+    n_blocks = -(-vals.numel() // per_block)
+    pad = n_blocks * per_block - vals.numel()
+    vals = torch.cat([vals, torch.zeros(pad, dtype=torch.bfloat16)]).view(n_blocks, per_block)
+    blocks = torch.cat([torch.full((n_blocks, 1), 448.0, dtype=torch.bfloat16), vals], dim=1)
+    n_rows = -(-n_blocks // 4)
+    blocks = torch.cat([blocks, torch.zeros(n_rows * 4 - n_blocks, 128, dtype=torch.bfloat16)])
+    x = torch.cat([blocks.view(n_rows, 512), torch.zeros(n_rows, 64, dtype=torch.bfloat16)], dim=1)
+    x = x.view(1, n_rows, 576)
+    bs = 8
+    n_pages = -(-n_rows // bs)
+    stack = torch.empty(n_pages, dtype=torch.int32, device=dev)
+    top = torch.empty(1, dtype=torch.int32, device=dev)
+    ops.free_stack_init(stack, top)
+    bt = torch.full((1, n_pages), -1, dtype=torch.int32, device=dev)
+    lens = torch.zeros(1, dtype=torch.int32, device=dev)
+    ops.reserve(stack, top, bt, lens, n_rows, bs)
+    pool = torch.zeros(n_pages, bs, 656, dtype=torch.uint8, device=dev)
+    ops.fp8_quant_append(pool, bt, lens, x.to(dev), n_rows)
+    got = torch.zeros(1, n_rows, 656, dtype=torch.uint8, device=dev)
+    ops.paged_gather(pool, bt, lens, got)
+    exp = ref.fp8_pack_entries(x.reshape(-1, 576)).reshape(1, n_rows, 656)
+    assert torch.equal(got.cpu(), exp)
+
+
+def test_fp8_decode_all_codes(dev) -> None:
+    """The GPU dequantizing gather over all 256 e4m3fn codes, at scale 1 and
+    at a scale that exercises the product's rounding to bf16 (NaN codes:
+    NaN out, payload aside)."""
+    from saint_kv import ops
+
+    codes = torch.arange(256, dtype=torch.int32).to(torch.uint8)
+    main = torch.cat([codes, codes.flip(0)])  # 512 codes: 4 blocks of 128
+    entries = []
+    for scale in (1.0, 0.3719):
+        sc = torch.full((4,), scale, dtype=torch.float32)
+        rope = torch.randn(64, generator=torch.Generator().manual_seed(1)).to(torch.bfloat16)
+        entries.append(torch.cat([main, sc.view(torch.uint8), rope.view(torch.uint8)]))
+    pool = torch.stack(entries).view(1, 2, 656).to(dev)
+    bt = torch.zeros(1, 1, dtype=torch.int32, device=dev)
+    n_ent = torch.full((1,), 2, dtype=torch.int32, device=dev)
+    idx = torch.tensor([[0, 1]], dtype=torch.int32, device=dev)
+    out = torch.zeros(1, 2, 576, dtype=torch.bfloat16, device=dev)
+    ops.topk_gather(pool, bt, n_ent, idx, out, 576)
+    exp = ref.fp8_unpack_entries(torch.stack(entries))
+    got = out.cpu()[0]
+    nan = torch.isnan(exp)
+    assert torch.equal(torch.isnan(got), nan)
+    assert torch.equal(got[~nan].view(torch.int16), exp[~nan].view(torch.int16))
+
+
 # ------------------------------------------------------------------ top-k ----
 @pytest.mark.parametrize("multi", [False, True])
 @pytest.mark.parametrize("n,k", [(64, 16), (16384, 512), (20000, 1024), (100_000, 1024), (5000, 2048)])
