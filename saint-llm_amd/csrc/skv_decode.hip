@@ -692,8 +692,9 @@ __device__ __forceinline__ int rank_lanes(int n_mine) {
 // own_pos (optional): instead of collecting the winners, record for the
 // part's j-th candidate (its sure ones first, then its ties) the output
 // position, or -1 for a tie past the winners.
-__device__ __forceinline__ void rank_candidates(RankRows& rr, const uint64_t* ck, int S, int C, int sel,
-                                                int part, int parts, int* own_pos = nullptr) {
+template <class KeyAt>
+__device__ __forceinline__ void rank_candidates(RankRows& rr, KeyAt ck, int S, int C, int sel, int part, int parts,
+                                                int* own_pos = nullptr) {
   const int n_sure_mine = (part < S) ? static_cast<int>(ceil_div24(S - part, parts)) : 0;
   const int tid = threadIdx.x;
 #pragma unroll 1
@@ -706,10 +707,10 @@ __device__ __forceinline__ void rank_candidates(RankRows& rr, const uint64_t* ck
     for (int j0 = 0; j0 < n_mine; j0 += kStepThreads / sub_n) {
       const int j = j0 + tid / sub_n;
       const bool valid = j < n_mine;
-      const uint64_t mine = valid ? ck[lo + part + j * parts] : ~0ull;
+      const uint64_t mine = valid ? ck(lo + part + j * parts) : ~0ull;
       int rank = 0;
 #pragma unroll 8
-      for (int q = lo + sub; q < hi; q += sub_n) rank += ck[q] > mine;
+      for (int q = lo + sub; q < hi; q += sub_n) rank += ck(q) > mine;
       for (int o = 1; o < sub_n; o <<= 1) rank += __shfl_xor(rank, o);  // within the lane group
       const int pos = lo + rank;
       if (valid && sub == 0) {
@@ -793,23 +794,28 @@ __global__ __launch_bounds__(kStepThreads) void k_decode_filter(const skv_decode
 }
 
 constexpr int kRankHead = 2 * kStepThreads;  // entries of each candidate list fetched with the counters
-constexpr int kRankBt = 16 * kStepThreads;   // block-table entries of the sequence staged in LDS
+constexpr int kRankBt = 16 * kStepThreads;   // most block-table entries of a sequence staged in LDS
+constexpr int kRankPf = kStepThreads / 8;    // own candidates whose entries are loaded before ranking
 
-constexpr int kRankPf = kStepThreads / 8;  // own candidates whose entries are loaded before ranking
-
-struct RankSmem {
+// Dynamic LDS of the rank launch, sized by the host for the launch's rows:
+//   RankHead | block-table row (bt_lds entries) | candidates (ck_cap order keys)
+//                                                  or the full-select fallback
+struct RankHead {
   RankRows rr;
-  int cnt[3];  // n_sure, n_tie, tie-overflow flag
   int own_pos[kRankPf];
-  int32_t bt[kRankBt];
-  union {
-    uint64_t ck[kTkCand];
-    struct {
-      TopkSmemT<kStepThreads> full;
-      int32_t order[kMaxTopK];
-    } f;
-  } u;
 };
+struct RankFallback {
+  TopkSmemT<kStepThreads> full;
+  int32_t order[kMaxTopK];
+};
+
+__host__ __device__ constexpr int64_t align16(int64_t x) { return (x + 15) & ~static_cast<int64_t>(15); }
+
+__host__ __device__ constexpr int64_t rank_lds_bytes(int bt_lds, int ck_cap) {
+  const int64_t region = static_cast<int64_t>(ck_cap) * 8 > static_cast<int64_t>(sizeof(RankFallback))
+                             ? static_cast<int64_t>(ck_cap) * 8 : static_cast<int64_t>(sizeof(RankFallback));
+  return align16(sizeof(RankHead)) + align16(static_cast<int64_t>(bt_lds) * 4) + region;
+}
 
 __device__ __forceinline__ uint64_t order_key(int2 v) {
   return (static_cast<uint64_t>(static_cast<uint32_t>(v.x)) << 32) | static_cast<uint32_t>(~v.y);
@@ -817,11 +823,17 @@ __device__ __forceinline__ uint64_t order_key(int2 v) {
 
 // One memory round trip brings the status, the length, the list counters,
 // the heads of both candidate lists and the sequence's block-table row;
-// longer lists take a second one.  Ranking then runs on LDS, page lookups
-// read the LDS table, and the entry copy is the last round trip.
+// longer lists take a second one.  Ranking then runs on LDS (or, for lists
+// longer than the launch's LDS holds, on the lists in global memory), page
+// lookups read the LDS table, and the entry copy is the last round trip.
 __global__ __launch_bounds__(kStepThreads) void k_decode_topk_rank(const skv_decode_desc* __restrict__ d,
-                                                                   int rank_out) {
-  __shared__ RankSmem sm;
+                                                                   int rank_out, int bt_lds, int ck_cap) {
+  extern __shared__ __align__(16) uint8_t rank_lds[];
+  RankHead& sm = *reinterpret_cast<RankHead*>(rank_lds);
+  int32_t* sm_bt = reinterpret_cast<int32_t*>(rank_lds + align16(sizeof(RankHead)));
+  uint8_t* region = rank_lds + align16(sizeof(RankHead)) + align16(static_cast<int64_t>(bt_lds) * 4);
+  uint64_t* sm_ck = reinterpret_cast<uint64_t*>(region);
+  RankFallback& fb = *reinterpret_cast<RankFallback*>(region);
   const skv_decode_layer* Lp = csa_layer(d, blockIdx.z);
   if (!Lp) return;
   const skv_decode_layer& Ly = *Lp;
@@ -836,7 +848,7 @@ __global__ __launch_bounds__(kStepThreads) void k_decode_topk_rank(const skv_dec
   const int2* sure_list = reinterpret_cast<const int2*>(ws + kTkWsSure);
   const int2* tie_list = reinterpret_cast<const int2*>(ws + kTkWsTie);
   const int32_t* bt_row = G.block_table + static_cast<int64_t>(b) * G.bt_stride;
-  const int n_bt = static_cast<int>(min<int64_t>(G.bt_stride, kRankBt));
+  const int n_bt = static_cast<int>(min<int64_t>(G.bt_stride, bt_lds));
   // every load of the first round trip, unconditional (clamped indices)
   const int status = *d->status;
   const int L = d->step_lens[b];
@@ -859,70 +871,74 @@ __global__ __launch_bounds__(kStepThreads) void k_decode_topk_rank(const skv_dec
   const int sel = topk_sel(k, n_cols, n_valid);
 #pragma unroll
   for (int u = 0; u < kRankBt / kStepThreads; ++u) {
-    if (tid + u * kStepThreads < n_bt) sm.bt[tid + u * kStepThreads] = btv[u];
+    if (tid + u * kStepThreads < n_bt) sm_bt[tid + u * kStepThreads] = btv[u];
   }
   if (tid == 0) sm.rr.n_rows = 0;
   const int o0 = part * rank_out;
   const int o1 = min(k, o0 + rank_out);
   if (sel > 0 && flag) {
     // tie bin over the list capacity: full select of the row, then this part's positions
-    topk_row<kStepThreads>(sm.u.f.full, nullptr, Ly.scores + static_cast<int64_t>(b) * Ly.score_stride,
-                           n_cols, n_valid, k, sm.u.f.order);
+    topk_row<kStepThreads>(fb.full, nullptr, Ly.scores + static_cast<int64_t>(b) * Ly.score_stride, n_cols,
+                           n_valid, k, fb.order);
     __syncthreads();
-    if (tid < o1 - o0) sm.rr.win[tid] = make_int2(o0 + tid, sm.u.f.order[o0 + tid]);
+    if (tid < o1 - o0) sm.rr.win[tid] = make_int2(o0 + tid, fb.order[o0 + tid]);
     __syncthreads();
-    finish_rows(sm.rr, o1 - o0, o1, o1, d, Ly, b, L, sm.bt, n_bt);
+    finish_rows(sm.rr, o1 - o0, o1, o1, d, Ly, b, L, sm_bt, n_bt);
     return;
   }
   if (sel > 0) {
     const int S = min(cnt0, kMaxTopK);
     const int T = min(cnt1, kTkTieCap);
     const int C = S + T;
+    const bool in_lds = C <= ck_cap;  // uniform
+    if (in_lds) {
 #pragma unroll
-    for (int u = 0; u < kRankHead / kStepThreads; ++u) {
-      const int c = tid + u * kStepThreads;
-      if (c < S) sm.u.ck[c] = order_key(sh[u]);
-      if (c < T) sm.u.ck[S + c] = order_key(th[u]);
-    }
-    if (S > kRankHead || T > kRankHead) {  // uniform: the rest of the lists
-      constexpr int kLoad = 8;  // list loads in flight per thread
-      for (int c0 = tid; c0 < C; c0 += kStepThreads * kLoad) {
-        int2 v[kLoad];
+      for (int u = 0; u < kRankHead / kStepThreads; ++u) {
+        const int c = tid + u * kStepThreads;
+        if (c < S) sm_ck[c] = order_key(sh[u]);
+        if (c < T) sm_ck[S + c] = order_key(th[u]);
+      }
+      if (S > kRankHead || T > kRankHead) {  // uniform: the rest of the lists
+        constexpr int kLoad = 8;  // list loads in flight per thread
+        for (int c0 = tid; c0 < C; c0 += kStepThreads * kLoad) {
+          int2 v[kLoad];
 #pragma unroll
-        for (int u = 0; u < kLoad; ++u) {
-          const int c = min(c0 + u * kStepThreads, C - 1);  // unconditional: C >= sel > 0
-          v[u] = (c < S ? sure_list : tie_list - S)[c];
-        }
+          for (int u = 0; u < kLoad; ++u) {
+            const int c = min(c0 + u * kStepThreads, C - 1);  // unconditional: C >= sel > 0
+            v[u] = (c < S ? sure_list : tie_list - S)[c];
+          }
 #pragma unroll
-        for (int u = 0; u < kLoad; ++u) {
-          const int c = c0 + u * kStepThreads;
-          const bool head = c < S ? c < kRankHead : c - S < kRankHead;
-          if (c < C && !head) sm.u.ck[c] = order_key(v[u]);
+          for (int u = 0; u < kLoad; ++u) {
+            const int c = c0 + u * kStepThreads;
+            const bool head = c < S ? c < kRankHead : c - S < kRankHead;
+            if (c < C && !head) sm_ck[c] = order_key(v[u]);
+          }
         }
       }
     }
     __syncthreads();
+    const auto lds_key = [&](int q) { return sm_ck[q]; };
+    const auto global_key = [&](int q) { return order_key(q < S ? sure_list[q] : tie_list[q - S]); };
     // a part with at most kRankPf candidates loads their entries first, so
     // that the loads overlap the ranking; the winners are stored after it
-    const int n_own = ((part < S) ? static_cast<int>(ceil_div24(S - part, parts)) : 0) +
-                      ((part < T) ? static_cast<int>(ceil_div24(T - part, parts)) : 0);
+    const int n_sure_mine = (part < S) ? static_cast<int>(ceil_div24(S - part, parts)) : 0;
+    const int n_own = n_sure_mine + ((part < T) ? static_cast<int>(ceil_div24(T - part, parts)) : 0);
     constexpr int kPfU = 9;  // 8 threads x 9 tasks cover a 576-channel row (bf16 72 chunks, fp8 40 tasks)
     const bool fp8 = Ly.format == SKV_FMT_FP8;
-    if (n_own <= kRankPf && entry_tasks<8, kPfU>(d->latent, fp8) <= 8 * kPfU) {  // uniform
-      const int n_sure_mine = (part < S) ? static_cast<int>(ceil_div24(S - part, parts)) : 0;
+    if (in_lds && n_own <= kRankPf && entry_tasks<8, kPfU>(d->latent, fp8) <= 8 * kPfU) {  // uniform
       const int r = tid / 8;
       int pick = -1, kind = 0;
       const uint8_t* src = nullptr;
       if (r < n_own) {
         const int c = (r < n_sure_mine) ? part + r * parts : S + part + (r - n_sure_mine) * parts;
-        const uint64_t v = sm.u.ck[c];
+        const uint64_t v = sm_ck[c];
         pick = key_finite(static_cast<uint32_t>(v >> 32)) ? static_cast<int>(~static_cast<uint32_t>(v)) : -1;
-        kind = entry_source(G, Ly, b, pick < 0 ? 0 : pick, static_cast<int>(udiv24(L, G.m)), &src, sm.bt, n_bt);
+        kind = entry_source(G, Ly, b, pick < 0 ? 0 : pick, static_cast<int>(udiv24(L, G.m)), &src, sm_bt, n_bt);
         if (kind == 0) kind = 3;
       }
       EntryShare<kPfU> share;
       entry_share_load<8, kPfU>(share, src, kind, d->latent, fp8, reinterpret_cast<const u32x4*>(d));
-      rank_candidates(sm.rr, sm.u.ck, S, C, sel, part, parts, sm.own_pos);
+      rank_candidates(sm.rr, lds_key, S, C, sel, part, parts, sm.own_pos);
       __syncthreads();
       const int pos = (r < n_own) ? sm.own_pos[r] : -1;
       if (pos >= 0) {
@@ -932,18 +948,43 @@ __global__ __launch_bounds__(kStepThreads) void k_decode_topk_rank(const skv_dec
                                               (static_cast<int64_t>(b) * k + pos) * out_row,
                                    kind, d->latent, fp8);
       }
-      finish_rows(sm.rr, 0, max(o0, sel), o1, d, Ly, b, L, sm.bt, n_bt);  // the fills
+      finish_rows(sm.rr, 0, max(o0, sel), o1, d, Ly, b, L, sm_bt, n_bt);  // the fills
       return;
     }
-    rank_candidates(sm.rr, sm.u.ck, S, C, sel, part, parts);
+    if (in_lds) rank_candidates(sm.rr, lds_key, S, C, sel, part, parts);
+    else rank_candidates(sm.rr, global_key, S, C, sel, part, parts);
   }
   __syncthreads();
-  finish_rows(sm.rr, sm.rr.n_rows, max(o0, sel), o1, d, Ly, b, L, sm.bt, n_bt);
+  finish_rows(sm.rr, sm.rr.n_rows, max(o0, sel), o1, d, Ly, b, L, sm_bt, n_bt);
 }
 
 }  // namespace skv
 
 using namespace skv;
+
+namespace {
+
+constexpr int64_t kLdsPerCu = 160 * 1024;
+
+// Most LDS bytes a rank workgroup may take while a CU still holds as many of
+// them as it does with `lds` bytes each (the register-limited count caps it).
+int64_t rank_lds_budget(int64_t lds) {
+  static const int by_regs = [] {
+    int n = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, k_decode_topk_rank, kStepThreads, 0) != hipSuccess ||
+        n <= 0) {
+      (void)hipGetLastError();
+      n = 1 << 20;
+    }
+    return n;
+  }();
+  int64_t wgs = kLdsPerCu / lds;
+  if (wgs > by_regs) wgs = by_regs;
+  if (wgs < 1) wgs = 1;
+  return kLdsPerCu / wgs;
+}
+
+}  // namespace
 
 extern "C" int skv_decode_desc_sizes(int64_t* out) {
   if (!out) return set_error(SKV_EINVAL, "skv_decode_desc_sizes: out is NULL");
@@ -1036,7 +1077,24 @@ extern "C" int skv_decode_step(const skv_decode_desc* h, const skv_decode_desc* 
     const int rank_out = (static_cast<int64_t>(h->batch) * n_csa * ceil_div(max_top_k, kRankOut) < 512)
                              ? kRankOutMin : kRankOut;
     const dim3 rgrid(static_cast<unsigned>(ceil_div(max_top_k, rank_out)), h->batch, n_csa);
-    hipLaunchKernelGGL(k_decode_topk_rank, rgrid, dim3(kStepThreads), 0, s, dd, rank_out);
+    // LDS sized for this launch: the longest block-table row of a CSA group
+    // (at most kRankBt entries) and at least the candidate lists of rows
+    // whose tie bin holds 2048 keys, grown while the workgroups a CU holds
+    // stay the same; rows with longer lists rank from global memory
+    int64_t bt_lds = 1;
+    for (int l = 0; l < h->n_layers; ++l) {
+      if (h->layers[l].kind == SKV_LAYER_CSA) bt_lds = max(bt_lds, h->groups[h->layers[l].group].bt_stride);
+    }
+    if (bt_lds > kRankBt) bt_lds = kRankBt;
+    const int bt = static_cast<int>(bt_lds);
+    int ck_cap = min(max_top_k + 2048, kTkCand);
+    const int64_t per_wg = rank_lds_budget(rank_lds_bytes(bt, ck_cap));
+    while (ck_cap < kTkCand && rank_lds_bytes(bt, min(ck_cap + 256, kTkCand)) <= per_wg) {
+      ck_cap = min(ck_cap + 256, kTkCand);
+    }
+    const int64_t lds = rank_lds_bytes(bt, ck_cap);
+    hipLaunchKernelGGL(k_decode_topk_rank, rgrid, dim3(kStepThreads), static_cast<size_t>(lds), s, dd, rank_out,
+                       bt, ck_cap);
   }
   return check_launch(what);
 }

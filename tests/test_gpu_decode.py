@@ -276,8 +276,9 @@ def test_decode_topk_rank_cases(dev, max_len) -> None:
     """Sparse selection of the decode step over score patterns that exercise
     every path of the rank step: sure and tie candidates, exact duplicates,
     sel < top_k fills across several parts, an empty row, non-finite scores,
-    and tie bins over the list capacity (the full-select fallback), at score
-    rows of 5120 and 17500 columns."""
+    candidate lists longer than the launch's LDS holds (ranked from global
+    memory) and tie bins over the list capacity (the full-select fallback),
+    at score rows of 5120 and 17500 columns."""
     from saint_kv.decode import DecodeCache, LayerSpec
 
     specs = [LayerSpec("csa", m=4, top_k=300), LayerSpec("csa", m=4, top_k=50, fp8=True)]
@@ -286,7 +287,7 @@ def test_decode_topk_rank_cases(dev, max_len) -> None:
     gen = torch.Generator(device=dev).manual_seed(5)
     cache.prefill(np.array([2, 900, 17000, max_len - 480]), generator=gen)
     g = torch.Generator().manual_seed(5)
-    patterns = ["normal", "const", "dup", "sparse", "nonfinite", "const_neg", "normal"]
+    patterns = ["normal", "const", "dup", "sparse", "nonfinite", "const_neg", "wide", "normal"]
     for step, pat in enumerate(patterns):
         for i in range(len(specs)):
             for v in cache.inputs[i].values():
@@ -305,6 +306,10 @@ def test_decode_topk_rank_cases(dev, max_len) -> None:
                 sc = torch.randint(0, 8, shape, generator=g).float()
             elif pat == "sparse":
                 sc = torch.relu(torch.randn(*shape, generator=g) - 1.3)
+            elif pat == "wide":  # 250 sure keys over one tie bin of 3900
+                sc = torch.full(shape, -1.0)
+                sc[:, :3900] = 0.5 + 0.1 * torch.rand(B, 3900, generator=g)
+                sc[:, 3900:4150] = 10.0 + torch.rand(B, 250, generator=g)
             else:
                 sc = torch.randn(*shape, generator=g)
                 sc[:, 5:40:3] = float("nan")
