@@ -22,18 +22,38 @@ namespace skv {
 
 constexpr int kDecodeMaxBatch = 1024;
 constexpr int kStepThreads = 256;  // every workgroup of the decode step
-constexpr int kGatherRowsD = 8;    // output rows per dense gather tile
+constexpr int kGatherRowsD = 32;   // output rows per dense gather tile
 // Longest sequence the step accepts (longer ones are refused with
 // SKV_STATUS_BADARG): lengths, entry counts, page indices and grid indices
 // stay below 2^24, so the kernels divide with udiv24.
 constexpr int kMaxTokLen = (1 << 24) - (1 << 16);
 static_assert(kTkPartThreads == kStepThreads, "top-k chunk workgroups are step workgroups");
 
-__device__ __forceinline__ const skv_decode_layer* csa_layer(const skv_decode_desc* d, int want) {
-  for (int li = 0; li < d->n_layers; ++li) {
-    if (d->layers[li].kind == SKV_LAYER_CSA && want-- == 0) return &d->layers[li];
-  }
-  return nullptr;
+// Where each workgroup's layer is, passed by value with every launch: kernel
+// arguments come with a workgroup's first scalar loads, so no workgroup
+// walks the descriptor's layer list through dependent loads to find it.
+struct StepMap {
+  int32_t batch;
+  int32_t n_layers;
+  int32_t n_csa;
+  uint32_t hca_mask;                  // bit l: layer l is an HCA layer
+  uint64_t csa;                       // layer of the i-th CSA layer in bits [4i, 4i + 4)
+  int32_t tiles[SKV_MAX_LAYERS];      // dense gather tiles per sequence of each layer
+  int32_t tile_end[SKV_MAX_LAYERS];   // dense workgroups of layers 0..l (tiles x batch, running sum)
+  int8_t group[SKV_MAX_LAYERS];       // page group of an HCA/CSA layer, -1 for an SWA layer
+  const int32_t* step_lens;           // the descriptor's
+  const int32_t* status;
+  const int32_t* block_table[SKV_MAX_GROUPS];  // the groups' (unused groups: bt_stride 1, block_size 1)
+  int32_t bt_stride[SKV_MAX_GROUPS];
+  int32_t block_size[SKV_MAX_GROUPS];
+  int32_t* topk_ws[SKV_MAX_LAYERS];   // of the i-th CSA layer
+};
+static_assert(SKV_MAX_LAYERS <= 16, "CSA layer indices are 4-bit fields");
+
+__device__ __forceinline__ const skv_decode_layer* csa_layer(const skv_decode_desc* d, const StepMap& map,
+                                                             int want) {
+  if (want < 0 || want >= map.n_csa) return nullptr;
+  return &d->layers[(map.csa >> (4 * want)) & 15];
 }
 
 // Score columns of a CSA query at length L (entries L/m; the causal mask
@@ -293,9 +313,9 @@ union AppendSmem {
 };
 
 __global__ __launch_bounds__(kStepThreads) void k_decode_append(const skv_decode_desc* __restrict__ d,
-                                                                int n_chunks) {
+                                                                int n_chunks, StepMap map) {
   __shared__ AppendSmem sm;
-  const int n_append = d->batch * d->n_layers;
+  const int n_append = map.batch * map.n_layers;
   const int tid = threadIdx.x;
   if (static_cast<int>(blockIdx.x) >= n_append) {
     // top-k histogram chunk (chunk, b, csa layer).  It assumes the step
@@ -305,9 +325,9 @@ __global__ __launch_bounds__(kStepThreads) void k_decode_append(const skv_decode
     const uint32_t u = blockIdx.x - n_append;  // grids stay below 2^24 workgroups
     const uint32_t ub = udiv24(u, n_chunks);
     const int chunk = static_cast<int>(u - ub * n_chunks);
-    const uint32_t uc = udiv24(ub, d->batch);
-    const int b = static_cast<int>(ub - uc * d->batch);
-    const skv_decode_layer* Ly = csa_layer(d, static_cast<int>(uc));
+    const uint32_t uc = udiv24(ub, map.batch);
+    const int b = static_cast<int>(ub - uc * map.batch);
+    const skv_decode_layer* Ly = csa_layer(d, map, static_cast<int>(uc));
     if (!Ly) return;
     int32_t* ws = Ly->topk_ws + static_cast<int64_t>(b) * kTkWsWords;
     if (chunk == 0 && tid < 3) ws[kTkWsCnt + tid] = 0;
@@ -317,8 +337,8 @@ __global__ __launch_bounds__(kStepThreads) void k_decode_append(const skv_decode
                     Ly->top_k, chunk, ws);
     return;
   }
-  const int l = static_cast<int>(udiv24(blockIdx.x, d->batch));
-  const int b = static_cast<int>(blockIdx.x) - l * d->batch;
+  const int l = static_cast<int>(udiv24(blockIdx.x, map.batch));
+  const int b = static_cast<int>(blockIdx.x) - l * map.batch;
   const skv_decode_layer& Ly = d->layers[l];
   const bool paged = Ly.kind != SKV_LAYER_SWA;
   const int wave = tid / kWave;
@@ -564,81 +584,80 @@ __device__ __forceinline__ void entry_share_store(const EntryShare<kU>& sh, uint
 // ---------------------------------------------------------------------------
 // 3. dense gather tiles (HCA entries and SWA windows) and the commit of the
 //    step: the filter launch ends its grid with these blocks.
-//    Tile t of (layer, sequence) copies rows [8t, 8t+8) of the layer's dense
-//    row space [HCA entries (out_rows) | window].  Tile 0 of (layer 0, b)
-//    commits the step's length of b (tokens and entry counts), tile 0 of
-//    (layer 0, 0) the free-stack tops; nothing in these launches reads them.
+//    Tile t of (layer, sequence) copies rows [32t, 32t+32) of the layer's
+//    dense row space [HCA entries (out_rows) | window], kDenseTPR threads
+//    per row.  Each thread loads its row's block-table entry together with
+//    the length and the status (one round trip), then the row.  Tile 0 of
+//    (layer 0, b) commits the step's length of b (tokens and entry counts),
+//    tile 0 of (layer 0, 0) the free-stack tops; nothing in these launches
+//    reads them.
 // ---------------------------------------------------------------------------
-struct GatherTileSmem {
-  const uint8_t* src_row[kGatherRowsD];
-  uint8_t* dst_row[kGatherRowsD];
-  int row_kind[kGatherRowsD];
-};
-
-__device__ __forceinline__ int dense_rows(const skv_decode_desc* d, const skv_decode_layer& Ly) {
-  return d->window + (Ly.kind == SKV_LAYER_HCA ? static_cast<int>(Ly.out_rows) : 0);
-}
-
-__device__ __forceinline__ void gather_tile(GatherTileSmem& sm, const skv_decode_desc* d,
-                                            const skv_decode_layer& Ly, int b, int tile, int L) {
-  const int latent = d->latent;
-  const int64_t out_row = static_cast<int64_t>(latent) * 2;
-  const int n_dense = (Ly.kind == SKV_LAYER_HCA) ? static_cast<int>(Ly.out_rows) : 0;
-  const int n_rows = n_dense + d->window;
-  const int r0 = tile * kGatherRowsD;
-  if (threadIdx.x < kGatherRowsD) {
-    const int r = r0 + threadIdx.x;
-    int kind = 0;
-    const uint8_t* s = nullptr;
-    uint8_t* o = nullptr;
-    if (r < n_dense) {
-      // dense HCA rows past the entries stay untouched
-      const skv_page_group& G = d->groups[Ly.group];
-      kind = entry_source(G, Ly, b, r, static_cast<int>(udiv24(L, G.m)), &s);
-      o = static_cast<uint8_t*>(Ly.out_entries) + (static_cast<int64_t>(b) * Ly.out_rows + r) * out_row;
-    } else if (r < n_rows) {
-      const int w = r - n_dense;
-      const int cnt = min(max(L, 0), d->window);
-      if (w < cnt) {
-        const int64_t slot = umod24(static_cast<uint32_t>(L - cnt + w), d->window);
-        s = static_cast<const uint8_t*>(Ly.ring) + (static_cast<int64_t>(b) * d->window + slot) * out_row;
-        o = static_cast<uint8_t*>(Ly.out_window) + (static_cast<int64_t>(b) * d->window + w) * out_row;
-        kind = 1;
-      }
-    }
-    sm.src_row[threadIdx.x] = s;
-    sm.dst_row[threadIdx.x] = o;
-    sm.row_kind[threadIdx.x] = kind;
-  }
-  __syncthreads();
-  copy_rows<kStepThreads / kGatherRowsD, 3>(
-      kGatherRowsD, [&](int r) { return RowRef{sm.src_row[r], sm.dst_row[r], sm.row_kind[r]}; }, latent,
-      Ly.format == SKV_FMT_FP8 && Ly.kind == SKV_LAYER_HCA, d);
-}
+constexpr int kDenseTPR = kStepThreads / kGatherRowsD;  // threads per dense row
+constexpr int kDenseU = 9;  // 16-byte chunks per thread and pass: 8 x 9 x 16 B = a 576-channel bf16 row
 
 // Block u of the dense part of the filter launch.
-__device__ __forceinline__ void dense_block(GatherTileSmem& sm, const skv_decode_desc* d, int u) {
-  const int batch = d->batch;
-  for (int l = 0; l < d->n_layers; ++l) {
-    const skv_decode_layer& Ly = d->layers[l];
-    const int tiles = (dense_rows(d, Ly) + kGatherRowsD - 1) / kGatherRowsD;
-    if (u < tiles * batch) {
-      const int b = static_cast<int>(udiv24(u, tiles));
-      const int tile = u - b * tiles;
-      const int L = d->step_lens[b];  // loaded with the status: one round trip
-      if (*d->status) return;         // refused step
-      if (l == 0 && tile == 0 && threadIdx.x == 0) {
-        d->tok_lens[b] = L;
-        for (int g = 0; g < d->n_groups; ++g) d->groups[g].n_entries[b] = udiv24(L, d->groups[g].m);
-        if (b == 0) {
-          for (int g = 0; g < d->n_groups; ++g) *d->groups[g].free_top = d->step_top[g];
-        }
-      }
-      gather_tile(sm, d, Ly, b, tile, L);
-      return;
+__device__ __forceinline__ void dense_block(const skv_decode_desc* d, const StepMap& map, int u) {
+  // the block's layer: the first l with u < tile_end[l] (kernel arguments only)
+  int l = 0, base = 0, tiles = map.tiles[0];
+#pragma unroll
+  for (int i = 0; i + 1 < SKV_MAX_LAYERS; ++i) {
+    if (u >= map.tile_end[i]) {
+      l = i + 1;
+      base = map.tile_end[i];
+      tiles = map.tiles[i + 1];
     }
-    u -= tiles * batch;
   }
+  const int rem = u - base;
+  const int b = static_cast<int>(udiv24(rem, tiles));
+  const int tile = rem - b * tiles;
+  const int g = ((map.hca_mask >> l) & 1) ? map.group[l] : -1;  // uniform; < 0: no HCA entries
+  const int r = tile * kGatherRowsD + static_cast<int>(threadIdx.x) / kDenseTPR;  // this thread's row
+  // one round trip: length, status and the row's block-table entry (clamped
+  // into the sequence's row, so that the load needs no branch)
+  const int gi = max(g, 0);
+  const int bs = map.block_size[gi];
+  const int pi = static_cast<int>(udiv24(r, bs));
+  const int32_t* bt = (g >= 0) ? map.block_table[gi] + static_cast<int64_t>(b) * map.bt_stride[gi] +
+                                     min(pi, map.bt_stride[gi] - 1)
+                               : map.step_lens + b;
+  const int32_t page = *bt;
+  const int L = map.step_lens[b];
+  if (*map.status) return;  // refused step
+  const skv_decode_layer& Ly = d->layers[l];
+  if (l == 0 && tile == 0 && threadIdx.x == 0) {
+    d->tok_lens[b] = L;
+    for (int gg = 0; gg < d->n_groups; ++gg) d->groups[gg].n_entries[b] = udiv24(L, d->groups[gg].m);
+    if (b == 0) {
+      for (int gg = 0; gg < d->n_groups; ++gg) *d->groups[gg].free_top = d->step_top[gg];
+    }
+  }
+  const int latent = d->latent;
+  const int64_t out_row = static_cast<int64_t>(latent) * 2;
+  const int n_dense = (g >= 0) ? static_cast<int>(Ly.out_rows) : 0;
+  RowRef rf{nullptr, nullptr, 0};
+  if (r < n_dense) {
+    // dense HCA rows past the entries stay untouched
+    const skv_page_group& G = d->groups[gi];
+    if (r < static_cast<int>(udiv24(L, G.m)) && pi < map.bt_stride[gi] && page >= 0 && page < G.n_pages) {
+      rf.src = static_cast<const uint8_t*>(Ly.pool) +
+               (static_cast<int64_t>(page) * bs + (r - pi * bs)) * Ly.entry_bytes;
+      rf.dst = static_cast<uint8_t*>(Ly.out_entries) + (static_cast<int64_t>(b) * Ly.out_rows + r) * out_row;
+      rf.kind = (Ly.format == SKV_FMT_FP8) ? 2 : 1;
+    }
+  } else if (r < n_dense + d->window) {
+    const int w = r - n_dense;
+    const int cnt = min(max(L, 0), d->window);
+    if (w < cnt) {
+      const int64_t slot = umod24(static_cast<uint32_t>(L - cnt + w), d->window);
+      rf.src = static_cast<const uint8_t*>(Ly.ring) + (static_cast<int64_t>(b) * d->window + slot) * out_row;
+      rf.dst = static_cast<uint8_t*>(Ly.out_window) + (static_cast<int64_t>(b) * d->window + w) * out_row;
+      rf.kind = 1;
+    }
+  }
+  // one pass of copy_rows covers the tile (kGatherRowsD rows at once), so
+  // row(r) is always this thread's own row
+  copy_rows<kDenseTPR, kDenseU>(
+      kGatherRowsD, [&](int) { return rf; }, latent, g >= 0 && Ly.format == SKV_FMT_FP8, d);
 }
 
 // ---------------------------------------------------------------------------
@@ -765,32 +784,27 @@ __device__ __forceinline__ void finish_rows(RankRows& rr, int n_rows, int f0, in
 //    ranks and gathers).  Part 0 of the rank launch zeroes the row's
 //    histogram for the next step, also after a refusal.
 // ---------------------------------------------------------------------------
-union FilterLaunchSmem {
-  TopkFilterSmem filter;
-  GatherTileSmem tile;
-};
-
 __global__ __launch_bounds__(kStepThreads) void k_decode_filter(const skv_decode_desc* __restrict__ d,
-                                                                int n_chunks, int n_csa) {
-  __shared__ FilterLaunchSmem sm;
+                                                                int n_chunks, StepMap map) {
+  __shared__ TopkFilterSmem sm;
   int u = blockIdx.x;
-  const int n_filter = n_chunks * d->batch * n_csa;
+  const int n_filter = n_chunks * map.batch * map.n_csa;
   if (u < n_filter) {
     const uint32_t ub = udiv24(u, n_chunks);
     const int chunk = static_cast<int>(u - ub * n_chunks);
-    const uint32_t uc = udiv24(ub, d->batch);
-    const int b = static_cast<int>(ub - uc * d->batch);
-    const skv_decode_layer* Ly = csa_layer(d, static_cast<int>(uc));
+    const uint32_t uc = udiv24(ub, map.batch);
+    const int b = static_cast<int>(ub - uc * map.batch);
+    const skv_decode_layer* Ly = csa_layer(d, map, static_cast<int>(uc));
     if (!Ly) return;  // uniform over the workgroup
-    const int L = d->step_lens[b];  // loaded with the status: one round trip
-    if (*d->status) return;         // refused step
+    const int L = map.step_lens[b];  // loaded with the status: one round trip
+    if (*map.status) return;         // refused step
     int n_cols, n_valid;
     score_cols(*Ly, d->groups[Ly->group].m, L, n_cols, n_valid);
-    topk_filter_chunk(sm.filter, Ly->scores + static_cast<int64_t>(b) * Ly->score_stride, n_cols, n_valid,
+    topk_filter_chunk(sm, Ly->scores + static_cast<int64_t>(b) * Ly->score_stride, n_cols, n_valid,
                       Ly->top_k, chunk, Ly->topk_ws + static_cast<int64_t>(b) * kTkWsWords);
     return;
   }
-  dense_block(sm.tile, d, u - n_filter);
+  dense_block(d, map, u - n_filter);
 }
 
 constexpr int kRankHead = 2 * kStepThreads;  // entries of each candidate list fetched with the counters
@@ -827,31 +841,28 @@ __device__ __forceinline__ uint64_t order_key(int2 v) {
 // longer than the launch's LDS holds, on the lists in global memory), page
 // lookups read the LDS table, and the entry copy is the last round trip.
 __global__ __launch_bounds__(kStepThreads) void k_decode_topk_rank(const skv_decode_desc* __restrict__ d,
-                                                                   int rank_out, int bt_lds, int ck_cap) {
+                                                                   int rank_out, int bt_lds, int ck_cap,
+                                                                   StepMap map) {
   extern __shared__ __align__(16) uint8_t rank_lds[];
   RankHead& sm = *reinterpret_cast<RankHead*>(rank_lds);
   int32_t* sm_bt = reinterpret_cast<int32_t*>(rank_lds + align16(sizeof(RankHead)));
   uint8_t* region = rank_lds + align16(sizeof(RankHead)) + align16(static_cast<int64_t>(bt_lds) * 4);
   uint64_t* sm_ck = reinterpret_cast<uint64_t*>(region);
   RankFallback& fb = *reinterpret_cast<RankFallback*>(region);
-  const skv_decode_layer* Lp = csa_layer(d, blockIdx.z);
-  if (!Lp) return;
-  const skv_decode_layer& Ly = *Lp;
-  const int k = Ly.top_k;
-  const int parts = static_cast<int>(ceil_div24(k, rank_out));
-  const int part = blockIdx.x;
-  if (part >= parts) return;  // the grid is sized for the largest top_k
+  const int z = blockIdx.z;  // the grid's z extent is the CSA layer count
+  const int li = static_cast<int>((map.csa >> (4 * z)) & 15);
+  const skv_decode_layer& Ly = d->layers[li];
+  const int gi = map.group[li];
   const int b = blockIdx.y;
   const int tid = threadIdx.x;
-  const skv_page_group& G = d->groups[Ly.group];
-  int32_t* ws = Ly.topk_ws + static_cast<int64_t>(b) * kTkWsWords;
+  int32_t* ws = map.topk_ws[z] + static_cast<int64_t>(b) * kTkWsWords;
   const int2* sure_list = reinterpret_cast<const int2*>(ws + kTkWsSure);
   const int2* tie_list = reinterpret_cast<const int2*>(ws + kTkWsTie);
-  const int32_t* bt_row = G.block_table + static_cast<int64_t>(b) * G.bt_stride;
-  const int n_bt = static_cast<int>(min<int64_t>(G.bt_stride, bt_lds));
+  const int32_t* bt_row = map.block_table[gi] + static_cast<int64_t>(b) * map.bt_stride[gi];
+  const int n_bt = min(map.bt_stride[gi], bt_lds);
   // every load of the first round trip, unconditional (clamped indices)
-  const int status = *d->status;
-  const int L = d->step_lens[b];
+  const int status = *map.status;
+  const int L = map.step_lens[b];
   const int cnt0 = ws[kTkWsCnt], cnt1 = ws[kTkWsCnt + 1], flag = ws[kTkWsCnt + 2];
   int2 sh[kRankHead / kStepThreads], th[kRankHead / kStepThreads];
 #pragma unroll
@@ -862,6 +873,11 @@ __global__ __launch_bounds__(kStepThreads) void k_decode_topk_rank(const skv_dec
   int32_t btv[kRankBt / kStepThreads];
 #pragma unroll
   for (int u = 0; u < kRankBt / kStepThreads; ++u) btv[u] = bt_row[min(tid + u * kStepThreads, n_bt - 1)];
+  const int k = Ly.top_k;
+  const int part = blockIdx.x;
+  const int parts = static_cast<int>(ceil_div24(k, rank_out));
+  if (part >= parts) return;  // the grid is sized for the largest top_k
+  const skv_page_group& G = d->groups[gi];
   if (part == 0) {
     for (int i = tid; i < kTkBins; i += kStepThreads) ws[kTkWsHist + i] = 0;
   }
@@ -1017,11 +1033,23 @@ extern "C" int skv_decode_step(const skv_decode_desc* h, const skv_decode_desc* 
         G.block_size <= 0 || G.bt_stride <= 0 || G.n_pages <= 0) {
       return set_error(SKV_EINVAL, "%s: page group %d is incomplete", what, g);
     }
+    if (G.bt_stride >= (1 << 24)) return set_error(SKV_EINVAL, "%s: page group %d bt_stride >= 2^24", what, g);
+  }
+  StepMap map{};
+  map.batch = h->batch;
+  map.n_layers = h->n_layers;
+  map.step_lens = h->step_lens;
+  map.status = h->status;
+  for (int g = 0; g < SKV_MAX_GROUPS; ++g) {
+    map.block_table[g] = g < h->n_groups ? h->groups[g].block_table : nullptr;
+    map.bt_stride[g] = g < h->n_groups ? static_cast<int32_t>(h->groups[g].bt_stride) : 1;
+    map.block_size[g] = g < h->n_groups ? h->groups[g].block_size : 1;
   }
   int n_csa = 0, max_top_k = 0;
   int64_t max_score_cols = 1, n_tiles = 0;
   for (int l = 0; l < h->n_layers; ++l) {
     const skv_decode_layer& Ly = h->layers[l];
+    map.group[l] = (Ly.kind == SKV_LAYER_SWA) ? -1 : static_cast<int8_t>(Ly.group);
     if (!Ly.ring || !Ly.kv_new || !Ly.out_window) return set_error(SKV_EINVAL, "%s: layer %d lacks ring/kv_new/out_window", what, l);
     int64_t dense = h->window;
     if (Ly.kind == SKV_LAYER_HCA || Ly.kind == SKV_LAYER_CSA) {
@@ -1043,9 +1071,12 @@ extern "C" int skv_decode_step(const skv_decode_desc* h, const skv_decode_desc* 
         if (Ly.idx_pool && (!Ly.idx_state || !Ly.idx_bias || !Ly.ci_new || !Ly.zi_new || h->c_indexer <= 0)) {
           return set_error(SKV_EINVAL, "%s: CSA layer %d indexer stream incomplete", what, l);
         }
+        map.csa |= static_cast<uint64_t>(l) << (4 * n_csa);
+        map.topk_ws[n_csa] = Ly.topk_ws;
         ++n_csa;
         max_top_k = max(max_top_k, Ly.top_k);
       } else {
+        map.hca_mask |= 1u << l;
         if (Ly.out_rows <= 0 || Ly.out_rows > (1 << 24)) {
           return set_error(SKV_EINVAL, "%s: HCA layer %d needs 0 < out_rows <= 2^24", what, l);
         }
@@ -1054,8 +1085,16 @@ extern "C" int skv_decode_step(const skv_decode_desc* h, const skv_decode_desc* 
     } else if (Ly.kind != SKV_LAYER_SWA) {
       return set_error(SKV_EINVAL, "%s: layer %d has unknown kind %d", what, l, Ly.kind);
     }
+    if (dense >= (1 << 24)) return set_error(SKV_EINVAL, "%s: layer %d has 2^24 dense rows or more", what, l);
+    map.tiles[l] = static_cast<int32_t>(ceil_div(dense, kGatherRowsD));
     n_tiles += ceil_div(dense, kGatherRowsD) * h->batch;
+    map.tile_end[l] = static_cast<int32_t>(n_tiles < (1 << 24) ? n_tiles : (1 << 24));
   }
+  for (int l = h->n_layers; l < SKV_MAX_LAYERS; ++l) {
+    map.tiles[l] = 1;
+    map.tile_end[l] = static_cast<int32_t>(n_tiles < (1 << 24) ? n_tiles : (1 << 24));
+  }
+  map.n_csa = n_csa;
   if (h->batch == 0 || h->n_layers == 0) return SKV_OK;
   const int n_chunks = static_cast<int>(ceil_div(max_score_cols, kTkChunk));
   const int64_t n_append = static_cast<int64_t>(h->batch) * h->n_layers +
@@ -1066,11 +1105,11 @@ extern "C" int skv_decode_step(const skv_decode_desc* h, const skv_decode_desc* 
   }
   hipStream_t s = static_cast<hipStream_t>(stream);
   hipLaunchKernelGGL(k_decode_append, dim3(static_cast<unsigned>(n_append)), dim3(kStepThreads), 0, s, dd,
-                     n_chunks);
+                     n_chunks, map);
   int rc = check_launch(what);
   if (rc) return rc;
   hipLaunchKernelGGL(k_decode_filter, dim3(static_cast<unsigned>(n_filter)), dim3(kStepThreads), 0, s, dd,
-                     n_chunks, n_csa);
+                     n_chunks, map);
   if ((rc = check_launch(what))) return rc;
   if (n_csa > 0) {
     // smaller parts when the rows alone would leave most CUs idle
@@ -1094,7 +1133,7 @@ extern "C" int skv_decode_step(const skv_decode_desc* h, const skv_decode_desc* 
     }
     const int64_t lds = rank_lds_bytes(bt, ck_cap);
     hipLaunchKernelGGL(k_decode_topk_rank, rgrid, dim3(kStepThreads), static_cast<size_t>(lds), s, dd, rank_out,
-                       bt, ck_cap);
+                       bt, ck_cap, map);
   }
   return check_launch(what);
 }
