@@ -666,15 +666,16 @@ __device__ __forceinline__ void dense_block(const skv_decode_desc* d, const Step
 //    The row's candidates sit in LDS as 64-bit order keys (key << 32 | ~idx:
 //    larger means earlier in the output), the sure list [0, S) then the tie
 //    list [S, C), each in the same order in every part.  A part ranks its
-//    candidates p, p + parts, ... of each list within that list (kRankSub
-//    lanes per candidate, each counting a strided share), writes every
+//    candidates p, p + parts, ... of each list within that list (a lane
+//    group per kRankR candidates, each lane comparing a strided share of the
+//    list with all of them), writes every
 //    winner's index and entry at its output position, and gives the
 //    positions in [sel, top_k) it owns index -1 and entry 0 (the reference's
 //    clamp(min=0) before its gather).
 // ---------------------------------------------------------------------------
 constexpr int kRankOutMin = 16;
 constexpr int kRankOut = 32;
-constexpr int kRankSub = 8;  // fewest lanes that rank one candidate together
+constexpr int kRankR = 4;  // candidates a lane compares with each key it reads
 constexpr int kRankMaxRows = 512;                    // rows one part can collect (checked below)
 
 // Rows a part collects, worst case over top_k and the part size: its sure
@@ -700,20 +701,20 @@ struct RankRows {
   uintptr_t src_kind[kRankMaxRows];  // entry address | row kind (entries are 4-byte aligned)
 };
 
-// Lanes that rank one candidate together: the largest power of two in
-// [8, 64] that still gives every candidate of the round a lane group.
-__device__ __forceinline__ int rank_lanes(int n_mine) {
+// Lanes that share a group of kRankR candidates: the largest power of two
+// in [1, 64] that still gives every group of the round its lanes.
+__device__ __forceinline__ int rank_lanes(int n_groups) {
   int sub_n = kWave;
-  while (sub_n > kRankSub && sub_n * n_mine > kStepThreads) sub_n >>= 1;
+  while (sub_n > 1 && sub_n * n_groups > kStepThreads) sub_n >>= 1;
   return sub_n;
 }
 
-// own_pos (optional): instead of collecting the winners, record for the
-// part's j-th candidate (its sure ones first, then its ties) the output
-// position, or -1 for a tie past the winners.
+// The part's first n_pf candidates (its sure ones first, then its ties)
+// get their output position, or -1 for a tie past the winners, in
+// own_pos[j] instead of being collected; the other winners are collected.
 template <class KeyAt>
 __device__ __forceinline__ void rank_candidates(RankRows& rr, KeyAt ck, int S, int C, int sel, int part, int parts,
-                                                int* own_pos = nullptr) {
+                                                int* own_pos = nullptr, int n_pf = 0) {
   const int n_sure_mine = (part < S) ? static_cast<int>(ceil_div24(S - part, parts)) : 0;
   const int tid = threadIdx.x;
 #pragma unroll 1
@@ -721,24 +722,50 @@ __device__ __forceinline__ void rank_candidates(RankRows& rr, KeyAt ck, int S, i
     const int lo = cls ? S : 0;
     const int hi = cls ? C : S;
     const int n_mine = (part < hi - lo) ? static_cast<int>(ceil_div24(hi - lo - part, parts)) : 0;
-    const int sub_n = rank_lanes(n_mine);  // uniform
+    const int n_groups = (n_mine + kRankR - 1) / kRankR;
+    const int sub_n = rank_lanes(n_groups);  // uniform
     const int sub = tid & (sub_n - 1);
-    for (int j0 = 0; j0 < n_mine; j0 += kStepThreads / sub_n) {
-      const int j = j0 + tid / sub_n;
-      const bool valid = j < n_mine;
-      const uint64_t mine = valid ? ck(lo + part + j * parts) : ~0ull;
-      int rank = 0;
-#pragma unroll 8
-      for (int q = lo + sub; q < hi; q += sub_n) rank += ck(q) > mine;
-      for (int o = 1; o < sub_n; o <<= 1) rank += __shfl_xor(rank, o);  // within the lane group
-      const int pos = lo + rank;
-      if (valid && sub == 0) {
-        if (own_pos) {
-          own_pos[(cls ? n_sure_mine : 0) + j] = (pos < sel) ? pos : -1;
-        } else if (pos < sel) {
-          const uint32_t key = static_cast<uint32_t>(mine >> 32);
-          const int idx = static_cast<int>(~static_cast<uint32_t>(mine));
-          rr.win[atomicAdd(&rr.n_rows, 1)] = make_int2(pos, key_finite(key) ? idx : -1);
+    for (int g0 = 0; g0 < n_groups; g0 += kStepThreads / sub_n) {
+      const int j0 = (g0 + tid / sub_n) * kRankR;  // the group's first candidate
+      uint64_t mine[kRankR];
+      int rank[kRankR];
+#pragma unroll
+      for (int r = 0; r < kRankR; ++r) {
+        mine[r] = (j0 + r < n_mine) ? ck(lo + part + (j0 + r) * parts) : ~0ull;
+        rank[r] = 0;
+      }
+#pragma unroll 4
+      for (int q = lo + sub; q < hi; q += sub_n) {
+        const uint64_t key = ck(q);
+#pragma unroll
+        for (int r = 0; r < kRankR; ++r) rank[r] += key > mine[r];
+      }
+      // sum over the lane group, two counts (< 2^16: a list holds at most
+      // kTkTieCap keys) per word
+      static_assert(kRankR == 4 && kTkTieCap < (1 << 16), "packed counts");
+      int p01 = rank[0] | (rank[1] << 16), p23 = rank[2] | (rank[3] << 16);
+      for (int o = 1; o < sub_n; o <<= 1) {
+        p01 += __shfl_xor(p01, o);
+        p23 += __shfl_xor(p23, o);
+      }
+      rank[0] = p01 & 0xffff;
+      rank[1] = p01 >> 16;
+      rank[2] = p23 & 0xffff;
+      rank[3] = p23 >> 16;
+      if (sub == 0) {
+#pragma unroll
+        for (int r = 0; r < kRankR; ++r) {
+          const int j = j0 + r;
+          if (j >= n_mine) break;
+          const int pos = lo + rank[r];
+          const int own = (cls ? n_sure_mine : 0) + j;
+          if (own < n_pf) {
+            own_pos[own] = (pos < sel) ? pos : -1;
+          } else if (pos < sel) {
+            const uint32_t key = static_cast<uint32_t>(mine[r] >> 32);
+            const int idx = static_cast<int>(~static_cast<uint32_t>(mine[r]));
+            rr.win[atomicAdd(&rr.n_rows, 1)] = make_int2(pos, key_finite(key) ? idx : -1);
+          }
         }
       }
     }
@@ -935,17 +962,20 @@ __global__ __launch_bounds__(kStepThreads) void k_decode_topk_rank(const skv_dec
     __syncthreads();
     const auto lds_key = [&](int q) { return sm_ck[q]; };
     const auto global_key = [&](int q) { return order_key(q < S ? sure_list[q] : tie_list[q - S]); };
-    // a part with at most kRankPf candidates loads their entries first, so
-    // that the loads overlap the ranking; the winners are stored after it
+    // the entries of up to kRankPf of the part's candidates (all of them, or
+    // else its sure ones, which always win) are loaded first, so that the
+    // loads overlap the ranking; they are stored after it, and the other
+    // winners are collected and copied after it
     const int n_sure_mine = (part < S) ? static_cast<int>(ceil_div24(S - part, parts)) : 0;
     const int n_own = n_sure_mine + ((part < T) ? static_cast<int>(ceil_div24(T - part, parts)) : 0);
     constexpr int kPfU = 9;  // 8 threads x 9 tasks cover a 576-channel row (bf16 72 chunks, fp8 40 tasks)
     const bool fp8 = Ly.format == SKV_FMT_FP8;
-    if (in_lds && n_own <= kRankPf && entry_tasks<8, kPfU>(d->latent, fp8) <= 8 * kPfU) {  // uniform
+    const int n_pf = (n_own <= kRankPf) ? n_own : min(n_sure_mine, kRankPf);
+    if (in_lds && n_pf > 0 && entry_tasks<8, kPfU>(d->latent, fp8) <= 8 * kPfU) {  // uniform
       const int r = tid / 8;
       int pick = -1, kind = 0;
       const uint8_t* src = nullptr;
-      if (r < n_own) {
+      if (r < n_pf) {
         const int c = (r < n_sure_mine) ? part + r * parts : S + part + (r - n_sure_mine) * parts;
         const uint64_t v = sm_ck[c];
         pick = key_finite(static_cast<uint32_t>(v >> 32)) ? static_cast<int>(~static_cast<uint32_t>(v)) : -1;
@@ -954,9 +984,9 @@ __global__ __launch_bounds__(kStepThreads) void k_decode_topk_rank(const skv_dec
       }
       EntryShare<kPfU> share;
       entry_share_load<8, kPfU>(share, src, kind, d->latent, fp8, reinterpret_cast<const u32x4*>(d));
-      rank_candidates(sm.rr, lds_key, S, C, sel, part, parts, sm.own_pos);
+      rank_candidates(sm.rr, lds_key, S, C, sel, part, parts, sm.own_pos, n_pf);
       __syncthreads();
-      const int pos = (r < n_own) ? sm.own_pos[r] : -1;
+      const int pos = (r < n_pf) ? sm.own_pos[r] : -1;
       if (pos >= 0) {
         const int64_t out_row = static_cast<int64_t>(d->latent) * 2;
         if ((tid & 7) == 0) Ly.topk_idx[static_cast<int64_t>(b) * k + pos] = pick;
@@ -964,7 +994,7 @@ __global__ __launch_bounds__(kStepThreads) void k_decode_topk_rank(const skv_dec
                                               (static_cast<int64_t>(b) * k + pos) * out_row,
                                    kind, d->latent, fp8);
       }
-      finish_rows(sm.rr, 0, max(o0, sel), o1, d, Ly, b, L, sm_bt, n_bt);  // the fills
+      finish_rows(sm.rr, sm.rr.n_rows, max(o0, sel), o1, d, Ly, b, L, sm_bt, n_bt);  // the rest and the fills
       return;
     }
     if (in_lds) rank_candidates(sm.rr, lds_key, S, C, sel, part, parts);
