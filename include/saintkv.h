@@ -284,13 +284,13 @@ int skv_compact(const skv_pool_ref* pools, int32_t n_pools, int32_t* block_table
  *            stream (bf16 entries) and histogram their score rows.  New
  *            lengths and free-stack tops go to step_lens / step_top.
  *   filter : per CSA layer the top-k candidate lists (skv_topk_select_decode
- *            semantics); HCA layers copy all their entries (dense read, rows
- *            past the sequence's entries are left untouched); every layer
- *            copies the last min(window, L) tokens of its ring in position
- *            order; the step's lengths and tops are committed.
- *   rank   : per CSA layer the ordered top_k picks and their gather (fp8
+ *            semantics; no launch without CSA layers).
+ *   gather : per CSA layer the ordered top_k picks and their gather (fp8
  *            dequantized to bf16; -1 reads entry 0, picks without an entry
- *            give zero rows).
+ *            give zero rows); HCA layers copy all their entries (dense read,
+ *            rows past the sequence's entries are left untouched); every
+ *            layer copies the last min(window, L) tokens of its ring in
+ *            position order; the step's lengths and tops are committed.
  * Mirrors one cached step of CSA/HCA/SWAttention.forward over a
  * KVCacheBundle (model.py:294-315; csa.py:299-331; hca.py:110-141;
  * swa.py:107-125).  The kernels read the descriptor from device memory:

@@ -2,10 +2,10 @@
 // whatever the number of layers:
 //   append : step page plan (computed by every workgroup) + SWA ring rows +
 //            pooling fold / entry emission + top-k histogram chunks
-//   filter : top-k candidate lists + dense HCA / window copies + commit of
-//            the step's lengths
-//   rank   : per (CSA layer, sequence, part) ordering of the candidates and
-//            the sparse gather of the winners' entries
+//   filter : top-k candidate lists
+//   gather : per (CSA layer, sequence, part) ordering of the candidates and
+//            the sparse gather of the winners' entries, interleaved with the
+//            dense HCA / window copies and the commit of the step's lengths
 // Every kernel boundary orders a producer before its consumers; no workgroup
 // waits for or fences against another.
 //
@@ -319,9 +319,9 @@ __global__ __launch_bounds__(kStepThreads) void k_decode_append(const skv_decode
   const int tid = threadIdx.x;
   if (static_cast<int>(blockIdx.x) >= n_append) {
     // top-k histogram chunk (chunk, b, csa layer).  It assumes the step
-    // goes ahead; on a refusal the rank launch still clears
+    // goes ahead; on a refusal the gather launch still clears
     // the histogram.  Chunk 0 zeroes the row's list counters, which the
-    // previous step's rank launch read.
+    // previous step's gather launch read.
     const uint32_t u = blockIdx.x - n_append;  // grids stay below 2^24 workgroups
     const uint32_t ub = udiv24(u, n_chunks);
     const int chunk = static_cast<int>(u - ub * n_chunks);
@@ -523,7 +523,7 @@ __device__ __forceinline__ int entry_source(const skv_page_group& G, const skv_d
 // takes tasks sub, sub + kTPR, ... (a bf16 layer: the row's 16-byte chunks;
 // an fp8 layer: 16-code chunks, each giving two output chunks, then the
 // rope chunks).  Kind 3 rows are written as zeros.  The loads of a share can
-// be issued long before its stores (see the rank launch).
+// be issued long before its stores (see the rank parts).
 template <int kU>
 struct EntryShare {
   u32x4 v[kU];
@@ -583,7 +583,7 @@ __device__ __forceinline__ void entry_share_store(const EntryShare<kU>& sh, uint
 
 // ---------------------------------------------------------------------------
 // 3. dense gather tiles (HCA entries and SWA windows) and the commit of the
-//    step: the filter launch ends its grid with these blocks.
+//    step: blocks of the gather launch.
 //    Tile t of (layer, sequence) copies rows [32t, 32t+32) of the layer's
 //    dense row space [HCA entries (out_rows) | window], kDenseTPR threads
 //    per row.  Each thread loads its row's block-table entry together with
@@ -595,7 +595,7 @@ __device__ __forceinline__ void entry_share_store(const EntryShare<kU>& sh, uint
 constexpr int kDenseTPR = kStepThreads / kGatherRowsD;  // threads per dense row
 constexpr int kDenseU = 9;  // 16-byte chunks per thread and pass: 8 x 9 x 16 B = a 576-channel bf16 row
 
-// Block u of the dense part of the filter launch.
+// Dense tile u of the gather launch.
 __device__ __forceinline__ void dense_block(const skv_decode_desc* d, const StepMap& map, int u) {
   // the block's layer: the first l with u < tile_end[l] (kernel arguments only)
   int l = 0, base = 0, tiles = map.tiles[0];
@@ -806,17 +806,17 @@ __device__ __forceinline__ void finish_rows(RankRows& rr, int n_rows, int f0, in
 }
 
 // ---------------------------------------------------------------------------
-// 5. filter launch (top-k filter chunks, see skv_topk.h, then the dense
-//    blocks) and rank launch (every part loads the row's candidate lists,
-//    ranks and gathers).  Part 0 of the rank launch zeroes the row's
-//    histogram for the next step, also after a refusal.
+// 5. filter launch (top-k filter chunks, see skv_topk.h) and gather launch
+//    (rank parts, each loading its row's candidate lists, ranking and
+//    gathering, interleaved with the dense tiles, whose copies keep HBM busy
+//    while the rank parts wait on their round trips).  Part 0 of a row
+//    zeroes the row's histogram for the next step, also after a refusal.
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(kStepThreads) void k_decode_filter(const skv_decode_desc* __restrict__ d,
                                                                 int n_chunks, StepMap map) {
   __shared__ TopkFilterSmem sm;
-  int u = blockIdx.x;
-  const int n_filter = n_chunks * map.batch * map.n_csa;
-  if (u < n_filter) {
+  const int u = blockIdx.x;  // the grid holds n_chunks x batch x CSA layers blocks
+  {
     const uint32_t ub = udiv24(u, n_chunks);
     const int chunk = static_cast<int>(u - ub * n_chunks);
     const uint32_t uc = udiv24(ub, map.batch);
@@ -829,16 +829,14 @@ __global__ __launch_bounds__(kStepThreads) void k_decode_filter(const skv_decode
     score_cols(*Ly, d->groups[Ly->group].m, L, n_cols, n_valid);
     topk_filter_chunk(sm, Ly->scores + static_cast<int64_t>(b) * Ly->score_stride, n_cols, n_valid,
                       Ly->top_k, chunk, Ly->topk_ws + static_cast<int64_t>(b) * kTkWsWords);
-    return;
   }
-  dense_block(d, map, u - n_filter);
 }
 
 constexpr int kRankHead = 2 * kStepThreads;  // entries of each candidate list fetched with the counters
 constexpr int kRankBt = 16 * kStepThreads;   // most block-table entries of a sequence staged in LDS
 constexpr int kRankPf = kStepThreads / 8;    // own candidates whose entries are loaded before ranking
 
-// Dynamic LDS of the rank launch, sized by the host for the launch's rows:
+// Dynamic LDS of the gather launch, sized by the host for the launch's rows:
 //   RankHead | block-table row (bt_lds entries) | candidates (ck_cap order keys)
 //                                                  or the full-select fallback
 struct RankHead {
@@ -867,20 +865,17 @@ __device__ __forceinline__ uint64_t order_key(int2 v) {
 // longer lists take a second one.  Ranking then runs on LDS (or, for lists
 // longer than the launch's LDS holds, on the lists in global memory), page
 // lookups read the LDS table, and the entry copy is the last round trip.
-__global__ __launch_bounds__(kStepThreads) void k_decode_topk_rank(const skv_decode_desc* __restrict__ d,
-                                                                   int rank_out, int bt_lds, int ck_cap,
-                                                                   StepMap map) {
-  extern __shared__ __align__(16) uint8_t rank_lds[];
+__device__ __forceinline__ void rank_part(const skv_decode_desc* __restrict__ d, const StepMap& map,
+                                          uint8_t* rank_lds, int part, int b, int z, int rank_out, int bt_lds,
+                                          int ck_cap) {
   RankHead& sm = *reinterpret_cast<RankHead*>(rank_lds);
   int32_t* sm_bt = reinterpret_cast<int32_t*>(rank_lds + align16(sizeof(RankHead)));
   uint8_t* region = rank_lds + align16(sizeof(RankHead)) + align16(static_cast<int64_t>(bt_lds) * 4);
   uint64_t* sm_ck = reinterpret_cast<uint64_t*>(region);
   RankFallback& fb = *reinterpret_cast<RankFallback*>(region);
-  const int z = blockIdx.z;  // the grid's z extent is the CSA layer count
   const int li = static_cast<int>((map.csa >> (4 * z)) & 15);
   const skv_decode_layer& Ly = d->layers[li];
   const int gi = map.group[li];
-  const int b = blockIdx.y;
   const int tid = threadIdx.x;
   int32_t* ws = map.topk_ws[z] + static_cast<int64_t>(b) * kTkWsWords;
   const int2* sure_list = reinterpret_cast<const int2*>(ws + kTkWsSure);
@@ -901,7 +896,6 @@ __global__ __launch_bounds__(kStepThreads) void k_decode_topk_rank(const skv_dec
 #pragma unroll
   for (int u = 0; u < kRankBt / kStepThreads; ++u) btv[u] = bt_row[min(tid + u * kStepThreads, n_bt - 1)];
   const int k = Ly.top_k;
-  const int part = blockIdx.x;
   const int parts = static_cast<int>(ceil_div24(k, rank_out));
   if (part >= parts) return;  // the grid is sized for the largest top_k
   const skv_page_group& G = d->groups[gi];
@@ -1004,6 +998,31 @@ __global__ __launch_bounds__(kStepThreads) void k_decode_topk_rank(const skv_dec
   finish_rows(sm.rr, sm.rr.n_rows, max(o0, sel), o1, d, Ly, b, L, sm_bt, n_bt);
 }
 
+// Blocks of the gather launch: rank part i (parts_max x batch x CSA layers
+// of them) is block i * period, every other block is the next dense tile.
+// period * n_rank <= n_rank + dense tiles, so every rank block is in the grid.
+struct GatherGrid {
+  int32_t n_rank;
+  int32_t parts_max;
+  int32_t period;
+};
+
+__global__ __launch_bounds__(kStepThreads) void k_decode_gather(const skv_decode_desc* __restrict__ d,
+                                                                GatherGrid gg, int rank_out, int bt_lds,
+                                                                int ck_cap, StepMap map) {
+  extern __shared__ __align__(16) uint8_t rank_lds[];
+  const uint32_t u = blockIdx.x;  // grids stay below 2^24 workgroups
+  const uint32_t grp = udiv24(u, gg.period);
+  if (u == grp * gg.period && static_cast<int>(grp) < gg.n_rank) {
+    const uint32_t rest = udiv24(grp, gg.parts_max);
+    const uint32_t z = udiv24(rest, map.batch);
+    rank_part(d, map, rank_lds, static_cast<int>(grp - rest * gg.parts_max),
+              static_cast<int>(rest - z * map.batch), static_cast<int>(z), rank_out, bt_lds, ck_cap);
+    return;
+  }
+  dense_block(d, map, static_cast<int>(u) - min(static_cast<int>(ceil_div24(u, gg.period)), gg.n_rank));
+}
+
 }  // namespace skv
 
 using namespace skv;
@@ -1017,7 +1036,7 @@ constexpr int64_t kLdsPerCu = 160 * 1024;
 int64_t rank_lds_budget(int64_t lds) {
   static const int by_regs = [] {
     int n = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, k_decode_topk_rank, kStepThreads, 0) != hipSuccess ||
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, k_decode_gather, kStepThreads, 0) != hipSuccess ||
         n <= 0) {
       (void)hipGetLastError();
       n = 1 << 20;
@@ -1129,8 +1148,14 @@ extern "C" int skv_decode_step(const skv_decode_desc* h, const skv_decode_desc* 
   const int n_chunks = static_cast<int>(ceil_div(max_score_cols, kTkChunk));
   const int64_t n_append = static_cast<int64_t>(h->batch) * h->n_layers +
                            static_cast<int64_t>(n_chunks) * h->batch * n_csa;
-  const int64_t n_filter = static_cast<int64_t>(n_chunks) * h->batch * n_csa + n_tiles;
-  if (n_append >= (1 << 24) || n_filter >= (1 << 24)) {
+  const int64_t n_filter = static_cast<int64_t>(n_chunks) * h->batch * n_csa;
+  // smaller parts when the rows alone would leave most CUs idle
+  const int rank_out = (static_cast<int64_t>(h->batch) * n_csa * ceil_div(max_top_k, kRankOut) < 512)
+                           ? kRankOutMin : kRankOut;
+  const int64_t parts_max = ceil_div(max_top_k, rank_out);
+  const int64_t n_rank = parts_max * h->batch * n_csa;
+  const int64_t n_gather = n_rank + n_tiles;
+  if (n_append >= (1 << 24) || n_filter >= (1 << 24) || n_gather >= (1 << 24)) {
     return set_error(SKV_EINVAL, "%s: score_stride/out_rows give a grid of 2^24 workgroups or more", what);
   }
   hipStream_t s = static_cast<hipStream_t>(stream);
@@ -1138,14 +1163,18 @@ extern "C" int skv_decode_step(const skv_decode_desc* h, const skv_decode_desc* 
                      n_chunks, map);
   int rc = check_launch(what);
   if (rc) return rc;
-  hipLaunchKernelGGL(k_decode_filter, dim3(static_cast<unsigned>(n_filter)), dim3(kStepThreads), 0, s, dd,
-                     n_chunks, map);
-  if ((rc = check_launch(what))) return rc;
+  if (n_filter > 0) {
+    hipLaunchKernelGGL(k_decode_filter, dim3(static_cast<unsigned>(n_filter)), dim3(kStepThreads), 0, s, dd,
+                       n_chunks, map);
+    if ((rc = check_launch(what))) return rc;
+  }
+  GatherGrid gg;
+  gg.n_rank = static_cast<int32_t>(n_rank);
+  gg.parts_max = static_cast<int32_t>(parts_max);
+  gg.period = n_rank > 0 ? static_cast<int32_t>(n_gather / n_rank) : 1;
+  int bt = 1, ck_cap = 0;
+  int64_t lds = 0;
   if (n_csa > 0) {
-    // smaller parts when the rows alone would leave most CUs idle
-    const int rank_out = (static_cast<int64_t>(h->batch) * n_csa * ceil_div(max_top_k, kRankOut) < 512)
-                             ? kRankOutMin : kRankOut;
-    const dim3 rgrid(static_cast<unsigned>(ceil_div(max_top_k, rank_out)), h->batch, n_csa);
     // LDS sized for this launch: the longest block-table row of a CSA group
     // (at most kRankBt entries) and at least the candidate lists of rows
     // whose tie bin holds 2048 keys, grown while the workgroups a CU holds
@@ -1155,15 +1184,15 @@ extern "C" int skv_decode_step(const skv_decode_desc* h, const skv_decode_desc* 
       if (h->layers[l].kind == SKV_LAYER_CSA) bt_lds = max(bt_lds, h->groups[h->layers[l].group].bt_stride);
     }
     if (bt_lds > kRankBt) bt_lds = kRankBt;
-    const int bt = static_cast<int>(bt_lds);
-    int ck_cap = min(max_top_k + 2048, kTkCand);
+    bt = static_cast<int>(bt_lds);
+    ck_cap = min(max_top_k + 2048, kTkCand);
     const int64_t per_wg = rank_lds_budget(rank_lds_bytes(bt, ck_cap));
     while (ck_cap < kTkCand && rank_lds_bytes(bt, min(ck_cap + 256, kTkCand)) <= per_wg) {
       ck_cap = min(ck_cap + 256, kTkCand);
     }
-    const int64_t lds = rank_lds_bytes(bt, ck_cap);
-    hipLaunchKernelGGL(k_decode_topk_rank, rgrid, dim3(kStepThreads), static_cast<size_t>(lds), s, dd, rank_out,
-                       bt, ck_cap, map);
+    lds = rank_lds_bytes(bt, ck_cap);
   }
+  hipLaunchKernelGGL(k_decode_gather, dim3(static_cast<unsigned>(n_gather)), dim3(kStepThreads),
+                     static_cast<size_t>(lds), s, dd, gg, rank_out, bt, ck_cap, map);
   return check_launch(what);
 }
