@@ -41,14 +41,34 @@ struct StepMap {
   int32_t tiles[SKV_MAX_LAYERS];      // dense gather tiles per sequence of each layer
   int32_t tile_end[SKV_MAX_LAYERS];   // dense workgroups of layers 0..l (tiles x batch, running sum)
   int8_t group[SKV_MAX_LAYERS];       // page group of an HCA/CSA layer, -1 for an SWA layer
-  const int32_t* step_lens;           // the descriptor's
-  const int32_t* status;
-  const int32_t* block_table[SKV_MAX_GROUPS];  // the groups' (unused groups: bt_stride 1, block_size 1)
+  uint32_t group_first;               // bit l: layer l is the first layer of its page group
+  int32_t n_groups;
+  int32_t* tok_lens;                  // the descriptor's
+  int32_t* status;
+  int32_t* step_lens;
+  int32_t* step_top;
+  // the groups' (unused groups: null pointers, bt_stride, block_size, m and n_pages 1)
+  int32_t* block_table[SKV_MAX_GROUPS];
+  int32_t* n_entries[SKV_MAX_GROUPS];
+  int32_t* free_stack[SKV_MAX_GROUPS];
+  int32_t* free_top[SKV_MAX_GROUPS];
   int32_t bt_stride[SKV_MAX_GROUPS];
   int32_t block_size[SKV_MAX_GROUPS];
+  int32_t m[SKV_MAX_GROUPS];
+  int32_t n_pages[SKV_MAX_GROUPS];
   int32_t* topk_ws[SKV_MAX_LAYERS];   // of the i-th CSA layer
 };
 static_assert(SKV_MAX_LAYERS <= 16, "CSA layer indices are 4-bit fields");
+
+// A page group's table and sizes, from the kernel arguments.
+struct GroupRef {
+  const int32_t* block_table;
+  int bt_stride, block_size, n_pages, m;
+};
+
+__device__ __forceinline__ GroupRef group_ref(const StepMap& map, int g) {
+  return GroupRef{map.block_table[g], map.bt_stride[g], map.block_size[g], map.n_pages[g], map.m[g]};
+}
 
 __device__ __forceinline__ const skv_decode_layer* csa_layer(const skv_decode_desc* d, const StepMap& map,
                                                              int want) {
@@ -81,6 +101,7 @@ struct PlanSmem {
 
 struct OwnPlan {
   int bad;   // SKV_STATUS_* bits, 0 when the step goes ahead
+  int len;   // tokens of sequence b before the step
   int top;   // free-stack top of group g_own before the step
   int off;   // pops of the sequences before b in group g_own
   int p0;    // pages sequence b held before the step
@@ -89,13 +110,13 @@ struct OwnPlan {
 
 // g_own < 0: no group (SWA layer).  write_tops: this workgroup also writes
 // the groups' tops after the step to step_top.
-__device__ __forceinline__ OwnPlan step_plan(PlanSmem& sm, const skv_decode_desc* d, int b, int g_own,
+__device__ __forceinline__ OwnPlan step_plan(PlanSmem& sm, const StepMap& map, int b, int g_own,
                                              bool write_tops) {
   constexpr int kPerT = kDecodeMaxBatch / kStepThreads;
   const int tid = threadIdx.x;
-  const int batch = d->batch;
-  const int ng = d->n_groups;
-  OwnPlan P{0, 0, 0, 0, 0};
+  const int batch = map.batch;
+  const int ng = map.n_groups;
+  OwnPlan P{0, map.tok_lens[b], 0, 0, 0, 0};
   if (ng == 0) return P;  // uniform: no page group, nothing to plan
   // every load first (clamped indices), so they are all in flight together
   int len1[kPerT];
@@ -103,13 +124,14 @@ __device__ __forceinline__ OwnPlan step_plan(PlanSmem& sm, const skv_decode_desc
 #pragma unroll
   for (int j = 0; j < kPerT; ++j) {
     const int s = min(tid + j * kStepThreads, batch - 1);
-    len1[j] = d->tok_lens[s] + 1;
+    len1[j] = map.tok_lens[s] + 1;
 #pragma unroll
-    for (int g = 0; g < SKV_MAX_GROUPS; ++g) cur[j][g] = d->groups[min(g, ng - 1)].n_entries[s];
+    for (int g = 0; g < SKV_MAX_GROUPS; ++g) cur[j][g] = map.n_entries[min(g, ng - 1)][s];
   }
   int top[SKV_MAX_GROUPS];
 #pragma unroll
-  for (int g = 0; g < SKV_MAX_GROUPS; ++g) top[g] = *d->groups[min(g, ng - 1)].free_top;
+  for (int g = 0; g < SKV_MAX_GROUPS; ++g) top[g] = *map.free_top[min(g, ng - 1)];
+  const int own_cur = map.n_entries[min(max(g_own, 0), ng - 1)][b];
   if (tid == 0) {
     sm.bad = 0;
 #pragma unroll
@@ -124,9 +146,8 @@ __device__ __forceinline__ OwnPlan step_plan(PlanSmem& sm, const skv_decode_desc
 #pragma unroll
   for (int g = 0; g < SKV_MAX_GROUPS; ++g) {
     if (g >= ng) continue;
-    const skv_page_group& G = d->groups[g];
-    const uint32_t m = static_cast<uint32_t>(G.m);
-    const uint32_t bs = static_cast<uint32_t>(G.block_size);
+    const uint32_t m = static_cast<uint32_t>(map.m[g]);
+    const uint32_t bs = static_cast<uint32_t>(map.block_size[g]);
 #pragma unroll
     for (int j = 0; j < kPerT; ++j) {
       const int s = tid + j * kStepThreads;
@@ -143,7 +164,7 @@ __device__ __forceinline__ OwnPlan step_plan(PlanSmem& sm, const skv_decode_desc
       }
       const uint32_t p0 = ceil_div24(c, bs);
       const uint32_t p1 = ceil_div24(target, bs);
-      if (p1 > G.bt_stride) bad |= SKV_STATUS_MAX_PAGES;
+      if (p1 > static_cast<uint32_t>(map.bt_stride[g])) bad |= SKV_STATUS_MAX_PAGES;
       const int need = static_cast<int>(p1 - p0);
       if (need) {
         atomicAdd(&sm.tot[g], need);
@@ -164,7 +185,7 @@ __device__ __forceinline__ OwnPlan step_plan(PlanSmem& sm, const skv_decode_desc
 #pragma unroll
   for (int g = 0; g < SKV_MAX_GROUPS; ++g) {
     if (g >= ng) continue;
-    if (top[g] < 0 || top[g] > d->groups[g].n_pages) bad |= SKV_STATUS_BADARG;
+    if (top[g] < 0 || top[g] > map.n_pages[g]) bad |= SKV_STATUS_BADARG;
     else if (tot[g] > top[g]) bad |= SKV_STATUS_NOSPC;
   }
   P.bad = bad;
@@ -172,19 +193,18 @@ __device__ __forceinline__ OwnPlan step_plan(PlanSmem& sm, const skv_decode_desc
   if (write_tops && tid == 0) {
 #pragma unroll
     for (int g = 0; g < SKV_MAX_GROUPS; ++g) {
-      if (g < ng) d->step_top[g] = top[g] - tot[g];
+      if (g < ng) map.step_top[g] = top[g] - tot[g];
     }
   }
 #pragma unroll
   for (int g = 0; g < SKV_MAX_GROUPS; ++g) {
     if (g == g_own) {
-      const skv_page_group& G = d->groups[g];
-      const uint32_t c0 = static_cast<uint32_t>(G.n_entries[b]);
-      const uint32_t target = udiv24(static_cast<uint32_t>(d->tok_lens[b] + 1), G.m);
+      const uint32_t c0 = static_cast<uint32_t>(own_cur);
+      const uint32_t target = udiv24(static_cast<uint32_t>(P.len + 1), map.m[g]);
       P.top = top[g];
       P.off = pre[g];
-      P.p0 = static_cast<int>(ceil_div24(c0, G.block_size));
-      P.need = static_cast<int>(ceil_div24(target, G.block_size)) - P.p0;
+      P.p0 = static_cast<int>(ceil_div24(c0, map.block_size[g]));
+      P.need = static_cast<int>(ceil_div24(target, map.block_size[g])) - P.p0;
     }
   }
   return P;
@@ -329,10 +349,10 @@ __global__ __launch_bounds__(kStepThreads) void k_decode_append(const skv_decode
     const int b = static_cast<int>(ub - uc * map.batch);
     const skv_decode_layer* Ly = csa_layer(d, map, static_cast<int>(uc));
     if (!Ly) return;
-    int32_t* ws = Ly->topk_ws + static_cast<int64_t>(b) * kTkWsWords;
+    int32_t* ws = map.topk_ws[uc] + static_cast<int64_t>(b) * kTkWsWords;
     if (chunk == 0 && tid < 3) ws[kTkWsCnt + tid] = 0;
     int n_cols, n_valid;
-    score_cols(*Ly, d->groups[Ly->group].m, d->tok_lens[b] + 1, n_cols, n_valid);
+    score_cols(*Ly, map.m[map.group[(map.csa >> (4 * uc)) & 15]], map.tok_lens[b] + 1, n_cols, n_valid);
     topk_hist_chunk(sm.hist, Ly->scores + static_cast<int64_t>(b) * Ly->score_stride, n_cols, n_valid,
                     Ly->top_k, chunk, ws);
     return;
@@ -352,15 +372,16 @@ __global__ __launch_bounds__(kStepThreads) void k_decode_append(const skv_decode
     fold_load(first, main_stream ? Ly.state : Ly.idx_state, main_stream ? Ly.c_new : Ly.ci_new,
               main_stream ? Ly.z_new : Ly.zi_new, b, channels, min(t, (channels >> 3) - 1));
   }
-  const OwnPlan P = step_plan(sm.plan, d, b, paged ? Ly.group : -1, blockIdx.x == 0);
+  const int g = map.group[l];  // < 0 for an SWA layer
+  const OwnPlan P = step_plan(sm.plan, map, b, g, blockIdx.x == 0);
   if (P.bad) {
-    if (blockIdx.x == 0 && tid == 0) *d->status = P.bad;
+    if (blockIdx.x == 0 && tid == 0) *map.status = P.bad;
     return;  // refused: nothing changes
   }
-  if (blockIdx.x == 0 && tid == 0) *d->status = 0;
-  const int L0 = d->tok_lens[b];
+  if (blockIdx.x == 0 && tid == 0) *map.status = 0;
+  const int L0 = P.len;
   const int64_t p = L0;  // position of the new token
-  if (l == 0 && tid == 0) d->step_lens[b] = L0 + 1;
+  if (l == 0 && tid == 0) map.step_lens[b] = L0 + 1;
   if (wave == 3) {
     const int row_chunks = d->latent >> 3;  // 16-byte chunks of a bf16 row
     const u32x4* src = static_cast<const u32x4*>(Ly.kv_new) + static_cast<int64_t>(b) * row_chunks;
@@ -369,35 +390,30 @@ __global__ __launch_bounds__(kStepThreads) void k_decode_append(const skv_decode
     return;
   }
   if (!paged) return;
-  const skv_page_group& G = d->groups[Ly.group];
+  const int m = map.m[g], bs = map.block_size[g];
+  int32_t* const bt_row = map.block_table[g] + static_cast<int64_t>(b) * map.bt_stride[g];
+  const int32_t* const stack = map.free_stack[g];
   // the group's first layer records the sequence's new pages in the table
-  bool first_layer = true;
-  for (int li = 0; li < l; ++li) {
-    if (d->layers[li].kind != SKV_LAYER_SWA && d->layers[li].group == Ly.group) first_layer = false;
-  }
-  if (first_layer && tid < P.need) {
-    G.block_table[b * G.bt_stride + P.p0 + tid] = G.free_stack[P.top - 1 - P.off - tid];
-  }
+  if (((map.group_first >> l) & 1) && tid < P.need) bt_row[P.p0 + tid] = stack[P.top - 1 - P.off - tid];
   // the page of the entry this token completes, if any (its load overlaps the fold)
-  const uint32_t e1 = udiv24(static_cast<uint32_t>(p + 1), G.m);  // entries after the token
+  const uint32_t e1 = udiv24(static_cast<uint32_t>(p + 1), m);  // entries after the token
   const uint32_t e = e1 > 0 ? e1 - 1 : 0;
-  const int pi = static_cast<int>(udiv24(e, G.block_size));
+  const int pi = static_cast<int>(udiv24(e, bs));
   int32_t page = -1;
-  if (e1 * G.m == static_cast<uint32_t>(p + 1)) {  // uniform
-    if (pi < P.p0) page = G.block_table[b * G.bt_stride + pi];
-    else if (pi - P.p0 < P.need) page = G.free_stack[P.top - 1 - P.off - (pi - P.p0)];
+  if (e1 * m == static_cast<uint32_t>(p + 1)) {  // uniform
+    if (pi < P.p0) page = bt_row[pi];
+    else if (pi - P.p0 < P.need) page = stack[P.top - 1 - P.off - (pi - P.p0)];
   }
-  const int in_page = static_cast<int>(e) - pi * G.block_size;
+  const int in_page = static_cast<int>(e) - pi * bs;
   if (main_stream) {
     const int fp8_main = (Ly.format == SKV_FMT_FP8) ? d->latent - SKV_FP8_ROPE_DIMS : 0;
-    const EmitSlot slot{static_cast<uint8_t*>(Ly.pool), Ly.entry_bytes, page, static_cast<int32_t>(G.n_pages),
-                        G.block_size, in_page};
-    decode_fold_part(G.m, b, p, slot, Ly.state, Ly.bias, Ly.c_new, Ly.z_new, d->latent, Ly.format, fp8_main,
+    const EmitSlot slot{static_cast<uint8_t*>(Ly.pool), Ly.entry_bytes, page, map.n_pages[g], bs, in_page};
+    decode_fold_part(m, b, p, slot, Ly.state, Ly.bias, Ly.c_new, Ly.z_new, d->latent, Ly.format, fp8_main,
                      tid, 2 * kWave, first);
   } else if (idx_stream) {
     const EmitSlot slot{static_cast<uint8_t*>(Ly.idx_pool), static_cast<int64_t>(d->c_indexer) * 2, page,
-                        static_cast<int32_t>(G.n_pages), G.block_size, in_page};
-    decode_fold_part(G.m, b, p, slot, Ly.idx_state, Ly.idx_bias, Ly.ci_new, Ly.zi_new, d->c_indexer,
+                        map.n_pages[g], bs, in_page};
+    decode_fold_part(m, b, p, slot, Ly.idx_state, Ly.idx_bias, Ly.ci_new, Ly.zi_new, d->c_indexer,
                      SKV_FMT_BF16, 0, tid - 2 * kWave, kWave, first);
   }
 }
@@ -506,13 +522,13 @@ __device__ __forceinline__ void copy_rows(int n, RowFn row, int latent, bool fp8
 // and its address, or 0 when e is past n_ent or its page is not mapped.
 // The first n_lds entries of the sequence's block-table row may be staged
 // in LDS (bt_lds).
-__device__ __forceinline__ int entry_source(const skv_page_group& G, const skv_decode_layer& Ly, int b, int e,
+__device__ __forceinline__ int entry_source(const GroupRef& G, const skv_decode_layer& Ly, int b, int e,
                                             int n_ent, const uint8_t** src, const int32_t* bt_lds = nullptr,
                                             int n_lds = 0) {
   if (e < 0 || e >= n_ent) return 0;
   const int pi = static_cast<int>(udiv24(e, G.block_size));  // e < 2^24
   const int32_t page = (pi < n_lds) ? bt_lds[pi]
-                       : (pi < G.bt_stride) ? G.block_table[b * G.bt_stride + pi] : -1;
+                       : (pi < G.bt_stride) ? G.block_table[static_cast<int64_t>(b) * G.bt_stride + pi] : -1;
   if (page < 0 || page >= G.n_pages) return 0;
   *src = static_cast<const uint8_t*>(Ly.pool) +
          (static_cast<int64_t>(page) * G.block_size + (e - pi * G.block_size)) * Ly.entry_bytes;
@@ -625,10 +641,10 @@ __device__ __forceinline__ void dense_block(const skv_decode_desc* d, const Step
   if (*map.status) return;  // refused step
   const skv_decode_layer& Ly = d->layers[l];
   if (l == 0 && tile == 0 && threadIdx.x == 0) {
-    d->tok_lens[b] = L;
-    for (int gg = 0; gg < d->n_groups; ++gg) d->groups[gg].n_entries[b] = udiv24(L, d->groups[gg].m);
+    map.tok_lens[b] = L;
+    for (int gg = 0; gg < map.n_groups; ++gg) map.n_entries[gg][b] = udiv24(L, map.m[gg]);
     if (b == 0) {
-      for (int gg = 0; gg < d->n_groups; ++gg) *d->groups[gg].free_top = d->step_top[gg];
+      for (int gg = 0; gg < map.n_groups; ++gg) *map.free_top[gg] = map.step_top[gg];
     }
   }
   const int latent = d->latent;
@@ -637,8 +653,8 @@ __device__ __forceinline__ void dense_block(const skv_decode_desc* d, const Step
   RowRef rf{nullptr, nullptr, 0};
   if (r < n_dense) {
     // dense HCA rows past the entries stay untouched
-    const skv_page_group& G = d->groups[gi];
-    if (r < static_cast<int>(udiv24(L, G.m)) && pi < map.bt_stride[gi] && page >= 0 && page < G.n_pages) {
+    if (r < static_cast<int>(udiv24(L, map.m[gi])) && pi < map.bt_stride[gi] && page >= 0 &&
+        page < map.n_pages[gi]) {
       rf.src = static_cast<const uint8_t*>(Ly.pool) +
                (static_cast<int64_t>(page) * bs + (r - pi * bs)) * Ly.entry_bytes;
       rf.dst = static_cast<uint8_t*>(Ly.out_entries) + (static_cast<int64_t>(b) * Ly.out_rows + r) * out_row;
@@ -775,13 +791,12 @@ __device__ __forceinline__ void rank_candidates(RankRows& rr, KeyAt ck, int S, i
 // Adds the fills [f0, o1), writes the indices and copies every collected row.
 // n_rows: rows collected so far (read after a barrier by the caller).
 __device__ __forceinline__ void finish_rows(RankRows& rr, int n_rows, int f0, int o1,
-                                            const skv_decode_desc* d, const skv_decode_layer& Ly, int b, int L,
-                                            const int32_t* bt_lds, int n_lds) {
+                                            const skv_decode_desc* d, const skv_decode_layer& Ly,
+                                            const GroupRef& G, int b, int L, const int32_t* bt_lds, int n_lds) {
   const int tid = threadIdx.x;
   if (tid < o1 - f0) rr.win[n_rows + tid] = make_int2(f0 + tid, -1);
   n_rows += max(0, o1 - f0);
   __syncthreads();
-  const skv_page_group& G = d->groups[Ly.group];
   const int n_ent = static_cast<int>(udiv24(L, G.m));
   const int k = Ly.top_k;
   const int64_t out_row = static_cast<int64_t>(d->latent) * 2;
@@ -826,7 +841,7 @@ __global__ __launch_bounds__(kStepThreads) void k_decode_filter(const skv_decode
     const int L = map.step_lens[b];  // loaded with the status: one round trip
     if (*map.status) return;         // refused step
     int n_cols, n_valid;
-    score_cols(*Ly, d->groups[Ly->group].m, L, n_cols, n_valid);
+    score_cols(*Ly, map.m[map.group[(map.csa >> (4 * uc)) & 15]], L, n_cols, n_valid);
     topk_filter_chunk(sm, Ly->scores + static_cast<int64_t>(b) * Ly->score_stride, n_cols, n_valid,
                       Ly->top_k, chunk, Ly->topk_ws + static_cast<int64_t>(b) * kTkWsWords);
   }
@@ -898,7 +913,7 @@ __device__ __forceinline__ void rank_part(const skv_decode_desc* __restrict__ d,
   const int k = Ly.top_k;
   const int parts = static_cast<int>(ceil_div24(k, rank_out));
   if (part >= parts) return;  // the grid is sized for the largest top_k
-  const skv_page_group& G = d->groups[gi];
+  const GroupRef G = group_ref(map, gi);
   if (part == 0) {
     for (int i = tid; i < kTkBins; i += kStepThreads) ws[kTkWsHist + i] = 0;
   }
@@ -920,7 +935,7 @@ __device__ __forceinline__ void rank_part(const skv_decode_desc* __restrict__ d,
     __syncthreads();
     if (tid < o1 - o0) sm.rr.win[tid] = make_int2(o0 + tid, fb.order[o0 + tid]);
     __syncthreads();
-    finish_rows(sm.rr, o1 - o0, o1, o1, d, Ly, b, L, sm_bt, n_bt);
+    finish_rows(sm.rr, o1 - o0, o1, o1, d, Ly, G, b, L, sm_bt, n_bt);
     return;
   }
   if (sel > 0) {
@@ -988,14 +1003,15 @@ __device__ __forceinline__ void rank_part(const skv_decode_desc* __restrict__ d,
                                               (static_cast<int64_t>(b) * k + pos) * out_row,
                                    kind, d->latent, fp8);
       }
-      finish_rows(sm.rr, sm.rr.n_rows, max(o0, sel), o1, d, Ly, b, L, sm_bt, n_bt);  // the rest and the fills
+      // the other winners and the fills
+      finish_rows(sm.rr, sm.rr.n_rows, max(o0, sel), o1, d, Ly, G, b, L, sm_bt, n_bt);
       return;
     }
     if (in_lds) rank_candidates(sm.rr, lds_key, S, C, sel, part, parts);
     else rank_candidates(sm.rr, global_key, S, C, sel, part, parts);
   }
   __syncthreads();
-  finish_rows(sm.rr, sm.rr.n_rows, max(o0, sel), o1, d, Ly, b, L, sm_bt, n_bt);
+  finish_rows(sm.rr, sm.rr.n_rows, max(o0, sel), o1, d, Ly, G, b, L, sm_bt, n_bt);
 }
 
 // Blocks of the gather launch: rank part i (parts_max x batch x CSA layers
@@ -1082,23 +1098,39 @@ extern "C" int skv_decode_step(const skv_decode_desc* h, const skv_decode_desc* 
         G.block_size <= 0 || G.bt_stride <= 0 || G.n_pages <= 0) {
       return set_error(SKV_EINVAL, "%s: page group %d is incomplete", what, g);
     }
-    if (G.bt_stride >= (1 << 24)) return set_error(SKV_EINVAL, "%s: page group %d bt_stride >= 2^24", what, g);
+    if (G.bt_stride >= (1 << 24) || G.n_pages > 0x7fffffff) {
+      return set_error(SKV_EINVAL, "%s: page group %d needs bt_stride < 2^24 and n_pages < 2^31", what, g);
+    }
   }
   StepMap map{};
   map.batch = h->batch;
   map.n_layers = h->n_layers;
-  map.step_lens = h->step_lens;
+  map.n_groups = h->n_groups;
+  map.tok_lens = h->tok_lens;
   map.status = h->status;
+  map.step_lens = h->step_lens;
+  map.step_top = h->step_top;
   for (int g = 0; g < SKV_MAX_GROUPS; ++g) {
-    map.block_table[g] = g < h->n_groups ? h->groups[g].block_table : nullptr;
-    map.bt_stride[g] = g < h->n_groups ? static_cast<int32_t>(h->groups[g].bt_stride) : 1;
-    map.block_size[g] = g < h->n_groups ? h->groups[g].block_size : 1;
+    const bool used = g < h->n_groups;
+    map.block_table[g] = used ? h->groups[g].block_table : nullptr;
+    map.n_entries[g] = used ? h->groups[g].n_entries : nullptr;
+    map.free_stack[g] = used ? h->groups[g].free_stack : nullptr;
+    map.free_top[g] = used ? h->groups[g].free_top : nullptr;
+    map.bt_stride[g] = used ? static_cast<int32_t>(h->groups[g].bt_stride) : 1;
+    map.block_size[g] = used ? h->groups[g].block_size : 1;
+    map.m[g] = used ? h->groups[g].m : 1;
+    map.n_pages[g] = used ? static_cast<int32_t>(h->groups[g].n_pages) : 1;
   }
+  uint32_t groups_seen = 0;
   int n_csa = 0, max_top_k = 0;
   int64_t max_score_cols = 1, n_tiles = 0;
   for (int l = 0; l < h->n_layers; ++l) {
     const skv_decode_layer& Ly = h->layers[l];
     map.group[l] = (Ly.kind == SKV_LAYER_SWA) ? -1 : static_cast<int8_t>(Ly.group);
+    if (Ly.kind != SKV_LAYER_SWA && Ly.group >= 0 && Ly.group < SKV_MAX_GROUPS && !((groups_seen >> Ly.group) & 1)) {
+      groups_seen |= 1u << Ly.group;
+      map.group_first |= 1u << l;
+    }
     if (!Ly.ring || !Ly.kv_new || !Ly.out_window) return set_error(SKV_EINVAL, "%s: layer %d lacks ring/kv_new/out_window", what, l);
     int64_t dense = h->window;
     if (Ly.kind == SKV_LAYER_HCA || Ly.kind == SKV_LAYER_CSA) {
