@@ -1,8 +1,9 @@
 // Fused decode step over a stack of heterogeneous layers in three launches,
-// whatever the number of layers:
+//   hist   : top-k histogram chunks of the CSA layers' score rows
 //   append : step page plan (computed by every workgroup) + SWA ring rows +
-//            pooling fold / entry emission + top-k histogram chunks
-//   filter : top-k candidate lists
+//            pooling fold / entry emission, beside the top-k filter chunks
+//            (candidate lists); the top-k of a step reads no output of its
+//            append, so it runs ahead of it
 //   gather : per (CSA layer, sequence, part) ordering of the candidates and
 //            the sparse gather of the winners' entries, interleaved with the
 //            dense HCA / window copies and the commit of the step's lengths
@@ -56,7 +57,11 @@ struct StepMap {
   int32_t block_size[SKV_MAX_GROUPS];
   int32_t m[SKV_MAX_GROUPS];
   int32_t n_pages[SKV_MAX_GROUPS];
-  int32_t* topk_ws[SKV_MAX_LAYERS];   // of the i-th CSA layer
+  // of the i-th CSA layer
+  int32_t* topk_ws[SKV_MAX_LAYERS];
+  const float* scores[SKV_MAX_LAYERS];
+  int32_t score_stride[SKV_MAX_LAYERS];
+  int32_t top_k[SKV_MAX_LAYERS];
 };
 static_assert(SKV_MAX_LAYERS <= 16, "CSA layer indices are 4-bit fields");
 
@@ -79,10 +84,26 @@ __device__ __forceinline__ const skv_decode_layer* csa_layer(const skv_decode_de
 // Score columns of a CSA query at length L (entries L/m; the causal mask
 // keeps (L-1)/m of them), clamped to the row's width so that no length can
 // send a read past the row.
-__device__ __forceinline__ void score_cols(const skv_decode_layer& Ly, int m, int L, int& n_cols, int& n_valid) {
+__device__ __forceinline__ void score_cols(int64_t score_stride, int m, int L, int& n_cols, int& n_valid) {
   const uint32_t Lc = static_cast<uint32_t>(min(max(L, 0), kMaxTokLen));
-  n_cols = static_cast<int>(min<int64_t>(udiv24(Lc, m), Ly.score_stride));
-  n_valid = Lc > 0 ? static_cast<int>(min<int64_t>(udiv24(Lc - 1, m), Ly.score_stride)) : 0;
+  n_cols = static_cast<int>(min<int64_t>(udiv24(Lc, m), score_stride));
+  n_valid = Lc > 0 ? static_cast<int>(min<int64_t>(udiv24(Lc - 1, m), score_stride)) : 0;
+}
+
+__device__ __forceinline__ void score_cols(const skv_decode_layer& Ly, int m, int L, int& n_cols, int& n_valid) {
+  score_cols(Ly.score_stride, m, L, n_cols, n_valid);
+}
+
+// Top-k chunk u of a launch: (chunk, sequence, CSA layer), chunk fastest.
+struct TopkChunk {
+  int chunk, b, z;
+};
+
+__device__ __forceinline__ TopkChunk topk_chunk(uint32_t u, int n_chunks, const StepMap& map) {
+  const uint32_t ub = udiv24(u, n_chunks);
+  const uint32_t uz = udiv24(ub, map.batch);
+  return TopkChunk{static_cast<int>(u - ub * n_chunks), static_cast<int>(ub - uz * map.batch),
+                   static_cast<int>(uz)};
 }
 
 // ---------------------------------------------------------------------------
@@ -216,7 +237,8 @@ __device__ __forceinline__ OwnPlan step_plan(PlanSmem& sm, const StepMap& map, i
 //                                      fold the main stream, wave 2 the
 //                                      indexer stream, wave 3 copies the ring
 //                                      row;
-//    then                            : top-k histogram chunks.
+//    then                            : top-k filter chunks (after the hist
+//                                      launch).
 // ---------------------------------------------------------------------------
 
 // Raw inputs of one 8-channel group of a stream: running state (max, sum,
@@ -327,9 +349,31 @@ __device__ __forceinline__ void decode_fold_part(int m, int b, int64_t p, const 
   }
 }
 
+// Score row extent of chunk c's sequence after the step (tokens + 1): the
+// top-k of the step runs beside the append, which a refusal discards.
+__device__ __forceinline__ void chunk_cols(const StepMap& map, const TopkChunk& c, int& n_cols, int& n_valid) {
+  score_cols(map.score_stride[c.z], map.m[map.group[(map.csa >> (4 * c.z)) & 15]], map.tok_lens[c.b] + 1, n_cols,
+             n_valid);
+}
+
+// Hist launch: top-k histogram chunks (the grid holds n_chunks x batch x CSA
+// layers blocks).  Chunk 0 zeroes the row's list counters, which the previous
+// step's gather launch read; the gather launch zeroes the histogram again,
+// also after a refusal.
+__global__ __launch_bounds__(kTkPartThreads) void k_decode_hist(int n_chunks, StepMap map) {
+  __shared__ TopkHistSmem sm;
+  const TopkChunk c = topk_chunk(blockIdx.x, n_chunks, map);
+  int32_t* ws = map.topk_ws[c.z] + static_cast<int64_t>(c.b) * kTkWsWords;
+  if (c.chunk == 0 && threadIdx.x < 3) ws[kTkWsCnt + threadIdx.x] = 0;
+  const int width = map.score_stride[c.z];
+  topk_hist_chunk_at(
+      sm, map.scores[c.z] + static_cast<int64_t>(c.b) * width, width,
+      [&](int& n_cols, int& n_valid) { chunk_cols(map, c, n_cols, n_valid); }, map.top_k[c.z], c.chunk, ws);
+}
+
 union AppendSmem {
   PlanSmem plan;
-  TopkHistSmem hist;
+  TopkFilterSmem filter;
 };
 
 __global__ __launch_bounds__(kStepThreads) void k_decode_append(const skv_decode_desc* __restrict__ d,
@@ -338,23 +382,13 @@ __global__ __launch_bounds__(kStepThreads) void k_decode_append(const skv_decode
   const int n_append = map.batch * map.n_layers;
   const int tid = threadIdx.x;
   if (static_cast<int>(blockIdx.x) >= n_append) {
-    // top-k histogram chunk (chunk, b, csa layer).  It assumes the step
-    // goes ahead; on a refusal the gather launch still clears
-    // the histogram.  Chunk 0 zeroes the row's list counters, which the
-    // previous step's gather launch read.
-    const uint32_t u = blockIdx.x - n_append;  // grids stay below 2^24 workgroups
-    const uint32_t ub = udiv24(u, n_chunks);
-    const int chunk = static_cast<int>(u - ub * n_chunks);
-    const uint32_t uc = udiv24(ub, map.batch);
-    const int b = static_cast<int>(ub - uc * map.batch);
-    const skv_decode_layer* Ly = csa_layer(d, map, static_cast<int>(uc));
-    if (!Ly) return;
-    int32_t* ws = map.topk_ws[uc] + static_cast<int64_t>(b) * kTkWsWords;
-    if (chunk == 0 && tid < 3) ws[kTkWsCnt + tid] = 0;
-    int n_cols, n_valid;
-    score_cols(*Ly, map.m[map.group[(map.csa >> (4 * uc)) & 15]], map.tok_lens[b] + 1, n_cols, n_valid);
-    topk_hist_chunk(sm.hist, Ly->scores + static_cast<int64_t>(b) * Ly->score_stride, n_cols, n_valid,
-                    Ly->top_k, chunk, ws);
+    // top-k filter chunk: candidate lists from the complete histogram
+    const TopkChunk c = topk_chunk(blockIdx.x - n_append, n_chunks, map);
+    const int width = map.score_stride[c.z];
+    topk_filter_chunk_at(
+        sm.filter, map.scores[c.z] + static_cast<int64_t>(c.b) * width, width,
+        [&](int& n_cols, int& n_valid) { chunk_cols(map, c, n_cols, n_valid); }, map.top_k[c.z], c.chunk,
+        map.topk_ws[c.z] + static_cast<int64_t>(c.b) * kTkWsWords);
     return;
   }
   const int l = static_cast<int>(udiv24(blockIdx.x, map.batch));
@@ -821,32 +855,12 @@ __device__ __forceinline__ void finish_rows(RankRows& rr, int n_rows, int f0, in
 }
 
 // ---------------------------------------------------------------------------
-// 5. filter launch (top-k filter chunks, see skv_topk.h) and gather launch
-//    (rank parts, each loading its row's candidate lists, ranking and
-//    gathering, interleaved with the dense tiles, whose copies keep HBM busy
-//    while the rank parts wait on their round trips).  Part 0 of a row
-//    zeroes the row's histogram for the next step, also after a refusal.
+// 5. gather launch: rank parts, each loading its row's candidate lists,
+//    ranking and gathering, interleaved with the dense tiles, whose copies
+//    keep HBM busy while the rank parts wait on their round trips.  Part 0
+//    of a row zeroes the row's histogram for the next step, also after a
+//    refusal.
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(kStepThreads) void k_decode_filter(const skv_decode_desc* __restrict__ d,
-                                                                int n_chunks, StepMap map) {
-  __shared__ TopkFilterSmem sm;
-  const int u = blockIdx.x;  // the grid holds n_chunks x batch x CSA layers blocks
-  {
-    const uint32_t ub = udiv24(u, n_chunks);
-    const int chunk = static_cast<int>(u - ub * n_chunks);
-    const uint32_t uc = udiv24(ub, map.batch);
-    const int b = static_cast<int>(ub - uc * map.batch);
-    const skv_decode_layer* Ly = csa_layer(d, map, static_cast<int>(uc));
-    if (!Ly) return;  // uniform over the workgroup
-    const int L = map.step_lens[b];  // loaded with the status: one round trip
-    if (*map.status) return;         // refused step
-    int n_cols, n_valid;
-    score_cols(*Ly, map.m[map.group[(map.csa >> (4 * uc)) & 15]], L, n_cols, n_valid);
-    topk_filter_chunk(sm, Ly->scores + static_cast<int64_t>(b) * Ly->score_stride, n_cols, n_valid,
-                      Ly->top_k, chunk, Ly->topk_ws + static_cast<int64_t>(b) * kTkWsWords);
-  }
-}
-
 constexpr int kRankHead = 2 * kStepThreads;  // entries of each candidate list fetched with the counters
 constexpr int kRankBt = 16 * kStepThreads;   // most block-table entries of a sequence staged in LDS
 constexpr int kRankPf = kStepThreads / 8;    // own candidates whose entries are loaded before ranking
@@ -1152,8 +1166,14 @@ extern "C" int skv_decode_step(const skv_decode_desc* h, const skv_decode_desc* 
         if (Ly.idx_pool && (!Ly.idx_state || !Ly.idx_bias || !Ly.ci_new || !Ly.zi_new || h->c_indexer <= 0)) {
           return set_error(SKV_EINVAL, "%s: CSA layer %d indexer stream incomplete", what, l);
         }
+        if (Ly.score_stride >= (1 << 24)) {
+          return set_error(SKV_EINVAL, "%s: CSA layer %d score_stride >= 2^24", what, l);
+        }
         map.csa |= static_cast<uint64_t>(l) << (4 * n_csa);
         map.topk_ws[n_csa] = Ly.topk_ws;
+        map.scores[n_csa] = Ly.scores;
+        map.score_stride[n_csa] = static_cast<int32_t>(Ly.score_stride);
+        map.top_k[n_csa] = Ly.top_k;
         ++n_csa;
         max_top_k = max(max_top_k, Ly.top_k);
       } else {
@@ -1180,26 +1200,26 @@ extern "C" int skv_decode_step(const skv_decode_desc* h, const skv_decode_desc* 
   const int n_chunks = static_cast<int>(ceil_div(max_score_cols, kTkChunk));
   const int64_t n_append = static_cast<int64_t>(h->batch) * h->n_layers +
                            static_cast<int64_t>(n_chunks) * h->batch * n_csa;
-  const int64_t n_filter = static_cast<int64_t>(n_chunks) * h->batch * n_csa;
+  const int64_t n_hist = static_cast<int64_t>(n_chunks) * h->batch * n_csa;
   // smaller parts when the rows alone would leave most CUs idle
   const int rank_out = (static_cast<int64_t>(h->batch) * n_csa * ceil_div(max_top_k, kRankOut) < 512)
                            ? kRankOutMin : kRankOut;
   const int64_t parts_max = ceil_div(max_top_k, rank_out);
   const int64_t n_rank = parts_max * h->batch * n_csa;
   const int64_t n_gather = n_rank + n_tiles;
-  if (n_append >= (1 << 24) || n_filter >= (1 << 24) || n_gather >= (1 << 24)) {
+  if (n_append >= (1 << 24) || n_gather >= (1 << 24)) {
     return set_error(SKV_EINVAL, "%s: score_stride/out_rows give a grid of 2^24 workgroups or more", what);
   }
   hipStream_t s = static_cast<hipStream_t>(stream);
-  hipLaunchKernelGGL(k_decode_append, dim3(static_cast<unsigned>(n_append)), dim3(kStepThreads), 0, s, dd,
-                     n_chunks, map);
-  int rc = check_launch(what);
-  if (rc) return rc;
-  if (n_filter > 0) {
-    hipLaunchKernelGGL(k_decode_filter, dim3(static_cast<unsigned>(n_filter)), dim3(kStepThreads), 0, s, dd,
-                       n_chunks, map);
+  int rc;
+  if (n_hist > 0) {
+    hipLaunchKernelGGL(k_decode_hist, dim3(static_cast<unsigned>(n_hist)), dim3(kTkPartThreads), 0, s, n_chunks,
+                       map);
     if ((rc = check_launch(what))) return rc;
   }
+  hipLaunchKernelGGL(k_decode_append, dim3(static_cast<unsigned>(n_append)), dim3(kStepThreads), 0, s, dd,
+                     n_chunks, map);
+  if ((rc = check_launch(what))) return rc;
   GatherGrid gg;
   gg.n_rank = static_cast<int32_t>(n_rank);
   gg.parts_max = static_cast<int32_t>(parts_max);

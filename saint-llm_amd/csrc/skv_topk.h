@@ -196,18 +196,25 @@ struct TopkHistSmem {
   int hist[kTkBins];
 };
 
-__device__ __forceinline__ void topk_hist_chunk(TopkHistSmem& sm, const float* row, int n_cols,
-                                                int n_valid, int k, int chunk, int32_t* ws) {
+// row holds at least `width` (>= 1) readable scores; cols(n_cols, n_valid)
+// gives the row's extent.  The score loads (indices clamped into the row,
+// all in flight together) are issued before cols is called, so that a
+// caller's loads of the extent overlap them.
+template <class Cols>
+__device__ __forceinline__ void topk_hist_chunk_at(TopkHistSmem& sm, const float* row, int width, Cols cols,
+                                                   int k, int chunk, int32_t* ws) {
   const int tid = threadIdx.x;
+  const int i0 = chunk * kTkChunk;
+  constexpr int kPer = kTkChunk / kTkPartThreads;
+  float f[kPer];
+#pragma unroll
+  for (int q = 0; q < kPer; ++q) f[q] = row[min(i0 + q * kTkPartThreads + tid, width - 1)];
+  int n_cols, n_valid;
+  cols(n_cols, n_valid);
   if (topk_sel(k, n_cols, n_valid) == 0) return;  // uniform
   n_valid = max(0, min(n_valid, n_cols));
-  const int i0 = chunk * kTkChunk;
   const int i1 = min(n_valid, i0 + kTkChunk);
   if (i0 >= i1) return;
-  constexpr int kPer = kTkChunk / kTkPartThreads;
-  float f[kPer];  // unconditional loads (clamped index), all in flight together
-#pragma unroll
-  for (int q = 0; q < kPer; ++q) f[q] = row[min(i0 + q * kTkPartThreads + tid, i1 - 1)];
   for (int b = tid; b < kTkBins; b += kTkPartThreads) sm.hist[b] = 0;
   __syncthreads();
 #pragma unroll
@@ -218,6 +225,18 @@ __device__ __forceinline__ void topk_hist_chunk(TopkHistSmem& sm, const float* r
   for (int b = tid; b < kTkBins; b += kTkPartThreads) {
     if (sm.hist[b]) atomicAdd(&ws[kTkWsHist + b], sm.hist[b]);
   }
+}
+
+__device__ __forceinline__ void topk_hist_chunk(TopkHistSmem& sm, const float* row, int n_cols,
+                                                int n_valid, int k, int chunk, int32_t* ws) {
+  if (topk_sel(k, n_cols, n_valid) == 0) return;  // uniform; otherwise at least one valid score
+  topk_hist_chunk_at(
+      sm, row, max(0, min(n_valid, n_cols)),
+      [&](int& c, int& v) {
+        c = n_cols;
+        v = n_valid;
+      },
+      k, chunk, ws);
 }
 
 // Threshold bin of rank sel from the row histogram (every thread gets it).
@@ -256,17 +275,18 @@ __device__ __forceinline__ void topk_threshold(const int* hist, int sel, int* sc
   __syncthreads();
 }
 
-// Stages the kTkBins-word row histogram in LDS (16-byte aligned).  Each of
-// the first kTkBins/8 threads copies two 16-byte pieces, both loads issued
-// before either LDS store.
-__device__ __forceinline__ void load_hist(int* lds, const int32_t* g) {
-  constexpr int kHalf = kTkBins / 8;  // threads taking part; each moves 2 x int4
-  if (threadIdx.x < kHalf) {
-    const int4 a = reinterpret_cast<const int4*>(g)[threadIdx.x];
-    const int4 b = reinterpret_cast<const int4*>(g)[threadIdx.x + kHalf];
-    reinterpret_cast<int4*>(lds)[threadIdx.x] = a;
-    reinterpret_cast<int4*>(lds)[threadIdx.x + kHalf] = b;
-  }
+// Stages the kTkBins-word row histogram in LDS (16-byte aligned): each of
+// kTkBins/8 threads (a 256-thread workgroup) fetches two 16-byte pieces and
+// later puts them, so that other loads can be issued in between.
+constexpr int kTkHistHalf = kTkBins / 8;
+static_assert(kTkHistHalf == kTkPartThreads, "one thread per hist piece pair");
+__device__ __forceinline__ void hist_fetch(int4& a, int4& b, const int32_t* g) {
+  a = reinterpret_cast<const int4*>(g)[threadIdx.x];
+  b = reinterpret_cast<const int4*>(g)[threadIdx.x + kTkHistHalf];
+}
+__device__ __forceinline__ void hist_put(int* lds, const int4& a, const int4& b) {
+  reinterpret_cast<int4*>(lds)[threadIdx.x] = a;
+  reinterpret_cast<int4*>(lds)[threadIdx.x + kTkHistHalf] = b;
 }
 
 struct TopkFilterSmem {
@@ -284,30 +304,37 @@ struct TopkFilterSmem {
 // scores are loaded before the histogram is read, so the two memory
 // latencies overlap.  A tie bin above kTkTieCap is flagged in ws[kTkWsFlag]
 // by chunk 0 and no list is written.
-__device__ __forceinline__ void topk_filter_chunk(TopkFilterSmem& sm, const float* row, int n_cols,
-                                                  int n_valid, int k, int chunk, int32_t* ws) {
+// row / width / cols as for topk_hist_chunk_at: the score and histogram
+// loads are issued before the row's extent is known.
+template <class Cols>
+__device__ __forceinline__ void topk_filter_chunk_at(TopkFilterSmem& sm, const float* row, int width, Cols cols,
+                                                     int k, int chunk, int32_t* ws) {
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
   const int wid = tid / kWave;
   constexpr int kWaves = kTkPartThreads / kWave;
   constexpr int kRun = kTkChunk / kWaves;  // each wave owns a contiguous run of scores
   constexpr int kPer = kRun / kWave;
-  const int sel = topk_sel(k, n_cols, n_valid);
-  if (sel == 0) return;  // uniform
-  n_valid = max(0, min(n_valid, n_cols));
   const int i0 = chunk * kTkChunk;
-  const int i1 = min(n_valid, i0 + kTkChunk);
-  if (i0 >= i1) return;
   const int r0 = i0 + wid * kRun;
-  // unconditional loads (index clamped into the chunk) so that all of them
+  // unconditional loads (index clamped into the row) so that all of them
   // are in flight together; lanes past the chunk drop the value
   float f[kPer];
 #pragma unroll
-  for (int q = 0; q < kPer; ++q) f[q] = row[min(r0 + q * kWave + lane, i1 - 1)];
+  for (int q = 0; q < kPer; ++q) f[q] = row[min(r0 + q * kWave + lane, width - 1)];
+  int4 ha, hb;
+  hist_fetch(ha, hb, ws + kTkWsHist);
+  int n_cols, n_valid;
+  cols(n_cols, n_valid);
+  hist_put(sm.hist, ha, hb);
+  const int sel = topk_sel(k, n_cols, n_valid);
+  if (sel == 0) return;  // uniform
+  n_valid = max(0, min(n_valid, n_cols));
+  const int i1 = min(n_valid, i0 + kTkChunk);
+  if (i0 >= i1) return;
   uint32_t keys[kPer];
 #pragma unroll
   for (int q = 0; q < kPer; ++q) keys[q] = (r0 + q * kWave + lane < i1) ? score_key(f[q]) : 0u;
-  load_hist(sm.hist, ws + kTkWsHist);
   __syncthreads();
   int t, above, ties;
   topk_threshold<kTkPartThreads>(sm.hist, sel, sm.scan_lds, sm.sh, t, above, ties);
@@ -359,6 +386,18 @@ __device__ __forceinline__ void topk_filter_chunk(TopkFilterSmem& sm, const floa
   }
 }
 
+__device__ __forceinline__ void topk_filter_chunk(TopkFilterSmem& sm, const float* row, int n_cols,
+                                                  int n_valid, int k, int chunk, int32_t* ws) {
+  if (topk_sel(k, n_cols, n_valid) == 0) return;  // uniform; otherwise at least one valid score
+  topk_filter_chunk_at(
+      sm, row, max(0, min(n_valid, n_cols)),
+      [&](int& c, int& v) {
+        c = n_cols;
+        v = n_valid;
+      },
+      k, chunk, ws);
+}
+
 constexpr int kTkBuckets = 4096;  // final ordering: buckets of the top 15 key bits
 constexpr int kTkCand = kMaxTopK + kTkTieCap;
 
@@ -399,7 +438,11 @@ __device__ __forceinline__ void topk_final_row(TopkFinalSmem& sm, const float* r
     return;
   }
   auto& F = sm.u.fin;
-  load_hist(F.hist, ws + kTkWsHist);
+  if (tid < kTkHistHalf) {
+    int4 ha, hb;
+    hist_fetch(ha, hb, ws + kTkWsHist);
+    hist_put(F.hist, ha, hb);
+  }
   for (int b = tid; b < kTkBuckets; b += kTopkThreads) F.cursor[b] = 0;
   __syncthreads();
   int t, above, ties;
