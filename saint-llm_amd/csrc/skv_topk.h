@@ -169,7 +169,7 @@ __device__ __forceinline__ void topk_row(TopkSmemT<kThreads>& sm, uint32_t* keys
 //            Standalone select: one workgroup per row (topk_final_row), which
 //            then zeroes the row's histogram and counters.  Decode step:
 //            several workgroups per row each rank a share of the candidates
-//            and gather their entries (k_decode_topk_rank).
+//            and gather their entries (the gather launch of skv_decode_step).
 // A tie bin larger than kTkTieCap makes final fall back to the single-
 // workgroup select over the row.
 // ===========================================================================

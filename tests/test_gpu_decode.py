@@ -87,8 +87,9 @@ def _rand_data(g, specs, B, T, C, CI):
 
 
 # score_cols: default width, or a wider buffer whose extra columns are NaN
-# (the step must read only the first L // m columns of a row)
-@pytest.mark.parametrize("score_cols", [None, 17412])
+# (the step must read only the first L // m columns of a row); rows wider
+# than 16 chunks of 2048 scores span 17 or more histogram chunks
+@pytest.mark.parametrize("score_cols", [None, 17412, 40000])
 def test_decode_step_matches_oracle(dev, score_cols) -> None:
     from saint_kv.decode import DecodeCache, LayerSpec
 
