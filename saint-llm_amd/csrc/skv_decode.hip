@@ -712,7 +712,7 @@ __device__ __forceinline__ void dense_block(const skv_decode_desc* d, const Step
 
 // ---------------------------------------------------------------------------
 // 4. top-k ordering + sparse gather of one part of a row.  Part p of a row
-//    owns output positions [p*rank_out, (p+1)*rank_out), rank_out 16 or 32.
+//    owns output positions [p*rank_out, (p+1)*rank_out), rank_out 8, 16 or 32.
 //    The row's candidates sit in LDS as 64-bit order keys (key << 32 | ~idx:
 //    larger means earlier in the output), the sure list [0, S) then the tie
 //    list [S, C), each in the same order in every part.  A part ranks its
@@ -723,7 +723,7 @@ __device__ __forceinline__ void dense_block(const skv_decode_desc* d, const Step
 //    positions in [sel, top_k) it owns index -1 and entry 0 (the reference's
 //    clamp(min=0) before its gather).
 // ---------------------------------------------------------------------------
-constexpr int kRankOutMin = 16;
+constexpr int kRankOutMin = 8;
 constexpr int kRankOut = 32;
 constexpr int kRankR = 4;  // candidates a lane compares with each key it reads
 constexpr int kRankMaxRows = 512;                    // rows one part can collect (checked below)
@@ -1202,8 +1202,10 @@ extern "C" int skv_decode_step(const skv_decode_desc* h, const skv_decode_desc* 
                            static_cast<int64_t>(n_chunks) * h->batch * n_csa;
   const int64_t n_hist = static_cast<int64_t>(n_chunks) * h->batch * n_csa;
   // smaller parts when the rows alone would leave most CUs idle
-  const int rank_out = (static_cast<int64_t>(h->batch) * n_csa * ceil_div(max_top_k, kRankOut) < 512)
-                           ? kRankOutMin : kRankOut;
+  int rank_out = kRankOut;
+  while (rank_out > kRankOutMin && static_cast<int64_t>(h->batch) * n_csa * ceil_div(max_top_k, rank_out) < 512) {
+    rank_out >>= 1;
+  }
   const int64_t parts_max = ceil_div(max_top_k, rank_out);
   const int64_t n_rank = parts_max * h->batch * n_csa;
   const int64_t n_gather = n_rank + n_tiles;
