@@ -354,6 +354,56 @@ def cpu_baseline_decode(seconds: float = 5.0, seed: int = 0) -> dict:
                       f"for 2 sequences at 64k context, torch/numpy CPU oracle, {dt:.1f} s"}
 
 
+def run_indexer_leg(dev, batch: int, n_ent: int, heads: int, channels: int, launches: int,
+                    bs: int = 64, n_pools: int = 16, seed: int = 6) -> dict:
+    """Lightning-indexer scores of one decode query per sequence over the paged
+    compressed indexer keys (skv_indexer_scores).  The launches rotate over
+    n_pools distinct pools and queries (> 1 GB in all), so every launch reads
+    its keys from HBM, not from the 256 MB Infinity Cache."""
+    from saint_kv import ops
+
+    g = torch.Generator(device=dev).manual_seed(seed)
+    pages_per_seq = -(-n_ent // bs)
+    n_pages = batch * pages_per_seq
+    perm = torch.randperm(n_pages, generator=torch.Generator().manual_seed(seed)).to(torch.int32)
+    table = perm.view(batch, pages_per_seq).to(dev)
+    n_entries = torch.full((batch,), n_ent, dtype=torch.int32, device=dev)
+    pools = [torch.empty(n_pages, bs, channels, dtype=torch.bfloat16, device=dev).normal_(generator=g)
+             for _ in range(n_pools)]
+    qs = [torch.empty(batch, 1, heads, channels, dtype=torch.bfloat16, device=dev).normal_(generator=g)
+          for _ in range(n_pools)]
+    ws = [torch.empty(batch, 1, heads, dtype=torch.float32, device=dev).normal_(generator=g)
+          for _ in range(n_pools)]
+    out = torch.empty(batch, 1, n_ent, dtype=torch.float32, device=dev)
+    for i in range(2 * n_pools):  # warm-up (kernel load, first touch)
+        ops.indexer_scores(qs[i % n_pools], ws[i % n_pools], pools[i % n_pools], table, n_entries, out)
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream(dev)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for i in range(launches):
+        ops.indexer_scores(qs[i % n_pools], ws[i % n_pools], pools[i % n_pools], table, n_entries, out)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / launches
+    alg = batch * n_ent * channels * 2 + batch * heads * (channels * 2 + 4) + batch * n_ent * 4 + \
+        batch * pages_per_seq * 4
+    flops = 2.0 * batch * heads * channels * n_ent
+    gbs = alg / (us * 1e-6) / 1e9
+    rec = {
+        "workload": f"B={batch}, {n_ent} compressed entries/seq (64k ctx, m=4), {heads} heads x {channels} bf16, "
+                    f"bs={bs}, paged, {n_pools} rotating pools",
+        "launches": launches, "us_per_launch": round(us, 2), "alg_bytes_per_launch": int(alg),
+        "gbs": round(gbs, 1), "pct_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 2),
+        "mfma_tflops": round(flops / (us * 1e-6) / 1e12, 1),
+    }
+    log(f"indexer_64k: {rec['us_per_launch']} us/launch, {rec['gbs']} GB/s ({rec['pct_hbm_peak']}%), "
+        f"{rec['mfma_tflops']} TFLOP/s bf16")
+    del pools, qs, ws
+    torch.cuda.empty_cache()
+    return rec
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -364,6 +414,7 @@ def main() -> int:
     ap.add_argument("--legs", default="csa_64k,mixed_8layer,fp8_1m",
                     help="comma list of decode-step legs to run after the headline ('' for none)")
     ap.add_argument("--leg-steps", type=int, default=200)
+    ap.add_argument("--no-indexer", action="store_true", help="skip the indexer-score leg")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); the cache shards by "
@@ -438,6 +489,8 @@ def main() -> int:
             rng.integers(262144, 1048577, size=4), args.leg_steps, seed=5, outlier_frac=0.01,
             evict_frac=0.3)
 
+    indexer = None if args.no_indexer else run_indexer_leg(dev, 16, 16384, 64, 128, 200)
+
     cpu = None
     cpu_dec = None
     if not args.no_cpu_baseline:
@@ -488,6 +541,7 @@ def main() -> int:
         "cpu_baseline": cpu,
         "decode_kv_tokens_per_s_64k": legs.get("csa_64k", {}).get("kv_tokens_per_s"),
         "decode_legs": legs,
+        "indexer_64k": indexer,
     }
     print(json.dumps(rec), flush=True)
     return 0

@@ -243,6 +243,25 @@ int skv_topk_gather(void* dst, const void* pool, int64_t entry_bytes, int64_t bl
                     int64_t rows, const int32_t* row_seq, int64_t channels, int32_t format,
                     void* stream);
 
+/* ---- lightning-indexer scores -------------------------------------------------
+ * scores[r, s] = sum_h w[r, h] * max(0, q[r, h, :] . k[b, s, :]) for query row
+ * r = b * t_per_seq + t and every entry s < min(n_entries[b], max_entries) of
+ * sequence b; k is the paged compressed indexer cache (bf16 [n_pages,
+ * block_size, channels], block_table [batch, bt_stride]).  q: bf16 [rows,
+ * n_heads, channels]; w: fp32 [rows, n_heads]; scores: fp32 [rows,
+ * score_stride], unmasked (the top-k applies the causal block mask), -inf for
+ * an entry whose page is not mapped; columns past the entry count are left
+ * untouched.  Bf16 products accumulate in fp32 (MFMA).  Replaces the einsum +
+ * clamp + weighted head sum of lightning_indexer_scores_reference
+ * (kernels/attention.py:33-50) and CSA._indexer_topk_cached (csa.py:405-409);
+ * no visual bias (the cached path ignores it, csa.py:396-399).
+ * n_heads <= 64, channels a multiple of 8 up to 128, rows <= 65535. */
+int skv_indexer_scores(const void* q, const float* w, const void* idx_pool, int64_t block_size,
+                       int64_t n_pages, const int32_t* block_table, int64_t bt_stride,
+                       const int32_t* n_entries, float* scores, int64_t score_stride, int64_t batch,
+                       int64_t t_per_seq, int64_t n_heads, int64_t channels, int64_t max_entries,
+                       void* stream);
+
 /* ---- eviction and compaction --------------------------------------------------
  * skv_release: push every page of each sequence with release_mask[b] != 0 back
  * on the free stack (ascending b; within b from the last logical page to the

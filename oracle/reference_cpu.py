@@ -23,6 +23,11 @@ Pinning (what fixes each function independently of this file):
   * compression pooling    — textbook per-channel softmax over the m tokens;
                              pinned by uniform-weight, one-hot and m=1 cases and
                              a pure-Python math.exp brute force.
+  * indexer scores         — einsum + clamp(min=0) + weighted head sum of
+                             kernels/attention.py:33-50 in fp64; pinned by a
+                             pure-Python loop, the reference test's invariant
+                             (positive weights give non-negative scores) and
+                             ReLU-before-weighting / orthogonal special cases.
   * top-k select           — torch.topk (the reference's library routine) on
                              distinct scores, causal-mask geometry of
                              kernels/attention.py:53-57, -1 padding.
@@ -383,6 +388,26 @@ def compress_pool_bf16_module(c: Tensor, z: Tensor, bias: Tensor) -> Tensor:
     zb = (z.to(torch.bfloat16) + bias.to(torch.bfloat16))
     w = torch.softmax(zb, dim=-2)
     return (w * c.to(torch.bfloat16)).sum(dim=-2)
+
+
+# ===========================================================================
+# Lightning-indexer scores (kernels/attention.py:33-50; csa.py:405-409)
+# ===========================================================================
+def indexer_scores(q: np.ndarray, k: np.ndarray, w: np.ndarray) -> np.ndarray:
+    """scores[b, t, s] = sum_h w[b, t, h] * max(0, q[b, t, h, :] . k[b, s, :]),
+    unmasked, in fp64: the einsum "bthc,bnc->bthn", clamp(min=0) and weighted
+    sum over heads of lightning_indexer_scores_reference (attention.py:47-50;
+    the cached path, csa.py:405-409).  q (B, T, H, c), k (B, S, c), w (B, T, H)."""
+    hs = np.einsum("bthc,bsc->bths", np.asarray(q, np.float64), np.asarray(k, np.float64))
+    return (np.asarray(w, np.float64)[..., None] * np.maximum(hs, 0.0)).sum(axis=2)
+
+
+def indexer_scores_bound(q: np.ndarray, k: np.ndarray, w: np.ndarray) -> np.ndarray:
+    """sum_h |w| * sum_c |q k| per score: the magnitude that fp32 accumulation
+    errors of indexer_scores scale with."""
+    aq = np.abs(np.asarray(q, np.float64))
+    ak = np.abs(np.asarray(k, np.float64))
+    return (np.abs(np.asarray(w, np.float64))[..., None] * np.einsum("bthc,bsc->bths", aq, ak)).sum(axis=2)
 
 
 # ===========================================================================

@@ -67,6 +67,7 @@ SIGNATURES: dict[str, list] = {
     "skv_fp8_decode_host": [_P, _P, _I64],
     "skv_topk_select": [_P, _I64, _I64, _P, _P, _I32, _I64, _P, _I64, _P, _P],
     "skv_topk_select_decode": [_P, _I64, _I64, _P, _I64, _I64, _P, _I64, _P, _P],
+    "skv_indexer_scores": [_P, _P, _P, _I64, _I64, _P, _I64, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _P],
     "skv_topk_workspace_words": [],
     "skv_topk_gather": [
         _P, _P, _I64, _I64, _I64, _P, _I64, _P, _P, _I64, _I64, _I64, _P, _I64, _I32, _P,

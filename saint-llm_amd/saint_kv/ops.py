@@ -491,6 +491,45 @@ def topk_gather(pool: torch.Tensor, block_table: torch.Tensor, n_entries: torch.
     return out
 
 
+def indexer_scores(q: torch.Tensor, w: torch.Tensor, idx_pool: torch.Tensor, block_table: torch.Tensor,
+                   n_entries: torch.Tensor, out: torch.Tensor, max_entries: int | None = None) -> torch.Tensor:
+    """Lightning-indexer scores over the paged compressed indexer keys.
+
+    out[b, t, s] = sum_h w[b, t, h] * relu(q[b, t, h, :] . k[b, s, :]) for
+    s < min(n_entries[b], max_entries) (default max_entries: out's last dim);
+    unmasked, -inf for unmapped pages, other columns untouched.
+    q: bf16 [B, T, H, c]; w: fp32 [B, T, H]; idx_pool: bf16 [n_pages,
+    block_size, c]; out: fp32 [B, T, n] with rows of unit stride.
+    """
+    _require_gpu(q, "q")
+    if q.dtype != torch.bfloat16 or q.dim() != 4 or not q.is_contiguous():
+        raise ValueError("q must be a contiguous bf16 [B, T, H, c] tensor")
+    batch, t, heads, c = q.shape
+    _require_gpu(w, "w")
+    if w.dtype != torch.float32 or tuple(w.shape) != (batch, t, heads) or not w.is_contiguous():
+        raise ValueError(f"w must be a contiguous fp32 [{batch}, {t}, {heads}] tensor")
+    _require_gpu(idx_pool, "idx_pool")
+    if idx_pool.dtype != torch.bfloat16 or idx_pool.dim() != 3 or idx_pool.shape[2] != c or \
+            not idx_pool.is_contiguous():
+        raise ValueError(f"idx_pool must be a contiguous bf16 [n_pages, block_size, {c}] tensor")
+    n_pages, bs = idx_pool.shape[0], idx_pool.shape[1]
+    _require_i32(block_table, "block_table")
+    if block_table.dim() != 2 or block_table.shape[0] != batch:
+        raise ValueError(f"block_table must be int32 [{batch}, max_pages]")
+    _require_i32(n_entries, "n_entries", (batch,))
+    _require_gpu(out, "out")
+    if out.dtype != torch.float32 or out.dim() != 3 or tuple(out.shape[:2]) != (batch, t) or out.stride(2) != 1 \
+            or out.stride(0) != t * out.stride(1):
+        raise ValueError(f"out must be fp32 [{batch}, {t}, n] with unit column stride and dense rows")
+    n = out.shape[2] if max_entries is None else int(max_entries)
+    if n > out.shape[2]:
+        raise ValueError(f"max_entries={n} exceeds out's {out.shape[2]} columns")
+    _lib.call("skv_indexer_scores", q.data_ptr(), w.data_ptr(), idx_pool.data_ptr(), bs, n_pages,
+              block_table.data_ptr(), block_table.shape[1], n_entries.data_ptr(), out.data_ptr(),
+              out.stride(1), batch, t, heads, c, n, _lib.stream_handle(q.device))
+    return out
+
+
 # ---------------------------------------------------------------------------
 # Eviction and compaction
 # ---------------------------------------------------------------------------

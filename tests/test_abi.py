@@ -70,6 +70,11 @@ def test_argument_errors_map_to_value_error() -> None:
     assert rc == _lib.SKV_EINVAL and "row_bytes" in _lib.last_error()
     rc = lib.skv_reserve(None, None, 8, None, 4, 8, None, None, 1, 1, 16, None, None)
     assert rc == _lib.SKV_EINVAL and "max_pages" in _lib.last_error()
+    fake = 16  # never dereferenced: the sizes are refused first
+    rc = lib.skv_indexer_scores(fake, fake, fake, 16, 8, fake, 4, fake, fake, 64, 2, 1, 65, 128, 64, None)
+    assert rc == _lib.SKV_EINVAL and "n_heads" in _lib.last_error()
+    rc = lib.skv_indexer_scores(fake, fake, fake, 16, 8, fake, 4, fake, fake, 64, 2, 1, 64, 100, 64, None)
+    assert rc == _lib.SKV_EINVAL and "channels" in _lib.last_error()
 
 
 def test_single_hip_runtime_mapped() -> None:

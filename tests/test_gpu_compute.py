@@ -1,5 +1,5 @@
-"""GPU parity of the SWA ring, compression pooling, FP8 codec, top-k select,
-top-k gather, release and compaction against the CPU oracle.
+"""GPU parity of the SWA ring, compression pooling, FP8 codec, indexer scores,
+top-k select, top-k gather, release and compaction against the CPU oracle.
 
 Bit-exact for indices, tables, copies and FP8 codes; pooled values within
 rtol=1e-2, atol=1e-2 of the fp32 oracle (bf16 output).
@@ -329,6 +329,69 @@ def test_topk_select_decode_masks(dev, multi) -> None:
 
 
 # ----------------------------------------------------------- top-k gather ----
+# --------------------------------------------------------- indexer scores ----
+# bf16 products accumulate in fp32: each score is within IDX_RTOL of
+# sum_h |w| * sum_c |q k| (the oracle's bound) of the fp64 oracle on the same
+# bf16-rounded inputs
+IDX_RTOL = 1e-5
+
+
+@pytest.mark.parametrize("t,h,c", [(1, 64, 128), (1, 4, 16), (3, 20, 40), (2, 17, 128)])
+def test_indexer_scores_paged(dev, t, h, c) -> None:
+    from saint_kv import ops
+
+    g = torch.Generator().manual_seed(h * 1000 + c)
+    batch, bs, n_max = 5, 16, 600
+    n_ent = np.array([600, 0, 1, 257, 33], dtype=np.int32)
+    bt_stride = -(-n_max // bs)
+    n_pages = batch * bt_stride + 3
+    perm = np.random.default_rng(h).permutation(n_pages)[:batch * bt_stride].reshape(batch, bt_stride)
+    table = perm.astype(np.int32)
+    table[3, 5] = -1  # an unmapped page: entries 80..95 of sequence 3 score -inf
+    pool = torch.randn(n_pages, bs, c, generator=g).to(torch.bfloat16)
+    q = torch.randn(batch, t, h, c, generator=g).to(torch.bfloat16)
+    w = torch.randn(batch, t, h, generator=g)
+    out = torch.full((batch, t, n_max + 7), float("nan"), device=dev)
+    ops.indexer_scores(q.to(dev), w.to(dev), pool.to(dev), _i32(table, dev), _i32(n_ent, dev), out,
+                       max_entries=n_max)
+    got = _np(out)
+    k_seq = np.zeros((batch, n_max, c))
+    for b in range(batch):
+        for e in range(n_max):
+            pg = table[b, e // bs]
+            if pg >= 0:
+                k_seq[b, e] = pool[pg, e % bs].float().numpy()
+    exp = ref.indexer_scores(q.float().numpy(), k_seq, w.numpy())
+    bound = ref.indexer_scores_bound(q.float().numpy(), k_seq, w.numpy())
+    for b in range(batch):
+        n = int(n_ent[b])
+        live = np.ones(n, dtype=bool)
+        if b == 3:
+            live[80:96] = False
+            assert (got[b, :, 80:96] == -np.inf).all()
+        err = np.abs(got[b, :, :n][:, live] - exp[b, :, :n][:, live])
+        assert (err <= IDX_RTOL * bound[b, :, :n][:, live] + 1e-30).all(), (b, float(err.max()))
+        assert np.isnan(got[b, :, n:]).all()  # columns past the entry count are untouched
+
+
+def test_indexer_scores_reference_shape(dev) -> None:
+    """lightning_indexer_scores in the reference's call shape (contiguous keys)
+    on test_lightning_indexer.py's default sizes, and its positive-weight invariant."""
+    from saint_kv.indexer import lightning_indexer_scores
+
+    g = torch.Generator().manual_seed(0)
+    q = torch.randn(2, 32, 4, 16, generator=g).to(torch.bfloat16)
+    k = torch.randn(2, 4, 16, generator=g).to(torch.bfloat16)
+    w = torch.randn(2, 32, 4, generator=g)
+    got = _np(lightning_indexer_scores(q.to(dev), k.to(dev), w.to(dev)))
+    assert got.shape == (2, 32, 4)
+    qn, kn, wn = q.float().numpy(), k.float().numpy(), w.numpy()
+    err = np.abs(got - ref.indexer_scores(qn, kn, wn))
+    assert (err <= IDX_RTOL * ref.indexer_scores_bound(qn, kn, wn) + 1e-30).all()
+    pos = _np(lightning_indexer_scores(q.to(dev), k.to(dev), torch.ones(2, 32, 4, device=dev)))
+    assert (pos >= 0).all()
+
+
 @pytest.mark.parametrize("fp8", [False, True])
 def test_topk_gather_paged(dev, fp8) -> None:
     from saint_kv import ops

@@ -119,6 +119,54 @@ def test_paged_compression_matches_contiguous_state_machine() -> None:
         torch.testing.assert_close(got.float(), comp, rtol=2e-2, atol=2e-2)
 
 
+# --------------------------------------------------------- indexer scores ----
+def _indexer_inputs(b=2, t=3, h=4, c=16, n=5, seed=0):
+    rng = np.random.default_rng(seed)
+    return (rng.standard_normal((b, t, h, c)), rng.standard_normal((b, n, c)), rng.standard_normal((b, t, h)))
+
+
+def test_indexer_scores_brute_force() -> None:
+    """attention.py:47-50 written out as plain loops."""
+    q, k, w = _indexer_inputs()
+    got = ref.indexer_scores(q, k, w)
+    b, t, h, c = q.shape
+    n = k.shape[1]
+    assert got.shape == (b, t, n)
+    for bi in range(b):
+        for ti in range(t):
+            for s in range(n):
+                tot = 0.0
+                for hi in range(h):
+                    dot = sum(float(q[bi, ti, hi, ci]) * float(k[bi, s, ci]) for ci in range(c))
+                    tot += float(w[bi, ti, hi]) * max(dot, 0.0)
+                assert math.isclose(got[bi, ti, s], tot, rel_tol=1e-12, abs_tol=1e-12)
+
+
+def test_indexer_scores_non_negative_with_positive_weights() -> None:
+    """test_lightning_indexer.py:37-43: ReLU before weighting, so all-positive
+    head weights give non-negative scores; negative weights may not."""
+    q, k, _ = _indexer_inputs(seed=1)
+    assert (ref.indexer_scores(q, k, np.ones(q.shape[:3])) >= 0).all()
+    assert (ref.indexer_scores(q, k, -np.ones(q.shape[:3])) <= 0).all()
+
+
+def test_indexer_scores_special_cases() -> None:
+    """One head: w * relu(q.k); negative dots contribute nothing whatever the
+    weight; orthogonal keys score 0; the weights are linear."""
+    q = np.zeros((1, 1, 2, 4))
+    q[0, 0, 0] = [1, 2, 0, 0]
+    q[0, 0, 1] = [0, 0, 3, 0]
+    k = np.array([[[1, 1, 0, 0], [-1, -1, 0, 0], [0, 0, 0, 5], [0, 0, 2, 0]]], dtype=np.float64)
+    w = np.array([[[2.0, -0.5]]])
+    got = ref.indexer_scores(q, k, w)[0, 0]
+    # entry 0: head0 dot 3 -> 6, head1 dot 0; entry 1: head0 dot -3 -> 0;
+    # entry 2: orthogonal to both; entry 3: head1 dot 6 * -0.5
+    assert got.tolist() == [6.0, 0.0, 0.0, -3.0]
+    q2, k2, w2 = _indexer_inputs(seed=2)
+    np.testing.assert_allclose(ref.indexer_scores(q2, k2, 3.0 * w2), 3.0 * ref.indexer_scores(q2, k2, w2),
+                               rtol=1e-12, atol=1e-12)
+
+
 # ------------------------------------------------------------------ top-k ----
 def test_topk_equals_torch_topk_on_distinct_scores() -> None:
     rng = np.random.default_rng(6)
