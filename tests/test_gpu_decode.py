@@ -272,6 +272,50 @@ def _check_csa_outputs(cache, i, scores, ctx):
     assert torch.equal(cache.out_entries[i].cpu(), exp_out), ctx
 
 
+def test_decode_scores_from_cached_indexer_keys(dev) -> None:
+    """The indexer scores of each step computed on the GPU from the cache's own
+    paged indexer keys (ops.indexer_scores) match the oracle, and the step
+    selects and gathers on exactly those scores (csa.py:403-422 end to end,
+    after the projections)."""
+    from saint_kv import ops
+    from saint_kv.decode import DecodeCache, LayerSpec
+
+    specs = [LayerSpec("csa", m=4, top_k=32)]
+    B, H = 3, 64
+    cache = DecodeCache(specs, B, 4096, block_size=16, window=16, device=dev, page_order_seed=7)
+    gen = torch.Generator(device=dev).manual_seed(7)
+    for v in cache.inputs[0].values():
+        v.normal_(generator=gen)
+    cache.bias[0].normal_(generator=gen)
+    cache.idx_bias[0].normal_(generator=gen)
+    cache.prefill(np.array([1000, 37, 2900]), generator=gen)
+    grp = cache.groups[cache.group_of_rate[4]]
+    g = torch.Generator().manual_seed(7)
+    for step in range(6):
+        for v in cache.inputs[0].values():
+            v.normal_(generator=gen)
+        q = torch.randn(B, 1, H, cache.c_indexer, generator=g).to(torch.bfloat16)
+        w = torch.randn(B, 1, H, generator=g)
+        cache.scores[0].fill_(float("nan"))
+        ops.indexer_scores(q.to(dev), w.to(dev), cache.idx_pool[0], grp.block_table, grp.n_entries,
+                           cache.scores[0].view(B, 1, -1))
+        torch.cuda.synchronize()
+        got = cache.scores[0].cpu()
+        ent, bt = _np(grp.n_entries), _np(grp.block_table)
+        ipool = cache.idx_pool[0].float().cpu().numpy()
+        for b in range(B):
+            n = int(ent[b])
+            keys = np.stack([ipool[bt[b, e // 16], e % 16] for e in range(n)])[None]
+            qn, wn = q[b:b + 1].float().numpy(), w[b:b + 1].numpy()
+            exp = ref.indexer_scores(qn, keys, wn)[0, 0]
+            bound = ref.indexer_scores_bound(qn, keys, wn)[0, 0]
+            assert (np.abs(got[b, :n].numpy() - exp) <= 1e-5 * bound + 1e-30).all(), (step, b)
+        cache.step()
+        torch.cuda.synchronize()
+        cache.check_status()
+        _check_csa_outputs(cache, 0, got.nan_to_num(nan=float("-inf")), step)
+
+
 @pytest.mark.parametrize("max_len", [20480, 70000])
 def test_decode_topk_rank_cases(dev, max_len) -> None:
     """Sparse selection of the decode step over score patterns that exercise
