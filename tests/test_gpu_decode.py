@@ -91,10 +91,26 @@ def _rand_data(g, specs, B, T, C, CI):
 # than 16 chunks of 2048 scores span 17 or more histogram chunks
 @pytest.mark.parametrize("score_cols", [None, 17412, 40000])
 def test_decode_step_matches_oracle(dev, score_cols) -> None:
-    from saint_kv.decode import DecodeCache, LayerSpec
+    from saint_kv.decode import LayerSpec
 
-    specs = [LayerSpec("csa", m=4, top_k=64, fp8=True), LayerSpec("csa", m=4, top_k=64),
-             LayerSpec("hca", m=128), LayerSpec("swa")]
+    _decode_oracle_steps(dev, [LayerSpec("csa", m=4, top_k=64, fp8=True), LayerSpec("csa", m=4, top_k=64),
+                               LayerSpec("hca", m=128), LayerSpec("swa")], score_cols)
+
+
+# steps without a CSA layer: no top-k launches, gather launch of dense tiles
+# only; the SWA-only stack has no page group at all
+@pytest.mark.parametrize("kinds", [("hca-fp8", "swa"), ("swa", "swa"), ("hca",)])
+def test_decode_step_without_csa_layers(dev, kinds) -> None:
+    from saint_kv.decode import LayerSpec
+
+    specs = [LayerSpec("hca", m=128, fp8=k.endswith("fp8")) if k.startswith("hca") else LayerSpec("swa")
+             for k in kinds]
+    _decode_oracle_steps(dev, specs, None)
+
+
+def _decode_oracle_steps(dev, specs, score_cols) -> None:
+    from saint_kv.decode import DecodeCache
+
     B, max_len, bs, W, C, CI = 5, 2048, 16, 32, 576, 128
     seed = 3
     cache = DecodeCache(specs, B, max_len, block_size=bs, window=W, device=dev, page_order_seed=seed,
@@ -118,8 +134,9 @@ def test_decode_step_matches_oracle(dev, score_cols) -> None:
     for step in range(40):
         data = _rand_data(g, specs, B, 1, C, CI)
         scores = [torch.randn(B, max_len // s.m, generator=g) if s.kind == "csa" else None for s in specs]
-        scores[0][1, :3] = float("nan")
-        if step == 5:
+        if scores[0] is not None:
+            scores[0][1, :3] = float("nan")
+        if step == 5 and len(scores) > 1 and scores[1] is not None:
             scores[1][:, :] = 0.0  # ties everywhere
         for i, s in enumerate(specs):
             for k, v in data[i].items():
