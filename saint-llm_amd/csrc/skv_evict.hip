@@ -96,13 +96,6 @@ struct PoolRefs {
   int n;
 };
 
-__global__ void k_fill_i32(int32_t* __restrict__ p, int64_t n, int32_t v) {
-  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
-       i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
-    p[i] = v;
-  }
-}
-
 // grid: (ceil(bt_stride / 256), batch)
 __global__ void k_mark_live(const int32_t* __restrict__ bt, int64_t bt_stride,
                             const int32_t* __restrict__ lens, int bs, int64_t n_pages,
@@ -117,6 +110,30 @@ __global__ void k_mark_live(const int32_t* __restrict__ bt, int64_t bt_stride,
 
 // One workgroup: n_live, hole and mover lists, remap, new free stack.
 // ws: [0, n) mark -> remap, [n, 2n) holes, [2n, 3n) movers.  info = {n_live, n_moved}.
+// The marks below n_live are cleared here and the remap of ids at or above
+// n_live holds a mover's hole (cleared by the rewrite that reads it) or 0, so
+// words [0, n) are zero again after the compaction.
+// Each thread takes kPlanRun consecutive ids per pass (four 16-byte loads of
+// the marks), so a pass costs one block scan per kEvictThreads * kPlanRun ids.
+constexpr int kPlanRun = 16;
+
+// The marks of ids [i0, i0 + kPlanRun) (0 past n).
+__device__ __forceinline__ void load_run(const int32_t* mark, int64_t i0, int64_t n, int* v) {
+  if (i0 + kPlanRun <= n) {  // whole run in range: 16-byte loads (i0 is a multiple of 16)
+#pragma unroll
+    for (int q = 0; q < kPlanRun / 4; ++q) {
+      const int4 w = reinterpret_cast<const int4*>(mark + i0)[q];
+      v[4 * q] = w.x;
+      v[4 * q + 1] = w.y;
+      v[4 * q + 2] = w.z;
+      v[4 * q + 3] = w.w;
+    }
+  } else {
+#pragma unroll
+    for (int k = 0; k < kPlanRun; ++k) v[k] = (i0 + k < n) ? mark[i0 + k] : 0;
+  }
+}
+
 __global__ __launch_bounds__(kEvictThreads) void k_compact_plan(int32_t* __restrict__ ws, int64_t n,
                                                                 int32_t* __restrict__ stack,
                                                                 int32_t* __restrict__ top_ptr,
@@ -126,88 +143,149 @@ __global__ __launch_bounds__(kEvictThreads) void k_compact_plan(int32_t* __restr
   int32_t* mark = ws;
   int32_t* holes = ws + n;
   int32_t* movers = ws + 2 * n;
-  int n_live = 0;
-  for (int64_t base = 0; base < n; base += kEvictThreads) {
-    const int64_t i = base + tid;
-    n_live += block_reduce_sum(i < n ? mark[i] : 0, scan_lds);
+  constexpr int64_t kSpan = static_cast<int64_t>(kEvictThreads) * kPlanRun;
+  int v[kPlanRun];
+  int64_t n_live = 0;
+  for (int64_t base = 0; base < n; base += kSpan) {
+    const int64_t i0 = base + static_cast<int64_t>(tid) * kPlanRun;
+    load_run(mark, i0, n, v);
+    int c = 0;
+#pragma unroll
+    for (int k = 0; k < kPlanRun; ++k) c += v[k] != 0 ? 1 : 0;
+    n_live += block_reduce_sum(c, scan_lds);
   }
+  // holes: the free ids below n_live, ranked in ascending order
   int carry = 0;
-  for (int64_t base = 0; base < n_live; base += kEvictThreads) {
-    const int64_t i = base + tid;
-    const int is_hole = (i < n_live && mark[i] == 0) ? 1 : 0;
+  for (int64_t base = 0; base < n_live; base += kSpan) {
+    const int64_t i0 = base + static_cast<int64_t>(tid) * kPlanRun;
+    load_run(mark, i0, n_live, v);
+    int c = 0;
+#pragma unroll
+    for (int k = 0; k < kPlanRun; ++k) c += (i0 + k < n_live && v[k] == 0) ? 1 : 0;
     int tot;
-    const int r = carry + block_exclusive_scan(is_hole, scan_lds, &tot);
-    if (is_hole) holes[r] = static_cast<int32_t>(i);
+    int r = carry + block_exclusive_scan(c, scan_lds, &tot);
+#pragma unroll
+    for (int k = 0; k < kPlanRun; ++k) {
+      if (i0 + k >= n_live) break;
+      if (v[k] == 0) holes[r++] = static_cast<int32_t>(i0 + k);
+      else mark[i0 + k] = 0;
+    }
     carry += tot;
   }
   __syncthreads();  // holes[] complete before the movers read it
   const int n_moved = carry;
+  // movers: the live ids at or above n_live, ranked; their remap is the hole
+  // of the same rank, other ids there remap to -1
   carry = 0;
-  for (int64_t base = n_live; base < n; base += kEvictThreads) {
-    const int64_t i = base + tid;
-    const int is_mover = (i < n && mark[i] != 0) ? 1 : 0;
+  for (int64_t base = n_live; base < n; base += kSpan) {
+    const int64_t i0 = base + static_cast<int64_t>(tid) * kPlanRun;
+    int c = 0;
+#pragma unroll
+    for (int k = 0; k < kPlanRun; ++k) {
+      v[k] = (i0 + k < n) ? mark[i0 + k] : 0;  // n_live need not be a multiple of 16
+      c += v[k] != 0 ? 1 : 0;
+    }
     int tot;
-    const int r = carry + block_exclusive_scan(is_mover, scan_lds, &tot);
-    if (i < n) mark[i] = is_mover ? holes[r] : -1;  // remap for ids >= n_live
-    if (is_mover) movers[r] = static_cast<int32_t>(i);
+    int r = carry + block_exclusive_scan(c, scan_lds, &tot);
+#pragma unroll
+    for (int k = 0; k < kPlanRun; ++k) {
+      if (i0 + k >= n) break;
+      if (v[k] != 0) {  // other ids keep mark 0 (their remap is never read)
+        mark[i0 + k] = holes[r];
+        movers[r] = static_cast<int32_t>(i0 + k);
+        ++r;
+      }
+    }
     carry += tot;
   }
   const int64_t n_free = n - n_live;
   for (int64_t i = tid; i < n_free; i += kEvictThreads) stack[i] = static_cast<int32_t>(n - 1 - i);
   if (tid == 0) {
     *top_ptr = static_cast<int32_t>(n_free);
-    info[0] = n_live;
+    info[0] = static_cast<int32_t>(n_live);
     info[1] = n_moved;
   }
 }
 
 constexpr int kCompactCopyThreads = 256;
+constexpr int kCopySlice = kCompactCopyThreads * 16;  // bytes per copy slice: 16 per thread
+constexpr int kCopySlices = 8;                        // slices per workgroup per iteration
 
-// Persistent grid over (mover rank, pool); each unit copies one page.
-__global__ __launch_bounds__(kCompactCopyThreads) void k_compact_copy(PoolRefs pools,
-                                                                     const int32_t* __restrict__ ws,
-                                                                     int64_t n,
+// Slices of the page copies: mover rank r owns slices [r * per_mover, (r+1) *
+// per_mover); slices [first[q], first[q+1]) of a mover are pool q's page.
+struct CopySlices {
+  int32_t first[kMaxPools + 1];
+  int32_t per_mover;
+};
+
+// Persistent grid over 4 KB slices of (mover, pool) pages.  A workgroup takes
+// kCopySlices slices per iteration: one round trip for their hole / mover
+// ids, one for their data (all loads issued before any store).
+// The same grid first rewrites the block tables: every table entry of a
+// live page at or above n_live takes its remap, which it then clears.
+struct TableRef {
+  int32_t* bt;
+  const int32_t* lens;
+  int32_t bt_stride;
+  int32_t batch;
+  int32_t block_size;
+};
+
+__global__ __launch_bounds__(kCompactCopyThreads) void k_compact_copy(PoolRefs pools, CopySlices cs, TableRef tr,
+                                                                     int32_t* __restrict__ ws, int64_t n,
                                                                      const int32_t* __restrict__ info) {
+  const int n_live = info[0];
   const int n_moved = info[1];
+  int32_t* remap = ws;
   const int32_t* holes = ws + n;
   const int32_t* movers = ws + 2 * n;
-  const int64_t units = static_cast<int64_t>(n_moved) * pools.n;
-  for (int64_t u = blockIdx.x; u < units; u += gridDim.x) {
-    const int r = static_cast<int>(u / pools.n);
-    const int q = static_cast<int>(u % pools.n);
-    const int64_t pb = pools.page_bytes[q];
-    const u32x4* src = reinterpret_cast<const u32x4*>(pools.base[q] + movers[r] * pb);
-    u32x4* dst = reinterpret_cast<u32x4*>(pools.base[q] + holes[r] * pb);
-    const int chunks = static_cast<int>(pb >> 4);
-    constexpr int U = 8;
-    for (int base = 0; base < chunks; base += kCompactCopyThreads * U) {
-      u32x4 v[U];
-#pragma unroll
-      for (int k = 0; k < U; ++k) {
-        const int c = base + k * kCompactCopyThreads + threadIdx.x;
-        if (c < chunks) v[k] = ld_stream(src + c);
-      }
-#pragma unroll
-      for (int k = 0; k < U; ++k) {
-        const int c = base + k * kCompactCopyThreads + threadIdx.x;
-        if (c < chunks) st_stream(dst + c, v[k]);
+  const int total = n_moved * cs.per_mover;  // < 2^24 (checked on the host)
+  const int tid = threadIdx.x;
+  const int entries = tr.batch * tr.bt_stride;  // < 2^24 (checked on the host)
+  for (int t = blockIdx.x * kCompactCopyThreads + tid; t < entries; t += gridDim.x * kCompactCopyThreads) {
+    const int b = static_cast<int>(udiv24(t, tr.bt_stride));
+    const int j = t - b * tr.bt_stride;
+    const int np = static_cast<int>(min<int64_t>(ceil_div24(max(tr.lens[b], 0), tr.block_size), tr.bt_stride));
+    if (j < np) {
+      const int32_t p = tr.bt[t];
+      if (p >= n_live && p < n) {
+        tr.bt[t] = remap[p];
+        remap[p] = 0;
       }
     }
   }
-}
-
-// grid: (ceil(bt_stride / 256), batch)
-__global__ void k_compact_rewrite(int32_t* __restrict__ bt, int64_t bt_stride,
-                                  const int32_t* __restrict__ lens, int bs,
-                                  const int32_t* __restrict__ remap,
-                                  const int32_t* __restrict__ info) {
-  const int b = blockIdx.y;
-  const int64_t j = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  const int64_t np = min<int64_t>(ceil_div(max(lens[b], 0), bs), bt_stride);
-  if (j >= np) return;
-  const int n_live = info[0];
-  const int32_t p = bt[b * bt_stride + j];
-  if (p >= n_live) bt[b * bt_stride + j] = remap[p];
+  for (int s0 = blockIdx.x * kCopySlices; s0 < total; s0 += gridDim.x * kCopySlices) {
+    int32_t src_id[kCopySlices], dst_id[kCopySlices];
+    int q_of[kCopySlices], off[kCopySlices];
+#pragma unroll
+    for (int k = 0; k < kCopySlices; ++k) {
+      const int s = min(s0 + k, total - 1);
+      const int r = static_cast<int>(udiv24(s, cs.per_mover));
+      const int j = s - r * cs.per_mover;
+      int q = 0;
+      for (int qq = 1; qq < pools.n; ++qq) q += (j >= cs.first[qq]) ? 1 : 0;
+      q_of[k] = q;
+      off[k] = (j - cs.first[q]) * kCopySlice + tid * 16;
+      src_id[k] = movers[r];
+      dst_id[k] = holes[r];
+    }
+    u32x4 v[kCopySlices];
+#pragma unroll
+    for (int k = 0; k < kCopySlices; ++k) {
+      const int64_t pb = pools.page_bytes[q_of[k]];
+      const bool live = s0 + k < total && off[k] < pb;
+      const uint8_t* src = pools.base[q_of[k]] + static_cast<int64_t>(src_id[k]) * pb + (live ? off[k] : 0);
+      v[k] = ld_stream(reinterpret_cast<const u32x4*>(src));
+    }
+#pragma unroll
+    for (int k = 0; k < kCopySlices; ++k) {
+      const int64_t pb = pools.page_bytes[q_of[k]];
+      if (s0 + k < total && off[k] < pb) {
+        st_stream(reinterpret_cast<u32x4*>(pools.base[q_of[k]] + static_cast<int64_t>(dst_id[k]) * pb + off[k]),
+                  v[k]);
+      }
+    }
+  }
 }
 
 }  // namespace skv
@@ -250,6 +328,7 @@ extern "C" int skv_compact(const skv_pool_ref* pools, int32_t n_pools, int32_t* 
   }
   PoolRefs refs{};
   refs.n = n_pools;
+  int64_t slices_per_mover = 0;
   for (int q = 0; q < n_pools; ++q) {
     if (!pools[q].base || pools[q].page_bytes <= 0 || (pools[q].page_bytes & 15) ||
         (reinterpret_cast<uintptr_t>(pools[q].base) & 15)) {
@@ -257,13 +336,16 @@ extern "C" int skv_compact(const skv_pool_ref* pools, int32_t n_pools, int32_t* 
     }
     refs.base[q] = static_cast<uint8_t*>(pools[q].base);
     refs.page_bytes[q] = pools[q].page_bytes;
+    slices_per_mover += ceil_div(pools[q].page_bytes, kCopySlice);
+  }
+  if (n_pages * slices_per_mover >= (1 << 24)) {
+    return set_error(SKV_EINVAL, "%s: n_pages x 4 KB slices per page must stay below 2^24", what);
+  }
+  if (batch * bt_stride >= (1 << 24)) {
+    return set_error(SKV_EINVAL, "%s: batch x bt_stride must stay below 2^24", what);
   }
   hipStream_t s = static_cast<hipStream_t>(stream);
-  const int64_t fill_blocks = ceil_div(n_pages, 256) < 4096 ? ceil_div(n_pages, 256) : 4096;
-  hipLaunchKernelGGL(k_fill_i32, dim3(static_cast<unsigned>(fill_blocks)), dim3(256), 0, s, workspace,
-                     n_pages, 0);
-  int rc = check_launch(what);
-  if (rc) return rc;
+  int rc;
   const dim3 tgrid(static_cast<unsigned>(ceil_div(bt_stride, 256)), static_cast<unsigned>(batch));
   if (batch > 0) {
     hipLaunchKernelGGL(k_mark_live, tgrid, dim3(256), 0, s, block_table, bt_stride, seq_lens,
@@ -273,13 +355,12 @@ extern "C" int skv_compact(const skv_pool_ref* pools, int32_t n_pools, int32_t* 
   hipLaunchKernelGGL(k_compact_plan, dim3(1), dim3(kEvictThreads), 0, s, workspace, n_pages,
                      free_stack, free_top, info);
   if ((rc = check_launch(what))) return rc;
-  hipLaunchKernelGGL(k_compact_copy, dim3(kPersistentBlocks), dim3(kCompactCopyThreads), 0, s, refs,
+  CopySlices cs{};
+  for (int q = 0; q < n_pools; ++q) cs.first[q + 1] = cs.first[q] + static_cast<int32_t>(ceil_div(refs.page_bytes[q], kCopySlice));
+  cs.per_mover = cs.first[n_pools];
+  const TableRef tr{block_table, seq_lens, static_cast<int32_t>(bt_stride), static_cast<int32_t>(batch),
+                    static_cast<int32_t>(block_size)};
+  hipLaunchKernelGGL(k_compact_copy, dim3(kPersistentBlocks), dim3(kCompactCopyThreads), 0, s, refs, cs, tr,
                      workspace, n_pages, info);
-  if ((rc = check_launch(what))) return rc;
-  if (batch > 0) {
-    hipLaunchKernelGGL(k_compact_rewrite, tgrid, dim3(256), 0, s, block_table, bt_stride, seq_lens,
-                       static_cast<int>(block_size), workspace, info);
-    if ((rc = check_launch(what))) return rc;
-  }
-  return SKV_OK;
+  return check_launch(what);
 }

@@ -126,6 +126,7 @@ class DecodeCache:
         self.latent, self.c_indexer, self.window, self.block_size = latent, c_indexer, window, block_size
         self.tok_lens = torch.zeros(batch, dtype=torch.int32, device=dev)
         self.status = torch.zeros(1, dtype=torch.int32, device=dev)
+
         self.step_lens = torch.zeros(batch, dtype=torch.int32, device=dev)
         self.step_top = torch.zeros(MAX_GROUPS, dtype=torch.int32, device=dev)
         self.host_lens = np.zeros(batch, dtype=np.int64)
@@ -151,6 +152,10 @@ class DecodeCache:
                 m=m, n_pages=n_pages, free_stack=stack, free_top=top,
                 block_table=torch.full((batch, bt_stride), -1, dtype=torch.int32, device=dev),
                 n_entries=torch.zeros(batch, dtype=torch.int32, device=dev)))
+        # compaction buffers: zeroed once, the compaction leaves the marks zero
+        self._compact_info = torch.zeros(max(len(self.groups), 1), 2, dtype=torch.int32, device=dev)
+        self._compact_ws = torch.zeros(3 * max([g.n_pages for g in self.groups] + [1]), dtype=torch.int32,
+                                       device=dev)
 
         bf = torch.bfloat16
         self.ring, self.pool, self.state, self.bias = [], [], [], []
@@ -364,15 +369,18 @@ class DecodeCache:
         for g in self.groups:
             ops.release(g.free_stack, g.free_top, g.block_table, g.n_entries, m_dev,
                         self.block_size, self.status)
-        self.tok_lens.masked_fill_(m_dev.bool(), 0)
+        self.tok_lens.masked_fill_(m_dev.view(torch.bool), 0)  # 0/1 bytes read as bool, no conversion
         self.host_lens[mask] = 0
 
     def compact(self, workspace: torch.Tensor | None = None, sync: bool = True):
         """Defragment every page group; returns [(n_live, n_moved)] per group.
 
         With ``sync=False`` nothing waits for the device: the result is an
-        int32 device tensor [n_groups, 2] holding the same pairs."""
-        info = torch.zeros(len(self.groups), 2, dtype=torch.int32, device=self.device)
+        int32 device tensor [n_groups, 2] holding the same pairs (reused by the
+        next call).  A caller's ``workspace`` must hold 3 * n_pages int32 of
+        the largest group, its first words zero before the first use (the
+        compaction leaves them zero)."""
+        info = self._compact_info
         for gi, g in enumerate(self.groups):
             pools = []
             for i, spec in enumerate(self.layers):
@@ -380,8 +388,9 @@ class DecodeCache:
                     pools.append(self.pool[i])
                     if self.idx_pool[i] is not None:
                         pools.append(self.idx_pool[i])
-            ws = workspace if workspace is not None and workspace.numel() >= 3 * g.n_pages else \
-                torch.empty(3 * g.n_pages, dtype=torch.int32, device=self.device)
+            ws = workspace if workspace is not None else self._compact_ws
+            if ws.numel() < 3 * g.n_pages:
+                raise ValueError(f"compaction workspace needs {3 * g.n_pages} int32")
             ops.compact(pools, g.block_table, g.n_entries, self.block_size, g.free_stack,
                         g.free_top, ws[: 3 * g.n_pages], info[gi])
         if not sync:

@@ -555,7 +555,11 @@ def release(free_stack: torch.Tensor, free_top: torch.Tensor, block_table: torch
 def compact(pools: list[torch.Tensor], block_table: torch.Tensor, seq_lens: torch.Tensor,
             block_size: int, free_stack: torch.Tensor, free_top: torch.Tensor,
             workspace: torch.Tensor, info: torch.Tensor) -> None:
-    """Defragment ``pools`` (sharing ``block_table``) so live pages occupy [0, n_live)."""
+    """Defragment ``pools`` (sharing ``block_table``) so live pages occupy [0, n_live).
+
+    ``workspace`` (int32 [3 * n_pages]): its first n_pages words must be zero
+    before the first call; every call leaves them zero.
+    """
     n_pages = free_stack.numel()
     refs = (_lib.PoolRef * len(pools))()
     for i, p in enumerate(pools):

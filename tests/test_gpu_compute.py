@@ -459,7 +459,8 @@ def test_release_and_compact(dev) -> None:
     assert st == 0 and int(status.item()) == 0
     assert int(top.item()) == r_top and np.array_equal(_np(stack)[:r_top], r_stack[:r_top])
     assert np.array_equal(_np(bt), r_bt) and np.array_equal(_np(lens), r_lens)
-    ws = torch.empty(3 * n_pages, dtype=torch.int32, device=dev)
+    ws = torch.zeros(3 * n_pages, dtype=torch.int32, device=dev)  # marks zero before the first call
+    ws[n_pages:] = -5  # the rest is scratch
     info = torch.zeros(2, dtype=torch.int32, device=dev)
     ops.compact([pool_a, pool_b], bt, lens, bs, stack, top, ws, info)
     r_stack, r_top, moved = ref.compact(r_pools, r_bt, r_lens, bs)
@@ -470,6 +471,14 @@ def test_release_and_compact(dev) -> None:
     live = ref.live_pages(r_bt, r_lens, bs)
     assert torch.equal(pool_a.cpu()[live], r_pools[0][live])
     assert torch.equal(pool_b.cpu()[live], r_pools[1][live])
+    assert not _np(ws)[:n_pages].any()  # the marks are left zero for the next call
+    # a second compaction of the now dense pools moves nothing and changes nothing
+    bt_before, top_before = bt.clone(), int(top.item())
+    ops.compact([pool_a, pool_b], bt, lens, bs, stack, top, ws, info)
+    torch.cuda.synchronize()
+    assert _np(info).tolist() == [len(live), 0]
+    assert torch.equal(bt, bt_before) and int(top.item()) == top_before
+    assert not _np(ws)[:n_pages].any()
     after = torch.zeros_like(before, device=dev)
     ops.paged_gather(pool_a, bt, lens, after)
     for b in range(batch):
