@@ -130,9 +130,12 @@ struct OwnPlan {
 };
 
 // g_own < 0: no group (SWA layer).  write_tops: this workgroup also writes
-// the groups' tops after the step to step_top.
+// the groups' tops after the step to step_top.  early(len) is called with
+// sequence b's token count once the plan's loads are in flight, so that the
+// caller's loads that depend on it overlap the plan's reductions.
+template <class Early>
 __device__ __forceinline__ OwnPlan step_plan(PlanSmem& sm, const StepMap& map, int b, int g_own,
-                                             bool write_tops) {
+                                             bool write_tops, Early early) {
   constexpr int kPerT = kDecodeMaxBatch / kStepThreads;
   const int tid = threadIdx.x;
   const int batch = map.batch;
@@ -153,6 +156,7 @@ __device__ __forceinline__ OwnPlan step_plan(PlanSmem& sm, const StepMap& map, i
 #pragma unroll
   for (int g = 0; g < SKV_MAX_GROUPS; ++g) top[g] = *map.free_top[min(g, ng - 1)];
   const int own_cur = map.n_entries[min(max(g_own, 0), ng - 1)][b];
+  early(P.len);
   if (tid == 0) {
     sm.bad = 0;
 #pragma unroll
@@ -246,7 +250,14 @@ __device__ __forceinline__ OwnPlan step_plan(PlanSmem& sm, const StepMap& map, i
 // append launch issues them before the step plan.
 struct FoldIn {
   u32x4 m0, m1, s0, s1, a0, a1, cv, zv;
+  u32x4 b0, b1;  // the bias row's 8 channels (token position p % m)
 };
+
+__device__ __forceinline__ void fold_bias(FoldIn& in, const float* bias, uint32_t pm, int channels, int grp) {
+  const u32x4* bp = reinterpret_cast<const u32x4*>(bias + pm * channels + grp * 8);
+  in.b0 = bp[0];
+  in.b1 = bp[1];
+}
 
 __device__ __forceinline__ void fold_load(FoldIn& in, const float* state, const void* c_all, const void* z_all,
                                           int b, int channels, int grp) {
@@ -288,16 +299,17 @@ __device__ __forceinline__ void decode_fold_part(int m, int b, int64_t p, const 
   const int groups = channels >> 3;
   float* sbase = state + static_cast<int64_t>(b) * 3 * channels;
   const uint32_t pm = umod24(static_cast<uint32_t>(p), m);  // p < 2^24
-  const float* brow = bias + pm * channels;
   const bool fresh = pm == 0;
   const bool emit = pm + 1 == static_cast<uint32_t>(m);
   for (int grp0 = t; grp0 < ((groups + nt - 1) / nt) * nt; grp0 += nt) {
     const bool mine = grp0 < groups;
     const int grp = mine ? grp0 : groups - 1;  // in-range address for every lane
-    FoldIn in = first;
-    if (grp0 != t) fold_load(in, state, c_all, z_all, b, channels, grp);
-    const u32x4 b0 = *reinterpret_cast<const u32x4*>(brow + grp * 8);
-    const u32x4 b1 = *(reinterpret_cast<const u32x4*>(brow + grp * 8) + 1);
+    FoldIn in = first;  // group t's inputs and bias row were loaded early
+    if (grp0 != t) {
+      fold_load(in, state, c_all, z_all, b, channels, grp);
+      fold_bias(in, bias, pm, channels, grp);
+    }
+    const u32x4 b0 = in.b0, b1 = in.b1;
     float mx[8], sum[8], acc[8], c[8], z[8], bb[8];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -407,7 +419,24 @@ __global__ __launch_bounds__(kStepThreads) void k_decode_append(const skv_decode
               main_stream ? Ly.z_new : Ly.zi_new, b, channels, min(t, (channels >> 3) - 1));
   }
   const int g = map.group[l];  // < 0 for an SWA layer
-  const OwnPlan P = step_plan(sm.plan, map, b, g, blockIdx.x == 0);
+  // with the token count: the bias rows of the fold and the block-table slot
+  // of the entry this token completes (a page held before the step)
+  int32_t held_page = -1;
+  const auto early = [&](int len) {
+    if (!paged) return;  // uniform
+    const uint32_t p1 = static_cast<uint32_t>(min(max(len, 0), kMaxTokLen - 1)) + 1;
+    const int mm = map.m[g];
+    if (main_stream || idx_stream) {
+      const int channels = main_stream ? d->latent : d->c_indexer;
+      const int t = main_stream ? tid : tid - 2 * kWave;
+      fold_bias(first, main_stream ? Ly.bias : Ly.idx_bias, umod24(p1 - 1, mm), channels,
+                min(t, (channels >> 3) - 1));
+    }
+    const uint32_t e1 = udiv24(p1, mm);
+    const int pi = static_cast<int>(udiv24(e1 > 0 ? e1 - 1 : 0, map.block_size[g]));
+    held_page = map.block_table[g][static_cast<int64_t>(b) * map.bt_stride[g] + min(pi, map.bt_stride[g] - 1)];
+  };
+  const OwnPlan P = step_plan(sm.plan, map, b, g, blockIdx.x == 0, early);
   if (P.bad) {
     if (blockIdx.x == 0 && tid == 0) *map.status = P.bad;
     return;  // refused: nothing changes
@@ -435,7 +464,7 @@ __global__ __launch_bounds__(kStepThreads) void k_decode_append(const skv_decode
   const int pi = static_cast<int>(udiv24(e, bs));
   int32_t page = -1;
   if (e1 * m == static_cast<uint32_t>(p + 1)) {  // uniform
-    if (pi < P.p0) page = bt_row[pi];
+    if (pi < P.p0) page = held_page;
     else if (pi - P.p0 < P.need) page = stack[P.top - 1 - P.off - (pi - P.p0)];
   }
   const int in_page = static_cast<int>(e) - pi * bs;
