@@ -404,6 +404,104 @@ def run_indexer_leg(dev, batch: int, n_ent: int, heads: int, channels: int, laun
     return rec
 
 
+def run_attention_leg(dev, name: str, kind: str, batch: int, lens: np.ndarray, launches: int,
+                      heads: int = 64, dim: int = 576, m: int = 4, top_k: int = 512, window: int = 128,
+                      bs: int = 64, n_sets: int = 8, seed: int = 7) -> dict:
+    """Decode attention of one layer (skv_decode_attention: per-split partial
+    softmax, then the merge) over the paged compressed entries and the K/V
+    window rings.  The launches rotate over n_sets distinct pools, rings,
+    queries and pick rows, so the keys come from HBM, not from the 256 MB
+    Infinity Cache."""
+    from saint_kv import decode_attention
+
+    g = torch.Generator(device=dev).manual_seed(seed)
+    rng = np.random.default_rng(seed)
+    lens = np.asarray(lens, dtype=np.int64)
+    n_ent = lens // m
+    pages = -(-n_ent // bs)
+    bt_stride = int(pages.max())
+    n_pages = int(pages.sum())
+    perm = rng.permutation(n_pages)
+    table = np.full((batch, bt_stride), -1, dtype=np.int32)
+    k = 0
+    for b in range(batch):
+        table[b, :pages[b]] = perm[k:k + pages[b]]
+        k += int(pages[b])
+    table_d = torch.as_tensor(table, device=dev)
+    n_ent_d = torch.as_tensor(n_ent.astype(np.int32), device=dev)
+    lens_d = torch.as_tensor(lens.astype(np.int32), device=dev)
+    knorm_w = (torch.rand(dim, generator=g, device=dev) + 0.5)
+    sink = torch.randn(heads, generator=g, device=dev)
+    sets = []
+    for _ in range(n_sets):
+        pool = torch.empty(n_pages, bs, dim, dtype=torch.bfloat16, device=dev).normal_(generator=g)
+        q = torch.empty(batch, heads, dim, dtype=torch.bfloat16, device=dev).normal_(generator=g)
+        wk = torch.empty(batch, window, dim, dtype=torch.bfloat16, device=dev).normal_(generator=g)
+        wv = torch.empty(batch, window, dim, dtype=torch.bfloat16, device=dev).normal_(generator=g)
+        picks = None
+        if kind == "csa":
+            pk = np.full((batch, top_k), -1, dtype=np.int32)
+            for b in range(batch):
+                kk = min(top_k, int(n_ent[b]))
+                pk[b, :kk] = rng.choice(int(n_ent[b]), size=kk, replace=False)
+            picks = torch.as_tensor(pk, device=dev)
+        sets.append((pool, q, wk, wv, picks))
+    out = torch.empty(batch, heads, dim, dtype=torch.float32, device=dev)
+
+    def launch(i):
+        pool, q, wk, wv, picks = sets[i % n_sets]
+        return decode_attention(q, kind, lens_d, wk, wv, pool=pool, block_table=table_d, n_entries=n_ent_d,
+                                m=m, picks=picks, knorm_w=knorm_w, sink=sink, out=out, workspace=ws)
+
+    ws = torch.empty(64 << 20, dtype=torch.float32, device=dev)  # 256 MB: more than any split needs here
+    for i in range(2 * n_sets):
+        launch(i)
+    torch.cuda.synchronize()
+    # one HIP graph of 2 x n_sets layer calls, replayed: the host's per-call
+    # argument checks stay out of the timed region
+    per_graph = 2 * n_sets
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for i in range(per_graph):
+            launch(i)
+    graph.replay()
+    torch.cuda.synchronize()
+    reps = max(1, launches // per_graph)
+    stream = torch.cuda.current_stream(dev)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(reps):
+        graph.replay()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    launches = reps * per_graph
+    us = e0.elapsed_time(e1) * 1e3 / launches
+    if kind == "csa":
+        keys = np.minimum(n_ent, top_k)
+        meta = batch * top_k * 4 + int(keys.sum()) * 4  # pick rows, block-table slots
+    else:
+        keys = np.maximum(lens - 1, 0) // m
+        meta = int(pages.sum()) * 4
+    cnt = np.minimum(lens, window)
+    alg = int(keys.sum()) * dim * 2 + int(cnt.sum()) * dim * 4 + batch * heads * dim * (2 + 4) + meta + batch * 8
+    flops = 4.0 * heads * dim * float(keys.sum() + cnt.sum())
+    gbs = alg / (us * 1e-6) / 1e9
+    rec = {
+        "workload": f"{kind.upper()} layer: B={batch}, {heads} heads x {dim} bf16, "
+                    + (f"top-k {top_k} of L/{m} entries" if kind == "csa" else f"all L/{m} entries")
+                    + f", W={window} K/V window, bs={bs}, L in [{int(lens.min())}, {int(lens.max())}], "
+                    f"{n_sets} rotating sets",
+        "launches": launches, "us_per_launch": round(us, 2), "alg_bytes_per_launch": alg,
+        "gbs": round(gbs, 1), "pct_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 2),
+        "mfma_tflops": round(flops / (us * 1e-6) / 1e12, 1),
+    }
+    log(f"{name}: {rec['us_per_launch']} us/launch, {rec['gbs']} GB/s ({rec['pct_hbm_peak']}%), "
+        f"{rec['mfma_tflops']} TFLOP/s bf16")
+    del sets, ws, graph
+    torch.cuda.empty_cache()
+    return rec
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -415,6 +513,7 @@ def main() -> int:
                     help="comma list of decode-step legs to run after the headline ('' for none)")
     ap.add_argument("--leg-steps", type=int, default=200)
     ap.add_argument("--no-indexer", action="store_true", help="skip the indexer-score leg")
+    ap.add_argument("--no-attention", action="store_true", help="skip the decode-attention legs")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); the cache shards by "
@@ -499,6 +598,12 @@ def main() -> int:
             evict_frac=0.3)
 
     indexer = None if args.no_indexer else run_indexer_leg(dev, 16, 16384, 64, 128, 200)
+    attention = {}
+    if not args.no_attention:
+        attention["attn_csa_64k"] = run_attention_leg(dev, "attn_csa_64k", "csa", 16, np.full(16, 65536), 200)
+        attention["attn_hca_mixed"] = run_attention_leg(
+            dev, "attn_hca_mixed", "hca", 32, np.random.default_rng(4).integers(32768, 131073, size=32), 200,
+            m=128)
 
     cpu = None
     cpu_dec = None
@@ -551,6 +656,7 @@ def main() -> int:
         "decode_kv_tokens_per_s_64k": legs.get("csa_64k", {}).get("kv_tokens_per_s"),
         "decode_legs": legs,
         "indexer_64k": indexer,
+        "attention": attention or None,
     }
     print(json.dumps(rec), flush=True)
     return 0

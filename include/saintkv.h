@@ -380,6 +380,59 @@ typedef struct skv_decode_desc {
 int skv_decode_step(const skv_decode_desc* host_desc, const skv_decode_desc* device_desc,
                     void* stream);
 
+/* Decode attention of one layer over the paged cache (one query token per
+ * sequence, MQA: one K/V head, n_heads query heads of head_dim), the gather
+ * fused in: replaces the cached-step attention of CSA.forward
+ * (csa.py:324-373: sparse branch over the top-k picks + window branch),
+ * HCA.forward (hca.py:126-169: dense branch over the visible entries + window
+ * branch) and SWAttention.forward (swa.py:115-137: window branch), with
+ * scaled_dot_product / softmax_with_sink / RMSNorm of common.py:12-124.
+ *   out[b,h,:] = compressed(b,h) + window(b,h), each its own softmax with
+ *   scores q.k / sqrt(head_dim):
+ *   compressed: K = V = k_norm(entry) = knorm_w * e * rsqrt(mean(e^2) + eps);
+ *     CSA: the picks picks[b, j] >= 0 (j < top_k; picks >= n_entries[b] are
+ *     masked), no sink; HCA: entries s < floor((lens[b]-1)/m) (s*m + m-1 <
+ *     q_pos), with the sink; SWA: none.  No live key: adds 0.
+ *   window: keys win_k and values win_v of positions [L - min(W, L), L),
+ *     L = lens[b], ring slot pos % W ([batch, window, head_dim] bf16, keys
+ *     already normed and roped as the reference caches them), the sink, and
+ *     the softcap c*tanh(s/c) when softcap > 0.
+ * The pool's entries are bf16 or fp8 (dequantized to bf16 as the gathers
+ * do).  Two launches: per (sequence, split, 64 heads) partial softmax
+ * statistics and outputs into `workspace`, then the merge into `out` (fp32).
+ * skv_attention_workspace returns the workspace bytes (or -1 on a bad
+ * descriptor). */
+typedef struct skv_attention_desc {
+  int32_t kind;             /* SKV_LAYER_SWA / SKV_LAYER_HCA / SKV_LAYER_CSA */
+  int32_t format;           /* SKV_FMT_* of the pool's entries */
+  int64_t batch, n_heads, head_dim; /* n_heads <= 256; head_dim a multiple of 32, <= 576 */
+  const void* q;            /* [batch, n_heads, head_dim] bf16 (roped, q_norm applied) */
+  float* out;               /* [batch, n_heads, head_dim] fp32 */
+  const int32_t* lens;      /* [batch] tokens after the step's append */
+  const void* pool;         /* compressed entries of head_dim channels */
+  int64_t entry_bytes, block_size, n_pages;
+  const int32_t* block_table;
+  int64_t bt_stride;        /* bt_stride * block_size < 2^24 */
+  const int32_t* n_entries; /* [batch] */
+  int64_t m;                /* HCA compression rate */
+  int64_t max_entries;      /* HCA: bound on entries per sequence (0: the table's capacity) */
+  const int32_t* picks;     /* CSA: [batch, pick_stride] */
+  int64_t pick_stride, top_k;
+  const float* knorm_w;     /* [head_dim] */
+  float eps;
+  float softcap;            /* <= 0: none */
+  const float* sink;        /* [n_heads] or NULL */
+  const void* win_k;        /* [batch, window, head_dim] bf16 */
+  const void* win_v;        /* [batch, window, head_dim] bf16 (may equal win_k) */
+  int64_t window;
+  int64_t splits;           /* 0: chosen by the library */
+} skv_attention_desc;
+
+int64_t skv_attention_workspace(const skv_attention_desc* desc);
+/* sizeof(skv_attention_desc), so bindings can check their struct layout. */
+int64_t skv_attention_desc_size(void);
+int skv_decode_attention(const skv_attention_desc* desc, void* workspace, int64_t ws_bytes, void* stream);
+
 /* sizeof(skv_decode_desc), sizeof(skv_decode_layer), sizeof(skv_page_group)
  * written to out[0..2], so bindings can check their struct layout. */
 int skv_decode_desc_sizes(int64_t* out);

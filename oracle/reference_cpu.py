@@ -36,6 +36,13 @@ Pinning (what fixes each function independently of this file):
   * FP8 e4m3fn             — torch's float8_e4m3fn cast (the call site of
                              quant/reference.py:109-110) on 1x128 blocks;
                              fmax, zero-block, saturation special cases.
+  * decode attention       — scaled_dot_product / softmax_with_sink /
+                             RMSNorm of common.py in fp64; pinned by torch's
+                             scaled_dot_product_attention and rms_norm
+                             (library routines), the sink's closed form
+                             (equal logits give 1/(n+1)), one-key and
+                             all-masked special cases, the HCA visibility
+                             rule by brute force, and a pure-Python loop.
 No function here is "parity unpinned".
 """
 
@@ -526,3 +533,102 @@ def fp8_unpack_entries(e: Tensor) -> Tensor:
     scales = e[..., FP8_MAIN:FP8_MAIN + 16].contiguous().view(torch.float32)
     rope = e[..., FP8_MAIN + 16:].contiguous().view(torch.bfloat16)
     return torch.cat([fp8_dequantize_blocks(codes, scales), rope], dim=-1)
+
+
+# ===========================================================================
+# Decode attention over the cache (csa.py:324-373, hca.py:126-169,
+# swa.py:115-137, common.py:12-20 and 77-124), one query token per sequence
+# ===========================================================================
+def rms_norm(x: np.ndarray, weight: np.ndarray, eps: float = 1.0e-6) -> np.ndarray:
+    """RMSNorm.forward (common.py:18-20) in fp64: weight * x / sqrt(mean(x^2) + eps)."""
+    x = np.asarray(x, np.float64)
+    var = (x * x).mean(axis=-1, keepdims=True)
+    return np.asarray(weight, np.float64) * x / np.sqrt(var + eps)
+
+
+def attention_row(q: np.ndarray, k: np.ndarray, v: np.ndarray, valid: np.ndarray,
+                  sink: np.ndarray | None = None, softcap: float | None = None) -> np.ndarray:
+    """scaled_dot_product (common.py:92-124) for one query row in fp64.
+
+    q (H, D), k and v (N, D), valid (N,) bool.  scores = q k^T / sqrt(D)
+    (:117), softcap c * tanh(s / c) (:120-121), masked keys -inf (:122-123),
+    softmax with the per-head sink logit in the denominator (:77-89), then
+    probs @ v (:124).  A row without a valid key gives 0: the reference's
+    outcome with a sink (all mass on the sink) and its row_has_pick /
+    row_has_block zeroing without one (csa.py:344-348, hca.py:137-141).
+    """
+    q = np.asarray(q, np.float64)
+    k = np.asarray(k, np.float64)
+    v = np.asarray(v, np.float64)
+    valid = np.asarray(valid, bool)
+    h, d = q.shape
+    if not valid.any():
+        return np.zeros((h, v.shape[-1]))
+    s = q @ k[valid].T / np.sqrt(d)
+    if softcap is not None:
+        s = softcap * np.tanh(s / softcap)
+    mx = s.max(axis=-1, keepdims=True)
+    if sink is not None:
+        mx = np.maximum(mx, np.asarray(sink, np.float64)[:, None])
+    e = np.exp(s - mx)
+    den = e.sum(axis=-1, keepdims=True)
+    if sink is not None:
+        den = den + np.exp(np.asarray(sink, np.float64)[:, None] - mx)
+    return (e @ v[valid]) / den
+
+
+def csa_sparse_attention(q: np.ndarray, entries: np.ndarray, picks: np.ndarray,
+                         knorm_w: np.ndarray, eps: float = 1.0e-6) -> np.ndarray:
+    """The sparse branch of CSA.forward (csa.py:324-350) for one query row:
+    entries[picks.clamp(0)] through k_norm, K = V, no sink and no softcap; a
+    -1 pick is masked.  q (H, D), entries (n_entries, D), picks (k,)."""
+    picks = np.asarray(picks, np.int64)
+    if not (picks >= 0).any():
+        return np.zeros(np.asarray(q).shape)
+    keys = rms_norm(np.asarray(entries, np.float64)[np.maximum(picks, 0)], knorm_w, eps)
+    return attention_row(q, keys, keys, picks >= 0)
+
+
+def hca_compressed_attention(q: np.ndarray, entries: np.ndarray, q_pos: int, m: int,
+                             knorm_w: np.ndarray, eps: float = 1.0e-6,
+                             sink: np.ndarray | None = None) -> np.ndarray:
+    """The compressed branch of HCA.forward (hca.py:126-141) for one query
+    row at position q_pos: every entry through k_norm, K = V, entry s visible
+    when s*m + m - 1 < q_pos (:128-131), the layer's sink, no softcap."""
+    entries = np.asarray(entries, np.float64)
+    n = entries.shape[0]
+    valid = np.arange(n) * m + (m - 1) < q_pos
+    keys = rms_norm(entries, knorm_w, eps) if n else entries
+    return attention_row(q, keys, keys, valid, sink)
+
+
+def window_attention(q: np.ndarray, win_k: np.ndarray, win_v: np.ndarray,
+                     sink: np.ndarray | None = None, softcap: float | None = None) -> np.ndarray:
+    """The sliding-window branch (swa.py:115-136, csa.py:352-371,
+    hca.py:143-167) of a decode query: the keys and values of the last
+    min(W, L) positions (the mask k_pos <= q_pos and q_pos - k_pos < W of
+    swa.py:121-124 keeps exactly those), as cached (k already normed and
+    roped by the caller), with the sink and the softcap."""
+    n = np.asarray(win_k).shape[0]
+    return attention_row(q, win_k, win_v, np.ones(n, bool), sink, softcap)
+
+
+def decode_attention(q: np.ndarray, kind: str, L: int, *, entries: np.ndarray | None = None,
+                     picks: np.ndarray | None = None, m: int = 1,
+                     knorm_w: np.ndarray | None = None, eps: float = 1.0e-6,
+                     sink: np.ndarray | None = None, softcap: float | None = None,
+                     win_k: np.ndarray | None = None, win_v: np.ndarray | None = None) -> np.ndarray:
+    """One layer's attention output before the output projection for the
+    query of a sequence whose length after the step's append is L:
+    compressed branch + window branch (csa.py:373, hca.py:169), window only
+    for "swa" (swa.py:137).  CSA's sparse branch takes no sink (csa.py:337-345),
+    HCA's compressed branch takes the layer's sink; the softcap applies to the
+    window branch only (csa.py:367-371, hca.py:163-167)."""
+    out = window_attention(q, win_k, win_v, sink, softcap)
+    if kind == "csa":
+        out = out + csa_sparse_attention(q, entries, picks, knorm_w, eps)
+    elif kind == "hca":
+        out = out + hca_compressed_attention(q, entries, L - 1, m, knorm_w, eps, sink)
+    else:
+        assert kind == "swa", kind
+    return out

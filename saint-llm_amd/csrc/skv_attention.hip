@@ -1,0 +1,744 @@
+// Decode attention of one layer over the paged cache, with the gather fused in.
+//
+// Reference (one query token per sequence, MQA: one K/V head, H query heads):
+//   CSA.forward   csa.py:324-373  sparse branch over the top-k picks (K = V =
+//                                 k_norm(entry), no sink) + window branch
+//   HCA.forward   hca.py:126-169  dense branch over the visible entries
+//                                 (K = V = k_norm(entry), sink) + window branch
+//   SWAttention   swa.py:115-137  window branch only
+//   scaled_dot_product / softmax_with_sink / RMSNorm   common.py:12-124
+// Each branch is its own softmax (scores q.k / sqrt(D); the window branch
+// with the softcap c*tanh(s/c)); the layer's output is their sum.
+//
+// k_norm is folded in, not applied to the keys: with r_j = rsqrt(mean(k_j^2)
+// + eps), q . (w*k_j*r_j) = ((q*w) . k_j) r_j and sum_j p_j w*k_j*r_j =
+// w * sum_j (p_j r_j) k_j, so the MFMAs read the raw entries (fp8 entries are
+// dequantized to bf16 exactly as the gathers do), q*w is formed once and w
+// scales the merged output.
+//
+// Launch 1 (k_attn_part): one workgroup per (sequence, unit, head group of
+// 64); a unit is a contiguous range of 32-key tiles of one branch.  Per tile:
+// the key rows go to LDS twice, row-major for S^T = K Q^T (MFMA A = keys,
+// B = queries: lane l holds key/head l%16 and dims 8*(l/16)..+7 of a 32-dim
+// step) and transposed for O = P V (A = P straight from the S^T accumulators,
+// B = V^T: lane l holds dim l%16 and 8 keys).  The transposed tile stores the
+// keys in the order the S^T accumulators hold them (slot group g = keys
+// 4g..4g+3 and 16+4g..16+4g+3), so P needs no shuffle.  Wave w owns heads
+// 16w..16w+15: online softmax per head (log2 domain), O in 36 accumulators.
+// The next tile's rows are loaded while the current one is multiplied
+// (barriers order LDS only).  The unit writes (max, sum, O) per head.
+// Launch 2 (k_attn_merge): per (sequence, head) merges the units of each
+// branch with the sink, applies 1/sum and w, and writes the sum of branches.
+#include <type_traits>
+
+#include "skv_common.h"
+#include "skv_entry.h"
+
+namespace skv {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kAtThreads = 512;
+constexpr int kAtWaves = kAtThreads / 64;
+constexpr int kAtHeads = 64;  // query heads per workgroup: 16 per pair of waves
+constexpr int kAtTile = 32;   // keys per tile
+constexpr int kAtMaxD = 576;
+constexpr int kAtRun = 512;   // keys whose source rows are resolved at once
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr int kAhead = 4;  // LDS operand reads in flight ahead of the products
+constexpr float kRescaleAt = 8.f;  // log2 headroom of the softmax weights over the reference max
+
+struct AttnArgs {
+  const uint8_t* q;  // [B, H, D] bf16
+  float* part;       // [B * U * Hp] x (max, sum), then [B * U * Hp][D] O
+  const int32_t* lens;
+  const uint8_t* pool;
+  const int32_t* block_table;
+  const int32_t* n_entries;
+  const int32_t* picks;
+  const float* knorm_w;
+  const uint8_t* win_k;
+  const uint8_t* win_v;
+  int64_t entry_bytes, pick_stride;
+  int32_t kind, fp8_main;  // fp8_main > 0: fp8 entries with that many coded dims
+  int32_t block_size, n_pages, bt_stride, m, top_k;
+  int32_t window, H, D, n_hg, n_cu, n_wu;
+  float eps, softcap;  // softcap <= 0: none
+};
+
+// Workgroup barrier that orders LDS only: global loads stay in flight.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+__device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
+
+// Key j (0..7) of slot group a (0..3) within a tile: keys 4a..4a+3, 16+4a..16+4a+3.
+__device__ __forceinline__ int slot_key(int a, int j) { return (j < 4) ? 4 * a + j : 16 + 4 * a + (j - 4); }
+
+template <int NKS>
+struct AtSmem {
+  static constexpr int kD = NKS * 32;
+  alignas(16) uint16_t kr[kAtTile][kD + 8];  // row-major keys (16 bytes of pad per row)
+  alignas(16) uint16_t vs[kAtTile][kD + 8];  // row-major window values, staged for the transpose
+  alignas(16) uint16_t vt[kD][kAtTile + 8];  // transposed values, slot-group key order
+  int64_t row[kAtRun];                       // byte offset of each key's source row in the run, -1 masked
+  f32x4 sx[kAtWaves][2][kWave];              // per wave: its half-dims S^T partial per key block
+  float ssx[2][2][16];                       // per half of the dims: the keys' sums of squares
+};
+
+// Zero bytes that dead chunks (masked keys, dims past D) are read from: no
+// select follows a load, so the loaded registers are first used when they are
+// stored to LDS, one tile later, and the loads stay in flight meanwhile.
+__device__ __align__(16) uint8_t g_zero_row[2 * kAtMaxD];
+
+template <int NKS>
+struct TileChunks {
+  static constexpr int kChunks = NKS * 4;  // 16-byte chunks of a bf16 row of kD dims
+  static constexpr int kTotal = kAtTile * kChunks;
+  static constexpr int kPer = (kTotal + kAtThreads - 1) / kAtThreads;
+};
+
+// A tile's bf16 rows spread over the threads: chunk q = tid + 512k is dims
+// 8(q % chunks).. of key q / chunks (consecutive threads read consecutive
+// chunks of a row).
+template <int NKS>
+struct RawBf16 {
+  u32x4 v[TileChunks<NKS>::kPer];
+};
+
+template <int NKS>
+__device__ __forceinline__ void load_tile(RawBf16<NKS>& r, const int64_t* rows, const uint8_t* base, int D) {
+  using TC = TileChunks<NKS>;
+#pragma unroll
+  for (int k = 0; k < TC::kPer; ++k) {
+    const int q = min(static_cast<int>(threadIdx.x) + k * kAtThreads, TC::kTotal - 1);
+    const int c = q % TC::kChunks;
+    const int64_t off = rows[q / TC::kChunks];
+    const bool live = off >= 0 && 8 * c < D;
+    const uint8_t* p = live ? base + off + c * 16 : g_zero_row + c * 16;
+    r.v[k] = *reinterpret_cast<const u32x4*>(p);
+  }
+}
+
+template <int NKS>
+__device__ __forceinline__ void store_tile(uint16_t (*dst)[NKS * 32 + 8], const RawBf16<NKS>& r) {
+  using TC = TileChunks<NKS>;
+#pragma unroll
+  for (int k = 0; k < TC::kPer; ++k) {
+    const int q = static_cast<int>(threadIdx.x) + k * kAtThreads;
+    if (TC::kTotal % kAtThreads == 0 || q < TC::kTotal) {
+      *reinterpret_cast<u32x4*>(&dst[q / TC::kChunks][8 * (q % TC::kChunks)]) = r.v[k];
+    }
+  }
+}
+
+// A tile's fp8 entries (576 dims: 512 e4m3 codes, 4 fp32 scales, 64 bf16
+// rope dims): 8-code chunks with their scale spread over the threads, then
+// the rope chunks on threads 0..255; dequantized (fp32 product rounded to
+// bf16, as the gathers do) when stored.
+constexpr int kFp8Main = kAtMaxD - SKV_FP8_ROPE_DIMS;
+constexpr int kFp8CodeChunks = kFp8Main / 8;         // per entry
+constexpr int kFp8RopeChunks = SKV_FP8_ROPE_DIMS / 8;  // per entry
+constexpr int kFp8CodePer = (kAtTile * kFp8CodeChunks + kAtThreads - 1) / kAtThreads;
+
+struct RawFp8 {
+  u32x2 codes[kFp8CodePer];
+  float scale[kFp8CodePer];
+  u32x4 rope;
+};
+
+__device__ __forceinline__ void load_tile(RawFp8& r, const int64_t* rows, const uint8_t* base) {
+  const int tid = threadIdx.x;
+#pragma unroll
+  for (int k = 0; k < kFp8CodePer; ++k) {
+    const int q = tid + k * kAtThreads;  // kAtTile * kFp8CodeChunks is a multiple of kAtThreads
+    const int c = q % kFp8CodeChunks;
+    const int64_t off = rows[q / kFp8CodeChunks];
+    const uint8_t* p = off >= 0 ? base + off : g_zero_row;
+    r.codes[k] = *reinterpret_cast<const u32x2*>(p + c * 8);
+    r.scale[k] = *reinterpret_cast<const float*>(p + kFp8Main + (c >> 4) * 4);
+  }
+  const int qr = min(tid, kAtTile * kFp8RopeChunks - 1);
+  const int64_t off = rows[qr / kFp8RopeChunks];
+  const uint8_t* p = off >= 0 ? base + off : g_zero_row;
+  r.rope = *reinterpret_cast<const u32x4*>(p + kFp8Main + (kFp8Main >> 7) * 4 + (qr % kFp8RopeChunks) * 16);
+}
+
+__device__ __forceinline__ void store_tile(uint16_t (*dst)[kAtMaxD + 8], const RawFp8& r) {
+  const int tid = threadIdx.x;
+#pragma unroll
+  for (int k = 0; k < kFp8CodePer; ++k) {
+    const int q = tid + k * kAtThreads;
+    float f[8];
+    e4m3fn_x4_to_f32(r.codes[k][0], f);
+    e4m3fn_x4_to_f32(r.codes[k][1], f + 4);
+    u32x4 o;
+#pragma unroll
+    for (int h = 0; h < 4; ++h) o[h] = bf16_pack2(f[2 * h] * r.scale[k], f[2 * h + 1] * r.scale[k]);
+    *reinterpret_cast<u32x4*>(&dst[q / kFp8CodeChunks][8 * (q % kFp8CodeChunks)]) = o;
+  }
+  if (tid < kAtTile * kFp8RopeChunks) {
+    *reinterpret_cast<u32x4*>(&dst[tid / kFp8RopeChunks][kFp8Main + 8 * (tid % kFp8RopeChunks)]) = r.rope;
+  }
+}
+
+// vt from row-major rows: task (slot group a, chunk c) transposes 8 keys x 8
+// dims; row 8c+i of vt gets element i of the 8 keys, at slots 8a..8a+7.
+template <int NKS>
+__device__ __forceinline__ void transpose_rows(AtSmem<NKS>& sm, const uint16_t (*src)[NKS * 32 + 8]) {
+  constexpr int kChunks = NKS * 4;
+  for (int task = threadIdx.x; task < 4 * kChunks; task += kAtThreads) {
+    const int a = task / kChunks, c = task % kChunks;
+    u32x4 v[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[j] = *reinterpret_cast<const u32x4*>(&src[slot_key(a, j)][8 * c]);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      u32x4 o;
+#pragma unroll
+      for (int p = 0; p < 4; ++p) {
+        const uint32_t lo = v[2 * p][i >> 1], hi = v[2 * p + 1][i >> 1];
+        o[p] = (i & 1) ? ((lo >> 16) | (hi & 0xffff0000u)) : ((lo & 0xffffu) | (hi << 16));
+      }
+      *reinterpret_cast<u32x4*>(&sm.vt[8 * c + i][8 * a]) = o;
+    }
+  }
+}
+
+// Unit s of ns of one branch (kComp: compressed entries, else the window).
+// Waves 2hb and 2hb+1 share heads 16hb..16hb+15 of the group: wave half h
+// multiplies key block h (keys 16h..16h+15) for S^T and dims
+// [kD/2 * h, kD/2 * (h+1)) for O; the pair exchanges its block maxima and P
+// through LDS.
+template <int NKS, bool kFp8, bool kComp>
+__device__ __forceinline__ void attn_unit(AtSmem<NKS>& sm, const AttnArgs& a, int b, int s, int ns, int hg) {
+  constexpr int kD = NKS * 32;
+  constexpr int kDbW = kD / 32;  // 16-dim blocks of O per wave
+  using TC = TileChunks<NKS>;
+  const int tid = threadIdx.x;
+  const int wave = tid / kWave, lane = tid % kWave;
+  const int hb = wave >> 1, half = wave & 1;
+  const int col = lane & 15, grp = lane >> 4;
+  const int L = min(max(a.lens[b], 0), (1 << 24) - 1);
+  // keys of this branch for sequence b
+  int n_keys;
+  if constexpr (!kComp) {
+    n_keys = min(L, a.window);
+  } else {
+    if (a.kind == SKV_LAYER_CSA) {
+      n_keys = a.top_k;
+    } else {
+      const int q_pos = max(L - 1, 0);
+      n_keys = min(static_cast<int>(udiv24(q_pos, a.m)), max(a.n_entries[b], 0));
+    }
+  }
+  const int n_tiles = (n_keys + kAtTile - 1) / kAtTile;
+  const int t_lo = static_cast<int>((static_cast<int64_t>(s) * n_tiles) / ns);
+  const int t_hi = static_cast<int>((static_cast<int64_t>(s + 1) * n_tiles) / ns);
+  const int head0 = hg * kAtHeads + hb * 16;  // the pair's first head
+  const int64_t unit = blockIdx.x;
+  float* part_ml = a.part + unit * kAtHeads * 2;
+  float* part_o = a.part + static_cast<int64_t>(gridDim.x) * kAtHeads * 2 + unit * kAtHeads * a.D;
+  const int D = a.D;
+  // query (times w for the compressed branch) as B operands for this wave's
+  // half of the dims: head head0+col, dims 32(ks0 + ks) + 8grp..+7, zero past
+  // H and D
+  constexpr int kHalfKs = NKS / 2;
+  const int ks0 = half * kHalfKs;
+  u32x4 qreg[kHalfKs];
+  {
+    const int h = head0 + col;
+    const uint8_t* qrow = a.q + (static_cast<int64_t>(b) * a.H + min(h, a.H - 1)) * D * 2;
+#pragma unroll
+    for (int ks = 0; ks < kHalfKs; ++ks) {
+      const int d0 = (ks0 + ks) * 32 + grp * 8;
+      const bool live = h < a.H && d0 < D;
+      u32x4 v = *reinterpret_cast<const u32x4*>(qrow + (live ? d0 : 0) * 2);
+      v = live ? v : u32x4{0u, 0u, 0u, 0u};
+      if constexpr (kComp) {
+        const float* wp = a.knorm_w + (live ? d0 : 0);
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          v[t] = bf16_pack2(__uint_as_float(v[t] << 16) * wp[2 * t], __uint_as_float(v[t] & 0xffff0000u) * wp[2 * t + 1]);
+        }
+      }
+      qreg[ks] = v;
+    }
+  }
+  const float inv_sqrt_d = rsqrtf(static_cast<float>(D));
+  const float inv_d = 1.f / static_cast<float>(D);
+  const float scale2 = inv_sqrt_d * kLog2e;
+  const bool capped = !kComp && a.softcap > 0.f;
+  const float inv_cap = capped ? 1.f / a.softcap : 0.f;
+  const float cap_log2e = a.softcap * kLog2e;
+  const int64_t row_bytes = kComp ? a.entry_bytes : static_cast<int64_t>(D) * 2;
+  const uint8_t* kbase = kComp ? a.pool : a.win_k;
+  float m_run = -__builtin_huge_valf(), l_run = 0.f;
+  f32x4 acc_o[kDbW];
+#pragma unroll
+  for (int db = 0; db < kDbW; ++db) acc_o[db] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  for (int k_lo = t_lo * kAtTile; k_lo < t_hi * kAtTile; k_lo += kAtRun) {
+    const int k_hi = min(t_hi * kAtTile, k_lo + kAtRun);
+    lds_barrier();  // the previous run's rows are no longer read
+    // source rows of keys [k_lo, k_hi): -1 for masked keys
+    for (int j = k_lo + tid; j < k_hi; j += kAtThreads) {
+      int64_t row = -1;
+      if (j < n_keys) {
+        if constexpr (!kComp) {
+          const int pos = L - n_keys + j;
+          row = (static_cast<int64_t>(b) * a.window + static_cast<int>(umod24(pos, a.window))) * row_bytes;
+        } else {
+          int e = j;
+          if (a.kind == SKV_LAYER_CSA) {
+            e = a.picks[static_cast<int64_t>(b) * a.pick_stride + j];
+            if (e >= max(a.n_entries[b], 0)) e = -1;
+          }
+          if (e >= 0) {
+            const int pi = static_cast<int>(udiv24(e, a.block_size));
+            if (pi < a.bt_stride) {
+              const int32_t page = a.block_table[static_cast<int64_t>(b) * a.bt_stride + pi];
+              if (page >= 0 && page < a.n_pages) {
+                row = (static_cast<int64_t>(page) * a.block_size + (e - pi * a.block_size)) * row_bytes;
+              }
+            }
+          }
+        }
+      }
+      sm.row[j - k_lo] = row;
+    }
+    lds_barrier();
+    const int n_run_tiles = (k_hi - k_lo) / kAtTile;
+    using Raw = std::conditional_t<kFp8, RawFp8, RawBf16<NKS>>;
+    Raw raw;
+    auto load = [&](Raw& r, const int64_t* rows, const uint8_t* base) {
+      if constexpr (kFp8) {
+        load_tile(r, rows, base);
+      } else {
+        load_tile<NKS>(r, rows, base, D);
+      }
+    };
+    if constexpr (kComp) load(raw, sm.row, kbase);
+    for (int t = 0; t < n_run_tiles; ++t) {
+      const int64_t* rows = sm.row + t * kAtTile;
+      lds_barrier();  // the previous tile's LDS reads are done
+      if constexpr (kComp) {
+        if constexpr (kFp8) {
+          store_tile(sm.kr, raw);
+        } else {
+          store_tile<NKS>(sm.kr, raw);
+        }
+        // the next tile's rows are in flight while this one is multiplied
+        if (t + 1 < n_run_tiles) load(raw, rows + kAtTile, kbase);
+      } else {
+        RawBf16<NKS> rk, rv;
+        load_tile<NKS>(rk, rows, kbase, D);  // keys and values in flight together
+        load_tile<NKS>(rv, rows, a.win_v, D);
+        store_tile<NKS>(sm.kr, rk);
+        store_tile<NKS>(sm.vs, rv);
+      }
+      lds_barrier();
+      transpose_rows<NKS>(sm, kComp ? sm.kr : sm.vs);  // read by O += P V, after the next barrier
+      // which keys of the tile are live (bits 0..31)
+      const uint64_t live = __ballot(lane < kAtTile && rows[lane & (kAtTile - 1)] >= 0);
+      // S^T = K (Q w)^T over this wave's half of the dims, both key blocks:
+      // keys 16kb + 4grp + i, head head0 + col
+      // operand o = 2ks + kb: reads run kAhead operands ahead of the
+      // products, and the two key blocks' products alternate (independent
+      // accumulators)
+      constexpr int kOps = 2 * kHalfKs;
+      u32x4 kv[kOps];
+      auto read_k = [&](int o) {
+        kv[o] = *reinterpret_cast<const u32x4*>(&sm.kr[16 * (o & 1) + col][(ks0 + (o >> 1)) * 32 + grp * 8]);
+      };
+#pragma unroll
+      for (int o = 0; o < kAhead; ++o) read_k(o);
+      f32x4 st[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+      // the keys' sums of squares for k_norm: diag(K K^T) over this wave's
+      // half of the dims, on the pair of head block 0 only
+      f32x4 sq[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+      if (kComp && hb == 0) {
+#pragma unroll
+        for (int o = 0; o < kOps; ++o) {
+          if (o + kAhead < kOps) read_k(o + kAhead);
+          const int kb = o & 1;
+          st[kb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(kv[o]), as_bf16x8(qreg[o >> 1]), st[kb], 0, 0, 0);
+          sq[kb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(kv[o]), as_bf16x8(kv[o]), sq[kb], 0, 0, 0);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+        // lane (col, grp) holds the diagonal element of key col when col - 4grp is in [0, 4)
+        const int i = col - 4 * grp;
+        if (i >= 0 && i < 4) {
+#pragma unroll
+          for (int kb = 0; kb < 2; ++kb) sm.ssx[half][kb][col] = i == 0 ? sq[kb][0] : i == 1 ? sq[kb][1] : i == 2 ? sq[kb][2] : sq[kb][3];
+        }
+      } else {
+#pragma unroll
+        for (int o = 0; o < kOps; ++o) {
+          if (o + kAhead < kOps) read_k(o + kAhead);
+          const int kb = o & 1;
+          st[kb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(kv[o]), as_bf16x8(qreg[o >> 1]), st[kb], 0, 0, 0);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      }
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) sm.sx[wave][kb][lane] = st[kb];
+      lds_barrier();  // the pair's partials; vt is complete
+      // full scores: own half + the pair's half; norm factors of the keys
+      // this lane's accumulators hold (16kb + 4grp + i)
+      float sc[2][4], rk[2][4];
+      float mx = -__builtin_huge_valf();
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) {
+        const f32x4 other = sm.sx[wave ^ 1][kb][lane];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int key = 16 * kb + 4 * grp + i;
+          if constexpr (kComp) {
+            const float ssum = sm.ssx[0][kb][4 * grp + i] + sm.ssx[1][kb][4 * grp + i];
+            rk[kb][i] = rsqrtf(fmaf(ssum, inv_d, a.eps));
+          } else {
+            rk[kb][i] = 1.f;
+          }
+          float v;
+          if (capped) {
+            v = (st[kb][i] + other[i]) * inv_sqrt_d;
+            v = cap_log2e * tanhf(v * inv_cap);
+          } else {
+            v = (st[kb][i] + other[i]) * (rk[kb][i] * scale2);
+          }
+          v = ((live >> key) & 1) ? v : -__builtin_huge_valf();
+          sc[kb][i] = v;
+          mx = fmaxf(mx, v);
+        }
+      }
+      mx = fmaxf(mx, __shfl_xor(mx, 16));
+      mx = fmaxf(mx, __shfl_xor(mx, 32));
+      // the reference max moves only when the tile's max passes it by more
+      // than kRescaleAt (log2): weights stay below 2^kRescaleAt otherwise, and
+      // O and the sum are rescaled rarely
+      const bool move = mx > m_run + kRescaleAt;
+      const float alpha = move ? __builtin_amdgcn_exp2f(m_run - mx) : 1.f;
+      if (move) m_run = mx;
+      const bool none = m_run == -__builtin_huge_valf();
+      float psum = 0.f;
+      u32x4 pa;  // P as A operand: slots 8grp..+3 = key block 0, +4..+7 = key block 1
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) {
+        float p[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          p[i] = none ? 0.f : __builtin_amdgcn_exp2f(sc[kb][i] - m_run);
+          psum += p[i];
+          p[i] *= rk[kb][i];
+        }
+        pa[2 * kb] = bf16_pack2(p[0], p[1]);
+        pa[2 * kb + 1] = bf16_pack2(p[2], p[3]);
+      }
+      l_run = l_run * alpha + psum;
+      // rescale O rows (heads head0 + 4grp + i) by their alpha
+      if (__ballot(alpha != 1.f)) {
+        float al[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) al[i] = __shfl(alpha, 4 * grp + i);
+#pragma unroll
+        for (int db = 0; db < kDbW; ++db) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) acc_o[db][i] *= al[i];
+        }
+      }
+      // O += P V over this wave's dims, reads kAhead operands ahead
+      u32x4 vv[kDbW];
+      auto read_v = [&](int db) {
+        vv[db] = *reinterpret_cast<const u32x4*>(&sm.vt[16 * (half * kDbW + db) + col][8 * grp]);
+      };
+#pragma unroll
+      for (int db = 0; db < kAhead; ++db) read_v(db);
+#pragma unroll
+      for (int db = 0; db < kDbW; ++db) {
+        if (db + kAhead < kDbW) read_v(db + kAhead);
+        acc_o[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(pa), as_bf16x8(vv[db]), acc_o[db], 0, 0, 0);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+  }
+  // the unit's (max, sum) per head and, when it saw a live key, its O
+  // both waves of the pair hold the same (max, sum): the sum over the lane
+  // groups of the per-lane partial sums
+  l_run += __shfl_xor(l_run, 16);
+  l_run += __shfl_xor(l_run, 32);
+  if (half == 0 && grp == 0) {
+    const int hl = hb * 16 + col;  // head within the group
+    part_ml[2 * hl] = m_run;
+    part_ml[2 * hl + 1] = l_run;
+  }
+  if (!__ballot(m_run != -__builtin_huge_valf())) return;  // no live key: O is not read
+#pragma unroll
+  for (int db = 0; db < kDbW; ++db) {
+    const int d = 16 * (half * kDbW + db) + col;
+    if (d < D) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) part_o[static_cast<int64_t>(hb * 16 + 4 * grp + i) * D + d] = acc_o[db][i];
+    }
+  }
+}
+
+template <int NKS, bool kFp8>
+__global__ __launch_bounds__(kAtThreads, 1) void k_attn_part(AttnArgs a) {
+  __shared__ AtSmem<NKS> sm;
+  const int U = a.n_cu + a.n_wu;
+  const int hg = blockIdx.x % a.n_hg;
+  const int bu = blockIdx.x / a.n_hg;
+  const int u = bu % U, b = bu / U;
+  if (u < a.n_cu) {
+    attn_unit<NKS, kFp8, true>(sm, a, b, u, a.n_cu, hg);
+  } else {
+    attn_unit<NKS, false, false>(sm, a, b, u - a.n_cu, a.n_wu, hg);
+  }
+}
+
+struct MergeArgs {
+  const float* part;
+  float* out;  // [B, H, D]
+  const float* knorm_w;
+  const float* sink;  // [H] or nullptr
+  int32_t H, D, n_hg, n_cu, n_wu;
+  int32_t sink_comp;  // the compressed branch takes the sink (HCA)
+};
+
+// One workgroup per (sequence, 4 heads), one wave per head.  Lane t holds
+// the (max, sum) of units t, t+64, ... of a branch; the wave reduces them,
+// then every lane sums its dims over the units, 4 units' loads at a time.
+__global__ __launch_bounds__(256) void k_attn_merge(MergeArgs a) {
+  const int b = blockIdx.x;
+  const int h = blockIdx.y * 4 + static_cast<int>(threadIdx.x) / kWave;
+  const int t = threadIdx.x % kWave;
+  if (h >= a.H) return;
+  const int U = a.n_cu + a.n_wu;
+  const int hg = h / kAtHeads, hl = h % kAtHeads;
+  const int64_t n_units = static_cast<int64_t>(gridDim.x) * U * a.n_hg;
+  const float* ml = a.part;
+  const float* po = a.part + n_units * kAtHeads * 2;
+  const float sink2 = a.sink ? a.sink[h] * kLog2e : 0.f;
+  constexpr int kJ = kAtMaxD / kWave;  // dims per lane
+  float res[kJ];
+#pragma unroll
+  for (int j = 0; j < kJ; ++j) res[j] = 0.f;
+  auto unit_of = [&](int u) { return (static_cast<int64_t>(b) * U + u) * a.n_hg + hg; };
+  for (int br = 0; br < 2; ++br) {
+    const int u0 = br == 0 ? 0 : a.n_cu, u1 = br == 0 ? a.n_cu : U;
+    if (u0 == u1) continue;
+    const bool with_sink = a.sink && (br == 1 || a.sink_comp);
+    // the branch's max over its units
+    float M = -__builtin_huge_valf();
+    for (int u = u0 + t; u < u1; u += kWave) M = fmaxf(M, ml[unit_of(u) * kAtHeads * 2 + 2 * hl]);
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) M = fmaxf(M, __shfl_xor(M, off));
+    if (M == -__builtin_huge_valf()) continue;  // no live key: the branch adds 0
+    if (with_sink) M = fmaxf(M, sink2);
+    float den = 0.f;
+    for (int u = u0 + t; u < u1; u += kWave) {
+      const int64_t i = unit_of(u) * kAtHeads * 2 + 2 * hl;
+      den += exp2f(ml[i] - M) * ml[i + 1];
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) den += __shfl_xor(den, off);
+    if (with_sink) den += exp2f(sink2 - M);
+    float acc[kJ];
+#pragma unroll
+    for (int j = 0; j < kJ; ++j) acc[j] = 0.f;
+    for (int u = u0; u < u1; u += 4) {
+      float w[4];
+      float o[4][kJ];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int uu = min(u + q, u1 - 1);
+        const float mu = ml[unit_of(uu) * kAtHeads * 2 + 2 * hl];
+        w[q] = (u + q < u1 && mu != -__builtin_huge_valf()) ? exp2f(mu - M) : 0.f;
+        const float* ou = po + (unit_of(uu) * kAtHeads + hl) * a.D;
+#pragma unroll
+        for (int j = 0; j < kJ; ++j) o[q][j] = ou[min(t + kWave * j, a.D - 1)];
+      }
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+#pragma unroll
+        for (int j = 0; j < kJ; ++j) acc[j] = w[q] > 0.f ? fmaf(w[q], o[q][j], acc[j]) : acc[j];
+      }
+    }
+    const float inv = 1.f / den;
+#pragma unroll
+    for (int j = 0; j < kJ; ++j) {
+      const int d = t + kWave * j;
+      if (d < a.D) res[j] += acc[j] * inv * (br == 0 ? a.knorm_w[d] : 1.f);
+    }
+  }
+  float* out = a.out + (static_cast<int64_t>(b) * a.H + h) * a.D;
+#pragma unroll
+  for (int j = 0; j < kJ; ++j) {
+    const int d = t + kWave * j;
+    if (d < a.D) out[d] = res[j];
+  }
+}
+
+struct AttnPlan {
+  int n_cu, n_wu, n_hg, nks;
+  int64_t ws_bytes;
+};
+
+int attn_plan(const skv_attention_desc* d, AttnPlan& p) {
+  const char* what = "skv_decode_attention";
+  if (!d) return set_error(SKV_EINVAL, "%s: NULL descriptor", what);
+  if (d->batch < 0) return set_error(SKV_EINVAL, "%s: negative batch", what);
+  if (d->kind != SKV_LAYER_SWA && d->kind != SKV_LAYER_HCA && d->kind != SKV_LAYER_CSA) {
+    return set_error(SKV_EINVAL, "%s: unknown layer kind %d", what, d->kind);
+  }
+  if (d->n_heads < 1 || d->n_heads > 4 * kAtHeads) {
+    return set_error(SKV_EINVAL, "%s: n_heads must be in [1, %d]", what, 4 * kAtHeads);
+  }
+  if (d->head_dim < 32 || d->head_dim > kAtMaxD || d->head_dim % 32) {
+    return set_error(SKV_EINVAL, "%s: head_dim must be a multiple of 32 in [32, %d]", what, kAtMaxD);
+  }
+  if (d->window < 1 || d->window >= (1 << 24)) return set_error(SKV_EINVAL, "%s: window must be in [1, 2^24)", what);
+  const bool comp = d->kind != SKV_LAYER_SWA;
+  int64_t comp_keys = 0;
+  if (comp) {
+    if (d->block_size <= 0 || d->n_pages <= 0 || d->n_pages > 0x7fffffff || d->bt_stride <= 0 ||
+        d->bt_stride * d->block_size >= (1 << 24)) {
+      return set_error(SKV_EINVAL, "%s: bad page geometry (bt_stride * block_size must be < 2^24)", what);
+    }
+    const int main = entry_layout(d->format, d->head_dim, d->entry_bytes);
+    if (main < 0) return set_error(SKV_EINVAL, "%s: entry_bytes/format do not match head_dim", what);
+    if (d->format == SKV_FMT_FP8 && d->head_dim != kAtMaxD) {
+      return set_error(SKV_EINVAL, "%s: fp8 entries need head_dim %d", what, kAtMaxD);
+    }
+    if (d->kind == SKV_LAYER_CSA) {
+      if (d->top_k < 0 || d->top_k >= (1 << 20) || d->pick_stride < d->top_k) {
+        return set_error(SKV_EINVAL, "%s: CSA needs 0 <= top_k <= pick_stride", what);
+      }
+      comp_keys = d->top_k;
+    } else {
+      if (d->m < 1 || d->m >= (1 << 24)) return set_error(SKV_EINVAL, "%s: HCA needs m >= 1", what);
+      comp_keys = d->max_entries > 0 ? d->max_entries : d->bt_stride * d->block_size;
+      if (comp_keys > d->bt_stride * d->block_size) comp_keys = d->bt_stride * d->block_size;
+    }
+  }
+  p.n_hg = static_cast<int>(ceil_div(d->n_heads, kAtHeads));
+  p.nks = d->head_dim <= 128 ? 4 : (d->head_dim <= 512 ? 16 : 18);
+  const int64_t tiles_c = ceil_div(comp_keys, kAtTile);
+  const int64_t tiles_w = ceil_div(d->window, kAtTile);
+  int64_t n_cu = tiles_c > 0 ? 1 : 0, n_wu = 1;
+  if (d->splits > 0) {
+    n_cu = tiles_c > 0 ? (d->splits < tiles_c ? d->splits : tiles_c) : 0;
+    const int64_t w = n_cu > 0 ? ceil_div(d->splits * 2 * tiles_w, tiles_c + 2 * tiles_w) : d->splits;
+    n_wu = w < 1 ? 1 : (w > tiles_w ? tiles_w : w);
+  } else {
+    // split the branch with the most tiles per unit (a window tile reads K
+    // and V) while the grid is short of two workgroups per CU and units keep
+    // at least 4 tiles' worth of reads
+    while (d->batch * p.n_hg * (n_cu + n_wu) < 512) {
+      const double pc = n_cu ? static_cast<double>(tiles_c) / n_cu : 0.0;
+      const double pw = 2.0 * tiles_w / n_wu;
+      if (pc >= pw && pc >= 8.0) {
+        ++n_cu;
+      } else if (pw >= 8.0) {
+        ++n_wu;
+      } else {
+        break;
+      }
+    }
+  }
+  p.n_cu = static_cast<int>(n_cu);
+  p.n_wu = static_cast<int>(n_wu);
+  const int64_t units = d->batch * (n_cu + n_wu) * p.n_hg;
+  if (units >= (1 << 30)) return set_error(SKV_EINVAL, "%s: too many workgroups", what);
+  p.ws_bytes = units * kAtHeads * (2 + d->head_dim) * static_cast<int64_t>(sizeof(float));
+  return SKV_OK;
+}
+
+}  // namespace skv
+
+using namespace skv;
+
+extern "C" int64_t skv_attention_desc_size(void) { return static_cast<int64_t>(sizeof(skv_attention_desc)); }
+
+extern "C" int64_t skv_attention_workspace(const skv_attention_desc* d) {
+  AttnPlan p;
+  if (attn_plan(d, p) != SKV_OK) return -1;
+  return p.ws_bytes;
+}
+
+extern "C" int skv_decode_attention(const skv_attention_desc* d, void* workspace, int64_t ws_bytes,
+                                    void* stream) {
+  const char* what = "skv_decode_attention";
+  AttnPlan p;
+  int rc = attn_plan(d, p);
+  if (rc != SKV_OK) return rc;
+  if (d->batch == 0) return SKV_OK;
+  const bool comp = d->kind != SKV_LAYER_SWA;
+  if (!d->q || !d->out || !d->lens || !d->win_k || !d->win_v ||
+      (comp && (!d->pool || !d->block_table || !d->n_entries || !d->knorm_w)) ||
+      (d->kind == SKV_LAYER_CSA && !d->picks)) {
+    return set_error(SKV_EINVAL, "%s: NULL pointer", what);
+  }
+  if (!workspace || ws_bytes < p.ws_bytes) {
+    return set_error(SKV_EINVAL, "%s: workspace of %lld bytes needed", what, (long long)p.ws_bytes);
+  }
+  AttnArgs a;
+  a.q = static_cast<const uint8_t*>(d->q);
+  a.part = static_cast<float*>(workspace);
+  a.lens = d->lens;
+  a.pool = static_cast<const uint8_t*>(d->pool);
+  a.block_table = d->block_table;
+  a.n_entries = d->n_entries;
+  a.picks = d->picks;
+  a.knorm_w = d->knorm_w;
+  a.win_k = static_cast<const uint8_t*>(d->win_k);
+  a.win_v = static_cast<const uint8_t*>(d->win_v);
+  a.entry_bytes = comp ? d->entry_bytes : 0;
+  a.pick_stride = d->pick_stride;
+  a.kind = d->kind;
+  a.fp8_main = comp && d->format == SKV_FMT_FP8 ? entry_layout(d->format, d->head_dim, d->entry_bytes) : 0;
+  a.block_size = static_cast<int32_t>(comp ? d->block_size : 1);
+  a.n_pages = static_cast<int32_t>(comp ? d->n_pages : 1);
+  a.bt_stride = static_cast<int32_t>(comp ? d->bt_stride : 1);
+  a.m = static_cast<int32_t>(d->kind == SKV_LAYER_HCA ? d->m : 1);
+  a.top_k = static_cast<int32_t>(d->kind == SKV_LAYER_CSA ? d->top_k : 0);
+  a.window = static_cast<int32_t>(d->window);
+  a.H = static_cast<int32_t>(d->n_heads);
+  a.D = static_cast<int32_t>(d->head_dim);
+  a.n_hg = p.n_hg;
+  a.n_cu = p.n_cu;
+  a.n_wu = p.n_wu;
+  a.eps = d->eps;
+  a.softcap = d->softcap;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const dim3 grid(static_cast<unsigned>(d->batch * (p.n_cu + p.n_wu) * p.n_hg));
+  if (a.fp8_main > 0) {
+    hipLaunchKernelGGL((k_attn_part<18, true>), grid, dim3(kAtThreads), 0, s, a);
+  } else if (p.nks == 4) {
+    hipLaunchKernelGGL((k_attn_part<4, false>), grid, dim3(kAtThreads), 0, s, a);
+  } else if (p.nks == 16) {
+    hipLaunchKernelGGL((k_attn_part<16, false>), grid, dim3(kAtThreads), 0, s, a);
+  } else {
+    hipLaunchKernelGGL((k_attn_part<18, false>), grid, dim3(kAtThreads), 0, s, a);
+  }
+  if ((rc = check_launch(what))) return rc;
+  MergeArgs mg;
+  mg.part = a.part;
+  mg.out = d->out;
+  mg.knorm_w = comp ? d->knorm_w : nullptr;
+  mg.sink = d->sink;
+  mg.H = a.H;
+  mg.D = a.D;
+  mg.n_hg = p.n_hg;
+  mg.n_cu = p.n_cu;
+  mg.n_wu = p.n_wu;
+  mg.sink_comp = d->kind == SKV_LAYER_HCA;
+  hipLaunchKernelGGL(k_attn_merge, dim3(static_cast<unsigned>(d->batch), static_cast<unsigned>(ceil_div(d->n_heads, 4))),
+                     dim3(256), 0, s, mg);
+  return check_launch(what);
+}

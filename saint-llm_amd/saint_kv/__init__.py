@@ -9,6 +9,7 @@ C-ABI call.
 """
 
 from saint_kv import ops
+from saint_kv.attention import decode_attention
 from saint_kv.decode import CapturedSteps, DecodeCache, LayerSpec
 from saint_kv.kv_cache import CSAKVCacheLayer, HCAKVCacheLayer, KVCacheBundle, SWAKVCacheLayer
 
@@ -20,6 +21,7 @@ __all__ = [
     "KVCacheBundle",
     "LayerSpec",
     "SWAKVCacheLayer",
+    "decode_attention",
     "ops",
 ]
 __version__ = "0.1.0"
