@@ -29,6 +29,7 @@
 // (barriers order LDS only).  The unit writes (max, sum, O) per head.
 // Launch 2 (k_attn_merge): per (sequence, head) merges the units of each
 // branch with the sink, applies 1/sum and w, and writes the sum of branches.
+#include <algorithm>
 #include <type_traits>
 
 #include "skv_common.h"
@@ -186,25 +187,44 @@ __device__ __forceinline__ void store_tile(uint16_t (*dst)[kAtMaxD + 8], const R
   }
 }
 
-// vt from row-major rows: task (slot group a, chunk c) transposes 8 keys x 8
-// dims; row 8c+i of vt gets element i of the 8 keys, at slots 8a..8a+7.
+// vt from row-major rows through the matrix cores: for the 16-dim block db,
+// D = K_kb E_sel (E_sel[k][n] = 1 where k = 16 sel + n, db = 2 ks + sel)
+// gives lane (n, grp) dim 16db + n of keys 16kb + 4grp + i, exactly (one
+// product per sum); the two key blocks together are slot group grp, one
+// 16-byte piece of row 16db + n.  The waves share the 2 kD/32 blocks.
 template <int NKS>
-__device__ __forceinline__ void transpose_rows(AtSmem<NKS>& sm, const uint16_t (*src)[NKS * 32 + 8]) {
-  constexpr int kChunks = NKS * 4;
-  for (int task = threadIdx.x; task < 4 * kChunks; task += kAtThreads) {
-    const int a = task / kChunks, c = task % kChunks;
-    u32x4 v[8];
+__device__ __forceinline__ void transpose_rows(AtSmem<NKS>& sm, const uint16_t (*src)[NKS * 32 + 8], int wave,
+                                               int col, int grp) {
+  constexpr int kDb = NKS * 2;
+  constexpr int kPer = (kDb + kAtWaves - 1) / kAtWaves;  // blocks per wave
+  // every operand read first, then the products, then the stores
+  u32x4 kv[kPer][2];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) v[j] = *reinterpret_cast<const u32x4*>(&src[slot_key(a, j)][8 * c]);
+  for (int k = 0; k < kPer; ++k) {
+    const int ks = min(wave + k * kAtWaves, kDb - 1) >> 1;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      u32x4 o;
+    for (int kb = 0; kb < 2; ++kb) kv[k][kb] = *reinterpret_cast<const u32x4*>(&src[16 * kb + col][ks * 32 + grp * 8]);
+  }
 #pragma unroll
-      for (int p = 0; p < 4; ++p) {
-        const uint32_t lo = v[2 * p][i >> 1], hi = v[2 * p + 1][i >> 1];
-        o[p] = (i & 1) ? ((lo >> 16) | (hi & 0xffff0000u)) : ((lo & 0xffffu) | (hi << 16));
-      }
-      *reinterpret_cast<u32x4*>(&sm.vt[8 * c + i][8 * a]) = o;
+  for (int k = 0; k < kPer; ++k) {
+    const int db = wave + k * kAtWaves;
+    // E_sel as B operand: lane (n, grp) holds 1 at slot t where 8grp + t = 16 sel + n
+    u32x4 esel;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int k0 = 8 * grp + 2 * q - 16 * (db & 1);
+      esel[q] = (k0 == col ? 0x3f80u : 0u) | (k0 + 1 == col ? 0x3f800000u : 0u);
+    }
+    f32x4 d[2];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+      d[kb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(kv[k][kb]), as_bf16x8(esel),
+                                                      f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+    }
+    if (db < kDb) {  // uniform per wave
+      const u32x4 o = {bf16_pack2(d[0][0], d[0][1]), bf16_pack2(d[0][2], d[0][3]), bf16_pack2(d[1][0], d[1][1]),
+                       bf16_pack2(d[1][2], d[1][3])};
+      *reinterpret_cast<u32x4*>(&sm.vt[16 * db + col][8 * grp]) = o;
     }
   }
 }
@@ -342,7 +362,7 @@ __device__ __forceinline__ void attn_unit(AtSmem<NKS>& sm, const AttnArgs& a, in
         store_tile<NKS>(sm.vs, rv);
       }
       lds_barrier();
-      transpose_rows<NKS>(sm, kComp ? sm.kr : sm.vs);  // read by O += P V, after the next barrier
+      transpose_rows<NKS>(sm, kComp ? sm.kr : sm.vs, wave, col, grp);  // read by O += P V, after the next barrier
       // which keys of the tile are live (bits 0..31)
       const uint64_t live = __ballot(lane < kAtTile && rows[lane & (kAtTile - 1)] >= 0);
       // S^T = K (Q w)^T over this wave's half of the dims, both key blocks:
@@ -510,9 +530,13 @@ struct MergeArgs {
   int32_t sink_comp;  // the compressed branch takes the sink (HCA)
 };
 
-// One workgroup per (sequence, 4 heads), one wave per head.  Lane t holds
-// the (max, sum) of units t, t+64, ... of a branch; the wave reduces them,
-// then every lane sums its dims over the units, 4 units' loads at a time.
+// One workgroup per (sequence, 4 heads), one wave per head.  Two memory
+// round trips: lane t loads the (max, sum) of unit t (units of both
+// branches), the wave reduces them per branch; then every lane loads its
+// dims of 8 units' outputs at a time and sums them with the weights.
+constexpr int kMergeUnits = 64;  // units per sequence the merge takes (one per lane)
+constexpr int kAttnCUs = 256;    // MI355X compute units
+
 __global__ __launch_bounds__(256) void k_attn_merge(MergeArgs a) {
   const int b = blockIdx.x;
   const int h = blockIdx.y * 4 + static_cast<int>(threadIdx.x) / kWave;
@@ -521,66 +545,70 @@ __global__ __launch_bounds__(256) void k_attn_merge(MergeArgs a) {
   const int U = a.n_cu + a.n_wu;
   const int hg = h / kAtHeads, hl = h % kAtHeads;
   const int64_t n_units = static_cast<int64_t>(gridDim.x) * U * a.n_hg;
-  const float* ml = a.part;
-  const float* po = a.part + n_units * kAtHeads * 2;
-  const float sink2 = a.sink ? a.sink[h] * kLog2e : 0.f;
-  constexpr int kJ = kAtMaxD / kWave;  // dims per lane
-  float res[kJ];
-#pragma unroll
-  for (int j = 0; j < kJ; ++j) res[j] = 0.f;
   auto unit_of = [&](int u) { return (static_cast<int64_t>(b) * U + u) * a.n_hg + hg; };
-  for (int br = 0; br < 2; ++br) {
-    const int u0 = br == 0 ? 0 : a.n_cu, u1 = br == 0 ? a.n_cu : U;
-    if (u0 == u1) continue;
-    const bool with_sink = a.sink && (br == 1 || a.sink_comp);
-    // the branch's max over its units
-    float M = -__builtin_huge_valf();
-    for (int u = u0 + t; u < u1; u += kWave) M = fmaxf(M, ml[unit_of(u) * kAtHeads * 2 + 2 * hl]);
+  const float* po = a.part + n_units * kAtHeads * 2;
+  const float ninf = -__builtin_huge_valf();
+  // lane t: unit t's (max, sum)
+  const int64_t mi = unit_of(min(t, U - 1)) * kAtHeads * 2 + 2 * hl;
+  const float m_t = t < U ? a.part[mi] : ninf;
+  const float l_t = t < U ? a.part[mi + 1] : 0.f;
+  const bool comp_t = t < a.n_cu;
+  const float sink2 = a.sink ? a.sink[h] * kLog2e : ninf;
+  // per branch: max over the units (and the sink), the denominator
+  float mc = comp_t ? m_t : ninf, mw = comp_t ? ninf : m_t;
 #pragma unroll
-    for (int off = 32; off > 0; off >>= 1) M = fmaxf(M, __shfl_xor(M, off));
-    if (M == -__builtin_huge_valf()) continue;  // no live key: the branch adds 0
-    if (with_sink) M = fmaxf(M, sink2);
-    float den = 0.f;
-    for (int u = u0 + t; u < u1; u += kWave) {
-      const int64_t i = unit_of(u) * kAtHeads * 2 + 2 * hl;
-      den += exp2f(ml[i] - M) * ml[i + 1];
+  for (int off = 32; off > 0; off >>= 1) {
+    mc = fmaxf(mc, __shfl_xor(mc, off));
+    mw = fmaxf(mw, __shfl_xor(mw, off));
+  }
+  const bool live_c = mc != ninf, live_w = mw != ninf;  // the branch saw a live key
+  if (a.sink_comp) mc = fmaxf(mc, sink2);
+  mw = fmaxf(mw, sink2);
+  const float mb = comp_t ? mc : mw;
+  const float w_t = m_t != ninf ? __builtin_amdgcn_exp2f(m_t - mb) : 0.f;
+  float dc = comp_t ? w_t * l_t : 0.f, dw = comp_t ? 0.f : w_t * l_t;
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    dc += __shfl_xor(dc, off);
+    dw += __shfl_xor(dw, off);
+  }
+  if (a.sink_comp && sink2 != ninf) dc += __builtin_amdgcn_exp2f(sink2 - mc);
+  if (sink2 != ninf) dw += __builtin_amdgcn_exp2f(sink2 - mw);
+  // unit t's weight in the output: its branch's 1/denominator folded in (0
+  // for a branch without a live key)
+  const float f_t = comp_t ? (live_c ? w_t / dc : 0.f) : (live_w ? w_t / dw : 0.f);
+  constexpr int kJ = kAtMaxD / kWave;  // dims per lane
+  float rc[kJ], rw[kJ];
+#pragma unroll
+  for (int j = 0; j < kJ; ++j) rc[j] = rw[j] = 0.f;
+  for (int u0 = 0; u0 < U; u0 += 8) {
+    float o[8][kJ];
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      const float* ou = po + (unit_of(min(u0 + q, U - 1)) * kAtHeads + hl) * a.D;
+#pragma unroll
+      for (int j = 0; j < kJ; ++j) o[q][j] = ou[min(t + kWave * j, a.D - 1)];
     }
 #pragma unroll
-    for (int off = 32; off > 0; off >>= 1) den += __shfl_xor(den, off);
-    if (with_sink) den += exp2f(sink2 - M);
-    float acc[kJ];
+    for (int q = 0; q < 8; ++q) {
+      const float f = __shfl(f_t, min(u0 + q, kWave - 1));
+      if (u0 + q < U && f > 0.f) {  // units without a live key wrote no output
 #pragma unroll
-    for (int j = 0; j < kJ; ++j) acc[j] = 0.f;
-    for (int u = u0; u < u1; u += 4) {
-      float w[4];
-      float o[4][kJ];
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int uu = min(u + q, u1 - 1);
-        const float mu = ml[unit_of(uu) * kAtHeads * 2 + 2 * hl];
-        w[q] = (u + q < u1 && mu != -__builtin_huge_valf()) ? exp2f(mu - M) : 0.f;
-        const float* ou = po + (unit_of(uu) * kAtHeads + hl) * a.D;
-#pragma unroll
-        for (int j = 0; j < kJ; ++j) o[q][j] = ou[min(t + kWave * j, a.D - 1)];
+        for (int j = 0; j < kJ; ++j) {
+          if (u0 + q < a.n_cu) {
+            rc[j] = fmaf(f, o[q][j], rc[j]);
+          } else {
+            rw[j] = fmaf(f, o[q][j], rw[j]);
+          }
+        }
       }
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-#pragma unroll
-        for (int j = 0; j < kJ; ++j) acc[j] = w[q] > 0.f ? fmaf(w[q], o[q][j], acc[j]) : acc[j];
-      }
-    }
-    const float inv = 1.f / den;
-#pragma unroll
-    for (int j = 0; j < kJ; ++j) {
-      const int d = t + kWave * j;
-      if (d < a.D) res[j] += acc[j] * inv * (br == 0 ? a.knorm_w[d] : 1.f);
     }
   }
   float* out = a.out + (static_cast<int64_t>(b) * a.H + h) * a.D;
 #pragma unroll
   for (int j = 0; j < kJ; ++j) {
     const int d = t + kWave * j;
-    if (d < a.D) out[d] = res[j];
+    if (d < a.D) out[d] = (live_c ? rc[j] * a.knorm_w[d] : 0.f) + rw[j];
   }
 }
 
@@ -632,24 +660,28 @@ int attn_plan(const skv_attention_desc* d, AttnPlan& p) {
   const int64_t tiles_w = ceil_div(d->window, kAtTile);
   int64_t n_cu = tiles_c > 0 ? 1 : 0, n_wu = 1;
   if (d->splits > 0) {
-    n_cu = tiles_c > 0 ? (d->splits < tiles_c ? d->splits : tiles_c) : 0;
+    const int64_t cap_c = kMergeUnits - 1;
+    n_cu = tiles_c > 0 ? std::min(std::min<int64_t>(d->splits, tiles_c), cap_c) : 0;
     const int64_t w = n_cu > 0 ? ceil_div(d->splits * 2 * tiles_w, tiles_c + 2 * tiles_w) : d->splits;
-    n_wu = w < 1 ? 1 : (w > tiles_w ? tiles_w : w);
+    n_wu = std::max<int64_t>(1, std::min(std::min(w, tiles_w), kMergeUnits - n_cu));
   } else {
     // split the branch with the most tiles per unit (a window tile reads K
-    // and V) while the grid is short of two workgroups per CU and units keep
-    // at least 4 tiles' worth of reads
-    while (d->batch * p.n_hg * (n_cu + n_wu) < 512) {
+    // and V) while the grid is short of one workgroup per CU (a CU holds
+    // one) and units keep at least 2 tiles' worth of reads
+    while (d->batch * p.n_hg * (n_cu + n_wu) < kAttnCUs && n_cu + n_wu < kMergeUnits) {
       const double pc = n_cu ? static_cast<double>(tiles_c) / n_cu : 0.0;
       const double pw = 2.0 * tiles_w / n_wu;
-      if (pc >= pw && pc >= 8.0) {
+      if (pc >= pw && pc >= 2.0) {
         ++n_cu;
-      } else if (pw >= 8.0) {
+      } else if (pw >= 2.0 && n_wu < tiles_w) {
         ++n_wu;
       } else {
         break;
       }
     }
+  }
+  if (n_cu + n_wu > kMergeUnits) {
+    return set_error(SKV_EINVAL, "%s: at most %d splits per sequence", what, kMergeUnits);
   }
   p.n_cu = static_cast<int>(n_cu);
   p.n_wu = static_cast<int>(n_wu);

@@ -197,3 +197,55 @@ def test_attention_bad_arguments(dev) -> None:
     with pytest.raises(ValueError):  # more than 256 heads
         decode_attention(torch.zeros(2, 300, 576, dtype=torch.bfloat16, device=dev), "swa", lens, ring, ring)
     assert math.isfinite(decode_attention(q, "swa", lens, ring, ring).sum().item())
+
+
+def test_attention_after_decode_step(dev) -> None:
+    """The attention of each layer of a DecodeCache right after its fused
+    step, over the cache's own pools, block tables, picks and rings, against
+    the oracle over the step's gathered outputs (out_entries / out_window)."""
+    from saint_kv import decode_attention
+    from saint_kv.decode import DecodeCache, LayerSpec
+
+    specs = [LayerSpec("csa", m=4, top_k=128), LayerSpec("csa", m=4, top_k=64, fp8=True),
+             LayerSpec("hca", m=16), LayerSpec("swa")]
+    B, W, H, D = 3, 32, 64, 576
+    cache = DecodeCache(specs, B, 8192, window=W, block_size=16, device=dev, page_order_seed=3)
+    gen = torch.Generator(device=dev).manual_seed(11)
+    cache.prefill(np.array([900, 2047, 37]), generator=gen)
+    g = torch.Generator().manual_seed(11)
+    for i, s in enumerate(specs):
+        for v in cache.inputs[i].values():
+            v.normal_(generator=gen)
+        if s.kind == "csa":
+            cache.scores[i].copy_(torch.randn(*cache.scores[i].shape, generator=g))
+    cache.step()
+    torch.cuda.synchronize()
+    cache.check_status()
+    lens = cache.tok_lens.cpu().numpy().astype(np.int64)
+    q = torch.randn(B, H, D, generator=g).to(torch.bfloat16)
+    knw = torch.rand(D, generator=g) + 0.5
+    sink = torch.randn(H, generator=g)
+    for i, s in enumerate(specs):
+        kw = {}
+        if s.kind != "swa":
+            grp = cache.groups[cache.group_of_rate[s.m]]
+            kw = dict(pool=cache.pool[i], fp8=s.fp8, block_table=grp.block_table, n_entries=grp.n_entries,
+                      m=s.m, knorm_w=knw.to(dev))
+            if s.kind == "csa":
+                kw["picks"] = cache.topk_idx[i]
+        got = decode_attention(q.to(dev), s.kind, cache.tok_lens, cache.ring[i], cache.ring[i],
+                               sink=sink.to(dev), **kw).cpu().numpy()
+        want = np.zeros((B, H, D))
+        for b in range(B):
+            L = int(lens[b])
+            win = cache.out_window[i][b, :min(W, L)].float().cpu().numpy().astype(np.float64)
+            ent = picks = None
+            if s.kind == "csa":
+                ent = cache.out_entries[i][b].float().cpu().numpy().astype(np.float64)
+                idx = cache.topk_idx[i][b].cpu().numpy()
+                picks = np.where(idx >= 0, np.arange(len(idx)), -1)
+            elif s.kind == "hca":
+                ent = cache.out_entries[i][b, :L // s.m].float().cpu().numpy().astype(np.float64)
+            want[b] = ref.decode_attention(q[b].float().numpy(), s.kind, L, entries=ent, picks=picks, m=s.m,
+                                           knorm_w=knw.numpy(), sink=sink.numpy(), win_k=win, win_v=win)
+        _assert_close(got, want, f"layer {i} {s.kind}")
