@@ -530,12 +530,13 @@ struct MergeArgs {
   int32_t sink_comp;  // the compressed branch takes the sink (HCA)
 };
 
-// One workgroup per (sequence, 4 heads), one wave per head.  Two memory
-// round trips: lane t loads the (max, sum) of unit t (units of both
-// branches), the wave reduces them per branch; then every lane loads its
-// dims of 8 units' outputs at a time and sums them with the weights.
+// One workgroup per (sequence, 4 heads, half of the dims), one wave per
+// head.  Two memory round trips: lane t loads the (max, sum) of unit t (units
+// of both branches), the wave reduces them per branch; then every lane loads
+// its dims of 16 units' outputs at a time and sums them with the weights.
 constexpr int kMergeUnits = 64;  // units per sequence the merge takes (one per lane)
 constexpr int kAttnCUs = 256;    // MI355X compute units
+constexpr int kMergeChunk = 16;  // units whose outputs are loaded at once
 
 __global__ __launch_bounds__(256) void k_attn_merge(MergeArgs a) {
   const int b = blockIdx.x;
@@ -548,6 +549,13 @@ __global__ __launch_bounds__(256) void k_attn_merge(MergeArgs a) {
   auto unit_of = [&](int u) { return (static_cast<int64_t>(b) * U + u) * a.n_hg + hg; };
   const float* po = a.part + n_units * kAtHeads * 2;
   const float ninf = -__builtin_huge_valf();
+  // this lane's dims: d0 + t + 64j, j < kJ, within this half
+  const int dh = (a.D + 1) / 2;
+  const int d0 = blockIdx.z * dh, d1 = min(a.D, d0 + dh);
+  constexpr int kJ = (kAtMaxD / 2 + kWave - 1) / kWave;
+  float kw[kJ];
+#pragma unroll
+  for (int j = 0; j < kJ; ++j) kw[j] = a.knorm_w ? a.knorm_w[min(d0 + t + kWave * j, a.D - 1)] : 0.f;
   // lane t: unit t's (max, sum)
   const int64_t mi = unit_of(min(t, U - 1)) * kAtHeads * 2 + 2 * hl;
   const float m_t = t < U ? a.part[mi] : ninf;
@@ -577,20 +585,19 @@ __global__ __launch_bounds__(256) void k_attn_merge(MergeArgs a) {
   // unit t's weight in the output: its branch's 1/denominator folded in (0
   // for a branch without a live key)
   const float f_t = comp_t ? (live_c ? w_t / dc : 0.f) : (live_w ? w_t / dw : 0.f);
-  constexpr int kJ = kAtMaxD / kWave;  // dims per lane
   float rc[kJ], rw[kJ];
 #pragma unroll
   for (int j = 0; j < kJ; ++j) rc[j] = rw[j] = 0.f;
-  for (int u0 = 0; u0 < U; u0 += 8) {
-    float o[8][kJ];
+  for (int u0 = 0; u0 < U; u0 += kMergeChunk) {
+    float o[kMergeChunk][kJ];
 #pragma unroll
-    for (int q = 0; q < 8; ++q) {
+    for (int q = 0; q < kMergeChunk; ++q) {
       const float* ou = po + (unit_of(min(u0 + q, U - 1)) * kAtHeads + hl) * a.D;
 #pragma unroll
-      for (int j = 0; j < kJ; ++j) o[q][j] = ou[min(t + kWave * j, a.D - 1)];
+      for (int j = 0; j < kJ; ++j) o[q][j] = ou[min(d0 + t + kWave * j, a.D - 1)];
     }
 #pragma unroll
-    for (int q = 0; q < 8; ++q) {
+    for (int q = 0; q < kMergeChunk; ++q) {
       const float f = __shfl(f_t, min(u0 + q, kWave - 1));
       if (u0 + q < U && f > 0.f) {  // units without a live key wrote no output
 #pragma unroll
@@ -607,8 +614,8 @@ __global__ __launch_bounds__(256) void k_attn_merge(MergeArgs a) {
   float* out = a.out + (static_cast<int64_t>(b) * a.H + h) * a.D;
 #pragma unroll
   for (int j = 0; j < kJ; ++j) {
-    const int d = t + kWave * j;
-    if (d < a.D) out[d] = (live_c ? rc[j] * a.knorm_w[d] : 0.f) + rw[j];
+    const int d = d0 + t + kWave * j;
+    if (d < d1) out[d] = (live_c ? rc[j] * kw[j] : 0.f) + rw[j];
   }
 }
 
@@ -770,7 +777,8 @@ extern "C" int skv_decode_attention(const skv_attention_desc* d, void* workspace
   mg.n_cu = p.n_cu;
   mg.n_wu = p.n_wu;
   mg.sink_comp = d->kind == SKV_LAYER_HCA;
-  hipLaunchKernelGGL(k_attn_merge, dim3(static_cast<unsigned>(d->batch), static_cast<unsigned>(ceil_div(d->n_heads, 4))),
+  hipLaunchKernelGGL(k_attn_merge,
+                     dim3(static_cast<unsigned>(d->batch), static_cast<unsigned>(ceil_div(d->n_heads, 4)), 2),
                      dim3(256), 0, s, mg);
   return check_launch(what);
 }
