@@ -262,7 +262,8 @@ __device__ __forceinline__ void attn_unit(AtSmem<NKS>& sm, const AttnArgs& a, in
   const int head0 = hg * kAtHeads + hb * 16;  // the pair's first head
   const int64_t unit = blockIdx.x;
   float* part_ml = a.part + unit * kAtHeads * 2;
-  float* part_o = a.part + static_cast<int64_t>(gridDim.x) * kAtHeads * 2 + unit * kAtHeads * a.D;
+  uint16_t* part_o =  // bf16 outputs after every unit's (max, sum)
+      reinterpret_cast<uint16_t*>(a.part + static_cast<int64_t>(gridDim.x) * kAtHeads * 2) + unit * kAtHeads * a.D;
   const int D = a.D;
   // query (times w for the compressed branch) as B operands for this wave's
   // half of the dims: head head0+col, dims 32(ks0 + ks) + 8grp..+7, zero past
@@ -502,7 +503,7 @@ __device__ __forceinline__ void attn_unit(AtSmem<NKS>& sm, const AttnArgs& a, in
     const int d = 16 * (half * kDbW + db) + col;
     if (d < D) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) part_o[static_cast<int64_t>(hb * 16 + 4 * grp + i) * D + d] = acc_o[db][i];
+      for (int i = 0; i < 4; ++i) part_o[static_cast<int64_t>(hb * 16 + 4 * grp + i) * D + d] = static_cast<uint16_t>(bf16_pack2(acc_o[db][i], 0.f));
     }
   }
 }
@@ -547,7 +548,7 @@ __global__ __launch_bounds__(256) void k_attn_merge(MergeArgs a) {
   const int hg = h / kAtHeads, hl = h % kAtHeads;
   const int64_t n_units = static_cast<int64_t>(gridDim.x) * U * a.n_hg;
   auto unit_of = [&](int u) { return (static_cast<int64_t>(b) * U + u) * a.n_hg + hg; };
-  const float* po = a.part + n_units * kAtHeads * 2;
+  const uint16_t* po = reinterpret_cast<const uint16_t*>(a.part + n_units * kAtHeads * 2);
   const float ninf = -__builtin_huge_valf();
   // this lane's dims: d0 + t + 64j, j < kJ, within this half
   const int dh = (a.D + 1) / 2;
@@ -592,9 +593,9 @@ __global__ __launch_bounds__(256) void k_attn_merge(MergeArgs a) {
     float o[kMergeChunk][kJ];
 #pragma unroll
     for (int q = 0; q < kMergeChunk; ++q) {
-      const float* ou = po + (unit_of(min(u0 + q, U - 1)) * kAtHeads + hl) * a.D;
+      const uint16_t* ou = po + (unit_of(min(u0 + q, U - 1)) * kAtHeads + hl) * a.D;
 #pragma unroll
-      for (int j = 0; j < kJ; ++j) o[q][j] = ou[min(d0 + t + kWave * j, a.D - 1)];
+      for (int j = 0; j < kJ; ++j) o[q][j] = bf16_to_f32(ou[min(d0 + t + kWave * j, a.D - 1)]);
     }
 #pragma unroll
     for (int q = 0; q < kMergeChunk; ++q) {
@@ -694,7 +695,7 @@ int attn_plan(const skv_attention_desc* d, AttnPlan& p) {
   p.n_wu = static_cast<int>(n_wu);
   const int64_t units = d->batch * (n_cu + n_wu) * p.n_hg;
   if (units >= (1 << 30)) return set_error(SKV_EINVAL, "%s: too many workgroups", what);
-  p.ws_bytes = units * kAtHeads * (2 + d->head_dim) * static_cast<int64_t>(sizeof(float));
+  p.ws_bytes = units * kAtHeads * (2 * static_cast<int64_t>(sizeof(float)) + d->head_dim * 2);  // (max, sum) fp32, O bf16
   return SKV_OK;
 }
 

@@ -2,7 +2,8 @@
 against the fp64 oracle (csa.py:324-373, hca.py:126-169, swa.py:115-137).
 
 Tolerance: the kernel rounds q*w and the softmax weights to bf16 for its MFMAs
-(relative 2^-9 each) and accumulates in fp32, so every output element is held
+and each split's partial output to bf16 (relative 2^-9 each), and accumulates
+in fp32, so every output element is held
 to |got - want| <= ATT_TOL * max|want| of its (sequence, head) row plus 1e-4,
 and the mean error to a tenth of that.
 """
