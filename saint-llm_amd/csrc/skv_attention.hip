@@ -84,8 +84,7 @@ template <int NKS>
 struct AtSmem {
   static constexpr int kD = NKS * 32;
   alignas(16) uint16_t kr[kAtTile][kD + 8];  // row-major keys (16 bytes of pad per row)
-  alignas(16) uint16_t vs[kAtTile][kD + 8];  // row-major window values, staged for the transpose
-  alignas(16) uint16_t vt[kD][kAtTile + 8];  // transposed values, slot-group key order
+  alignas(16) uint16_t vs[kAtTile][kD + 8];  // row-major window values
   int64_t row[kAtRun];                       // byte offset of each key's source row in the run, -1 masked
   f32x4 sx[kAtWaves][2][kWave];              // per wave: its half-dims S^T partial per key block
   float ssx[2][2][16];                       // per half of the dims: the keys' sums of squares
@@ -187,46 +186,17 @@ __device__ __forceinline__ void store_tile(uint16_t (*dst)[kAtMaxD + 8], const R
   }
 }
 
-// vt from row-major rows through the matrix cores: for the 16-dim block db,
-// D = K_kb E_sel (E_sel[k][n] = 1 where k = 16 sel + n, db = 2 ks + sel)
-// gives lane (n, grp) dim 16db + n of keys 16kb + 4grp + i, exactly (one
-// product per sum); the two key blocks together are slot group grp, one
-// 16-byte piece of row 16db + n.  The waves share the 2 kD/32 blocks.
-template <int NKS>
-__device__ __forceinline__ void transpose_rows(AtSmem<NKS>& sm, const uint16_t (*src)[NKS * 32 + 8], int wave,
-                                               int col, int grp) {
-  constexpr int kDb = NKS * 2;
-  constexpr int kPer = (kDb + kAtWaves - 1) / kAtWaves;  // blocks per wave
-  // every operand read first, then the products, then the stores
-  u32x4 kv[kPer][2];
-#pragma unroll
-  for (int k = 0; k < kPer; ++k) {
-    const int ks = min(wave + k * kAtWaves, kDb - 1) >> 1;
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb) kv[k][kb] = *reinterpret_cast<const u32x4*>(&src[16 * kb + col][ks * 32 + grp * 8]);
-  }
-#pragma unroll
-  for (int k = 0; k < kPer; ++k) {
-    const int db = wave + k * kAtWaves;
-    // E_sel as B operand: lane (n, grp) holds 1 at slot t where 8grp + t = 16 sel + n
-    u32x4 esel;
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const int k0 = 8 * grp + 2 * q - 16 * (db & 1);
-      esel[q] = (k0 == col ? 0x3f80u : 0u) | (k0 + 1 == col ? 0x3f800000u : 0u);
-    }
-    f32x4 d[2];
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
-      d[kb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(kv[k][kb]), as_bf16x8(esel),
-                                                      f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-    }
-    if (db < kDb) {  // uniform per wave
-      const u32x4 o = {bf16_pack2(d[0][0], d[0][1]), bf16_pack2(d[0][2], d[0][3]), bf16_pack2(d[1][0], d[1][1]),
-                       bf16_pack2(d[1][2], d[1][3])};
-      *reinterpret_cast<u32x4*>(&sm.vt[16 * db + col][8 * grp]) = o;
-    }
-  }
+typedef short short4v __attribute__((ext_vector_type(4)));
+
+// Four keys of one dim from row-major rows, by gfx950's transposing LDS read:
+// in each group of 16 lanes, source lane s gives the address of 4 bf16 and
+// lane i receives element i%4 of sources i/4, i/4+4, i/4+8, i/4+12.  With
+// source lane s pointing at dims c + 4(s%4).. of key row r0 + s/4, lane i gets
+// dim c + i of rows r0..r0+3.
+__device__ __forceinline__ u32x2 read_tr(const uint16_t* p) {
+  const short4v v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) short4v*)(p));
+  return __builtin_bit_cast(u32x2, v);
 }
 
 // Unit s of ns of one branch (kComp: compressed entries, else the window).
@@ -363,7 +333,6 @@ __device__ __forceinline__ void attn_unit(AtSmem<NKS>& sm, const AttnArgs& a, in
         store_tile<NKS>(sm.vs, rv);
       }
       lds_barrier();
-      transpose_rows<NKS>(sm, kComp ? sm.kr : sm.vs, wave, col, grp);  // read by O += P V, after the next barrier
       // which keys of the tile are live (bits 0..31)
       const uint64_t live = __ballot(lane < kAtTile && rows[lane & (kAtTile - 1)] >= 0);
       // S^T = K (Q w)^T over this wave's half of the dims, both key blocks:
@@ -408,7 +377,7 @@ __device__ __forceinline__ void attn_unit(AtSmem<NKS>& sm, const AttnArgs& a, in
       }
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb) sm.sx[wave][kb][lane] = st[kb];
-      lds_barrier();  // the pair's partials; vt is complete
+      lds_barrier();  // the pair's partials
       // full scores: own half + the pair's half; norm factors of the keys
       // this lane's accumulators hold (16kb + 4grp + i)
       float sc[2][4], rk[2][4];
@@ -472,10 +441,16 @@ __device__ __forceinline__ void attn_unit(AtSmem<NKS>& sm, const AttnArgs& a, in
           for (int i = 0; i < 4; ++i) acc_o[db][i] *= al[i];
         }
       }
-      // O += P V over this wave's dims, reads kAhead operands ahead
+      // O += P V over this wave's dims, reads kAhead operands ahead.  The B
+      // operand of lane (n, grp) is dim 16db + n of the slot group's keys
+      // 4grp..4grp+3 and 16+4grp..16+4grp+3, read transposed from the rows
       u32x4 vv[kDbW];
+      const uint16_t(*vrows)[kD + 8] = kComp ? sm.kr : sm.vs;
       auto read_v = [&](int db) {
-        vv[db] = *reinterpret_cast<const u32x4*>(&sm.vt[16 * (half * kDbW + db) + col][8 * grp]);
+        const int c = 16 * (half * kDbW + db) + 4 * (col & 3);
+        const u32x2 lo = read_tr(&vrows[4 * grp + (col >> 2)][c]);
+        const u32x2 hi = read_tr(&vrows[16 + 4 * grp + (col >> 2)][c]);
+        vv[db] = u32x4{lo[0], lo[1], hi[0], hi[1]};
       };
 #pragma unroll
       for (int db = 0; db < kAhead; ++db) read_v(db);
