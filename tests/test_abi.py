@@ -77,6 +77,42 @@ def test_argument_errors_map_to_value_error() -> None:
     assert rc == _lib.SKV_EINVAL and "channels" in _lib.last_error()
 
 
+def test_attention_descriptor_and_workspace() -> None:
+    """skv_attention_desc layout and the host-only workspace query: its size
+    formula and the argument checks that precede any device work."""
+    import ctypes
+
+    from saint_kv import _lib
+    from saint_kv.attention import KIND, AttentionDesc
+
+    lib = _lib.load()
+    assert lib.skv_attention_desc_size() == ctypes.sizeof(AttentionDesc)
+    d = AttentionDesc()
+    d.kind, d.format = KIND["csa"], _lib.SKV_FMT_BF16
+    d.batch, d.n_heads, d.head_dim = 16, 64, 576
+    d.entry_bytes, d.block_size, d.n_pages, d.bt_stride = 1152, 64, 4096, 256
+    d.pick_stride = d.top_k = 512
+    d.window = 128
+    ws = lib.skv_attention_workspace(ctypes.byref(d))
+    # units x 64 heads x ((max, sum) fp32 + head_dim bf16), units a multiple of the batch
+    per_unit = 64 * (8 + 2 * 576)
+    assert ws > 0 and ws % (16 * per_unit) == 0 and ws // per_unit <= 16 * 64
+    d.splits = 3
+    assert lib.skv_attention_workspace(ctypes.byref(d)) % per_unit == 0
+    for field, value, msg in (("head_dim", 100, "head_dim"), ("n_heads", 300, "n_heads"),
+                              ("window", 0, "window"), ("top_k", 600, "top_k")):
+        bad = AttentionDesc.from_buffer_copy(d)
+        setattr(bad, field, value)
+        assert lib.skv_attention_workspace(ctypes.byref(bad)) == -1
+        assert msg in _lib.last_error()
+    bad = AttentionDesc.from_buffer_copy(d)
+    bad.format, bad.head_dim, bad.entry_bytes = _lib.SKV_FMT_FP8, 320, _lib.fp8_entry_bytes(320)
+    assert lib.skv_attention_workspace(ctypes.byref(bad)) == -1 and "fp8" in _lib.last_error()
+    bad = AttentionDesc.from_buffer_copy(d)
+    bad.kind, bad.m = KIND["hca"], 0
+    assert lib.skv_attention_workspace(ctypes.byref(bad)) == -1 and "m >= 1" in _lib.last_error()
+
+
 def test_single_hip_runtime_mapped() -> None:
     """The library binds to the HIP runtime torch already mapped (one libamdhip64)."""
     import torch  # noqa: F401
