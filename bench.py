@@ -502,6 +502,44 @@ def run_attention_leg(dev, name: str, kind: str, batch: int, lens: np.ndarray, l
     return rec
 
 
+def run_state_leg(dev, seed: int = 9) -> dict:
+    """Save and restore of one 64k-token request of a CSA layer (m=4, with the
+    indexer stream, W=128): its 16,384 compressed entries (main and indexer),
+    tail states and SWA rows, through a file (saint_kv.state).  Host-side IO:
+    device-to-host and host-to-device copies plus the file system."""
+    import tempfile
+
+    from saint_kv.decode import DecodeCache, LayerSpec
+
+    L = 65536
+    cache = DecodeCache([LayerSpec("csa", m=4, top_k=512)], 2, L + 64, device=dev, page_order_seed=seed)
+    cache.prefill(np.array([L, 0]), generator=torch.Generator(device=dev).manual_seed(seed))
+    torch.cuda.synchronize()
+    with tempfile.TemporaryDirectory() as tmp:
+        path = os.path.join(tmp, "req.skv")
+        cache.save(0, path)  # warm-up (allocations, file creation)
+        t0 = time.perf_counter()
+        cache.save(0, path)
+        t1 = time.perf_counter()
+        nbytes = os.path.getsize(path)
+        cache.load(1, path)
+        torch.cuda.synchronize()
+        cache.release(np.array([False, True]))
+        torch.cuda.synchronize()
+        t2 = time.perf_counter()
+        cache.load(1, path)
+        torch.cuda.synchronize()
+        t3 = time.perf_counter()
+    rec = {"workload": "one 64k-token CSA request (m=4, indexer stream, W=128): save to and load from a file",
+           "bytes": nbytes, "save_ms": round((t1 - t0) * 1e3, 2), "load_ms": round((t3 - t2) * 1e3, 2),
+           "save_gbs": round(nbytes / (t1 - t0) / 1e9, 2), "load_gbs": round(nbytes / (t3 - t2) / 1e9, 2)}
+    log(f"state_64k: {nbytes / 1e6:.1f} MB, save {rec['save_ms']} ms ({rec['save_gbs']} GB/s), "
+        f"load {rec['load_ms']} ms ({rec['load_gbs']} GB/s)")
+    del cache
+    torch.cuda.empty_cache()
+    return rec
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -514,6 +552,7 @@ def main() -> int:
     ap.add_argument("--leg-steps", type=int, default=200)
     ap.add_argument("--no-indexer", action="store_true", help="skip the indexer-score leg")
     ap.add_argument("--no-attention", action="store_true", help="skip the decode-attention legs")
+    ap.add_argument("--no-state", action="store_true", help="skip the request save/load leg")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); the cache shards by "
@@ -598,6 +637,7 @@ def main() -> int:
             evict_frac=0.3)
 
     indexer = None if args.no_indexer else run_indexer_leg(dev, 16, 16384, 64, 128, 200)
+    state_io = None if args.no_state else run_state_leg(dev)
     attention = {}
     if not args.no_attention:
         attention["attn_csa_64k"] = run_attention_leg(dev, "attn_csa_64k", "csa", 16, np.full(16, 65536), 200)
@@ -657,6 +697,7 @@ def main() -> int:
         "decode_legs": legs,
         "indexer_64k": indexer,
         "attention": attention or None,
+        "state_64k": state_io,
     }
     print(json.dumps(rec), flush=True)
     return 0

@@ -354,6 +354,21 @@ class DecodeCache:
             ops.fp8_quant_append(pool, g.block_table, tmp_lens, x, torch.as_tensor(n, device=self.device))
             done += n
 
+    # ------------------------------------------------------------ persistence --
+    def save(self, b: int, path, swa: str = "full", period: int | None = None) -> dict:
+        """Write sequence b's snapshot (compressed entries, tail states, SWA rows
+        by strategy "full" / "periodic" / "zero"); see saint_kv.state."""
+        from saint_kv import state
+
+        return state.save_sequence(self, b, path, swa, period)
+
+    def load(self, b: int, path) -> tuple[int, int]:
+        """Restore a snapshot into the empty slot b; returns the positions whose
+        SWA rows the caller appends before the next step; see saint_kv.state."""
+        from saint_kv import state
+
+        return state.load_sequence(self, b, path)
+
     # -------------------------------------------------- eviction / compaction --
     def release(self, mask: np.ndarray, mask_dev: torch.Tensor | None = None) -> None:
         """Finish the sequences with mask[b]: their pages return to the free lists.
