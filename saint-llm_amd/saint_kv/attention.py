@@ -154,10 +154,21 @@ def decode_attention(q: torch.Tensor, kind: str, lens: torch.Tensor, win_k: torc
     need = int(_lib.load().skv_attention_workspace(ctypes.byref(d)))
     if need < 0:
         _lib.check(-1, "skv_attention_workspace")
+    global _LAST_WS
     if workspace is None:
-        workspace = torch.empty(max(need, 4) // 4, dtype=torch.float32, device=q.device)
+        workspace = torch.empty(max(need, 4) // 4 + 1, dtype=torch.float32, device=q.device)
     elif workspace.device != q.device or workspace.numel() * workspace.element_size() < need:
         raise ValueError(f"workspace must hold {need} bytes on {q.device}")
     _lib.call("skv_decode_attention", ctypes.byref(d), workspace.data_ptr(),
               workspace.numel() * workspace.element_size(), _lib.stream_handle(q.device))
+    _LAST_WS = workspace
     return out
+
+
+_LAST_WS: torch.Tensor | None = None
+
+
+def last_workspace() -> torch.Tensor | None:
+    """The workspace the last decode_attention call used (allocated by it when
+    none was passed), for callers that keep it for later calls."""
+    return _LAST_WS

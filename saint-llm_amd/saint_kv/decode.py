@@ -130,6 +130,7 @@ class DecodeCache:
         self.step_lens = torch.zeros(batch, dtype=torch.int32, device=dev)
         self.step_top = torch.zeros(MAX_GROUPS, dtype=torch.int32, device=dev)
         self.host_lens = np.zeros(batch, dtype=np.int64)
+        self._attn_ws: dict[int, torch.Tensor] = {}
 
         # page groups: one per compression rate
         rates = sorted({s.m for s in layers if s.kind in ("csa", "hca")})
@@ -353,6 +354,38 @@ class DecodeCache:
             tmp_lens.copy_(torch.as_tensor((done + n).astype(np.int32)))
             ops.fp8_quant_append(pool, g.block_table, tmp_lens, x, torch.as_tensor(n, device=self.device))
             done += n
+
+    # -------------------------------------------------------------- attention --
+    def attention(self, i: int, q: torch.Tensor, knorm_w: torch.Tensor | None = None,
+                  sink: torch.Tensor | None = None, softcap: float | None = None,
+                  v_ring: torch.Tensor | None = None, eps: float = 1.0e-6,
+                  out: torch.Tensor | None = None) -> torch.Tensor:
+        """Layer i's attention for the query of every sequence after the last
+        step (saint_kv.attention.decode_attention over this cache's pool, block
+        table, picks and ring).  ``v_ring``: the window's values, a [batch,
+        window, latent] ring kept by the caller (default: the K ring, K = V).
+        The workspace is kept per layer between calls."""
+        from saint_kv.attention import decode_attention
+
+        spec = self.layers[i]
+        kw = {}
+        if spec.kind != "swa":
+            if knorm_w is None:
+                raise ValueError(f"layer {i} ({spec.kind}) needs knorm_w")
+            g = self.groups[self.group_of_rate[spec.m]]
+            kw = dict(pool=self.pool[i], fp8=spec.fp8, block_table=g.block_table, n_entries=g.n_entries,
+                      m=spec.m, knorm_w=knorm_w)
+            if spec.kind == "csa":
+                kw["picks"] = self.topk_idx[i]
+        ws = self._attn_ws.get(i)
+        out = decode_attention(q, spec.kind, self.tok_lens, self.ring[i],
+                               self.ring[i] if v_ring is None else v_ring, sink=sink, softcap=softcap,
+                               eps=eps, out=out, workspace=ws, **kw)
+        if ws is None:  # keep the workspace decode_attention sized for this layer
+            from saint_kv.attention import last_workspace
+
+            self._attn_ws[i] = last_workspace()
+        return out
 
     # ------------------------------------------------------------ persistence --
     def save(self, b: int, path, swa: str = "full", period: int | None = None) -> dict:

@@ -236,6 +236,10 @@ def test_attention_after_decode_step(dev) -> None:
                 kw["picks"] = cache.topk_idx[i]
         got = decode_attention(q.to(dev), s.kind, cache.tok_lens, cache.ring[i], cache.ring[i],
                                sink=sink.to(dev), **kw).cpu().numpy()
+        # the cache's own entry point (workspace kept per layer), twice
+        for _ in range(2):
+            mine = cache.attention(i, q.to(dev), knw.to(dev) if s.kind != "swa" else None, sink=sink.to(dev))
+            assert np.array_equal(mine.cpu().numpy(), got), (i, s.kind)
         want = np.zeros((B, H, D))
         for b in range(B):
             L = int(lens[b])
