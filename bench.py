@@ -625,6 +625,10 @@ def main() -> int:
         legs["csa_64k"] = run_decode_leg(
             dev, "csa_64k", [LayerSpec("csa", m=4, top_k=512)], 16,
             np.full(16, 65536, dtype=np.int64), args.leg_steps, seed=3)
+    if "csa_64k_b256" in wanted:
+        legs["csa_64k_b256"] = run_decode_leg(
+            dev, "csa_64k_b256", [LayerSpec("csa", m=4, top_k=512)], 256,
+            np.full(256, 65536, dtype=np.int64), args.leg_steps, seed=6)
     if "mixed_8layer" in wanted:
         specs = [LayerSpec("csa", m=4, top_k=512) if i % 2 == 0 else LayerSpec("hca", m=128)
                  for i in range(8)]

@@ -549,11 +549,14 @@ __device__ __forceinline__ void copy_rows(int n, RowFn row, int latent, bool fp8
       }
     }
     if (!fp8) continue;
-    for (int c0 = sub; c0 < fp8_tasks; c0 += kTPR * kU) {
-      u32x4 v[kU];
-      float scale[kU];
+    // an fp8 row of 576 channels is 40 tasks: fewer chunks in flight than a
+    // bf16 row needs (and fewer registers)
+    constexpr int kUF = (40 + kTPR - 1) / kTPR < kU ? (40 + kTPR - 1) / kTPR : kU;
+    for (int c0 = sub; c0 < fp8_tasks; c0 += kTPR * kUF) {
+      u32x4 v[kUF];
+      float scale[kUF];
 #pragma unroll
-      for (int u = 0; u < kU; ++u) {
+      for (int u = 0; u < kUF; ++u) {
         const int c = min(c0 + u * kTPR, fp8_tasks - 1);
         const bool live = rf.kind == 2;
         const bool is_code = c < code_chunks;
@@ -564,7 +567,7 @@ __device__ __forceinline__ void copy_rows(int n, RowFn row, int latent, bool fp8
                                      : reinterpret_cast<const float*>(safe4));
       }
 #pragma unroll
-      for (int u = 0; u < kU; ++u) {
+      for (int u = 0; u < kUF; ++u) {
         const int c = c0 + u * kTPR;
         if (c >= fp8_tasks || rf.kind != 2) continue;
         u32x4* o = reinterpret_cast<u32x4*>(rf.dst);
