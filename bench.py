@@ -204,6 +204,8 @@ def decode_step_bytes(specs, lens_after: np.ndarray, window: int, latent: int = 
             n_valid = np.maximum(p, 0) // s.m
             k_eff = np.minimum(s.top_k, n_ent)
             total += int((n_valid * 4 + s.top_k * 4).sum())  # scores read, indices written
+            if s.idx_heads:  # scores computed in the step: indexer keys, query and weights read, scores written
+                total += int((n_valid * (c_indexer * 2 + 4) + s.idx_heads * (c_indexer * 2 + 4)).sum())
             total += int((k_eff * (ent_bytes + E + 8) + (s.top_k - k_eff) * E).sum())
         else:
             total += int((n_ent * (ent_bytes + E) + (-(-n_ent // bs)) * 4).sum())
@@ -226,7 +228,8 @@ def decode_kv_tokens(specs, lens_after: np.ndarray, window: int) -> int:
 
 def run_decode_leg(dev, name: str, specs, batch: int, lens0: np.ndarray, steps: int,
                    per_graph: int = 20, window: int = 128, seed: int = 0,
-                   outlier_frac: float = 0.0, evict_frac: float | None = None) -> dict:
+                   outlier_frac: float = 0.0, evict_frac: float | None = None,
+                   separate_scores: int = 0) -> dict:
     from saint_kv.decode import DecodeCache
 
     max_len = int(lens0.max()) + steps + 2 * per_graph + 8
@@ -246,7 +249,24 @@ def run_decode_leg(dev, name: str, specs, batch: int, lens0: np.ndarray, steps: 
     cache.prefill(lens0, generator=gen, outlier_frac=outlier_frac)
     torch.cuda.synchronize()
     log(f"{name}: prefilled {batch} x mean {int(lens0.mean())} tokens in {time.perf_counter() - t0:.1f} s")
-    graph = cache.capture(per_graph)
+    before = None
+    if separate_scores:
+        # the caller's own indexer-score launch before each step (skv_indexer_scores
+        # over the entries before the step), in place of the step computing them
+        from saint_kv import ops
+
+        iq = torch.empty(batch, 1, separate_scores, cache.c_indexer, dtype=torch.bfloat16, device=dev)
+        iw = torch.empty(batch, 1, separate_scores, dtype=torch.float32, device=dev)
+        iq.normal_(generator=gen)
+        iw.normal_(generator=gen)
+        score_layers = [i for i, s in enumerate(specs) if s.kind == "csa"]
+
+        def before():
+            for i in score_layers:
+                g = cache.groups[cache.group_of_rate[specs[i].m]]
+                ops.indexer_scores(iq, iw, cache.idx_pool[i], g.block_table, g.n_entries,
+                                   cache.scores[i].unsqueeze(1))
+    graph = cache.capture(per_graph, before)
     graph.replay()  # warm-up replay
     torch.cuda.synchronize()
     cache.check_status()
@@ -261,6 +281,10 @@ def run_decode_leg(dev, name: str, specs, batch: int, lens0: np.ndarray, steps: 
     cache.check_status()
     n_steps = reps * per_graph
     ms = e0.elapsed_time(e1) / n_steps
+    if separate_scores:  # the same bytes as the step that computes its own scores
+        import dataclasses
+
+        specs = [dataclasses.replace(s, idx_heads=separate_scores) if s.kind == "csa" else s for s in specs]
     alg = sum(decode_step_bytes(specs, lens_start + i + 1, window) for i in range(n_steps)) / n_steps
     toks = sum(decode_kv_tokens(specs, lens_start + i + 1, window) for i in range(n_steps)) / n_steps
     gbs = alg / (ms * 1e-3) / 1e9
@@ -269,7 +293,10 @@ def run_decode_leg(dev, name: str, specs, batch: int, lens0: np.ndarray, steps: 
         "mean_ctx": int(lens0.mean()), "steps": n_steps, "us_per_step": round(ms * 1e3, 2),
         "alg_bytes_per_step": int(alg), "gbs": round(gbs, 1), "pct_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 2),
         "kv_tokens_per_step": int(toks), "kv_tokens_per_s": round(toks / (ms * 1e-3), 1),
-        "launches_per_step": 3, "hip_graph_steps": per_graph,
+        "launches_per_step": 3 + (sum(s.kind == "csa" for s in specs) if separate_scores else 0),
+        "hip_graph_steps": per_graph,
+        "scores": ("computed in the step" if any(s.idx_heads for s in specs) and not separate_scores
+                   else "skv_indexer_scores launch before each step" if separate_scores else "input"),
     }
     log(f"{name}: {rec['us_per_step']} us/step, {rec['gbs']} GB/s ({rec['pct_hbm_peak']}%), "
         f"{rec['kv_tokens_per_s'] / 1e6:.1f} M KV tok/s")
@@ -547,7 +574,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
-    ap.add_argument("--legs", default="csa_64k,mixed_8layer,fp8_1m",
+    ap.add_argument("--legs", default="csa_64k,csa_64k_idx,mixed_8layer,fp8_1m",
                     help="comma list of decode-step legs to run after the headline ('' for none)")
     ap.add_argument("--leg-steps", type=int, default=200)
     ap.add_argument("--no-indexer", action="store_true", help="skip the indexer-score leg")
@@ -629,6 +656,14 @@ def main() -> int:
         legs["csa_64k_b256"] = run_decode_leg(
             dev, "csa_64k_b256", [LayerSpec("csa", m=4, top_k=512)], 256,
             np.full(256, 65536, dtype=np.int64), args.leg_steps, seed=6)
+    if "csa_64k_idx" in wanted:
+        legs["csa_64k_idx"] = run_decode_leg(
+            dev, "csa_64k_idx", [LayerSpec("csa", m=4, top_k=512, idx_heads=64)], 16,
+            np.full(16, 65536, dtype=np.int64), args.leg_steps, seed=3)
+    if "csa_64k_idx_sep" in wanted:
+        legs["csa_64k_idx_sep"] = run_decode_leg(
+            dev, "csa_64k_idx_sep", [LayerSpec("csa", m=4, top_k=512)], 16,
+            np.full(16, 65536, dtype=np.int64), args.leg_steps, seed=3, separate_scores=64)
     if "mixed_8layer" in wanted:
         specs = [LayerSpec("csa", m=4, top_k=512) if i % 2 == 0 else LayerSpec("hca", m=128)
                  for i in range(8)]

@@ -360,6 +360,16 @@ typedef struct skv_decode_layer {
   void* out_entries;      /* CSA: [batch, top_k, latent]; HCA: [batch, out_rows, latent] bf16 */
   int64_t out_rows;       /* HCA: rows per sequence of out_entries */
   void* out_window;       /* [batch, window, latent] bf16 */
+  /* CSA with an indexer stream, optional: the step's indexer query.  When
+   * idx_q is set, the step computes the layer's scores itself (written to
+   * scores, as skv_indexer_scores would over the entries before the step)
+   * in its first launch, fused with the top-k histogram; the caller's
+   * separate score launch and the histogram's read of the scores go away.
+   * Either every CSA layer of the step sets it or none does. */
+  const void* idx_q;      /* [batch, idx_heads, c_indexer] bf16 */
+  const float* idx_w;     /* [batch, idx_heads] fp32 head weights */
+  int32_t idx_heads;      /* 1..64 (c_indexer <= 128) */
+  int32_t idx_pad_;
 } skv_decode_layer;
 
 typedef struct skv_decode_desc {

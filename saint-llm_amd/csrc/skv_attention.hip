@@ -68,13 +68,6 @@ struct AttnArgs {
   float eps, softcap;  // softcap <= 0: none
 };
 
-// Workgroup barrier that orders LDS only: global loads stay in flight.
-__device__ __forceinline__ void lds_barrier() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-  __builtin_amdgcn_s_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
-}
-
 __device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
 
 // Key j (0..7) of slot group a (0..3) within a tile: keys 4a..4a+3, 16+4a..16+4a+3.

@@ -214,4 +214,12 @@ __device__ __forceinline__ uint32_t ceil_div24(uint32_t a, uint32_t b) { return 
 // all 256 CUs several times over.
 constexpr int kPersistentBlocks = 2048;
 
+// Workgroup barrier that orders LDS only: global loads and stores stay in
+// flight (__syncthreads also waits for them).
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 }  // namespace skv

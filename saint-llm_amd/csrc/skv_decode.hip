@@ -18,6 +18,7 @@
 // (hca.py:126-141) and the SWA window (swa.py:115-125).
 #include "skv_pool_state.h"
 #include "skv_topk.h"
+#include "skv_indexer_tile.h"
 
 namespace skv {
 
@@ -381,6 +382,63 @@ __global__ __launch_bounds__(kTkPartThreads) void k_decode_hist(int n_chunks, St
   topk_hist_chunk_at(
       sm, map.scores[c.z] + static_cast<int64_t>(c.b) * width, width,
       [&](int& n_cols, int& n_valid) { chunk_cols(map, c, n_cols, n_valid); }, map.top_k[c.z], c.chunk, ws);
+}
+
+// Score launch (in place of the hist launch when the step computes its own
+// scores): workgroup (tile, sequence, CSA layer) scores kIdxTile of the
+// layer's indexer entries before the step (the n_valid visible to the new
+// token: floor(L / m) of L tokens before it), writes them to the layer's
+// score row and adds their 11-bit key histogram to the row's, exactly as
+// the hist launch would from the written row.  Tile 0 zeroes the row's list
+// counters.
+struct ScoreMap {
+  const uint8_t* q[SKV_MAX_LAYERS];     // of the i-th CSA layer: [batch, heads, c] bf16
+  const float* w[SKV_MAX_LAYERS];       // [batch, heads]
+  const uint8_t* pool[SKV_MAX_LAYERS];  // indexer stream pages
+  int32_t heads[SKV_MAX_LAYERS];
+  int32_t c;                            // indexer channels
+};
+
+__global__ __launch_bounds__(kIdxThreads, 2) void k_decode_score_hist(int n_tiles, StepMap map, ScoreMap sc) {
+  __shared__ IndexerSmem sm;
+  __shared__ TopkHistSmem hs;
+  const TopkChunk c = topk_chunk(blockIdx.x, n_tiles, map);
+  const int tid = threadIdx.x;
+  int32_t* ws = map.topk_ws[c.z] + static_cast<int64_t>(c.b) * kTkWsWords;
+  if (c.chunk == 0 && tid < 3) ws[kTkWsCnt + tid] = 0;
+  const int li = static_cast<int>((map.csa >> (4 * c.z)) & 15);
+  const GroupRef G = group_ref(map, map.group[li]);
+  const int heads = sc.heads[c.z];
+  const IndexerRow r{sc.q[c.z] + static_cast<int64_t>(c.b) * heads * sc.c * 2,
+                     sc.w[c.z] + static_cast<int64_t>(c.b) * heads,
+                     sc.pool[c.z],
+                     G.block_table + static_cast<int64_t>(c.b) * G.bt_stride,
+                     G.bt_stride,
+                     G.block_size,
+                     G.n_pages,
+                     heads,
+                     sc.c};
+  for (int i = tid; i < kTkBins; i += kIdxThreads) hs.hist[i] = 0;  // ordered by the tile's barrier
+  const int width = map.score_stride[c.z];
+  float* row = const_cast<float*>(map.scores[c.z]) + static_cast<int64_t>(c.b) * width;
+  bool hist = false;
+  const bool live = indexer_tile(
+      sm, r, c.chunk,
+      [&] {
+        int n_cols, n_valid;
+        score_cols(width, G.m, map.tok_lens[c.b] + 1, n_cols, n_valid);
+        hist = topk_sel(map.top_k[c.z], n_cols, n_valid) > 0;
+        return max(0, min(n_valid, n_cols));
+      },
+      [&](int e, float v) {
+        row[e] = v;
+        if (hist) atomicAdd(&hs.hist[score_key(v) >> kTkShift], 1);
+      });
+  if (!live || !hist) return;  // uniform
+  lds_barrier();  // the histogram is complete; the score stores stay in flight
+  for (int i = tid; i < kTkBins; i += kIdxThreads) {
+    if (hs.hist[i]) atomicAdd(&ws[kTkWsHist + i], hs.hist[i]);
+  }
 }
 
 union AppendSmem {
@@ -1168,7 +1226,9 @@ extern "C" int skv_decode_step(const skv_decode_desc* h, const skv_decode_desc* 
     map.n_pages[g] = used ? static_cast<int32_t>(h->groups[g].n_pages) : 1;
   }
   uint32_t groups_seen = 0;
-  int n_csa = 0, max_top_k = 0;
+  int n_csa = 0, max_top_k = 0, n_scored = 0;
+  ScoreMap sc{};
+  sc.c = h->c_indexer;
   int64_t max_score_cols = 1, n_tiles = 0;
   for (int l = 0; l < h->n_layers; ++l) {
     const skv_decode_layer& Ly = h->layers[l];
@@ -1197,6 +1257,20 @@ extern "C" int skv_decode_step(const skv_decode_desc* h, const skv_decode_desc* 
         max_score_cols = max(max_score_cols, Ly.score_stride);
         if (Ly.idx_pool && (!Ly.idx_state || !Ly.idx_bias || !Ly.ci_new || !Ly.zi_new || h->c_indexer <= 0)) {
           return set_error(SKV_EINVAL, "%s: CSA layer %d indexer stream incomplete", what, l);
+        }
+        if (Ly.idx_q) {
+          if (!Ly.idx_pool || !Ly.idx_w || Ly.idx_heads < 1 || Ly.idx_heads > 16 * kIdxMaxHB ||
+              h->c_indexer > 32 * kIdxMaxKS) {
+            return set_error(SKV_EINVAL,
+                             "%s: CSA layer %d: step scores need the indexer stream, idx_w, 1 <= idx_heads <= %d "
+                             "and c_indexer <= %d",
+                             what, l, 16 * kIdxMaxHB, 32 * kIdxMaxKS);
+          }
+          sc.q[n_csa] = static_cast<const uint8_t*>(Ly.idx_q);
+          sc.w[n_csa] = Ly.idx_w;
+          sc.pool[n_csa] = static_cast<const uint8_t*>(Ly.idx_pool);
+          sc.heads[n_csa] = Ly.idx_heads;
+          ++n_scored;
         }
         if (Ly.score_stride >= (1 << 24)) {
           return set_error(SKV_EINVAL, "%s: CSA layer %d score_stride >= 2^24", what, l);
@@ -1228,6 +1302,9 @@ extern "C" int skv_decode_step(const skv_decode_desc* h, const skv_decode_desc* 
     map.tile_end[l] = static_cast<int32_t>(n_tiles < (1 << 24) ? n_tiles : (1 << 24));
   }
   map.n_csa = n_csa;
+  if (n_scored != 0 && n_scored != n_csa) {
+    return set_error(SKV_EINVAL, "%s: either every CSA layer sets idx_q or none does", what);
+  }
   if (h->batch == 0 || h->n_layers == 0) return SKV_OK;
   const int n_chunks = static_cast<int>(ceil_div(max_score_cols, kTkChunk));
   const int64_t n_append = static_cast<int64_t>(h->batch) * h->n_layers +
@@ -1246,7 +1323,14 @@ extern "C" int skv_decode_step(const skv_decode_desc* h, const skv_decode_desc* 
   }
   hipStream_t s = static_cast<hipStream_t>(stream);
   int rc;
-  if (n_hist > 0) {
+  if (n_hist > 0 && n_scored > 0) {
+    const int n_score_tiles = static_cast<int>(ceil_div(max_score_cols, kIdxTile));
+    const int64_t n_score = static_cast<int64_t>(n_score_tiles) * h->batch * n_csa;
+    if (n_score >= (1 << 24)) return set_error(SKV_EINVAL, "%s: score grid of 2^24 workgroups or more", what);
+    hipLaunchKernelGGL(k_decode_score_hist, dim3(static_cast<unsigned>(n_score)), dim3(kIdxThreads), 0, s,
+                       n_score_tiles, map, sc);
+    if ((rc = check_launch(what))) return rc;
+  } else if (n_hist > 0) {
     hipLaunchKernelGGL(k_decode_hist, dim3(static_cast<unsigned>(n_hist)), dim3(kTkPartThreads), 0, s, n_chunks,
                        map);
     if ((rc = check_launch(what))) return rc;

@@ -54,6 +54,7 @@ class DecodeLayerC(ctypes.Structure):
         ("kv_new", _P), ("c_new", _P), ("z_new", _P), ("ci_new", _P), ("zi_new", _P),
         ("scores", _P), ("score_stride", ctypes.c_int64), ("topk_idx", _P), ("topk_ws", _P),
         ("out_entries", _P), ("out_rows", ctypes.c_int64), ("out_window", _P),
+        ("idx_q", _P), ("idx_w", _P), ("idx_heads", ctypes.c_int32), ("idx_pad_", ctypes.c_int32),
     ]
 
 
@@ -84,6 +85,10 @@ class LayerSpec:
     top_k: int = 512
     fp8: bool = False
     indexer: bool = True
+    # CSA with an indexer: > 0 makes the step compute the layer's scores from
+    # inputs["iq"] (bf16 [batch, idx_heads, c_indexer]) and inputs["iw"]
+    # (fp32 [batch, idx_heads]) instead of reading them from ``scores``
+    idx_heads: int = 0
 
 
 @dataclass
@@ -111,6 +116,11 @@ class DecodeCache:
                  hca_out_rows: int | None = None, score_cols: int | None = None) -> None:
         if not 0 < len(layers) <= MAX_LAYERS:
             raise ValueError(f"1..{MAX_LAYERS} layers supported; got {len(layers)}")
+        scored = [s.idx_heads > 0 for s in layers if s.kind == "csa"]
+        if any(scored) and not all(scored):
+            raise ValueError("either every CSA layer computes its scores in the step (idx_heads > 0) or none does")
+        if any(not 0 <= s.idx_heads <= 64 for s in layers):
+            raise ValueError("idx_heads must be in [0, 64]")
         if not 0 < batch <= MAX_BATCH:
             raise ValueError(f"batch must be in [1, {MAX_BATCH}]; got {batch}")
         if max_len <= 0:
@@ -189,6 +199,11 @@ class DecodeCache:
                         ibias = torch.zeros(spec.m, c_indexer, dtype=torch.float32, device=dev)
                         inp["ci"] = torch.zeros(batch, c_indexer, dtype=bf, device=dev)
                         inp["zi"] = torch.zeros(batch, c_indexer, dtype=bf, device=dev)
+                        if spec.idx_heads > 0:
+                            inp["iq"] = torch.zeros(batch, spec.idx_heads, c_indexer, dtype=bf, device=dev)
+                            inp["iw"] = torch.zeros(batch, spec.idx_heads, dtype=torch.float32, device=dev)
+                    elif spec.idx_heads > 0:
+                        raise ValueError("idx_heads needs the layer's indexer stream (indexer=True)")
                     # default width rounded up to 4 columns (16-byte rows)
                     cols = -(-max(1, max_len // spec.m) // 4) * 4 if score_cols is None else int(score_cols)
                     if cols < max_len // spec.m:
@@ -247,6 +262,9 @@ class DecodeCache:
                         Ly.idx_pool, Ly.idx_state = p(self.idx_pool[i]), p(self.idx_state[i])
                         Ly.idx_bias = p(self.idx_bias[i])
                         Ly.ci_new, Ly.zi_new = p(self.inputs[i]["ci"]), p(self.inputs[i]["zi"])
+                        if spec.idx_heads > 0:
+                            Ly.idx_q, Ly.idx_w = p(self.inputs[i]["iq"]), p(self.inputs[i]["iw"])
+                            Ly.idx_heads = spec.idx_heads
                 else:
                     Ly.out_rows = self.out_entries[i].shape[1]
         self._desc = d
@@ -255,16 +273,20 @@ class DecodeCache:
 
     # ------------------------------------------------------------------ step --
     def step(self) -> None:
-        """One decode step of every sequence from the current ``inputs`` and ``scores``."""
+        """One decode step of every sequence from the current ``inputs`` and ``scores``
+        (for layers with ``idx_heads``, from ``inputs["iq"]`` / ``inputs["iw"]``: the step
+        writes ``scores`` itself)."""
         if (self.host_lens + 1 > self.max_len).any():
             raise RuntimeError(f"DecodeCache overflow: a sequence would exceed max_len={self.max_len}")
         _lib.call("skv_decode_step", ctypes.addressof(self._desc), self._desc_dev.data_ptr(),
                   _lib.stream_handle(self.device))
         self.host_lens += 1
 
-    def capture(self, steps: int) -> "CapturedSteps":
-        """Capture ``steps`` decode steps in one HIP graph (see CapturedSteps)."""
-        return CapturedSteps(self, steps)
+    def capture(self, steps: int, before_step=None) -> "CapturedSteps":
+        """Capture ``steps`` decode steps in one HIP graph (see CapturedSteps);
+        ``before_step()`` (optional) records the caller's own launches ahead of
+        each step, e.g. its indexer-score launch."""
+        return CapturedSteps(self, steps, before_step)
 
     def check_status(self) -> None:
         """Synchronise and raise if a page reservation was refused.
@@ -456,7 +478,7 @@ class CapturedSteps:
     surface a refused page reservation.
     """
 
-    def __init__(self, cache: DecodeCache, steps: int) -> None:
+    def __init__(self, cache: DecodeCache, steps: int, before_step=None) -> None:
         if steps <= 0:
             raise ValueError("steps must be positive")
         self.cache, self.steps = cache, steps
@@ -464,6 +486,8 @@ class CapturedSteps:
         lens_before = cache.host_lens.copy()
         with torch.cuda.graph(self.graph):
             for _ in range(steps):
+                if before_step is not None:
+                    before_step()
                 _lib.call("skv_decode_step", ctypes.addressof(cache._desc), cache._desc_dev.data_ptr(),
                           _lib.stream_handle(cache.device))
         cache.host_lens = lens_before  # capture records, it does not run

@@ -440,3 +440,71 @@ def test_decode_refused_step_changes_nothing(dev) -> None:
     cache.step()
     cache.check_status()
     assert cache.tok_lens.tolist() == [1, 14]
+
+
+# the step computes its own scores (LayerSpec.idx_heads): the scores it writes
+# equal skv_indexer_scores over the entries before the step, bit for bit, and
+# its top-k and gathered entries equal the oracle's on those scores
+def test_decode_step_computes_scores(dev) -> None:
+    from saint_kv import ops
+    from saint_kv.decode import DecodeCache, LayerSpec
+
+    specs = [LayerSpec("csa", m=4, top_k=64, idx_heads=64), LayerSpec("hca", m=128),
+             LayerSpec("csa", m=4, top_k=24, fp8=True, idx_heads=20)]
+    B, max_len, bs, C = 5, 4096, 16, 576
+    cache = DecodeCache(specs, B, max_len, block_size=bs, window=32, device=dev, page_order_seed=7)
+    gen = torch.Generator(device=dev).manual_seed(7)
+    for i in range(len(specs)):
+        for t in (cache.bias[i], cache.idx_bias[i]):
+            if t is not None:
+                t.normal_(generator=gen)
+    cache.prefill(np.array([0, 3, 4, 2051, 3000]), generator=gen)
+    for step in range(9):
+        for i in range(len(specs)):
+            for v in cache.inputs[i].values():
+                v.normal_(generator=gen)
+        if step == 4:
+            cache.inputs[0]["iw"].zero_()  # every score 0: one tie bin
+        exp = [None] * len(specs)
+        for i, s in enumerate(specs):
+            if s.kind == "csa":
+                g = cache.groups[cache.group_of_rate[s.m]]
+                exp[i] = torch.full_like(cache.scores[i], float("nan"))
+                ops.indexer_scores(cache.inputs[i]["iq"].unsqueeze(1), cache.inputs[i]["iw"].unsqueeze(1),
+                                   cache.idx_pool[i], g.block_table, g.n_entries, exp[i].unsqueeze(1))
+        before = cache.host_lens.copy()
+        cache.step()
+        torch.cuda.synchronize()
+        cache.check_status()
+        for i, s in enumerate(specs):
+            if exp[i] is None:
+                continue
+            gi = cache.group_of_rate[s.m]
+            got, want = cache.scores[i].cpu(), exp[i].cpu()
+            idx = _np(cache.topk_idx[i])
+            for b in range(B):
+                n = int(before[b]) // s.m
+                assert ref.n_valid_blocks(int(before[b]), s.m) == n
+                assert torch.equal(got[b, :n], want[b, :n]), (step, i, b)
+                sel = ref.topk_select(want[b:b + 1].numpy(), np.array([n]), s.top_k, (int(before[b]) + 1) // s.m)[0]
+                assert np.array_equal(idx[b, :len(sel)], sel), (step, i, b)
+                assert (idx[b, len(sel):] == -1).all(), (step, i, b)
+            pool = cache.pool[i].cpu()
+            src = ref.fp8_unpack_entries(pool.reshape(-1, 656)).reshape(*pool.shape[:2], C) if s.fp8 else pool
+            out = cache.out_entries[i].cpu()
+            exp_out = torch.zeros_like(out)
+            ref.topk_gather(src, _np(cache.groups[gi].block_table), np.arange(B), idx, exp_out)
+            ent = _np(cache.groups[gi].n_entries)
+            for b in range(B):
+                if ent[b] == 0:
+                    exp_out[b] = 0
+            assert torch.equal(out, exp_out), (step, i)
+
+
+def test_decode_step_scores_all_or_none(dev) -> None:
+    from saint_kv.decode import DecodeCache, LayerSpec
+
+    with pytest.raises(ValueError, match="every CSA layer"):
+        DecodeCache([LayerSpec("csa", idx_heads=8), LayerSpec("csa")], 2, 256, device=dev)
+    with pytest.raises(ValueError, match="indexer stream"):
+        DecodeCache([LayerSpec("csa", indexer=False, idx_heads=8)], 2, 256, device=dev)
