@@ -508,3 +508,63 @@ def test_decode_step_scores_all_or_none(dev) -> None:
         DecodeCache([LayerSpec("csa", idx_heads=8), LayerSpec("csa")], 2, 256, device=dev)
     with pytest.raises(ValueError, match="indexer stream"):
         DecodeCache([LayerSpec("csa", indexer=False, idx_heads=8)], 2, 256, device=dev)
+
+
+# the same steps two ways, replayed from HIP graphs three times with eager
+# input fills between the replays: scores computed in the step (idx_heads)
+# and a caller's skv_indexer_scores launch recorded before each step
+# (capture's before_step); every table, score, pick and gathered row agrees
+def test_step_scores_fused_equals_separate_launch_in_graphs(dev) -> None:
+    from saint_kv import ops
+    from saint_kv.decode import DecodeCache, LayerSpec
+
+    B, IH, lens0 = 3, 16, np.array([5, 700, 1999])
+
+    def make(fused):
+        specs = [LayerSpec("csa", m=4, top_k=32, idx_heads=IH if fused else 0), LayerSpec("hca", m=16)]
+        c = DecodeCache(specs, B, 4096, block_size=16, window=32, device=dev, page_order_seed=9)
+        gen = torch.Generator(device=dev).manual_seed(9)
+        for i in range(len(specs)):
+            for t in (c.bias[i], c.idx_bias[i]):
+                if t is not None:
+                    t.normal_(generator=gen)
+        c.prefill(lens0, generator=gen)
+        return c
+
+    fused, sep = make(True), make(False)
+    iq = torch.empty(B, 1, IH, 128, dtype=torch.bfloat16, device=dev)
+    iw = torch.empty(B, 1, IH, dtype=torch.float32, device=dev)
+    g0 = sep.groups[sep.group_of_rate[4]]
+
+    def scores_launch():
+        ops.indexer_scores(iq, iw, sep.idx_pool[0], g0.block_table, g0.n_entries, sep.scores[0].unsqueeze(1))
+
+    graph_f, graph_s = fused.capture(2), sep.capture(2, scores_launch)
+    gen = torch.Generator(device=dev).manual_seed(10)
+    for rep in range(3):
+        for i in range(2):
+            for k, v in fused.inputs[i].items():
+                v.normal_(generator=gen)
+                if k == "iq":
+                    iq.copy_(v.unsqueeze(1))
+                elif k == "iw":
+                    iw.copy_(v.unsqueeze(1))
+                else:
+                    sep.inputs[i][k].copy_(v)
+        torch.cuda.synchronize()
+        graph_f.replay()
+        graph_s.replay()
+        torch.cuda.synchronize()
+        fused.check_status()
+        sep.check_status()
+        assert torch.equal(fused.tok_lens, sep.tok_lens)
+        for a, b in zip(fused.groups, sep.groups):
+            assert torch.equal(a.block_table, b.block_table) and torch.equal(a.n_entries, b.n_entries)
+        for b in range(B):
+            n = int(sep.host_lens[b] - 1) // 4
+            assert torch.equal(fused.scores[0][b, :n], sep.scores[0][b, :n]), (rep, b)
+        for i in range(2):
+            assert torch.equal(fused.out_entries[i], sep.out_entries[i]), (rep, i)
+            assert torch.equal(fused.out_window[i], sep.out_window[i]), (rep, i)
+            assert torch.equal(fused.pool[i], sep.pool[i]), (rep, i)
+        assert torch.equal(fused.topk_idx[0], sep.topk_idx[0]), rep
