@@ -574,7 +574,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
-    ap.add_argument("--legs", default="csa_64k,csa_64k_idx,mixed_8layer,fp8_1m",
+    ap.add_argument("--legs", default="csa_64k,csa_64k_b256,csa_64k_idx,mixed_8layer,fp8_1m",
                     help="comma list of decode-step legs to run after the headline ('' for none)")
     ap.add_argument("--leg-steps", type=int, default=200)
     ap.add_argument("--no-indexer", action="store_true", help="skip the indexer-score leg")

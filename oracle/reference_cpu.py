@@ -5,8 +5,8 @@ This module restates, on the CPU with torch-eager and numpy, what the reference
 ``packages/core`` / ``packages/kernels``) computes on this path, extended to the
 paged / ragged form the HIP library implements.  Only ``tests/``,
 ``__graft_entry__.smoke()`` and ``bench.py``'s ``cpu_baseline`` leg may import
-it, and only as the checker or as the timed CPU baseline — never as a product
-code path.  The HIP library never calls into it.
+it, and only to verify results or as the timed CPU baseline — never as a
+product code path.  The HIP library never calls into it.
 
 Pinning (what fixes each function independently of this file):
   * contiguous caches      — restate kv_cache.py:32-327 line for line in
