@@ -295,6 +295,10 @@ int skv_compact(const skv_pool_ref* pools, int32_t n_pools, int32_t* block_table
 /* ---- fused decode step ----------------------------------------------------
  * One decode step (one new token per sequence) of a stack of heterogeneous
  * layers in three launches, whatever the layer count:
+ *   histogram : per CSA layer the 11-bit key histogram of the score row
+ *            (with idx_q set: the scores themselves, computed from the
+ *            indexer stream and written to scores, and their histogram);
+ *            no launch without CSA layers.
  *   append : every workgroup computes the step's page plan (for each page
  *            group, the page of any compressed entry this token completes,
  *            popped in skv_reserve order: groups in order, ascending
@@ -303,10 +307,9 @@ int skv_compact(const skv_pool_ref* pools, int32_t n_pools, int32_t* block_table
  *            row goes into its SWA ring; HCA/CSA layers fold (c, z) into the
  *            running pooling state and emit the entry when the block
  *            completes (bf16 or fp8); CSA layers do the same for the indexer
- *            stream (bf16 entries) and histogram their score rows.  New
+ *            stream (bf16 entries).  Beside it, per CSA layer, the top-k
+ *            candidate lists (skv_topk_select_decode semantics).  New
  *            lengths and free-stack tops go to step_lens / step_top.
- *   filter : per CSA layer the top-k candidate lists (skv_topk_select_decode
- *            semantics; no launch without CSA layers).
  *   gather : per CSA layer the ordered top_k picks and their gather (fp8
  *            dequantized to bf16; -1 reads entry 0, picks without an entry
  *            give zero rows); HCA layers copy all their entries (dense read,
