@@ -123,3 +123,45 @@ def test_single_hip_runtime_mapped() -> None:
     maps = Path("/proc/self/maps").read_text()
     libs = {ln.split()[-1] for ln in maps.splitlines() if "libamdhip64" in ln}
     assert len(libs) == 1, libs
+
+
+def test_decode_step_score_fields_checked_on_host() -> None:
+    """skv_decode_step refuses, before any device work, a step whose CSA
+    layers disagree on computing their scores (idx_q), or whose step scores
+    lack the indexer stream or exceed 64 heads.  The pointers are never
+    dereferenced on these paths (placeholders)."""
+    import ctypes
+
+    from saint_kv import _lib
+    from saint_kv.decode import DecodeDescC
+
+    lib = _lib.load()
+    fake = 0x1000  # placeholder address: the checks fail before any use
+    d = DecodeDescC()
+    d.batch, d.n_layers, d.n_groups = 2, 2, 1
+    d.latent, d.c_indexer, d.window = 576, 128, 128
+    d.tok_lens = d.status = d.step_lens = d.step_top = fake
+    G = d.groups[0]
+    G.free_stack = G.free_top = G.block_table = G.n_entries = fake
+    G.n_pages, G.bt_stride, G.m, G.block_size = 64, 8, 4, 64
+    for i in range(2):
+        Ly = d.layers[i]
+        Ly.kind, Ly.group, Ly.format, Ly.top_k = 2, 0, _lib.SKV_FMT_BF16, 16  # CSA
+        Ly.ring = Ly.kv_new = Ly.out_window = Ly.pool = Ly.state = Ly.bias = fake
+        Ly.c_new = Ly.z_new = Ly.out_entries = Ly.scores = Ly.topk_idx = Ly.topk_ws = fake
+        Ly.entry_bytes, Ly.score_stride = 1152, 128
+        Ly.idx_pool = Ly.idx_state = Ly.idx_bias = Ly.ci_new = Ly.zi_new = fake
+
+    def step(desc):
+        return lib.skv_decode_step(ctypes.byref(desc), ctypes.c_void_p(fake), None)
+
+    one = DecodeDescC.from_buffer_copy(d)
+    one.layers[0].idx_q, one.layers[0].idx_w, one.layers[0].idx_heads = fake, fake, 8
+    assert step(one) == _lib.SKV_EINVAL and "every CSA layer" in _lib.last_error()
+    many = DecodeDescC.from_buffer_copy(one)
+    many.layers[1].idx_q, many.layers[1].idx_w, many.layers[1].idx_heads = fake, fake, 65
+    assert step(many) == _lib.SKV_EINVAL and "idx_heads" in _lib.last_error()
+    no_stream = DecodeDescC.from_buffer_copy(one)
+    no_stream.layers[1].idx_q, no_stream.layers[1].idx_w, no_stream.layers[1].idx_heads = fake, fake, 8
+    no_stream.layers[1].idx_pool = None
+    assert step(no_stream) == _lib.SKV_EINVAL
