@@ -9,8 +9,10 @@ allocation) + fused append+gather of every sequence into a packed buffer.
 
 Prints one JSON line (see the keys below).  Progress goes to stderr.
 
-A step is one skv_decode_append_gather call: a one-workgroup planner (page
-reservation + page-unit table) and the fused append + gather over 4 KB slices.
+A step is the two launches of skv_decode_append_gather (ops.plan_units +
+ops.copy_slices): a one-workgroup planner (page reservation + page-unit table)
+and the fused append + gather over 4 KB slices.  The planner of step i+1 runs
+on a second stream into a second unit table while step i's copy runs.
 
 Algorithmic bytes per step (read + write of every gathered row, the appended
 row read + written, one int32 block-table entry per page):
@@ -109,7 +111,13 @@ class PagedDecode:
         self.out = torch.empty(int(cap.sum()), ROW, dtype=torch.bfloat16, device=dev)
         self.tokens = torch.empty(steps_total, batch, 1, ROW, dtype=torch.bfloat16, device=dev)
         self.tokens.normal_(generator=gen)
-        self.units = ops.unit_table(batch * max_pages, dev)
+        # two page-unit tables: step i+1's planner (on its own stream, default
+        # priority) fills one while step i's copy reads the other; the copy reads
+        # only its unit table, the pool, the new tokens and the output
+        self.units = [ops.unit_table(batch * max_pages, dev) for _ in range(2)]
+        self.plan_stream = torch.cuda.Stream(device=dev)
+        self.plan_done = [torch.cuda.Event() for _ in range(2)]
+        self.copy_done = [torch.cuda.Event() for _ in range(2)]
         self.step_idx = 0
         torch.cuda.synchronize()
         if int(self.status.item()) != 0:
@@ -118,16 +126,30 @@ class PagedDecode:
     def host_lens(self) -> np.ndarray:
         return self.lens0 + self.step_idx
 
+    def start(self) -> None:
+        """Order the planner stream after everything issued so far on the current stream."""
+        self.plan_stream.wait_stream(torch.cuda.current_stream())
+
     def step(self, ev: tuple | None = None) -> None:
-        """skv_decode_append_gather: planner (reserve + page-unit table) + 4 KB-slice copy."""
+        """skv_decode_append_gather: planner (reserve + page-unit table) + 4 KB-slice copy.
+
+        The planner runs on its own stream and overlaps the previous step's copy."""
         max_units = int((-(-(self.host_lens() + 1) // self.bs)).sum())
-        self.ops.plan_units(self.stack, self.top, self.bt, self.lens, 1, self.bs, self.out,
-                            ROW_BYTES, self.units, max_units, self.offsets, self.status)
+        k = self.step_idx % 2
+        main = torch.cuda.current_stream()
+        ps = self.plan_stream
+        ps.wait_event(self.copy_done[k])  # the copy two steps back has read units[k]
+        with torch.cuda.stream(ps):
+            self.ops.plan_units(self.stack, self.top, self.bt, self.lens, 1, self.bs, self.out,
+                                ROW_BYTES, self.units[k], max_units, self.offsets, self.status)
+        self.plan_done[k].record(ps)
+        main.wait_event(self.plan_done[k])
         if ev is not None:
             ev[0].record()
-        self.ops.copy_slices(self.pool, self.tokens[self.step_idx], self.out, self.units, max_units)
+        self.ops.copy_slices(self.pool, self.tokens[self.step_idx], self.out, self.units[k], max_units)
         if ev is not None:
             ev[1].record()
+        self.copy_done[k].record(main)
         self.step_idx += 1
 
 
@@ -614,6 +636,7 @@ def main() -> int:
         lens_steps.append(w.host_lens() + i + 1)
     torch.cuda.synchronize()
     t_start.record(stream)
+    w.start()  # the first planner after t_start
     for i in range(args.steps):
         w.step()
     t_end.record(stream)
@@ -630,6 +653,7 @@ def main() -> int:
     for i in range(args.steps):
         alg_kern += alg_bytes_append_gather(w.host_lens() + i + 1, bs)
     torch.cuda.synchronize()
+    w.start()
     for i in range(args.steps):
         w.step(evs[i])
     torch.cuda.synchronize()
@@ -710,7 +734,8 @@ def main() -> int:
         "data": "synthetic N(0,1) KV rows, seeded; random-permutation page pool",
         "config": {
             "workload": "paged decode append + full block-table gather (B=64, L~U[1k,32k], "
-                        "latent 512+64 bf16, bs=64, 200k-page pool, 1 token/seq/step)",
+                        "latent 512+64 bf16, bs=64, 200k-page pool, 1 token/seq/step; each step's "
+                        "planner overlaps the previous step's copy on a second stream)",
             "batch": batch,
             "block_size": bs,
             "row_bytes": ROW_BYTES,

@@ -263,3 +263,56 @@ def test_decode_append_gather_matches_two_call_path(dev) -> None:
     assert int(a.status.item()) == 16  # SKV_STATUS_UNITS
     assert torch.equal(a.bt, before[0]) and torch.equal(a.lens, before[1])
     assert torch.equal(a.top, before[2]) and torch.equal(out_a, before[3])
+
+
+def test_pipelined_planner_matches_sequential(dev) -> None:
+    """The planner of step i+1 on a second stream, into the other of two unit
+    tables, overlapping step i's copy (the headline bench loop): every step's
+    output, the tables and the pool equal the sequential two-call path."""
+    from saint_kv import ops
+
+    rng = np.random.default_rng(8)
+    g = torch.Generator().manual_seed(8)
+    batch, bs, n_pages, d, steps = 9, 64, 3000, 576, 12
+    order = rng.permutation(n_pages).astype(np.int32)
+    a = _State(dev, batch, n_pages, 80, bs, (d,), torch.bfloat16, order)
+    b = _State(dev, batch, n_pages, 80, bs, (d,), torch.bfloat16, order)
+    lens0 = rng.integers(0, 4000, size=batch).astype(np.int32)
+    lens0[2] = 63  # crosses a page boundary on the first step
+    pre = torch.randn(batch, int(lens0.max()), d, generator=g).to(torch.bfloat16).to(dev)
+    for s in (a, b):
+        s.reserve(lens0)
+        s.ops.paged_append(s.pool, s.bt, s.lens, pre, torch.as_tensor(lens0, device=dev))
+    cap = lens0.astype(np.int64) + steps
+    offs = torch.as_tensor(np.concatenate([[0], np.cumsum(cap)[:-1]]), device=dev)
+    outs_a = [torch.zeros(int(cap.sum()), d, dtype=torch.bfloat16, device=dev) for _ in range(steps)]
+    out_b = torch.zeros_like(outs_a[0])
+    toks = [torch.randn(batch, 1, d, generator=g).to(torch.bfloat16).to(dev) for _ in range(steps)]
+    units = [ops.unit_table(batch * 80, dev) for _ in range(2)]
+    ps = torch.cuda.Stream(device=dev)
+    plan_done = [torch.cuda.Event() for _ in range(2)]
+    copy_done = [torch.cuda.Event() for _ in range(2)]
+    main = torch.cuda.current_stream(dev)
+    ps.wait_stream(main)
+    lens = lens0.astype(np.int64)
+    for step in range(steps):
+        k = step % 2
+        max_units = int((-(-(lens + 1) // bs)).sum())
+        ps.wait_event(copy_done[k])  # the copy two steps back has read units[k]
+        with torch.cuda.stream(ps):
+            ops.plan_units(a.stack, a.top, a.bt, a.lens, 1, bs, outs_a[step], 2 * d, units[k], max_units,
+                           offs, a.status)
+        plan_done[k].record(ps)
+        main.wait_event(plan_done[k])
+        ops.copy_slices(a.pool, toks[step], outs_a[step], units[k], max_units)
+        copy_done[k].record(main)
+        lens += 1
+    torch.cuda.synchronize()
+    assert int(a.status.item()) == 0
+    for step in range(steps):
+        b.reserve(1)
+        ops.append_gather(b.pool, b.bt, b.lens, toks[step], 1, out_b, offs)
+        torch.cuda.synchronize()
+        assert torch.equal(outs_a[step], out_b), step
+    assert torch.equal(a.bt, b.bt) and torch.equal(a.lens, b.lens) and torch.equal(a.top, b.top)
+    assert torch.equal(a.pool, b.pool)
