@@ -588,6 +588,125 @@ __global__ __launch_bounds__(256) void k_attn_merge(MergeArgs a) {
   }
 }
 
+// The merge for sequences of at most kMergeChunkQ units: one wave per (head,
+// third of the dims), lane t takes the 4-dim quad t + 64z, so that every load
+// and store of the wave covers consecutive bytes; one memory round trip
+// brings lane t's (max, sum) of unit t and its quad of every unit's output.
+constexpr int kMergeChunkQ = 8;
+constexpr int kQLane = 1;  // quads per lane
+
+__global__ __launch_bounds__(256) void k_attn_merge_q(MergeArgs a) {
+  const int b = blockIdx.x;
+  const int h = blockIdx.y * 4 + static_cast<int>(threadIdx.x) / kWave;
+  const int t = threadIdx.x % kWave;
+  if (h >= a.H) return;  // whole waves
+  const int U = a.n_cu + a.n_wu;
+  const int hg = h / kAtHeads, hl = h % kAtHeads;
+  const int64_t n_units = static_cast<int64_t>(gridDim.x) * U * a.n_hg;
+  auto unit_of = [&](int u) { return (static_cast<int64_t>(b) * U + u) * a.n_hg + hg; };
+  const uint16_t* po = reinterpret_cast<const uint16_t*>(a.part + n_units * kAtHeads * 2);
+  const float ninf = -__builtin_huge_valf();
+  const int n_quads = a.D / 4;  // D is a multiple of 32
+  int qj[kQLane];  // this lane's quads (clamped; stores check the bound)
+#pragma unroll
+  for (int j = 0; j < kQLane; ++j) qj[j] = min(t + kWave * (blockIdx.z + gridDim.z * j), n_quads - 1);
+  typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+  auto load_units = [&](u32x2 (&o)[kMergeChunkQ][kQLane], int u0) {
+#pragma unroll
+    for (int q = 0; q < kMergeChunkQ; ++q) {
+      const u32x2* ou = reinterpret_cast<const u32x2*>(po + (unit_of(min(u0 + q, U - 1)) * kAtHeads + hl) * a.D);
+#pragma unroll
+      for (int j = 0; j < kQLane; ++j) o[q][j] = ou[qj[j]];
+    }
+  };
+  // every load of the round trip before any use
+  const int64_t mi = unit_of(min(t, U - 1)) * kAtHeads * 2 + 2 * hl;
+  const float m_raw = a.part[mi];
+  const float l_raw = a.part[mi + 1];
+  u32x2 o[kMergeChunkQ][kQLane];
+  load_units(o, 0);
+  float kw[kQLane][4];  // knorm_w and out may be only 4-byte aligned
+#pragma unroll
+  for (int j = 0; j < kQLane; ++j) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) kw[j][e] = a.knorm_w ? a.knorm_w[4 * qj[j] + e] : 0.f;
+  }
+  const float m_t = t < U ? m_raw : ninf;
+  const float l_t = t < U ? l_raw : 0.f;
+  const bool comp_t = t < a.n_cu;
+  const float sink2 = a.sink ? a.sink[h] * kLog2e : ninf;
+  // per branch: max over the units (and the sink), the denominator
+  float mc = comp_t ? m_t : ninf, mw = comp_t ? ninf : m_t;
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    mc = fmaxf(mc, __shfl_xor(mc, off));
+    mw = fmaxf(mw, __shfl_xor(mw, off));
+  }
+  const bool live_c = mc != ninf, live_w = mw != ninf;  // the branch saw a live key
+  if (a.sink_comp) mc = fmaxf(mc, sink2);
+  mw = fmaxf(mw, sink2);
+  const float mb = comp_t ? mc : mw;
+  const float w_t = m_t != ninf ? __builtin_amdgcn_exp2f(m_t - mb) : 0.f;
+  float dc = comp_t ? w_t * l_t : 0.f, dw = comp_t ? 0.f : w_t * l_t;
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    dc += __shfl_xor(dc, off);
+    dw += __shfl_xor(dw, off);
+  }
+  if (a.sink_comp && sink2 != ninf) dc += __builtin_amdgcn_exp2f(sink2 - mc);
+  if (sink2 != ninf) dw += __builtin_amdgcn_exp2f(sink2 - mw);
+  // unit t's weight in the output: its branch's 1/denominator folded in (0
+  // for a branch without a live key)
+  const float f_t = comp_t ? (live_c ? w_t / dc : 0.f) : (live_w ? w_t / dw : 0.f);
+  float rc[kQLane][4], rw[kQLane][4];
+#pragma unroll
+  for (int j = 0; j < kQLane; ++j) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) rc[j][e] = rw[j][e] = 0.f;
+  }
+  for (int u0 = 0; u0 < U; u0 += kMergeChunkQ) {
+    if (u0 > 0) load_units(o, u0);
+#pragma unroll
+    for (int q = 0; q < kMergeChunkQ; ++q) {
+      const float f = __shfl(f_t, min(u0 + q, kWave - 1));
+      if (u0 + q < U && f > 0.f) {  // units without a live key wrote no output
+        const bool comp = u0 + q < a.n_cu;
+#pragma unroll
+        for (int j = 0; j < kQLane; ++j) {
+#pragma unroll
+          for (int e = 0; e < 2; ++e) {
+            const uint32_t w2 = o[q][j][e];
+            const float lo = __uint_as_float(w2 << 16), hi = __uint_as_float(w2 & 0xffff0000u);
+            if (comp) {
+              rc[j][2 * e] = fmaf(f, lo, rc[j][2 * e]);
+              rc[j][2 * e + 1] = fmaf(f, hi, rc[j][2 * e + 1]);
+            } else {
+              rw[j][2 * e] = fmaf(f, lo, rw[j][2 * e]);
+              rw[j][2 * e + 1] = fmaf(f, hi, rw[j][2 * e + 1]);
+            }
+          }
+        }
+      }
+    }
+  }
+  float* out = a.out + (static_cast<int64_t>(b) * a.H + h) * a.D;
+  const bool al16 = (reinterpret_cast<uintptr_t>(out) & 15) == 0;  // uniform
+#pragma unroll
+  for (int j = 0; j < kQLane; ++j) {
+    const int c = t + kWave * (blockIdx.z + gridDim.z * j);
+    if (c >= n_quads) continue;
+    f32x4 v;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[e] = (live_c ? rc[j][e] * kw[j][e] : 0.f) + rw[j][e];
+    if (al16) {
+      reinterpret_cast<f32x4*>(out)[c] = v;
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) out[4 * c + e] = v[e];
+    }
+  }
+}
+
 struct AttnPlan {
   int n_cu, n_wu, n_hg, nks;
   int64_t ws_bytes;
@@ -746,8 +865,15 @@ extern "C" int skv_decode_attention(const skv_attention_desc* d, void* workspace
   mg.n_cu = p.n_cu;
   mg.n_wu = p.n_wu;
   mg.sink_comp = d->kind == SKV_LAYER_HCA;
-  hipLaunchKernelGGL(k_attn_merge,
-                     dim3(static_cast<unsigned>(d->batch), static_cast<unsigned>(ceil_div(d->n_heads, 4)), 2),
-                     dim3(256), 0, s, mg);
+  if (p.n_cu + p.n_wu <= kMergeChunkQ) {
+    hipLaunchKernelGGL(k_attn_merge_q,
+                       dim3(static_cast<unsigned>(d->batch), static_cast<unsigned>(ceil_div(d->n_heads, 4)),
+                            static_cast<unsigned>(ceil_div(d->head_dim / 4, kWave))),
+                       dim3(256), 0, s, mg);
+  } else {
+    hipLaunchKernelGGL(k_attn_merge,
+                       dim3(static_cast<unsigned>(d->batch), static_cast<unsigned>(ceil_div(d->n_heads, 4)), 2),
+                       dim3(256), 0, s, mg);
+  }
   return check_launch(what);
 }
