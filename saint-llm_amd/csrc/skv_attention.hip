@@ -27,7 +27,8 @@
 // 16w..16w+15: online softmax per head (log2 domain), O in 36 accumulators.
 // The next tile's rows are loaded while the current one is multiplied
 // (barriers order LDS only).  The unit writes (max, sum, O) per head.
-// Launch 2 (k_attn_merge): per (sequence, head) merges the units of each
+// Launch 2 (k_attn_merge, or k_attn_merge_q for sequences of at most 8
+// units): per (sequence, head) merges the units of each
 // branch with the sink, applies 1/sum and w, and writes the sum of branches.
 #include <algorithm>
 #include <type_traits>
