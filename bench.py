@@ -340,10 +340,11 @@ def run_decode_leg(dev, name: str, specs, batch: int, lens0: np.ndarray, steps: 
         # device time of the release and compaction launches (no host copies or syncs inside)
         c0, c1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         c0.record()
-        cache.release(mask, m_dev)
+        cache.release(mask, m_dev, check=False)
         info_dev = cache.compact(ws, sync=False)
         c1.record()
         torch.cuda.synchronize()
+        cache.check_release()
         info = [tuple(int(v) for v in row) for row in info_dev.cpu()]
         page_bytes = 0
         for i, s in enumerate(specs):

@@ -139,6 +139,9 @@ class DecodeCache:
 
         self.step_lens = torch.zeros(batch, dtype=torch.int32, device=dev)
         self.step_top = torch.zeros(MAX_GROUPS, dtype=torch.int32, device=dev)
+        # one status word per page group for the host-driven reserve / release
+        # calls (a later group's success must not hide an earlier refusal)
+        self.group_status = torch.zeros(MAX_GROUPS, dtype=torch.int32, device=dev)
         self.host_lens = np.zeros(batch, dtype=np.int64)
         self._attn_ws: dict[int, torch.Tensor] = {}
 
@@ -299,6 +302,40 @@ class DecodeCache:
             self.host_lens = self.tok_lens.cpu().numpy().astype(np.int64)
             raise RuntimeError(f"DecodeCache page reservation refused (status bits {st})")
 
+    # ------------------------------------------------------------ page plans --
+    def reserve_entries(self, rows: slice, n_new: list) -> None:
+        """Pop pages for ``n_new[gi]`` more entries (an int or an int32 tensor
+        over ``rows``) of every sequence in ``rows``, in every page group.
+
+        Each group's ``skv_reserve`` is all-or-nothing and reports into its own
+        status word.  If any group refuses, the groups that did reserve give
+        their pages of ``rows`` back (``skv_release``), so every sequence in
+        ``rows`` is left empty and the free lists hold what they held before,
+        and RuntimeError is raised.  ``rows`` must hold sequences without
+        entries."""
+        if not self.groups:
+            return
+        gst = self.group_status
+        gst.zero_()
+        for gi, g in enumerate(self.groups):
+            ops.reserve(g.free_stack, g.free_top, g.block_table[rows], g.n_entries[rows], n_new[gi],
+                        self.block_size, gst[gi:gi + 1])
+        bad = gst[: len(self.groups)].cpu().tolist()
+        if not any(bad):
+            return
+        n_rows = g.n_entries[rows].numel()
+        ones = torch.ones(n_rows, dtype=torch.uint8, device=self.device)
+        for gi, g in enumerate(self.groups):
+            if bad[gi] == 0:
+                ops.release(g.free_stack, g.free_top, g.block_table[rows], g.n_entries[rows], ones,
+                            self.block_size, gst[gi:gi + 1])
+        undo = gst[: len(self.groups)].cpu().tolist()
+        failed = [f"group m={g.m}: status bits {b}" for g, b in zip(self.groups, bad) if b]
+        if any(u for u, b in zip(undo, bad) if b == 0):
+            raise RuntimeError("DecodeCache page reservation refused (" + "; ".join(failed) +
+                               ") and the undo of the other groups failed")
+        raise RuntimeError("DecodeCache page reservation refused (" + "; ".join(failed) + ")")
+
     # --------------------------------------------------------------- prefill --
     def prefill(self, lens: np.ndarray, generator: torch.Generator | None = None,
                 data: dict | None = None, outlier_frac: float = 0.0,
@@ -320,10 +357,8 @@ class DecodeCache:
             raise RuntimeError("prefill needs empty sequences")
         dev = self.device
         lens_t = torch.as_tensor(lens.astype(np.int32), device=dev)
-        for g in self.groups:
-            n_ent = torch.as_tensor((lens // g.m).astype(np.int32), device=dev)
-            ops.reserve(g.free_stack, g.free_top, g.block_table, g.n_entries, n_ent,
-                        self.block_size, self.status)
+        self.reserve_entries(slice(None), [torch.as_tensor((lens // g.m).astype(np.int32), device=dev)
+                                           for g in self.groups])
         for i, spec in enumerate(self.layers):
             if data is not None:
                 src = data[i]["kv"]
@@ -353,7 +388,6 @@ class DecodeCache:
                                         torch.as_tensor(tail.astype(np.int32), device=dev))
         self.tok_lens.copy_(lens_t)
         self.host_lens = lens.copy()
-        self.check_status()
 
     def _fill_entries(self, pool: torch.Tensor, g: _Group, n_ent: np.ndarray, ch: int,
                       generator: torch.Generator | None, outlier_frac: float,
@@ -425,22 +459,36 @@ class DecodeCache:
         return state.load_sequence(self, b, path)
 
     # -------------------------------------------------- eviction / compaction --
-    def release(self, mask: np.ndarray, mask_dev: torch.Tensor | None = None) -> None:
+    def release(self, mask: np.ndarray, mask_dev: torch.Tensor | None = None, check: bool = True) -> None:
         """Finish the sequences with mask[b]: their pages return to the free lists.
 
         ``mask_dev`` (optional): the same mask already on the device as uint8,
-        so that the call issues no host-to-device copy."""
+        so that the call issues no host-to-device copy.  Each group's release
+        reports into its own status word; ``check`` synchronises and raises
+        RuntimeError if any group refused (a free stack that would overflow or
+        an invalid page id: the pool's bookkeeping is already corrupt).  With
+        ``check=False`` nothing waits; ``check_release()`` reads the words
+        later."""
         mask = np.asarray(mask, dtype=bool)
         if mask.shape != (self.batch,):
             raise ValueError("mask must be [batch]")
         if (mask & (self.host_lens == 0)).any():
             raise RuntimeError("release of a sequence that holds no tokens (double free)")
         m_dev = torch.as_tensor(mask.astype(np.uint8), device=self.device) if mask_dev is None else mask_dev
-        for g in self.groups:
+        for gi, g in enumerate(self.groups):
             ops.release(g.free_stack, g.free_top, g.block_table, g.n_entries, m_dev,
-                        self.block_size, self.status)
+                        self.block_size, self.group_status[gi:gi + 1])
         self.tok_lens.masked_fill_(m_dev.view(torch.bool), 0)  # 0/1 bytes read as bool, no conversion
         self.host_lens[mask] = 0
+        if check:
+            self.check_release()
+
+    def check_release(self) -> None:
+        """Synchronise and raise if the last release() was refused by any page group."""
+        bad = self.group_status[: len(self.groups)].cpu().tolist()
+        if any(bad):
+            raise RuntimeError("DecodeCache release refused (" + "; ".join(
+                f"group m={g.m}: status bits {b}" for g, b in zip(self.groups, bad) if b) + ")")
 
     def compact(self, workspace: torch.Tensor | None = None, sync: bool = True):
         """Defragment every page group; returns [(n_live, n_moved)] per group.

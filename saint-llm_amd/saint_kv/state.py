@@ -171,13 +171,9 @@ def load_sequence(cache, b: int, path: str | Path) -> tuple[int, int]:
         t = blob[s["offset"]: s["offset"] + s["nbytes"]]
         return t.view(_DTYPES[s["dtype"]]).reshape(s["shape"])
 
-    # pages for the entries, from each page group's free list
-    for gi, g in enumerate(cache.groups):
-        n_ent = L // g.m
-        if n_ent:
-            ops.reserve(g.free_stack, g.free_top, g.block_table[b:b + 1], g.n_entries[b:b + 1], n_ent,
-                        cache.block_size, cache.status)
-    cache.check_status()
+    # pages for the entries, from each page group's free list; on a refusal
+    # the slot is left empty and every group's free list as it was
+    cache.reserve_entries(slice(b, b + 1), [L // g.m for g in cache.groups])
     lo, hi = header["swa_rows"]
     for i, spec in enumerate(cache.layers):
         if hi > lo:
