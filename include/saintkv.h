@@ -4,7 +4,9 @@
  * Plain C: raw device pointers, int64 sizes, a hipStream_t (passed as void*).
  * Every entry point returns 0 on success or a negative SKV_E* code; the text
  * of the last error on the calling thread is available from skv_last_error().
- * The library allocates nothing: every buffer is owned by the caller.
+ * The library allocates nothing: every buffer is owned by the caller (the
+ * one static device array is the unit table of
+ * skv_decode_append_gather_noalloc, 2 MiB per GPU).
  *
  * Page-indexed entry points take n_pages: a block-table entry outside
  * [0, n_pages) is treated as unmapped and never dereferenced.
@@ -148,6 +150,29 @@ int skv_copy_slices(void* dst, int64_t dst_capacity_rows, void* pool, int64_t ro
                     int64_t block_size, int64_t n_pages, const void* src, int64_t src_seq_stride,
                     int64_t src_row_stride, int64_t src_len, const int32_t* units,
                     int64_t max_units, void* stream);
+
+/* Allocation-free form of skv_decode_append_gather: the same two launches
+ * and results, with the page-unit table in a static device array of
+ * SKV_NOALLOC_MAX_UNITS units (2 MiB, one per GPU the library runs on, held
+ * until the process ends) instead of the caller's `units` workspace.  It
+ * calls no hipMalloc/hipFree and allocates nothing; max_units above
+ * SKV_NOALLOC_MAX_UNITS is refused with SKV_EINVAL.  The stream must belong
+ * to the calling thread's current device.  Every call on one GPU shares that
+ * GPU's table, which keeps the last call's contents: calls that overlap on
+ * one GPU (concurrent streams, or threads) race.
+ * No counterpart in the reference: for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc). */
+#define SKV_NOALLOC_MAX_UNITS 65536
+int skv_decode_append_gather_noalloc(int32_t* free_stack, int32_t* free_top, int64_t n_pages,
+                                     int32_t* block_table, int64_t bt_stride, int32_t* seq_lens,
+                                     const int32_t* n_new, int32_t n_new_uniform, int32_t* status,
+                                     void* dst, const int64_t* dst_row_offsets,
+                                     int64_t dst_seq_stride_rows, int64_t dst_capacity_rows,
+                                     void* pool, int64_t row_bytes, int64_t block_size,
+                                     const void* src, int64_t src_seq_stride,
+                                     int64_t src_row_stride, int64_t src_len, int64_t max_units,
+                                     int64_t batch, void* stream);
 
 /* ---- SWA ring -------------------------------------------------------------
  * ring: [batch, window, row_bytes]; token at position p of sequence b lives

@@ -6,6 +6,8 @@
 //   view    self.k[:, :L]                             (:83)
 // Here the rows live in fixed-size pages reached through an int32 block table,
 // and each sequence has its own length.
+#include <mutex>
+
 #include "skv_common.h"
 
 namespace skv {
@@ -444,6 +446,51 @@ __global__ __launch_bounds__(kSliceThreads) void k_copy_slices(SliceArgs a) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// Allocation-free decode step: the page-unit table of k_plan_units /
+// k_copy_slices lives in a file-scope device array (one copy per GPU, held
+// until the process ends) instead of a caller workspace.  Its host-side name
+// is not a device address: host code uses only the per-device pointer that
+// hipGetSymbolAddress returns.
+// ---------------------------------------------------------------------------
+static __device__ __align__(256) int32_t scratch[kUnitHeader + kUnitWords * SKV_NOALLOC_MAX_UNITS];
+
+constexpr int kMaxDevices = 64;
+static std::mutex g_scratch_mu;
+static int32_t* g_scratch[kMaxDevices];
+
+// The unit table of the calling thread's current device (the stream's
+// device), resolved once per device.
+static int scratch_units(hipStream_t stream, int32_t** out, const char* what) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return set_error(SKV_EHIP, "%s: hipGetDevice failed: %s", what, hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxDevices) return set_error(SKV_EINVAL, "%s: device %d out of range", what, dev);
+  if (stream) {
+    hipDevice_t sdev = -1;
+    e = hipStreamGetDevice(stream, &sdev);
+    if (e != hipSuccess) {
+      return set_error(SKV_EHIP, "%s: hipStreamGetDevice failed: %s", what, hipGetErrorString(e));
+    }
+    if (sdev != dev) {
+      return set_error(SKV_EINVAL, "%s: the stream belongs to device %d, the current device is %d", what,
+                       static_cast<int>(sdev), dev);
+    }
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) {
+      return set_error(SKV_EHIP, "%s: hipGetSymbolAddress(scratch) failed on device %d: %s", what, dev,
+                       hipGetErrorString(e));
+    }
+    g_scratch[dev] = static_cast<int32_t*>(p);
+  }
+  *out = g_scratch[dev];
+  return SKV_OK;
+}
+
 }  // namespace skv
 
 using namespace skv;
@@ -639,6 +686,33 @@ extern "C" int skv_decode_append_gather(int32_t* free_stack, int32_t* free_top, 
   if (rc) return rc;
   if ((rc = validate_src(what, src, src_seq_stride, src_row_stride))) return rc;
   if (batch == 0) return SKV_OK;
+  rc = skv_plan_units(free_stack, free_top, n_pages, block_table, bt_stride, seq_lens, n_new,
+                      n_new_uniform, status, dst_row_offsets, dst_seq_stride_rows, block_size, units,
+                      max_units, batch, stream);
+  if (rc) return rc;
+  return skv_copy_slices(dst, dst_capacity_rows, pool, row_bytes, block_size, n_pages, src,
+                         src_seq_stride, src_row_stride, src_len, units, max_units, stream);
+}
+
+extern "C" int skv_decode_append_gather_noalloc(
+    int32_t* free_stack, int32_t* free_top, int64_t n_pages, int32_t* block_table, int64_t bt_stride,
+    int32_t* seq_lens, const int32_t* n_new, int32_t n_new_uniform, int32_t* status, void* dst,
+    const int64_t* dst_row_offsets, int64_t dst_seq_stride_rows, int64_t dst_capacity_rows, void* pool,
+    int64_t row_bytes, int64_t block_size, const void* src, int64_t src_seq_stride,
+    int64_t src_row_stride, int64_t src_len, int64_t max_units, int64_t batch, void* stream) {
+  const char* what = "skv_decode_append_gather_noalloc";
+  if (max_units < 0 || max_units > SKV_NOALLOC_MAX_UNITS) {
+    return set_error(SKV_EINVAL, "%s: max_units must be in [0, %d] (the static unit table); got %lld", what,
+                     SKV_NOALLOC_MAX_UNITS, (long long)max_units);
+  }
+  int rc = validate_copy(what, row_bytes, block_size, batch, bt_stride, pool, dst);
+  if (rc) return rc;
+  if ((rc = validate_src(what, src, src_seq_stride, src_row_stride))) return rc;
+  if (batch == 0) return SKV_OK;
+  int32_t* units = nullptr;
+  if ((rc = scratch_units(static_cast<hipStream_t>(stream), &units, what))) return rc;
+  // k_plan_units writes the table's count word on every path (0 on a
+  // refusal), so nothing of the previous call's table is read.
   rc = skv_plan_units(free_stack, free_top, n_pages, block_table, bt_stride, seq_lens, n_new,
                       n_new_uniform, status, dst_row_offsets, dst_seq_stride_rows, block_size, units,
                       max_units, batch, stream);

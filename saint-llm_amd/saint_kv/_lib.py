@@ -52,6 +52,10 @@ SIGNATURES: dict[str, list] = {
         _P, _P, _I64, _P, _I64, _P, _P, _I32, _P, _P, _P, _I64, _I64, _P, _I64, _I64, _P, _I64,
         _I64, _I64, _P, _I64, _I64, _P,
     ],
+    "skv_decode_append_gather_noalloc": [
+        _P, _P, _I64, _P, _I64, _P, _P, _I32, _P, _P, _P, _I64, _I64, _P, _I64, _I64, _P, _I64,
+        _I64, _I64, _I64, _I64, _P,
+    ],
     "skv_plan_units": [_P, _P, _I64, _P, _I64, _P, _P, _I32, _P, _P, _I64, _I64, _P, _I64, _I64, _P],
     "skv_copy_slices": [_P, _I64, _P, _I64, _I64, _I64, _P, _I64, _I64, _I64, _P, _I64, _P],
     "skv_ring_append": [_P, _I64, _I64, _P, _P, _I32, _P, _I64, _I64, _I64, _I64, _P],

@@ -262,6 +262,39 @@ def decode_append_gather(free_stack: torch.Tensor, free_top: torch.Tensor, block
     return out
 
 
+NOALLOC_MAX_UNITS = 65536  # SKV_NOALLOC_MAX_UNITS
+
+
+def decode_append_gather_noalloc(free_stack: torch.Tensor, free_top: torch.Tensor,
+                                 block_table: torch.Tensor, seq_lens: torch.Tensor, pool: torch.Tensor,
+                                 src: torch.Tensor, n_new: int | torch.Tensor, out: torch.Tensor,
+                                 max_units: int, row_offsets: torch.Tensor | None = None,
+                                 status: torch.Tensor | None = None) -> torch.Tensor:
+    """decode_append_gather with the library's static page-unit table
+    (skv_decode_append_gather_noalloc): no workspace, no device allocation;
+    ``max_units`` <= NOALLOC_MAX_UNITS.  Calls that overlap on one GPU race."""
+    n_pages, bs, rb = _check_pool(pool)
+    _require_i32(free_stack, "free_stack", (n_pages,))
+    _require_i32(free_top, "free_top", (1,))
+    _require_i32(block_table, "block_table")
+    batch, bt_stride = block_table.shape
+    _require_i32(seq_lens, "seq_lens", (batch,))
+    _require_gpu(src, "src")
+    if src.shape[0] != batch:
+        raise ValueError(f"src batch {src.shape[0]} != block_table batch {batch}")
+    s_seq, s_row = _row_view_strides(src, rb, "src")
+    n_ptr, n_uni = _n_new_args(n_new, batch)
+    off_ptr, seq_rows, cap = _dst_args(out, rb, batch, row_offsets)
+    if status is not None:
+        _require_i32(status, "status", (1,))
+    _lib.call("skv_decode_append_gather_noalloc", free_stack.data_ptr(), free_top.data_ptr(), n_pages,
+              block_table.data_ptr(), bt_stride, seq_lens.data_ptr(), n_ptr, n_uni,
+              _lib.ptr(status), out.data_ptr(), off_ptr, seq_rows, cap, pool.data_ptr(), rb, bs,
+              src.data_ptr(), s_seq, s_row, src.shape[1], max_units, batch,
+              _lib.stream_handle(pool.device))
+    return out
+
+
 # ---------------------------------------------------------------------------
 # SWA ring
 # ---------------------------------------------------------------------------
