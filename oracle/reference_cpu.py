@@ -11,7 +11,7 @@ product code path.  The HIP library never calls into it.
 Pinning (what fixes each function independently of this file):
   * contiguous caches      — restate kv_cache.py:32-327 line for line in
                              behaviour; pinned by the reference test behaviours
-                             (tests/test_oracle_contiguous.py).
+                             (tests/test_oracle_paged.py, test_oracle_compute.py).
   * paged append / gather  — closed form: the gather of a paged sequence equals
                              the concatenation of everything appended to it
                              (tests/test_oracle_paged.py, brute force).
@@ -353,15 +353,37 @@ def compress_pool(c: Tensor, z: Tensor, bias: Tensor) -> Tensor:
     return (w * c.float()).sum(dim=-2)  # csa.py:87
 
 
+# Pooling parity: 1e-2 relative to the entry, plus a cancellation term.  A
+# GPU entry is the same fp32 softmax-weighted sum in another order (online
+# softmax, hardware exp), rounded once to bf16 (2^-9 relative, inside the
+# 1e-2).  Each weight and product carries a few fp32 ulps of relative error,
+# so the absolute error of the sum scales with sum_i w_i |c_i|, not with the
+# result, which is near zero when the terms cancel; 1e-4 of that sum covers
+# m=128 terms of ~1e-7 relative error each with a margin of about 8.
+POOL_REL = 1.0e-2
+POOL_CANCEL = 1.0e-4
+
+
+def pooling_bound(c: Tensor, z: Tensor, bias: Tensor) -> Tensor:
+    """Per-channel tolerance of a pooled entry against compress_pool:
+    POOL_REL * |out| + POOL_CANCEL * sum_i w_i |c_i| (fp32, shape of the output)."""
+    w = torch.softmax(z.float() + bias.float(), dim=-2)
+    out = (w * c.float()).sum(dim=-2)
+    return POOL_REL * out.abs() + POOL_CANCEL * (w * c.float().abs()).sum(dim=-2)
+
+
 def compress_append(pool: Tensor, block_table: np.ndarray, tail_c: Tensor, tail_z: Tensor,
                     c_new: Tensor, z_new: Tensor, bias: Tensor, seq_lens: np.ndarray,
-                    n_new: np.ndarray | int, fp8: bool = False) -> list[tuple[int, int, Tensor]]:
+                    n_new: np.ndarray | int, fp8: bool = False,
+                    bound_pool: Tensor | None = None) -> list[tuple[int, int, Tensor]]:
     """Emission state machine of kv_cache.py:170-195 / 291-315 on paged entries.
 
     seq_lens are token counts after the append.  Every block of m tokens
     completed by the n_new tokens is pooled (compress_pool, rounded to bf16)
     into entry floor(p/m); the incomplete block's new tokens go to the tails
-    (slot p % m).  Returns [(b, entry, bf16 value)] of the emitted entries.
+    (slot p % m).  With bound_pool (fp32, the pool's pages and slots), the
+    entry's pooling_bound goes to the same slot.  Returns [(b, entry, bf16
+    value)] of the emitted entries.
     """
     m = tail_c.shape[1]
     bs = pool.shape[1]
@@ -382,6 +404,8 @@ def compress_append(pool: Tensor, block_table: np.ndarray, tail_c: Tensor, tail_
             val = compress_pool(cs, zs, bias).to(torch.bfloat16)
             page, slot = int(block_table[b, e // bs]), e % bs
             pool[page, slot] = fp8_pack_entries(val.unsqueeze(0))[0] if fp8 else val
+            if bound_pool is not None:
+                bound_pool[page, slot] = pooling_bound(cs, zs, bias)
             emitted.append((b, e, val))
         for p in range(max(first_new, (L // m) * m), L):
             tail_c[b, p % m] = c_new[b, p - first_new]

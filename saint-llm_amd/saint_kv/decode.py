@@ -339,7 +339,7 @@ class DecodeCache:
     # --------------------------------------------------------------- prefill --
     def prefill(self, lens: np.ndarray, generator: torch.Generator | None = None,
                 data: dict | None = None, outlier_frac: float = 0.0,
-                outlier_scale: float = 20.0) -> None:
+                outlier_scale: float = 20.0, tails: list | None = None) -> None:
         """Bring every sequence from empty to ``lens[b]`` tokens.
 
         With ``data`` (per layer dicts of bf16 [B, T, ...] tensors "kv", "c", "z",
@@ -348,7 +348,9 @@ class DecodeCache:
         filled with N(0,1) values (synthetic contexts for benchmarking; fp8
         pools quantize N(0,1) rows in which a fraction ``outlier_frac`` of the
         values is multiplied by ``outlier_scale``) and the incomplete blocks'
-        states are folded from N(0,1) tokens.
+        states are folded from N(0,1) tokens, or, with ``tails`` (per layer a
+        dict of bf16 [B, T >= max(lens % m), ch] tensors "c", "z", "ci", "zi";
+        None for SWA layers), from the first ``lens[b] % m`` rows of those.
         """
         lens = np.asarray(lens, dtype=np.int64)
         if lens.shape != (self.batch,) or (lens < 0).any() or (lens > self.max_len).any():
@@ -382,8 +384,11 @@ class DecodeCache:
                 tail = lens % spec.m
                 if tail.max() > 0:
                     t = int(tail.max())
-                    c = torch.randn(self.batch, t, ch, generator=generator, device=dev).to(torch.bfloat16)
-                    z = torch.randn(self.batch, t, ch, generator=generator, device=dev).to(torch.bfloat16)
+                    if tails is not None:
+                        c, z = tails[i][kc][:, :t], tails[i][kz][:, :t]
+                    else:
+                        c = torch.randn(self.batch, t, ch, generator=generator, device=dev).to(torch.bfloat16)
+                        z = torch.randn(self.batch, t, ch, generator=generator, device=dev).to(torch.bfloat16)
                     ops.compress_append(pool, g.block_table, state, c, z, bias, lens_t,
                                         torch.as_tensor(tail.astype(np.int32), device=dev))
         self.tok_lens.copy_(lens_t)

@@ -186,8 +186,10 @@ def test_empty_batch_and_zero_lengths(dev) -> None:
 
 def test_full_size_decode_gather_config(dev) -> None:
     """B=64, D=576 bf16, L~U[1k,32k], bs=64, pool of 200k pages (random permutation):
-    after a one-token decode step the gather of every sequence equals what was
-    appended (size-independent check at full size)."""
+    after a one-token decode step (skv_append_gather), then a second through the
+    headline path (skv_decode_append_gather: planner + 4 KB slices), the gather
+    of every sequence equals what was appended and the tables equal the
+    oracle's (size-independent check at full size)."""
     torch.manual_seed(0)
     rng = np.random.default_rng(0)
     from saint_kv import ops
@@ -217,6 +219,25 @@ def test_full_size_decode_gather_config(dev) -> None:
         o = int(offs[b]) + b
         assert torch.equal(out[o: o + lens0[b]], src[offs[b]: offs[b] + lens0[b]])
         assert torch.equal(out[o + lens0[b]], tok[b, 0])
+    del out
+    # a second step through the headline path: k_plan_units (reserve + unit
+    # table) and k_copy_slices (4 KB slices), at the same full size
+    tok2 = torch.randn(batch, 1, d, device=dev, dtype=torch.bfloat16)
+    units_n = int((-(-(lens0.astype(np.int64) + 2) // bs)).sum())
+    units = ops.unit_table(units_n, dev)
+    out_offs2 = torch.as_tensor(offs + 2 * np.arange(batch), device=dev)
+    out2 = torch.empty(total + 2 * batch, d, dtype=torch.bfloat16, device=dev)
+    ops.decode_append_gather(s.stack, s.top, s.bt, s.lens, s.pool, tok2, 1, out2, units, units_n,
+                             out_offs2, s.status)
+    st, s.r_top = ref.reserve(s.r_stack, s.r_top, s.r_bt, s.r_lens, 1, bs)
+    assert st == 0
+    s.check_tables()
+    assert int(s.status.item()) == 0
+    for b in range(batch):
+        o = int(offs[b]) + 2 * b
+        assert torch.equal(out2[o: o + lens0[b]], src[offs[b]: offs[b] + lens0[b]])
+        assert torch.equal(out2[o + lens0[b]], tok[b, 0])
+        assert torch.equal(out2[o + lens0[b] + 1], tok2[b, 0])
 
 
 def test_decode_append_gather_matches_two_call_path(dev) -> None:

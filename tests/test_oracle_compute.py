@@ -309,3 +309,25 @@ def test_library_codec_encode_matches_torch_exhaustively() -> None:
     exp = x.to(torch.float8_e4m3fn).view(torch.uint8)
     bad = (got != exp).nonzero()
     assert bad.numel() == 0, [(float(x[i]), int(got[i]), int(exp[i])) for i in bad[:5, 0]]
+
+
+def test_pooling_bound_covers_reordering_and_catches_a_dropped_term() -> None:
+    """ref.pooling_bound holds the fp32 pooling of another summation order and
+    exp (fp64 reference, reversed fp32 order) and is violated by a planted
+    mistake: one token's term dropped, or the bias ignored."""
+    g = torch.Generator().manual_seed(4)
+    for m in (4, 128):
+        c = torch.randn(64, m, 576, generator=g).to(torch.bfloat16)
+        z = torch.randn(64, m, 576, generator=g).to(torch.bfloat16)
+        bias = torch.randn(m, 576, generator=g)
+        want = ref.compress_pool(c, z, bias)
+        bound = ref.pooling_bound(c, z, bias)
+        w64 = torch.softmax(z.double() + bias.double(), dim=-2)
+        exact = (w64 * c.double()).sum(dim=-2)
+        rev = (torch.softmax(z.float().flip(-2) + bias.flip(-2), dim=-2) * c.float().flip(-2)).sum(dim=-2)
+        for got in (exact.float(), rev, rev.to(torch.bfloat16).float()):
+            assert ((got - want).abs() <= bound).all()
+        dropped = (w64[:, 1:] * c.double()[:, 1:]).sum(dim=-2).float()
+        no_bias = ref.compress_pool(c, z, torch.zeros_like(bias))
+        for bad in (dropped, no_bias):
+            assert ((bad - want).abs() > bound).float().mean() > 0.5
