@@ -38,16 +38,23 @@ import torch  # noqa: E402
 
 HBM_PEAK_GBS = 8000.0  # MI355X HBM3E peak, 8 TB/s
 TRAFFIC_FILE = ROOT / "profiles" / "hbm_traffic_k_copy_slices_b64_L1k-32k.json"
+DECODE_TRAFFIC_FILE = ROOT / "profiles" / "hbm_traffic_decode_legs.json"
 
 
-def measured_traffic(alg_bytes: float) -> int | None:
-    """HBM bytes per launch of k_copy_slices from the committed FETCH_SIZE/WRITE_SIZE
-    passes (counted traffic / algorithmic bytes, applied to this run's launch)."""
+def committed_traffic(path: Path, key: str | None, alg_bytes: float) -> tuple[int | None, str | None]:
+    """(HBM bytes, source label) for this run's algorithmic bytes: the ratio of
+    counted FETCH_SIZE + WRITE_SIZE bytes to algorithmic bytes that the
+    committed profile holds (rocprofv3 counter passes, calibrated on a plain
+    copy), times this run's bytes.  Not a counter reading of this run."""
     try:
-        ratio = json.loads(TRAFFIC_FILE.read_text())["traffic_over_alg"]
-    except (OSError, KeyError, ValueError):
-        return None
-    return int(round(ratio * alg_bytes))
+        d = json.loads(path.read_text())
+        rec = d if key is None else d["legs"][key]
+        ratio = rec["traffic_over_alg"]
+    except (OSError, KeyError, ValueError, TypeError):
+        return None, None
+    return int(round(ratio * alg_bytes)), (
+        f"committed counter ratio x this run's bytes: {path.relative_to(ROOT)}"
+        + ("" if key is None else f" [{key}]") + f", ratio {ratio}")
 ROW = 576  # 512 latent + 64 rope, bf16
 ROW_BYTES = ROW * 2
 
@@ -251,23 +258,30 @@ def decode_kv_tokens(specs, lens_after: np.ndarray, window: int) -> int:
 def run_decode_leg(dev, name: str, specs, batch: int, lens0: np.ndarray, steps: int,
                    per_graph: int = 20, window: int = 128, seed: int = 0,
                    outlier_frac: float = 0.0, evict_frac: float | None = None,
-                   separate_scores: int = 0) -> dict:
+                   separate_scores: int = 0, input_sets: int = 20) -> dict:
+    """Decode steps of a DecodeCache replayed from HIP graphs of ``per_graph``
+    steps.  The steps cycle through ``input_sets`` sets of new-token rows and
+    N(0,1) scores (one per step of a graph by default), so every step gathers
+    other picks than the step before: a pick is reused only ``input_sets``
+    steps later, after hundreds of MB of other traffic."""
     from saint_kv.decode import DecodeCache
 
     max_len = int(lens0.max()) + steps + 2 * per_graph + 8
     t0 = time.perf_counter()
+    n_sets = 1 if separate_scores else input_sets
     cache = DecodeCache(specs, batch, max_len, window=window, device=dev, page_order_seed=seed,
-                        hca_out_rows=max(1, max_len // 128))
+                        hca_out_rows=max(1, max_len // 128), input_sets=n_sets)
     gen = torch.Generator(device=dev).manual_seed(seed)
     for i, s in enumerate(specs):
         if cache.bias[i] is not None:
             cache.bias[i].normal_(generator=gen)
         if cache.idx_bias[i] is not None:
             cache.idx_bias[i].normal_(generator=gen)
-        for v in cache.inputs[i].values():
-            v.normal_(generator=gen)
-        if cache.scores[i] is not None:
-            cache.scores[i].normal_(generator=gen)
+        for k in range(n_sets):
+            for v in cache.inputs_by_set[k][i].values():
+                v.normal_(generator=gen)
+            if cache.scores_by_set[k][i] is not None:
+                cache.scores_by_set[k][i].normal_(generator=gen)
     cache.prefill(lens0, generator=gen, outlier_frac=outlier_frac)
     torch.cuda.synchronize()
     log(f"{name}: prefilled {batch} x mean {int(lens0.mean())} tokens in {time.perf_counter() - t0:.1f} s")
@@ -294,11 +308,12 @@ def run_decode_leg(dev, name: str, specs, batch: int, lens0: np.ndarray, steps: 
     cache.check_status()
     reps = max(1, steps // per_graph)
     lens_start = cache.host_lens.copy()
+    stream = torch.cuda.current_stream(dev)  # the graphs replay on it
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record()
+    e0.record(stream)
     for _ in range(reps):
         graph.replay()
-    e1.record()
+    e1.record(stream)
     torch.cuda.synchronize()
     cache.check_status()
     n_steps = reps * per_graph
@@ -315,10 +330,19 @@ def run_decode_leg(dev, name: str, specs, batch: int, lens0: np.ndarray, steps: 
         "mean_ctx": int(lens0.mean()), "steps": n_steps, "us_per_step": round(ms * 1e3, 2),
         "alg_bytes_per_step": int(alg), "gbs": round(gbs, 1), "pct_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 2),
         "kv_tokens_per_step": int(toks), "kv_tokens_per_s": round(toks / (ms * 1e-3), 1),
-        "launches_per_step": 3 + (sum(s.kind == "csa" for s in specs) if separate_scores else 0),
+        "launches_per_step": cache.step_launches() + (sum(s.kind == "csa" for s in specs) if separate_scores else 0),
         "hip_graph_steps": per_graph,
+        "input_sets": n_sets,
         "scores": ("computed in the step" if any(s.idx_heads for s in specs) and not separate_scores
                    else "skv_indexer_scores launch before each step" if separate_scores else "input"),
+    }
+    traffic, source = committed_traffic(DECODE_TRAFFIC_FILE, name, alg)
+    rec["roofline"] = {
+        "bound": "hbm",
+        "kernel": f"skv_decode_step ({cache.step_launches()} launch(es) per step; the step as the unit)",
+        "achieved": rec["gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+        "frac": round(rec["gbs"] / HBM_PEAK_GBS, 4), "traffic": traffic, "traffic_source": source,
+        "alg_bytes_per_launch": int(alg), "avg_launch_us": rec["us_per_step"],
     }
     log(f"{name}: {rec['us_per_step']} us/step, {rec['gbs']} GB/s ({rec['pct_hbm_peak']}%), "
         f"{rec['kv_tokens_per_s'] / 1e6:.1f} M KV tok/s")
@@ -337,12 +361,17 @@ def run_decode_leg(dev, name: str, specs, batch: int, lens0: np.ndarray, steps: 
         ws = torch.zeros(3 * max(g.n_pages for g in cache.groups), dtype=torch.int32, device=dev)
         m_dev = torch.as_tensor(mask.astype(np.uint8), device=dev)
         torch.cuda.synchronize()
-        # device time of the release and compaction launches (no host copies or syncs inside)
+        # the release and compaction launches recorded in one HIP graph and
+        # replayed once: the interval holds their kernels, not their host calls
+        g_ev = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g_ev):
+            cache.release(mask, m_dev, check=False)
+            info_dev = cache.compact(ws, sync=False)
+        torch.cuda.synchronize()
         c0, c1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        c0.record()
-        cache.release(mask, m_dev, check=False)
-        info_dev = cache.compact(ws, sync=False)
-        c1.record()
+        c0.record(stream)
+        g_ev.replay()
+        c1.record(stream)
         torch.cuda.synchronize()
         cache.check_release()
         info = [tuple(int(v) for v in row) for row in info_dev.cpu()]
@@ -402,6 +431,75 @@ def cpu_baseline_decode(seconds: float = 5.0, seed: int = 0) -> dict:
             "cores": torch.get_num_threads(), "kind": "port",
             "sample": f"{steps} CSA read steps (top-512 of 16384 scores + gather + 128-row window) "
                       f"for 2 sequences at 64k context, torch/numpy CPU oracle, {dt:.1f} s"}
+
+
+def run_layer_seq_leg(dev, n_layers: int = 8, batch: int = 16, L: int = 65536, steps: int = 100,
+                      per_graph: int = 10, heads: int = 64, window: int = 128, seed: int = 8) -> dict:
+    """What a model's decode step sees at 64k context: n_layers CSA layers
+    (m=4, top-k 512, W=128), one after another, each layer's cache step
+    followed by its decode attention over the step's picks and window (the
+    next layer's inputs come from that attention, so the layers cannot be
+    stepped together).  Each layer has its own cache and input sets; the
+    sequence of layers is replayed from HIP graphs of ``per_graph`` model
+    steps."""
+    from saint_kv.decode import DecodeCache, LayerSpec
+
+    max_len = L + steps + 2 * per_graph + 8
+    gen = torch.Generator(device=dev).manual_seed(seed)
+    caches, qs, knorm, outs = [], [], [], []
+    for li in range(n_layers):
+        c = DecodeCache([LayerSpec("csa", m=4, top_k=512)], batch, max_len, window=window, device=dev,
+                        page_order_seed=seed + li, input_sets=per_graph)
+        c.bias[0].normal_(generator=gen)
+        c.idx_bias[0].normal_(generator=gen)
+        for k in range(per_graph):
+            for v in c.inputs_by_set[k][0].values():
+                v.normal_(generator=gen)
+            c.scores_by_set[k][0].normal_(generator=gen)
+        c.prefill(np.full(batch, L), generator=gen)
+        caches.append(c)
+        qs.append(torch.empty(batch, heads, 576, dtype=torch.bfloat16, device=dev).normal_(generator=gen))
+        knorm.append(torch.empty(576, dtype=torch.float32, device=dev).uniform_(0.5, 1.5, generator=gen))
+        outs.append(torch.empty(batch, heads, 576, dtype=torch.float32, device=dev))
+    for li, c in enumerate(caches):  # warm-up: kernel loads and each layer's attention workspace
+        c.step()
+        c.attention(0, qs[li], knorm[li], out=outs[li])
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for s in range(per_graph):
+            for li, c in enumerate(caches):
+                c._launch_step(s % c.n_input_sets)
+                c.attention(0, qs[li], knorm[li], out=outs[li])
+    graph.replay()  # warm-up replay
+    for c in caches:
+        c.host_lens += per_graph
+    torch.cuda.synchronize()
+    reps = max(1, steps // per_graph)
+    stream = torch.cuda.current_stream(dev)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(reps):
+        graph.replay()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    for c in caches:
+        c.host_lens += reps * per_graph
+        c.check_status()
+    us = e0.elapsed_time(e1) * 1e3 / (reps * per_graph)
+    rec = {
+        "workload": f"{n_layers} CSA layers (m=4, top-k 512, W=128) in sequence, B={batch}, L={L}: per layer "
+                    f"one decode step, then its decode attention ({heads} heads x 576) over the picks",
+        "model_steps": reps * per_graph, "us_per_model_step": round(us, 2),
+        "us_per_layer": round(us / n_layers, 2),
+        "launches_per_layer": caches[0].step_launches() + 2,
+        "kv_tokens_per_s": round(n_layers * batch * (512 + window) / (us * 1e-6), 1),
+    }
+    log(f"layer_seq_64k: {rec['us_per_model_step']} us per {n_layers}-layer model step, "
+        f"{rec['us_per_layer']} us per layer (step + attention)")
+    del caches
+    torch.cuda.empty_cache()
+    return rec
 
 
 def run_indexer_leg(dev, batch: int, n_ent: int, heads: int, channels: int, launches: int,
@@ -597,7 +695,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
-    ap.add_argument("--legs", default="csa_64k,csa_64k_b256,csa_64k_idx,mixed_8layer,fp8_1m",
+    ap.add_argument("--legs", default="csa_64k,csa_64k_b256,csa_64k_idx,mixed_8layer,fp8_1m,layer_seq_64k",
                     help="comma list of decode-step legs to run after the headline ('' for none)")
     ap.add_argument("--leg-steps", type=int, default=200)
     ap.add_argument("--no-indexer", action="store_true", help="skip the indexer-score leg")
@@ -666,6 +764,7 @@ def main() -> int:
     log(f"step {ms_per_step * 1e3:.1f} us, kernel {kern_avg_ms * 1e3:.1f} us, "
         f"{value:.0f} GB/s, kernel {achieved:.0f} GB/s")
 
+    head_traffic, head_traffic_source = committed_traffic(TRAFFIC_FILE, None, alg_per_launch)
     del w
     torch.cuda.empty_cache()
     legs = {}
@@ -700,6 +799,7 @@ def main() -> int:
             rng.integers(262144, 1048577, size=4), args.leg_steps, seed=5, outlier_frac=0.01,
             evict_frac=0.3)
 
+    layer_seq = run_layer_seq_leg(dev) if "layer_seq_64k" in wanted else None
     indexer = None if args.no_indexer else run_indexer_leg(dev, 16, 16384, 64, 128, 200)
     state_io = None if args.no_state else run_state_leg(dev)
     attention = {}
@@ -753,13 +853,15 @@ def main() -> int:
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": measured_traffic(alg_per_launch),
+            "traffic": head_traffic,
+            "traffic_source": head_traffic_source,
             "alg_bytes_per_launch": int(alg_per_launch),
             "avg_launch_us": round(kern_avg_ms * 1e3, 2),
         },
         "cpu_baseline": cpu,
         "decode_kv_tokens_per_s_64k": legs.get("csa_64k", {}).get("kv_tokens_per_s"),
         "decode_legs": legs,
+        "layer_seq_64k": layer_seq,
         "indexer_64k": indexer,
         "attention": attention or None,
         "state_64k": state_io,

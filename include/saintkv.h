@@ -341,6 +341,9 @@ int skv_compact(const skv_pool_ref* pools, int32_t n_pools, int32_t* block_table
  *            rows past the sequence's entries are left untouched); every
  *            layer copies the last min(window, L) tokens of its ring in
  *            position order; the step's lengths and tops are committed.
+ * skv_decode_step_launches returns the launches a step of the descriptor
+ * takes (2 without CSA layers, else 3; 0 for an empty step; negative on a
+ * bad descriptor).
  * Mirrors one cached step of CSA/HCA/SWAttention.forward over a
  * KVCacheBundle (model.py:294-315; csa.py:299-331; hca.py:110-141;
  * swa.py:107-125).  The kernels read the descriptor from device memory:
@@ -417,6 +420,7 @@ typedef struct skv_decode_desc {
 
 int skv_decode_step(const skv_decode_desc* host_desc, const skv_decode_desc* device_desc,
                     void* stream);
+int skv_decode_step_launches(const skv_decode_desc* host_desc);
 
 /* Decode attention of one layer over the paged cache (one query token per
  * sequence, MQA: one K/V head, n_heads query heads of head_dim), the gather
@@ -437,7 +441,8 @@ int skv_decode_step(const skv_decode_desc* host_desc, const skv_decode_desc* dev
  *     the softcap c*tanh(s/c) when softcap > 0.
  * The pool's entries are bf16 or fp8 (dequantized to bf16 as the gathers
  * do).  Two launches: per (sequence, split, 64 heads) partial softmax
- * statistics and outputs into `workspace`, then the merge into `out` (fp32).
+ * statistics and outputs into `workspace` (16-byte aligned), then the merge
+ * into `out` (fp32).
  * skv_attention_workspace returns the workspace bytes (or -1 on a bad
  * descriptor). */
 typedef struct skv_attention_desc {

@@ -815,6 +815,9 @@ extern "C" int skv_decode_attention(const skv_attention_desc* d, void* workspace
   if (!workspace || ws_bytes < p.ws_bytes) {
     return set_error(SKV_EINVAL, "%s: workspace of %lld bytes needed", what, (long long)p.ws_bytes);
   }
+  if (reinterpret_cast<uintptr_t>(workspace) & 15) {
+    return set_error(SKV_EINVAL, "%s: workspace must be 16-byte aligned (the merge reads it in vectors)", what);
+  }
   AttnArgs a;
   a.q = static_cast<const uint8_t*>(d->q);
   a.part = static_cast<float*>(workspace);

@@ -1179,6 +1179,15 @@ extern "C" int skv_decode_desc_sizes(int64_t* out) {
   return SKV_OK;
 }
 
+extern "C" int skv_decode_step_launches(const skv_decode_desc* h) {
+  if (!h) return set_error(SKV_EINVAL, "skv_decode_step_launches: NULL descriptor");
+  if (h->batch <= 0 || h->n_layers <= 0) return 0;
+  for (int l = 0; l < h->n_layers && l < SKV_MAX_LAYERS; ++l) {
+    if (h->layers[l].kind == SKV_LAYER_CSA) return 3;
+  }
+  return 2;
+}
+
 extern "C" int skv_decode_step(const skv_decode_desc* h, const skv_decode_desc* dd, void* stream) {
   const char* what = "skv_decode_step";
   if (!h || !dd) return set_error(SKV_EINVAL, "%s: NULL descriptor", what);

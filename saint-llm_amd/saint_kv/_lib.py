@@ -78,6 +78,7 @@ SIGNATURES: dict[str, list] = {
     ],
     "skv_release": [_P, _P, _I64, _P, _I64, _P, _P, _I64, _I64, _P, _P],
     "skv_decode_step": [_P, _P, _P],
+    "skv_decode_step_launches": [_P],
     "skv_decode_desc_sizes": [_P],
     "skv_attention_workspace": [_P],
     "skv_decode_attention": [_P, _P, _I64, _P],

@@ -159,6 +159,8 @@ def decode_attention(q: torch.Tensor, kind: str, lens: torch.Tensor, win_k: torc
         workspace = torch.empty(max(need, 4) // 4 + 1, dtype=torch.float32, device=q.device)
     elif workspace.device != q.device or workspace.numel() * workspace.element_size() < need:
         raise ValueError(f"workspace must hold {need} bytes on {q.device}")
+    elif not workspace.is_contiguous() or workspace.data_ptr() % 16:
+        raise ValueError("workspace must be a contiguous tensor whose data is 16-byte aligned")
     _lib.call("skv_decode_attention", ctypes.byref(d), workspace.data_ptr(),
               workspace.numel() * workspace.element_size(), _lib.stream_handle(q.device))
     _LAST_WS = workspace

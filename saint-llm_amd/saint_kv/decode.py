@@ -107,13 +107,21 @@ class DecodeCache:
     ``score_cols`` sets the width of each CSA layer's indexer-score buffer
     (default ``max_len // m`` rounded up to a multiple of 4); the step reads
     only the first ``L // m`` columns of a row.
+
+    ``input_sets`` > 1 allocates that many sets of per-step input buffers
+    (``inputs_by_set[k]``: the new tokens' rows; ``scores_by_set[k]``: the CSA
+    scores), each with its own descriptor: ``step(k)`` reads set k, and a
+    captured sequence of steps cycles through the sets, so that a caller can
+    stage the next steps' inputs while earlier ones run.  ``inputs`` and
+    ``scores`` are set 0.
     """
 
     def __init__(self, layers: list[LayerSpec], batch: int, max_len: int, *,
                  latent: int = 576, c_indexer: int = 128, window: int = 128,
                  block_size: int = 64, device: torch.device | str | None = None,
                  page_order_seed: int | None = 0, pages_per_group: dict[int, int] | None = None,
-                 hca_out_rows: int | None = None, score_cols: int | None = None) -> None:
+                 hca_out_rows: int | None = None, score_cols: int | None = None,
+                 input_sets: int = 1) -> None:
         if not 0 < len(layers) <= MAX_LAYERS:
             raise ValueError(f"1..{MAX_LAYERS} layers supported; got {len(layers)}")
         scored = [s.idx_heads > 0 for s in layers if s.kind == "csa"]
@@ -125,6 +133,8 @@ class DecodeCache:
             raise ValueError(f"batch must be in [1, {MAX_BATCH}]; got {batch}")
         if max_len <= 0:
             raise ValueError(f"max_len must be positive; got {max_len}")
+        if input_sets < 1:
+            raise ValueError(f"input_sets must be positive; got {input_sets}")
         dev = torch.device("cuda", torch.cuda.current_device()) if device is None else torch.device(device)
         if dev.type != "cuda":
             raise RuntimeError("DecodeCache runs only on a ROCm GPU (no CPU fallback)")
@@ -174,15 +184,16 @@ class DecodeCache:
         bf = torch.bfloat16
         self.ring, self.pool, self.state, self.bias = [], [], [], []
         self.idx_pool, self.idx_state, self.idx_bias = [], [], []
-        self.inputs: list[dict[str, torch.Tensor]] = []
-        self.scores, self.topk_idx, self.out_entries, self.out_window = [], [], [], []
+        self.inputs_by_set: list[list[dict[str, torch.Tensor]]] = [[] for _ in range(input_sets)]
+        self.scores_by_set: list[list[torch.Tensor | None]] = [[] for _ in range(input_sets)]
+        self.topk_idx, self.out_entries, self.out_window = [], [], []
         self.topk_ws = []
         for spec in layers:
             if spec.kind not in KIND:
                 raise ValueError(f"unknown layer kind {spec.kind!r}")
             self.ring.append(torch.zeros(batch, window, latent, dtype=bf, device=dev))
             self.out_window.append(torch.zeros(batch, window, latent, dtype=bf, device=dev))
-            inp = {"kv": torch.zeros(batch, latent, dtype=bf, device=dev)}
+            inp = {"kv": (batch, latent)}  # shapes; one tensor per input set below
             pool = state = bias = ipool = istate = ibias = sc = tk = oe = ws = None
             if spec.kind in ("csa", "hca"):
                 g = self.groups[self.group_of_rate[spec.m]]
@@ -193,25 +204,23 @@ class DecodeCache:
                     pool = torch.zeros(g.n_pages, block_size, latent, dtype=bf, device=dev)
                 state = torch.zeros(batch, 3, latent, dtype=torch.float32, device=dev)
                 bias = torch.zeros(spec.m, latent, dtype=torch.float32, device=dev)
-                inp["c"] = torch.zeros(batch, latent, dtype=bf, device=dev)
-                inp["z"] = torch.zeros(batch, latent, dtype=bf, device=dev)
+                inp["c"] = inp["z"] = (batch, latent)
                 if spec.kind == "csa":
                     if spec.indexer:
                         ipool = torch.zeros(g.n_pages, block_size, c_indexer, dtype=bf, device=dev)
                         istate = torch.zeros(batch, 3, c_indexer, dtype=torch.float32, device=dev)
                         ibias = torch.zeros(spec.m, c_indexer, dtype=torch.float32, device=dev)
-                        inp["ci"] = torch.zeros(batch, c_indexer, dtype=bf, device=dev)
-                        inp["zi"] = torch.zeros(batch, c_indexer, dtype=bf, device=dev)
+                        inp["ci"] = inp["zi"] = (batch, c_indexer)
                         if spec.idx_heads > 0:
-                            inp["iq"] = torch.zeros(batch, spec.idx_heads, c_indexer, dtype=bf, device=dev)
-                            inp["iw"] = torch.zeros(batch, spec.idx_heads, dtype=torch.float32, device=dev)
+                            inp["iq"] = (batch, spec.idx_heads, c_indexer)
+                            inp["iw"] = (batch, spec.idx_heads)
                     elif spec.idx_heads > 0:
                         raise ValueError("idx_heads needs the layer's indexer stream (indexer=True)")
                     # default width rounded up to 4 columns (16-byte rows)
                     cols = -(-max(1, max_len // spec.m) // 4) * 4 if score_cols is None else int(score_cols)
                     if cols < max_len // spec.m:
                         raise ValueError(f"score_cols must be >= max_len // m = {max_len // spec.m}")
-                    sc = torch.zeros(batch, cols, dtype=torch.float32, device=dev)
+                    sc = (batch, cols)
                     tk = torch.full((batch, spec.top_k), -1, dtype=torch.int32, device=dev)
                     ws = ops.topk_workspace(batch, dev)
                     oe = torch.zeros(batch, spec.top_k, latent, dtype=bf, device=dev)
@@ -224,15 +233,34 @@ class DecodeCache:
             self.idx_pool.append(ipool)
             self.idx_state.append(istate)
             self.idx_bias.append(ibias)
-            self.inputs.append(inp)
-            self.scores.append(sc)
+            for k in range(input_sets):
+                self.inputs_by_set[k].append({
+                    n: torch.zeros(shp, dtype=torch.float32 if n == "iw" else bf, device=dev)
+                    for n, shp in inp.items()})
+                self.scores_by_set[k].append(
+                    None if sc is None else torch.zeros(sc, dtype=torch.float32, device=dev))
             self.topk_idx.append(tk)
             self.topk_ws.append(ws)
             self.out_entries.append(oe)
-        self._build_desc()
+        self.inputs = self.inputs_by_set[0]
+        self.scores = self.scores_by_set[0]
+        self._descs = [self._build_desc(k) for k in range(input_sets)]
+        self._desc, self._desc_dev = self._descs[0]
+
+    @property
+    def n_input_sets(self) -> int:
+        return len(self.inputs_by_set)
+
+    def step_launches(self) -> int:
+        """Kernel launches of one step, as skv_decode_step_launches reports them."""
+        n = int(_lib.load().skv_decode_step_launches(ctypes.addressof(self._desc)))
+        _lib.check(min(n, 0), "skv_decode_step_launches")
+        return n
 
     # ----------------------------------------------------------- descriptor --
-    def _build_desc(self) -> None:
+    def _build_desc(self, k: int) -> tuple[DecodeDescC, torch.Tensor]:
+        """Host and device descriptors of the step reading input set k."""
+        inputs, scores = self.inputs_by_set[k], self.scores_by_set[k]
         d = DecodeDescC()
         d.batch, d.n_layers, d.n_groups = self.batch, len(self.layers), len(self.groups)
         d.latent, d.c_indexer, d.window = self.latent, self.c_indexer, self.window
@@ -248,47 +276,50 @@ class DecodeCache:
             Ly = d.layers[i]
             Ly.kind = KIND[spec.kind]
             Ly.ring, Ly.out_window = p(self.ring[i]), p(self.out_window[i])
-            Ly.kv_new = p(self.inputs[i]["kv"])
+            Ly.kv_new = p(inputs[i]["kv"])
             if spec.kind in ("csa", "hca"):
                 Ly.group = self.group_of_rate[spec.m]
                 Ly.format = _lib.SKV_FMT_FP8 if spec.fp8 else _lib.SKV_FMT_BF16
                 Ly.pool, Ly.entry_bytes = p(self.pool[i]), ops.row_bytes_of(self.pool[i])
                 Ly.state, Ly.bias = p(self.state[i]), p(self.bias[i])
-                Ly.c_new, Ly.z_new = p(self.inputs[i]["c"]), p(self.inputs[i]["z"])
+                Ly.c_new, Ly.z_new = p(inputs[i]["c"]), p(inputs[i]["z"])
                 Ly.out_entries = p(self.out_entries[i])
                 if spec.kind == "csa":
                     Ly.top_k = spec.top_k
-                    Ly.scores, Ly.score_stride = p(self.scores[i]), self.scores[i].shape[1]
+                    Ly.scores, Ly.score_stride = p(scores[i]), scores[i].shape[1]
                     Ly.topk_idx = p(self.topk_idx[i])
                     Ly.topk_ws = p(self.topk_ws[i])
                     if spec.indexer:
                         Ly.idx_pool, Ly.idx_state = p(self.idx_pool[i]), p(self.idx_state[i])
                         Ly.idx_bias = p(self.idx_bias[i])
-                        Ly.ci_new, Ly.zi_new = p(self.inputs[i]["ci"]), p(self.inputs[i]["zi"])
+                        Ly.ci_new, Ly.zi_new = p(inputs[i]["ci"]), p(inputs[i]["zi"])
                         if spec.idx_heads > 0:
-                            Ly.idx_q, Ly.idx_w = p(self.inputs[i]["iq"]), p(self.inputs[i]["iw"])
+                            Ly.idx_q, Ly.idx_w = p(inputs[i]["iq"]), p(inputs[i]["iw"])
                             Ly.idx_heads = spec.idx_heads
                 else:
                     Ly.out_rows = self.out_entries[i].shape[1]
-        self._desc = d
         raw = bytes(memoryview(d))
-        self._desc_dev = torch.tensor(list(raw), dtype=torch.uint8, device=self.device)
+        return d, torch.tensor(list(raw), dtype=torch.uint8, device=self.device)
 
     # ------------------------------------------------------------------ step --
-    def step(self) -> None:
-        """One decode step of every sequence from the current ``inputs`` and ``scores``
-        (for layers with ``idx_heads``, from ``inputs["iq"]`` / ``inputs["iw"]``: the step
-        writes ``scores`` itself)."""
+    def step(self, input_set: int = 0) -> None:
+        """One decode step of every sequence from input set ``input_set`` (default
+        ``inputs`` and ``scores``; for layers with ``idx_heads``, from ``inputs["iq"]`` /
+        ``inputs["iw"]``: the step writes the set's ``scores`` itself)."""
         if (self.host_lens + 1 > self.max_len).any():
             raise RuntimeError(f"DecodeCache overflow: a sequence would exceed max_len={self.max_len}")
-        _lib.call("skv_decode_step", ctypes.addressof(self._desc), self._desc_dev.data_ptr(),
-                  _lib.stream_handle(self.device))
+        self._launch_step(input_set)
         self.host_lens += 1
+
+    def _launch_step(self, input_set: int) -> None:
+        d, d_dev = self._descs[input_set]
+        _lib.call("skv_decode_step", ctypes.addressof(d), d_dev.data_ptr(), _lib.stream_handle(self.device))
 
     def capture(self, steps: int, before_step=None) -> "CapturedSteps":
         """Capture ``steps`` decode steps in one HIP graph (see CapturedSteps);
-        ``before_step()`` (optional) records the caller's own launches ahead of
-        each step, e.g. its indexer-score launch."""
+        step s reads input set s % input_sets.  ``before_step()`` (optional)
+        records the caller's own launches ahead of each step, e.g. its
+        indexer-score launch."""
         return CapturedSteps(self, steps, before_step)
 
     def check_status(self) -> None:
@@ -538,11 +569,10 @@ class CapturedSteps:
         self.graph = torch.cuda.CUDAGraph()
         lens_before = cache.host_lens.copy()
         with torch.cuda.graph(self.graph):
-            for _ in range(steps):
+            for s in range(steps):
                 if before_step is not None:
                     before_step()
-                _lib.call("skv_decode_step", ctypes.addressof(cache._desc), cache._desc_dev.data_ptr(),
-                          _lib.stream_handle(cache.device))
+                cache._launch_step(s % cache.n_input_sets)
         cache.host_lens = lens_before  # capture records, it does not run
 
     def replay(self) -> None:

@@ -315,6 +315,17 @@ class CSAKVCacheLayer(_CompressedLayer):
 _CacheLayer = SWAKVCacheLayer | HCAKVCacheLayer | CSAKVCacheLayer | None
 
 
+def _attention_kind(attention: object) -> str | None:
+    """"SWAttention", "HCA" or "CSA" if one of those class names is on the
+    module's MRO, tried in that order (the isinstance chain of
+    kv_cache.py:395-426); None otherwise."""
+    names = {c.__name__ for c in type(attention).__mro__}
+    for kind in ("SWAttention", "HCA", "CSA"):
+        if kind in names:
+            return kind
+    return None
+
+
 class KVCacheBundle:
     """Per-layer KV cache container indexed by transformer block index (kv_cache.py:333-427)."""
 
@@ -347,15 +358,17 @@ class KVCacheBundle:
                   dtype: torch.dtype = torch.float32) -> KVCacheBundle:
         """Build a bundle by walking ``model.blocks`` (kv_cache.py:369-427).
 
-        Attention modules are recognised by class name (``SWAttention``, ``HCA``,
-        ``CSA``), so the bundle needs no import of the model package.
+        Attention modules are recognised by the class names along their MRO
+        (``SWAttention``, ``HCA``, ``CSA``, checked in the reference's
+        isinstance order), so subclasses map as they do in the reference and
+        the bundle needs no import of the model package.
         """
         cfg = model.cfg  # type: ignore[attr-defined]
         head_dim = cfg.attention.head_dim
         hidden_dim = cfg.hidden_dim
         layers: list[_CacheLayer] = []
         for block in model.blocks:  # type: ignore[attr-defined]
-            kind = type(block.attention).__name__
+            kind = _attention_kind(block.attention)
             if kind == "SWAttention":
                 layers.append(SWAKVCacheLayer(max_seq_len=max_seq_len, head_dim=head_dim,
                                               batch_size=batch_size, device=device, dtype=dtype))

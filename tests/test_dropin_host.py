@@ -51,3 +51,34 @@ def test_decode_descriptor_layout_matches_library() -> None:
     from saint_kv import decode
 
     decode.check_struct_layout()
+
+
+def test_for_model_maps_subclasses_like_isinstance() -> None:
+    """for_model matches the attention classes along the MRO, in the
+    reference's isinstance order (kv_cache.py:395-426): subclasses of SWAttention,
+    HCA and CSA map to their cache layer, other modules to None."""
+    from saint_kv.kv_cache import _attention_kind
+
+    class SWAttention:
+        pass
+
+    class HCA:
+        pass
+
+    class CSA:
+        pass
+
+    class WrappedCSA(CSA):
+        pass
+
+    class DeepHCA(type("Mid", (HCA,), {})):
+        pass
+
+    class Both(SWAttention, CSA):  # the isinstance chain tests SWAttention first
+        pass
+
+    class Dense:
+        pass
+
+    kinds = [_attention_kind(x()) for x in (SWAttention, HCA, CSA, WrappedCSA, DeepHCA, Both, Dense)]
+    assert kinds == ["SWAttention", "HCA", "CSA", "CSA", "HCA", "SWAttention", None]

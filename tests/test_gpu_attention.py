@@ -198,6 +198,14 @@ def test_attention_bad_arguments(dev) -> None:
     with pytest.raises(ValueError):  # more than 256 heads
         decode_attention(torch.zeros(2, 300, 576, dtype=torch.bfloat16, device=dev), "swa", lens, ring, ring)
     assert math.isfinite(decode_attention(q, "swa", lens, ring, ring).sum().item())
+    # a workspace view off the 16-byte grid is refused, by the wrapper and by the library
+    from saint_kv import attention
+
+    ws = attention.last_workspace()
+    buf = torch.empty(ws.numel() + 8, dtype=torch.float32, device=dev)
+    with pytest.raises(ValueError, match="aligned"):
+        decode_attention(q, "swa", lens, ring, ring, workspace=buf[1:])
+    decode_attention(q, "swa", lens, ring, ring, workspace=buf[4:])  # 16-byte offset: accepted
 
 
 def test_attention_after_decode_step(dev) -> None:
