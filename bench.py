@@ -434,14 +434,16 @@ def cpu_baseline_decode(seconds: float = 5.0, seed: int = 0) -> dict:
 
 
 def run_layer_seq_leg(dev, n_layers: int = 8, batch: int = 16, L: int = 65536, steps: int = 100,
-                      per_graph: int = 10, heads: int = 64, window: int = 128, seed: int = 8) -> dict:
+                      per_graph: int = 10, heads: int = 64, window: int = 128, seed: int = 8,
+                      materialize: bool = False) -> dict:
     """What a model's decode step sees at 64k context: n_layers CSA layers
     (m=4, top-k 512, W=128), one after another, each layer's cache step
     followed by its decode attention over the step's picks and window (the
     next layer's inputs come from that attention, so the layers cannot be
     stepped together).  Each layer has its own cache and input sets; the
     sequence of layers is replayed from HIP graphs of ``per_graph`` model
-    steps."""
+    steps.  The steps write no gathered copies unless ``materialize``: the
+    attention reads the picks' entries and the window rows in place."""
     from saint_kv.decode import DecodeCache, LayerSpec
 
     max_len = L + steps + 2 * per_graph + 8
@@ -449,7 +451,7 @@ def run_layer_seq_leg(dev, n_layers: int = 8, batch: int = 16, L: int = 65536, s
     caches, qs, knorm, outs = [], [], [], []
     for li in range(n_layers):
         c = DecodeCache([LayerSpec("csa", m=4, top_k=512)], batch, max_len, window=window, device=dev,
-                        page_order_seed=seed + li, input_sets=per_graph)
+                        page_order_seed=seed + li, input_sets=per_graph, materialize=materialize)
         c.bias[0].normal_(generator=gen)
         c.idx_bias[0].normal_(generator=gen)
         for k in range(per_graph):
@@ -493,6 +495,7 @@ def run_layer_seq_leg(dev, n_layers: int = 8, batch: int = 16, L: int = 65536, s
         "model_steps": reps * per_graph, "us_per_model_step": round(us, 2),
         "us_per_layer": round(us / n_layers, 2),
         "launches_per_layer": caches[0].step_launches() + 2,
+        "gathered_copies": materialize,
         "kv_tokens_per_s": round(n_layers * batch * (512 + window) / (us * 1e-6), 1),
     }
     log(f"layer_seq_64k: {rec['us_per_model_step']} us per {n_layers}-layer model step, "
@@ -799,7 +802,10 @@ def main() -> int:
             rng.integers(262144, 1048577, size=4), args.leg_steps, seed=5, outlier_frac=0.01,
             evict_frac=0.3)
 
-    layer_seq = run_layer_seq_leg(dev) if "layer_seq_64k" in wanted else None
+    layer_seq = None
+    if "layer_seq_64k" in wanted:
+        layer_seq = run_layer_seq_leg(dev)
+        layer_seq["with_gathered_copies"] = run_layer_seq_leg(dev, materialize=True)
     indexer = None if args.no_indexer else run_indexer_leg(dev, 16, 16384, 64, 128, 200)
     state_io = None if args.no_state else run_state_leg(dev)
     attention = {}

@@ -341,6 +341,9 @@ int skv_compact(const skv_pool_ref* pools, int32_t n_pools, int32_t* block_table
  *            rows past the sequence's entries are left untouched); every
  *            layer copies the last min(window, L) tokens of its ring in
  *            position order; the step's lengths and tops are committed.
+ *            A layer whose out_entries / out_window is NULL skips that copy
+ *            (a consumer that reads the picks, entries and ring rows in
+ *            place, as skv_decode_attention does, needs none of them).
  * skv_decode_step_launches returns the launches a step of the descriptor
  * takes (2 without CSA layers, else 3; 0 for an empty step; negative on a
  * bad descriptor).
@@ -388,9 +391,10 @@ typedef struct skv_decode_layer {
   int64_t score_stride;
   int32_t* topk_idx;      /* CSA out: [batch, top_k] */
   int32_t* topk_ws;       /* CSA: [batch, skv_topk_workspace_words()] int32, zeroed once */
-  void* out_entries;      /* CSA: [batch, top_k, latent]; HCA: [batch, out_rows, latent] bf16 */
+  void* out_entries;      /* CSA: [batch, top_k, latent]; HCA: [batch, out_rows, latent] bf16;
+                           * NULL: no copy (a CSA layer still writes topk_idx) */
   int64_t out_rows;       /* HCA: rows per sequence of out_entries */
-  void* out_window;       /* [batch, window, latent] bf16 */
+  void* out_window;       /* [batch, window, latent] bf16; NULL: no copy */
   /* CSA with an indexer stream, optional: the step's indexer query.  When
    * idx_q is set, the step computes the layer's scores itself (written to
    * scores, as skv_indexer_scores would over the entries before the step)

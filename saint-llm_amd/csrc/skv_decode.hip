@@ -773,7 +773,9 @@ __device__ __forceinline__ void dense_block(const skv_decode_desc* d, const Step
   }
   const int latent = d->latent;
   const int64_t out_row = static_cast<int64_t>(latent) * 2;
-  const int n_dense = (g >= 0) ? static_cast<int>(Ly.out_rows) : 0;
+  // row space of the layer's tile: HCA entries if they are copied, then the
+  // window if it is copied
+  const int n_dense = (g >= 0 && Ly.out_entries) ? static_cast<int>(Ly.out_rows) : 0;
   RowRef rf{nullptr, nullptr, 0};
   if (r < n_dense) {
     // dense HCA rows past the entries stay untouched
@@ -784,7 +786,7 @@ __device__ __forceinline__ void dense_block(const skv_decode_desc* d, const Step
       rf.dst = static_cast<uint8_t*>(Ly.out_entries) + (static_cast<int64_t>(b) * Ly.out_rows + r) * out_row;
       rf.kind = (Ly.format == SKV_FMT_FP8) ? 2 : 1;
     }
-  } else if (r < n_dense + d->window) {
+  } else if (Ly.out_window && r < n_dense + d->window) {
     const int w = r - n_dense;
     const int cnt = min(max(L, 0), d->window);
     if (w < cnt) {
@@ -925,6 +927,10 @@ __device__ __forceinline__ void finish_rows(RankRows& rr, int n_rows, int f0, in
   const int k = Ly.top_k;
   const int64_t out_row = static_cast<int64_t>(d->latent) * 2;
   int32_t* out_idx = Ly.topk_idx + static_cast<int64_t>(b) * k;
+  if (!Ly.out_entries) {  // uniform: the step writes the indices only
+    for (int w = tid; w < n_rows; w += kStepThreads) out_idx[rr.win[w].x] = rr.win[w].y;
+    return;
+  }
   uint8_t* out_base = static_cast<uint8_t*>(Ly.out_entries) + static_cast<int64_t>(b) * k * out_row;
   for (int w = tid; w < n_rows; w += kStepThreads) {
     const int2 pw = rr.win[w];
@@ -1084,7 +1090,7 @@ __device__ __forceinline__ void rank_part(const skv_decode_desc* __restrict__ d,
     constexpr int kPfU = 9;  // 8 threads x 9 tasks cover a 576-channel row (bf16 72 chunks, fp8 40 tasks)
     const bool fp8 = Ly.format == SKV_FMT_FP8;
     const int n_pf = (n_own <= kRankPf) ? n_own : min(n_sure_mine, kRankPf);
-    if (in_lds && n_pf > 0 && entry_tasks<8, kPfU>(d->latent, fp8) <= 8 * kPfU) {  // uniform
+    if (in_lds && n_pf > 0 && Ly.out_entries && entry_tasks<8, kPfU>(d->latent, fp8) <= 8 * kPfU) {  // uniform
       const int r = tid / 8;
       int pick = -1, kind = 0;
       const uint8_t* src = nullptr;
@@ -1246,12 +1252,12 @@ extern "C" int skv_decode_step(const skv_decode_desc* h, const skv_decode_desc* 
       groups_seen |= 1u << Ly.group;
       map.group_first |= 1u << l;
     }
-    if (!Ly.ring || !Ly.kv_new || !Ly.out_window) return set_error(SKV_EINVAL, "%s: layer %d lacks ring/kv_new/out_window", what, l);
-    int64_t dense = h->window;
+    if (!Ly.ring || !Ly.kv_new) return set_error(SKV_EINVAL, "%s: layer %d lacks ring/kv_new", what, l);
+    int64_t dense = Ly.out_window ? h->window : 0;
     if (Ly.kind == SKV_LAYER_HCA || Ly.kind == SKV_LAYER_CSA) {
       if (Ly.group < 0 || Ly.group >= h->n_groups) return set_error(SKV_EINVAL, "%s: layer %d group out of range", what, l);
-      if (!Ly.pool || !Ly.state || !Ly.bias || !Ly.c_new || !Ly.z_new || !Ly.out_entries) {
-        return set_error(SKV_EINVAL, "%s: layer %d lacks pool/state/bias/c/z/out", what, l);
+      if (!Ly.pool || !Ly.state || !Ly.bias || !Ly.c_new || !Ly.z_new) {
+        return set_error(SKV_EINVAL, "%s: layer %d lacks pool/state/bias/c/z", what, l);
       }
       if (entry_layout(Ly.format, h->latent, Ly.entry_bytes) < 0) {
         return set_error(SKV_EINVAL, "%s: layer %d entry_bytes %lld does not match format %d", what, l,
@@ -1293,17 +1299,22 @@ extern "C" int skv_decode_step(const skv_decode_desc* h, const skv_decode_desc* 
         max_top_k = max(max_top_k, Ly.top_k);
       } else {
         map.hca_mask |= 1u << l;
-        if (Ly.out_rows <= 0 || Ly.out_rows > (1 << 24)) {
-          return set_error(SKV_EINVAL, "%s: HCA layer %d needs 0 < out_rows <= 2^24", what, l);
+        if (Ly.out_entries) {
+          if (Ly.out_rows <= 0 || Ly.out_rows > (1 << 24)) {
+            return set_error(SKV_EINVAL, "%s: HCA layer %d needs 0 < out_rows <= 2^24", what, l);
+          }
+          dense += Ly.out_rows;
         }
-        dense += Ly.out_rows;
       }
     } else if (Ly.kind != SKV_LAYER_SWA) {
       return set_error(SKV_EINVAL, "%s: layer %d has unknown kind %d", what, l, Ly.kind);
     }
     if (dense >= (1 << 24)) return set_error(SKV_EINVAL, "%s: layer %d has 2^24 dense rows or more", what, l);
-    map.tiles[l] = static_cast<int32_t>(ceil_div(dense, kGatherRowsD));
-    n_tiles += ceil_div(dense, kGatherRowsD) * h->batch;
+    // layer 0 keeps a tile per sequence even with nothing to copy: its tile 0
+    // commits the step
+    const int64_t tiles = (l == 0 && dense == 0) ? 1 : ceil_div(dense, kGatherRowsD);
+    map.tiles[l] = static_cast<int32_t>(tiles);
+    n_tiles += tiles * h->batch;
     map.tile_end[l] = static_cast<int32_t>(n_tiles < (1 << 24) ? n_tiles : (1 << 24));
   }
   for (int l = h->n_layers; l < SKV_MAX_LAYERS; ++l) {

@@ -114,6 +114,11 @@ class DecodeCache:
     captured sequence of steps cycles through the sets, so that a caller can
     stage the next steps' inputs while earlier ones run.  ``inputs`` and
     ``scores`` are set 0.
+
+    ``materialize=False`` drops the gathered copies (``out_entries`` of
+    CSA/HCA layers and ``out_window``): the step then writes the top-k
+    indices, pools, states, rings and lengths only, which is all a consumer
+    reading the cache in place (``attention``) needs.
     """
 
     def __init__(self, layers: list[LayerSpec], batch: int, max_len: int, *,
@@ -121,7 +126,7 @@ class DecodeCache:
                  block_size: int = 64, device: torch.device | str | None = None,
                  page_order_seed: int | None = 0, pages_per_group: dict[int, int] | None = None,
                  hca_out_rows: int | None = None, score_cols: int | None = None,
-                 input_sets: int = 1) -> None:
+                 input_sets: int = 1, materialize: bool = True) -> None:
         if not 0 < len(layers) <= MAX_LAYERS:
             raise ValueError(f"1..{MAX_LAYERS} layers supported; got {len(layers)}")
         scored = [s.idx_heads > 0 for s in layers if s.kind == "csa"]
@@ -192,7 +197,7 @@ class DecodeCache:
             if spec.kind not in KIND:
                 raise ValueError(f"unknown layer kind {spec.kind!r}")
             self.ring.append(torch.zeros(batch, window, latent, dtype=bf, device=dev))
-            self.out_window.append(torch.zeros(batch, window, latent, dtype=bf, device=dev))
+            self.out_window.append(torch.zeros(batch, window, latent, dtype=bf, device=dev) if materialize else None)
             inp = {"kv": (batch, latent)}  # shapes; one tensor per input set below
             pool = state = bias = ipool = istate = ibias = sc = tk = oe = ws = None
             if spec.kind in ("csa", "hca"):
@@ -223,8 +228,8 @@ class DecodeCache:
                     sc = (batch, cols)
                     tk = torch.full((batch, spec.top_k), -1, dtype=torch.int32, device=dev)
                     ws = ops.topk_workspace(batch, dev)
-                    oe = torch.zeros(batch, spec.top_k, latent, dtype=bf, device=dev)
-                else:
+                    oe = torch.zeros(batch, spec.top_k, latent, dtype=bf, device=dev) if materialize else None
+                elif materialize:
                     rows = hca_out_rows or max(1, max_len // spec.m)
                     oe = torch.zeros(batch, rows, latent, dtype=bf, device=dev)
             self.pool.append(pool)
@@ -283,7 +288,7 @@ class DecodeCache:
                 Ly.pool, Ly.entry_bytes = p(self.pool[i]), ops.row_bytes_of(self.pool[i])
                 Ly.state, Ly.bias = p(self.state[i]), p(self.bias[i])
                 Ly.c_new, Ly.z_new = p(inputs[i]["c"]), p(inputs[i]["z"])
-                Ly.out_entries = p(self.out_entries[i])
+                Ly.out_entries = p(self.out_entries[i])  # None: not copied
                 if spec.kind == "csa":
                     Ly.top_k = spec.top_k
                     Ly.scores, Ly.score_stride = p(scores[i]), scores[i].shape[1]
@@ -296,7 +301,7 @@ class DecodeCache:
                         if spec.idx_heads > 0:
                             Ly.idx_q, Ly.idx_w = p(inputs[i]["iq"]), p(inputs[i]["iw"])
                             Ly.idx_heads = spec.idx_heads
-                else:
+                elif self.out_entries[i] is not None:
                     Ly.out_rows = self.out_entries[i].shape[1]
         raw = bytes(memoryview(d))
         return d, torch.tensor(list(raw), dtype=torch.uint8, device=self.device)

@@ -576,3 +576,63 @@ def test_step_scores_fused_equals_separate_launch_in_graphs(dev) -> None:
             assert torch.equal(fused.out_window[i], sep.out_window[i]), (rep, i)
             assert torch.equal(fused.pool[i], sep.pool[i]), (rep, i)
         assert torch.equal(fused.topk_idx[0], sep.topk_idx[0]), rep
+
+
+def test_step_without_copies_equals_materialized_step(dev) -> None:
+    """DecodeCache(materialize=False): the step skips the gathered copies
+    (CSA picks' entries, HCA entries, windows) and writes everything else
+    exactly as the materializing step does: indices, pools, states, rings,
+    tables, lengths; the attention over either cache gives the same output."""
+    from saint_kv.decode import DecodeCache, LayerSpec
+
+    specs = [LayerSpec("csa", m=4, top_k=64, fp8=True), LayerSpec("hca", m=128), LayerSpec("csa", m=4, top_k=48),
+             LayerSpec("swa")]
+    B, max_len = 6, 4096
+    caches = [DecodeCache(specs, B, max_len, block_size=16, window=32, device=dev, page_order_seed=4,
+                          materialize=mat) for mat in (True, False)]
+    assert caches[1].out_window[0] is None and caches[1].out_entries[0] is None
+    lens0 = np.array([0, 3, 127, 500, 1300, 2047])
+    for c in caches:
+        for i in range(len(specs)):
+            g0 = torch.Generator(device=dev).manual_seed(40 + i)
+            if c.bias[i] is not None:
+                c.bias[i].normal_(generator=g0)
+            if c.idx_bias[i] is not None:
+                c.idx_bias[i].normal_(generator=g0)
+        c.prefill(lens0, generator=torch.Generator(device=dev).manual_seed(41))
+    g = torch.Generator().manual_seed(42)
+    q = torch.randn(B, 16, 576, generator=g).to(torch.bfloat16).to(dev)
+    knorm = torch.rand(576, generator=g).to(dev) + 0.5
+    for step in range(10):
+        for i in range(len(specs)):
+            vals = {k: torch.randn(v.shape, generator=g).to(v.dtype) for k, v in caches[0].inputs[i].items()}
+            sc = torch.randn(caches[0].scores[i].shape, generator=g) if caches[0].scores[i] is not None else None
+            for c in caches:
+                for k, v in vals.items():
+                    c.inputs[i][k].copy_(v)
+                if sc is not None:
+                    c.scores[i].copy_(sc)
+        for c in caches:
+            c.step()
+        torch.cuda.synchronize()
+        for c in caches:
+            c.check_status()
+        a, b = caches
+        assert torch.equal(a.tok_lens, b.tok_lens)
+        for ga, gb in zip(a.groups, b.groups):
+            assert torch.equal(ga.block_table, gb.block_table) and torch.equal(ga.n_entries, gb.n_entries)
+            assert torch.equal(ga.free_top, gb.free_top)
+        for i, s in enumerate(specs):
+            assert torch.equal(a.ring[i], b.ring[i])
+            if s.kind == "swa":
+                continue
+            assert torch.equal(a.pool[i], b.pool[i]) and torch.equal(a.state[i], b.state[i])
+            if s.kind == "csa":
+                assert torch.equal(a.topk_idx[i], b.topk_idx[i]), (step, i)
+                assert torch.equal(a.idx_pool[i], b.idx_pool[i])
+    for i, s in enumerate(specs):
+        kw = {} if s.kind == "swa" else {"knorm_w": knorm}
+        oa = caches[0].attention(i, q, **kw)
+        ob = caches[1].attention(i, q, **kw)
+        torch.cuda.synchronize()
+        assert torch.equal(oa, ob), i
