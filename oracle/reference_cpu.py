@@ -413,6 +413,36 @@ def compress_append(pool: Tensor, block_table: np.ndarray, tail_c: Tensor, tail_
     return emitted
 
 
+class TokenLevelCompressor(torch.nn.Module):
+    """csa.py:41-88 restated: two branches of projections (a, b) and
+    positional biases; the forward pools every m hidden states with the
+    b-branch only (softmax over the m tokens per channel, weighted sum of the
+    b-branch values); the a-branch is computed and unused, as there.  Plain
+    nn.Linear projections without bias (the default linear factory)."""
+
+    def __init__(self, hidden_dim: int, c: int, m: int) -> None:
+        super().__init__()
+        self.c, self.m = c, m
+        self.w_a_kv = torch.nn.Linear(hidden_dim, c, bias=False)
+        self.w_b_kv = torch.nn.Linear(hidden_dim, c, bias=False)
+        self.w_a_z = torch.nn.Linear(hidden_dim, c, bias=False)
+        self.w_b_z = torch.nn.Linear(hidden_dim, c, bias=False)
+        self.bias_a = torch.nn.Parameter(torch.zeros(m, c))
+        self.bias_b = torch.nn.Parameter(torch.zeros(m, c))
+
+    def forward(self, h: Tensor) -> Tensor:
+        b, t, _ = h.shape
+        usable = (t // self.m) * self.m  # csa.py:67-70
+        if usable == 0:
+            return h.new_zeros(b, 0, self.c)
+        h_use = h[:, :usable]
+        n = usable // self.m
+        _ = self.w_a_kv(h_use), self.w_a_z(h_use)  # computed, unused (csa.py:73-76, 84-85)
+        c_b = self.w_b_kv(h_use).view(b, n, self.m, self.c)
+        z_b = self.w_b_z(h_use).view(b, n, self.m, self.c) + self.bias_b  # csa.py:82
+        return (torch.softmax(z_b, dim=-2) * c_b).sum(dim=-2)  # csa.py:86-87
+
+
 def compress_pool_bf16_module(c: Tensor, z: Tensor, bias: Tensor) -> Tensor:
     """The same pooling with the rounding a bf16 module applies at every op
     (z + bias, softmax and the product each rounded to bf16; csa.py:82-87)."""

@@ -21,7 +21,14 @@ Differences in mechanism (not in results):
   CPU device raises.  There is no CPU code path.
 * ``compressor`` callables are invoked exactly as the reference does (on the
   m-aligned prefix of ``cat(h_buffer, h_new)``); their output is copied into
-  the paged compressed cache.
+  the paged compressed cache.  Fast path: when every compressor of a bf16
+  cache is a ``TokenLevelCompressor``-shaped module (``w_b_kv``, ``w_b_z``,
+  ``bias_b``, ``m``, ``c``; csa.py:59-64), only the two projections its
+  forward pools with are run (torch), and the per-channel softmax pooling
+  and entry emission run in ``skv_compress_append`` straight into the pages,
+  token by token, through a carried fp32 pooling state (csa.py:79-87), so
+  no block is replayed from ``h_buffer``.  ``h_buffer`` / ``h_buf_count``
+  keep the reference's contents either way.
 """
 
 from __future__ import annotations
@@ -105,6 +112,19 @@ class _PagedRows:
             ops.release(self.free_stack, self.free_top, self.block_table, self.lens, mask,
                         self.block_size, self.status)
         self.length = 0
+
+
+def _fast_compressor(comp: object, m: int, c: int) -> tuple | None:
+    """(w_b_kv, w_b_z, bias_b) of a TokenLevelCompressor-shaped module with
+    this cache's compression rate and channels (csa.py:59-64): the b-branch
+    projections and positional bias its forward pools with (csa.py:73-87; the
+    a-branch is computed there but unused).  None for any other callable."""
+    w_kv, w_z, bias = (getattr(comp, n, None) for n in ("w_b_kv", "w_b_z", "bias_b"))
+    if not (callable(w_kv) and callable(w_z) and isinstance(bias, Tensor)):
+        return None
+    if getattr(comp, "m", None) != m or getattr(comp, "c", None) != c or tuple(bias.shape) != (m, c):
+        return None
+    return w_kv, w_z, bias
 
 
 def _check_3d(what: str, *ts: Tensor) -> None:
@@ -193,6 +213,11 @@ class _CompressedLayer:
                          for d in head_dims]
         self.h_buffer = torch.zeros(batch_size, compression_rate, hidden_dim, device=dev, dtype=dtype)
         self.h_buf_count = 0
+        # fast path: per stream the online-softmax state of the block being
+        # filled; _tail_folded says whether it holds the buffered tokens
+        self._tails = [torch.zeros(batch_size, 3, d, dtype=torch.float32, device=dev) for d in head_dims]
+        self._tail_folded = True
+        self.fast_appends = 0  # appends that took the fast path
 
     @property
     def length(self) -> int:
@@ -230,8 +255,21 @@ class _CompressedLayer:
         total = self.h_buf_count + n
         n_complete = total // self.compression_rate
         n_consumed = n_complete * self.compression_rate
+        fast = self._fast_path(compressors)
+        if fast is not None:
+            # 3') fold the tokens into the pooling state, emit completed blocks
+            if n_complete > 0 and self.n_blocks + n_complete > self._max_blocks:
+                raise RuntimeError(
+                    f"{name} overflow: {self.n_blocks + n_complete} compressed blocks exceed "
+                    f"{self._max_blocks}",
+                )
+            # the tokens the state has not folded yet: the new ones, or the
+            # buffered ones too after a compressor call left them out
+            fold = (h_new, n) if self._tail_folded else (combined, total)
+            self._fold(fast, *fold, n_complete, self.n_blocks * self.compression_rate + total)
+            self.fast_appends += 1
         # 3) emit complete blocks through the caller's compressors (kv_cache.py:182-189)
-        if n_complete > 0:
+        elif n_complete > 0:
             tail = combined[:, :n_consumed]
             outs = [c(tail) for c in compressors]
             if any(o.shape[1] != n_complete for o in outs):
@@ -249,14 +287,53 @@ class _CompressedLayer:
         if leftover > 0:
             self.h_buffer[:, :leftover] = combined[:, n_consumed:]
         self.h_buf_count = leftover
+        # a compressor call leaves the buffered tokens out of the fold state
+        self._tail_folded = fast is not None or leftover == 0
         compressed = [s.out[:, : s.length] for s in self._streams]
         return [*compressed, sw[:, :, 0], sw[:, :, 1]]
+
+    def _fast_path(self, compressors: list) -> list | None:
+        """The streams' (w_kv, w_z, bias) when every compressor takes the fast path."""
+        if self.dtype != torch.bfloat16:
+            return None
+        out = []
+        for comp, stream in zip(compressors, self._streams, strict=True):
+            if stream.d % 8 or stream.d > 2048:
+                return None
+            f = _fast_compressor(comp, self.compression_rate, stream.d)
+            if f is None:
+                return None
+            out.append(f)
+        return out
+
+    def _fold(self, fast: list, h: Tensor, n_fold: int, n_complete: int, tok_after: int) -> None:
+        """Fold the last n_fold tokens of the compressor token stream, whose
+        hidden states are h (the first at a block start or right after the
+        tokens already folded), into each stream's pooling state; tok_after is
+        the stream's token count after them.  Completed blocks go to the
+        stream's pages (skv_compress_append) and its gather buffer."""
+        lens = torch.full((self.batch_size,), tok_after, dtype=torch.int32, device=self.h_buffer.device)
+        for stream, state, (w_kv, w_z, bias) in zip(self._streams, self._tails, fast, strict=True):
+            if n_complete > 0:
+                ops.reserve(stream.free_stack, stream.free_top, stream.block_table, stream.lens, n_complete,
+                            stream.block_size, stream.status)
+            if n_fold > 0:
+                hh = h.to(bias.dtype)  # the module's own dtype, as its forward sees it
+                with torch.no_grad():  # the kernel consumes raw buffers; no autograd graph
+                    c = w_kv(hh).to(torch.bfloat16).contiguous()
+                    z = w_z(hh).to(torch.bfloat16).contiguous()
+                ops.compress_append(stream.pool, stream.block_table, state, c, z,
+                                    bias.detach().to(torch.float32).contiguous(), lens, n_fold)
+            if n_complete > 0:
+                stream.length += n_complete
+                ops.paged_gather(stream.pool, stream.block_table, stream.lens, stream._out)
 
     def reset(self) -> None:
         self._sw.reset()
         for s in self._streams:
             s.reset()
         self.h_buf_count = 0
+        self._tail_folded = True
 
 
 class HCAKVCacheLayer(_CompressedLayer):

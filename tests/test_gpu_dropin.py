@@ -217,3 +217,81 @@ def test_bundle_for_model(dev) -> None:
                      "CSAKVCacheLayer", None]
     csa = bundle.for_layer(2)
     assert csa.c_indexer == 16 and csa.compression_rate == 4 and bundle.for_layer(3).compression_rate == 8
+
+
+def _exact_compressor(hidden: int, c: int, m: int, g: torch.Generator):
+    """A TokenLevelCompressor whose projections of integer hidden states in
+    [-2, 2] are exact in any summation order (weights in {0, +-1/2, +-1}, at
+    most 8 nonzero per output), so that projecting tokens in one call or in
+    several gives the same bf16 values."""
+    comp = ref.TokenLevelCompressor(hidden, c, m)
+    for lin in (comp.w_a_kv, comp.w_b_kv, comp.w_a_z, comp.w_b_z):
+        w = torch.zeros(c, hidden)
+        for o in range(c):
+            cols = torch.randperm(hidden, generator=g)[:8]
+            w[o, cols] = torch.tensor([-1.0, -0.5, 0.5, 1.0])[torch.randint(0, 4, (8,), generator=g)]
+        lin.weight.data = w
+    comp.bias_a.data = torch.randn(m, c, generator=g).to(torch.bfloat16).float()
+    comp.bias_b.data = torch.randn(m, c, generator=g).to(torch.bfloat16).float()
+    return comp
+
+
+def test_compressor_fast_path_matches_reference_formula(dev) -> None:
+    """A bf16 CSA/HCA drop-in layer given TokenLevelCompressor modules runs
+    the fast path (two projections + skv_compress_append into the pages): the
+    block counts, h-buffer and SW views match the reference state machine,
+    and every compressed entry equals the reference pooling formula
+    (csa.py:79-87) on the module's own b-branch projections within the
+    pooling bound, and the module's bf16 forward within 1e-2 in norm.  A plain
+    callable mid-block switches that append to the reference's call-and-copy
+    path; the next fast append folds the buffered tokens first."""
+    import copy
+
+    from saint_kv.kv_cache import CSAKVCacheLayer, HCAKVCacheLayer
+
+    g = torch.Generator().manual_seed(0)
+    H, D, CI, B = 64, 64, 32, 3
+    bf = torch.bfloat16
+    for m, layer_cls in ((4, CSAKVCacheLayer), (16, HCAKVCacheLayer)):
+        kw = {"c_indexer": CI} if layer_cls is CSAKVCacheLayer else {}
+        n_streams = 2 if kw else 1
+        cpu_comps = [_exact_compressor(H, d, m, g) for d in [D, CI][:n_streams]]
+        comps = [copy.deepcopy(c).to(dev, bf) for c in cpu_comps]
+        layer = layer_cls(max_seq_len=200, hidden_dim=H, head_dim=D, compression_rate=m, batch_size=B,
+                          device=dev, dtype=bf, **kw)
+        cont = ref.ContiguousCompressed(200, H, [D, CI][:n_streams], m, batch_size=B, dtype=bf)
+        hist_h = []
+        for step, n in enumerate((3, 6, 1, 5, 4, 9, 1, 1, 2, 17, 1)):
+            h = torch.randint(-2, 3, (B, n, H), generator=g).to(bf).to(dev)
+            sk = torch.randn(B, n, D, generator=g).to(bf).to(dev)
+            sv = torch.randn(B, n, D, generator=g).to(bf).to(dev)
+            hist_h.append(h)
+            plain = step == 6  # a plain callable: the reference path for this append
+            use = [(lambda x, c=c: c(x)) if plain else c for c in comps]
+            args = {"compressor": use[0]}
+            if kw:
+                args["indexer_compressor"] = use[1]
+            out = layer.append(h, sk, sv, **args)
+            with torch.no_grad():
+                want = cont.append(h.cpu(), sk.cpu(), sv.cpu(),
+                                   [lambda x, c=c: c(x.float()).to(bf) for c in cpu_comps])
+            assert layer.n_blocks == cont.n_blocks and layer.h_buf_count == cont.h_buf_count
+            assert layer.length == cont.length
+            assert torch.equal(out[-2].cpu(), want[-2]) and torch.equal(out[-1].cpu(), want[-1])
+            assert torch.equal(layer.h_buffer[:, :layer.h_buf_count].cpu(), cont.h_buffer[:, :cont.h_buf_count])
+        assert layer.fast_appends == 10
+        allh = torch.cat(hist_h, dim=1).cpu().float()
+        nb = layer.n_blocks
+        for si, c in enumerate(cpu_comps):
+            got = out[si].float().cpu()
+            hh = allh[:, : nb * m]
+            with torch.no_grad():
+                cz = c.w_b_kv(hh).view(B, nb, m, -1)  # exact, and exact in bf16
+                zz = c.w_b_z(hh).view(B, nb, m, -1)
+            want_f = ref.compress_pool(cz, zz, c.bias_b)
+            bound = ref.pooling_bound(cz, zz, c.bias_b)
+            assert ((got - want_f).abs() <= bound).all(), (m, si, float((got - want_f).abs().max()))
+            # the module's bf16 forward rounds at every op: within 1e-2 in norm
+            with torch.no_grad():
+                mod = comps[si](hh.to(bf).to(dev)).float().cpu()
+            assert float((got - mod).norm() / mod.norm()) < 1e-2

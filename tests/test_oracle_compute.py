@@ -331,3 +331,24 @@ def test_pooling_bound_covers_reordering_and_catches_a_dropped_term() -> None:
         no_bias = ref.compress_pool(c, z, torch.zeros_like(bias))
         for bad in (dropped, no_bias):
             assert ((bad - want).abs() > bound).float().mean() > 0.5
+
+
+def test_token_level_compressor_restatement_pools_its_b_branch() -> None:
+    """The oracle TokenLevelCompressor equals compress_pool of its own b-branch
+    projections (the formula the fast path of the drop-in uses), ignores its
+    a-branch, drops an incomplete trailing block and returns no block for
+    fewer than m tokens."""
+    g = torch.Generator().manual_seed(9)
+    comp = ref.TokenLevelCompressor(24, 16, 4)
+    for p in comp.parameters():
+        p.data = torch.randn(p.shape, generator=g)
+    h = torch.randn(2, 11, 24, generator=g)
+    out = comp(h)
+    assert out.shape == (2, 2, 16)
+    c = comp.w_b_kv(h[:, :8]).view(2, 2, 4, 16)
+    z = comp.w_b_z(h[:, :8]).view(2, 2, 4, 16)
+    torch.testing.assert_close(out, ref.compress_pool(c, z, comp.bias_b), rtol=1e-6, atol=1e-6)
+    comp.w_a_kv.weight.data.zero_()
+    comp.bias_a.data.fill_(5.0)
+    torch.testing.assert_close(comp(h), out)
+    assert comp(h[:, :3]).shape == (2, 0, 16)
