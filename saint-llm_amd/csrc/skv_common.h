@@ -38,6 +38,29 @@ __device__ __forceinline__ void st_stream(u32x4* p, u32x4 v) {
 }
 
 // ---------------------------------------------------------------------------
+// Device pointers that a kernel loads from memory (descriptor fields).  The
+// compiler knows kernel arguments point to global memory, but a pointer it
+// loads from memory is generic, and accesses through it become FLAT
+// instructions, which count against lgkmcnt as well as vmcnt: every later
+// LDS or scalar-load wait would also wait for them.  global_field loads the
+// field as a global-address-space pointer; the accesses derived from it
+// become global_load / global_store.
+// ---------------------------------------------------------------------------
+template <class T>
+using global_ptr = __attribute__((address_space(1))) T*;
+
+template <class T>
+__device__ __forceinline__ T* global_field(T* const& field) {
+  return (T*)*reinterpret_cast<global_ptr<T> const*>(&field);
+}
+
+// A device address kept as an integer (in LDS), back to a pointer.
+template <class T>
+__device__ __forceinline__ T* global_from_bits(uintptr_t bits) {
+  return (T*)(global_ptr<T>)bits;
+}
+
+// ---------------------------------------------------------------------------
 // bf16 <-> fp32.  Round-to-nearest-even with quiet-NaN canonicalisation,
 // the rounding torch applies in Tensor.to(torch.bfloat16).
 // ---------------------------------------------------------------------------

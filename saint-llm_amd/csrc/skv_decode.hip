@@ -473,8 +473,9 @@ __global__ __launch_bounds__(kStepThreads) void k_decode_append(const skv_decode
   if (paged && (main_stream || idx_stream)) {
     const int channels = main_stream ? d->latent : d->c_indexer;
     const int t = main_stream ? tid : tid - 2 * kWave;
-    fold_load(first, main_stream ? Ly.state : Ly.idx_state, main_stream ? Ly.c_new : Ly.ci_new,
-              main_stream ? Ly.z_new : Ly.zi_new, b, channels, min(t, (channels >> 3) - 1));
+    fold_load(first, global_field(main_stream ? Ly.state : Ly.idx_state),
+              global_field(main_stream ? Ly.c_new : Ly.ci_new), global_field(main_stream ? Ly.z_new : Ly.zi_new), b,
+              channels, min(t, (channels >> 3) - 1));
   }
   const int g = map.group[l];  // < 0 for an SWA layer
   // with the token count: the bias rows of the fold and the block-table slot
@@ -487,7 +488,7 @@ __global__ __launch_bounds__(kStepThreads) void k_decode_append(const skv_decode
     if (main_stream || idx_stream) {
       const int channels = main_stream ? d->latent : d->c_indexer;
       const int t = main_stream ? tid : tid - 2 * kWave;
-      fold_bias(first, main_stream ? Ly.bias : Ly.idx_bias, umod24(p1 - 1, mm), channels,
+      fold_bias(first, global_field(main_stream ? Ly.bias : Ly.idx_bias), umod24(p1 - 1, mm), channels,
                 min(t, (channels >> 3) - 1));
     }
     const uint32_t e1 = udiv24(p1, mm);
@@ -505,8 +506,8 @@ __global__ __launch_bounds__(kStepThreads) void k_decode_append(const skv_decode
   if (l == 0 && tid == 0) map.step_lens[b] = L0 + 1;
   if (wave == 3) {
     const int row_chunks = d->latent >> 3;  // 16-byte chunks of a bf16 row
-    const u32x4* src = static_cast<const u32x4*>(Ly.kv_new) + static_cast<int64_t>(b) * row_chunks;
-    u32x4* dst = static_cast<u32x4*>(Ly.ring) + (static_cast<int64_t>(b) * d->window + umod24(static_cast<uint32_t>(p), d->window)) * row_chunks;
+    const u32x4* src = static_cast<const u32x4*>(global_field(Ly.kv_new)) + static_cast<int64_t>(b) * row_chunks;
+    u32x4* dst = static_cast<u32x4*>(global_field(Ly.ring)) + (static_cast<int64_t>(b) * d->window + umod24(static_cast<uint32_t>(p), d->window)) * row_chunks;
     for (int c = tid - 3 * kWave; c < row_chunks; c += kWave) dst[c] = src[c];
     return;
   }
@@ -528,13 +529,16 @@ __global__ __launch_bounds__(kStepThreads) void k_decode_append(const skv_decode
   const int in_page = static_cast<int>(e) - pi * bs;
   if (main_stream) {
     const int fp8_main = (Ly.format == SKV_FMT_FP8) ? d->latent - SKV_FP8_ROPE_DIMS : 0;
-    const EmitSlot slot{static_cast<uint8_t*>(Ly.pool), Ly.entry_bytes, page, map.n_pages[g], bs, in_page};
-    decode_fold_part(m, b, p, slot, Ly.state, Ly.bias, Ly.c_new, Ly.z_new, d->latent, Ly.format, fp8_main,
+    const EmitSlot slot{static_cast<uint8_t*>(global_field(Ly.pool)), Ly.entry_bytes, page, map.n_pages[g], bs,
+                        in_page};
+    decode_fold_part(m, b, p, slot, global_field(Ly.state), global_field(Ly.bias), global_field(Ly.c_new),
+                     global_field(Ly.z_new), d->latent, Ly.format, fp8_main,
                      tid, 2 * kWave, first);
   } else if (idx_stream) {
-    const EmitSlot slot{static_cast<uint8_t*>(Ly.idx_pool), static_cast<int64_t>(d->c_indexer) * 2, page,
-                        map.n_pages[g], bs, in_page};
-    decode_fold_part(m, b, p, slot, Ly.idx_state, Ly.idx_bias, Ly.ci_new, Ly.zi_new, d->c_indexer,
+    const EmitSlot slot{static_cast<uint8_t*>(global_field(Ly.idx_pool)), static_cast<int64_t>(d->c_indexer) * 2,
+                        page, map.n_pages[g], bs, in_page};
+    decode_fold_part(m, b, p, slot, global_field(Ly.idx_state), global_field(Ly.idx_bias), global_field(Ly.ci_new),
+                     global_field(Ly.zi_new), d->c_indexer,
                      SKV_FMT_BF16, 0, tid - 2 * kWave, kWave, first);
   }
 }
@@ -646,7 +650,43 @@ __device__ __forceinline__ void copy_rows(int n, RowFn row, int latent, bool fp8
 // and its address, or 0 when e is past n_ent or its page is not mapped.
 // The first n_lds entries of the sequence's block-table row may be staged
 // in LDS (bt_lds).
-__device__ __forceinline__ int entry_source(const GroupRef& G, const skv_decode_layer& Ly, int b, int e,
+// The descriptor fields of a layer that the gather launch reads.  A
+// workgroup loads them at its start and holds them (hold_fields) once its
+// first round trip is in flight: scalar loads left at their first use would
+// be issued after the status check, one more dependent round trip.
+struct GatherLayer {
+  const uint8_t* pool;
+  int64_t entry_bytes;
+  void* out_entries;
+  int32_t* topk_idx;      // CSA
+  const uint8_t* ring;    // dense tiles
+  void* out_window;       // dense tiles
+  int64_t out_rows;       // dense tiles (HCA)
+  int32_t format;
+  int32_t latent;
+  int32_t window;
+};
+
+__device__ __forceinline__ GatherLayer gather_layer(const skv_decode_desc* d, const skv_decode_layer& Ly) {
+  return GatherLayer{static_cast<const uint8_t*>(global_field(Ly.pool)), Ly.entry_bytes,
+                     global_field(Ly.out_entries), global_field(Ly.topk_idx),
+                     static_cast<const uint8_t*>(global_field(Ly.ring)), global_field(Ly.out_window), Ly.out_rows,
+                     Ly.format, d->latent, d->window};
+}
+
+// The values must be loaded here (scalar registers): the compiler keeps the
+// loads ahead of this point instead of sinking them to their uses.
+__device__ __forceinline__ void hold_fields(const GatherLayer& g, bool dense) {
+  if (dense) {
+    asm volatile("" ::"s"(g.pool), "s"(g.entry_bytes), "s"(g.out_entries), "s"(g.ring), "s"(g.out_window),
+                 "s"(g.out_rows), "s"(g.format), "s"(g.latent), "s"(g.window));
+  } else {
+    asm volatile("" ::"s"(g.pool), "s"(g.entry_bytes), "s"(g.out_entries), "s"(g.topk_idx), "s"(g.format),
+                 "s"(g.latent));
+  }
+}
+
+__device__ __forceinline__ int entry_source(const GroupRef& G, const GatherLayer& Ly, int b, int e,
                                             int n_ent, const uint8_t** src, const int32_t* bt_lds = nullptr,
                                             int n_lds = 0) {
   if (e < 0 || e >= n_ent) return 0;
@@ -654,8 +694,7 @@ __device__ __forceinline__ int entry_source(const GroupRef& G, const skv_decode_
   const int32_t page = (pi < n_lds) ? bt_lds[pi]
                        : (pi < G.bt_stride) ? G.block_table[static_cast<int64_t>(b) * G.bt_stride + pi] : -1;
   if (page < 0 || page >= G.n_pages) return 0;
-  *src = static_cast<const uint8_t*>(Ly.pool) +
-         (static_cast<int64_t>(page) * G.block_size + (e - pi * G.block_size)) * Ly.entry_bytes;
+  *src = Ly.pool + (static_cast<int64_t>(page) * G.block_size + (e - pi * G.block_size)) * Ly.entry_bytes;
   return (Ly.format == SKV_FMT_FP8) ? 2 : 1;
 }
 
@@ -760,10 +799,12 @@ __device__ __forceinline__ void dense_block(const skv_decode_desc* d, const Step
   const int32_t* bt = (g >= 0) ? map.block_table[gi] + static_cast<int64_t>(b) * map.bt_stride[gi] +
                                      min(pi, map.bt_stride[gi] - 1)
                                : map.step_lens + b;
+  const GatherLayer Ly = gather_layer(d, d->layers[l]);
   const int32_t page = *bt;
   const int L = map.step_lens[b];
-  if (*map.status) return;  // refused step
-  const skv_decode_layer& Ly = d->layers[l];
+  const int status = *map.status;
+  hold_fields(Ly, true);
+  if (status) return;  // refused step
   if (l == 0 && tile == 0 && threadIdx.x == 0) {
     map.tok_lens[b] = L;
     for (int gg = 0; gg < map.n_groups; ++gg) map.n_entries[gg][b] = udiv24(L, map.m[gg]);
@@ -771,7 +812,7 @@ __device__ __forceinline__ void dense_block(const skv_decode_desc* d, const Step
       for (int gg = 0; gg < map.n_groups; ++gg) *map.free_top[gg] = map.step_top[gg];
     }
   }
-  const int latent = d->latent;
+  const int latent = Ly.latent;
   const int64_t out_row = static_cast<int64_t>(latent) * 2;
   // row space of the layer's tile: HCA entries if they are copied, then the
   // window if it is copied
@@ -781,18 +822,17 @@ __device__ __forceinline__ void dense_block(const skv_decode_desc* d, const Step
     // dense HCA rows past the entries stay untouched
     if (r < static_cast<int>(udiv24(L, map.m[gi])) && pi < map.bt_stride[gi] && page >= 0 &&
         page < map.n_pages[gi]) {
-      rf.src = static_cast<const uint8_t*>(Ly.pool) +
-               (static_cast<int64_t>(page) * bs + (r - pi * bs)) * Ly.entry_bytes;
+      rf.src = Ly.pool + (static_cast<int64_t>(page) * bs + (r - pi * bs)) * Ly.entry_bytes;
       rf.dst = static_cast<uint8_t*>(Ly.out_entries) + (static_cast<int64_t>(b) * Ly.out_rows + r) * out_row;
       rf.kind = (Ly.format == SKV_FMT_FP8) ? 2 : 1;
     }
-  } else if (Ly.out_window && r < n_dense + d->window) {
+  } else if (Ly.out_window && r < n_dense + Ly.window) {
     const int w = r - n_dense;
-    const int cnt = min(max(L, 0), d->window);
+    const int cnt = min(max(L, 0), Ly.window);
     if (w < cnt) {
-      const int64_t slot = umod24(static_cast<uint32_t>(L - cnt + w), d->window);
-      rf.src = static_cast<const uint8_t*>(Ly.ring) + (static_cast<int64_t>(b) * d->window + slot) * out_row;
-      rf.dst = static_cast<uint8_t*>(Ly.out_window) + (static_cast<int64_t>(b) * d->window + w) * out_row;
+      const int64_t slot = umod24(static_cast<uint32_t>(L - cnt + w), Ly.window);
+      rf.src = Ly.ring + (static_cast<int64_t>(b) * Ly.window + slot) * out_row;
+      rf.dst = static_cast<uint8_t*>(Ly.out_window) + (static_cast<int64_t>(b) * Ly.window + w) * out_row;
       rf.kind = 1;
     }
   }
@@ -917,15 +957,14 @@ __device__ __forceinline__ void rank_candidates(RankRows& rr, KeyAt ck, int S, i
 // Adds the fills [f0, o1), writes the indices and copies every collected row.
 // n_rows: rows collected so far (read after a barrier by the caller).
 __device__ __forceinline__ void finish_rows(RankRows& rr, int n_rows, int f0, int o1,
-                                            const skv_decode_desc* d, const skv_decode_layer& Ly,
+                                            const skv_decode_desc* d, const GatherLayer& Ly, int k,
                                             const GroupRef& G, int b, int L, const int32_t* bt_lds, int n_lds) {
   const int tid = threadIdx.x;
   if (tid < o1 - f0) rr.win[n_rows + tid] = make_int2(f0 + tid, -1);
   n_rows += max(0, o1 - f0);
   __syncthreads();
   const int n_ent = static_cast<int>(udiv24(L, G.m));
-  const int k = Ly.top_k;
-  const int64_t out_row = static_cast<int64_t>(d->latent) * 2;
+  const int64_t out_row = static_cast<int64_t>(Ly.latent) * 2;
   int32_t* out_idx = Ly.topk_idx + static_cast<int64_t>(b) * k;
   if (!Ly.out_entries) {  // uniform: the step writes the indices only
     for (int w = tid; w < n_rows; w += kStepThreads) out_idx[rr.win[w].x] = rr.win[w].y;
@@ -944,10 +983,10 @@ __device__ __forceinline__ void finish_rows(RankRows& rr, int n_rows, int f0, in
       n_rows,
       [&](int r) {
         const uintptr_t sk = rr.src_kind[r];
-        return RowRef{reinterpret_cast<const uint8_t*>(sk & ~static_cast<uintptr_t>(3)),
+        return RowRef{global_from_bits<const uint8_t>(sk & ~static_cast<uintptr_t>(3)),
                       out_base + rr.win[r].x * out_row, static_cast<int>(sk & 3)};
       },
-      d->latent, Ly.format == SKV_FMT_FP8, d);
+      Ly.latent, Ly.format == SKV_FMT_FP8, d);
 }
 
 // ---------------------------------------------------------------------------
@@ -999,7 +1038,7 @@ __device__ __forceinline__ void rank_part(const skv_decode_desc* __restrict__ d,
   uint64_t* sm_ck = reinterpret_cast<uint64_t*>(region);
   RankFallback& fb = *reinterpret_cast<RankFallback*>(region);
   const int li = static_cast<int>((map.csa >> (4 * z)) & 15);
-  const skv_decode_layer& Ly = d->layers[li];
+  const GatherLayer Ly = gather_layer(d, d->layers[li]);
   const int gi = map.group[li];
   const int tid = threadIdx.x;
   int32_t* ws = map.topk_ws[z] + static_cast<int64_t>(b) * kTkWsWords;
@@ -1020,7 +1059,8 @@ __device__ __forceinline__ void rank_part(const skv_decode_desc* __restrict__ d,
   int32_t btv[kRankBt / kStepThreads];
 #pragma unroll
   for (int u = 0; u < kRankBt / kStepThreads; ++u) btv[u] = bt_row[min(tid + u * kStepThreads, n_bt - 1)];
-  const int k = Ly.top_k;
+  hold_fields(Ly, false);
+  const int k = map.top_k[z];
   const int parts = static_cast<int>(ceil_div24(k, rank_out));
   if (part >= parts) return;  // the grid is sized for the largest top_k
   const GroupRef G = group_ref(map, gi);
@@ -1029,7 +1069,7 @@ __device__ __forceinline__ void rank_part(const skv_decode_desc* __restrict__ d,
   }
   if (status) return;  // refused step
   int n_cols, n_valid;
-  score_cols(Ly, G.m, L, n_cols, n_valid);
+  score_cols(map.score_stride[z], G.m, L, n_cols, n_valid);
   const int sel = topk_sel(k, n_cols, n_valid);
 #pragma unroll
   for (int u = 0; u < kRankBt / kStepThreads; ++u) {
@@ -1040,12 +1080,12 @@ __device__ __forceinline__ void rank_part(const skv_decode_desc* __restrict__ d,
   const int o1 = min(k, o0 + rank_out);
   if (sel > 0 && flag) {
     // tie bin over the list capacity: full select of the row, then this part's positions
-    topk_row<kStepThreads>(fb.full, nullptr, Ly.scores + static_cast<int64_t>(b) * Ly.score_stride, n_cols,
-                           n_valid, k, fb.order);
+    topk_row<kStepThreads>(fb.full, nullptr, map.scores[z] + static_cast<int64_t>(b) * map.score_stride[z],
+                           n_cols, n_valid, k, fb.order);
     __syncthreads();
     if (tid < o1 - o0) sm.rr.win[tid] = make_int2(o0 + tid, fb.order[o0 + tid]);
     __syncthreads();
-    finish_rows(sm.rr, o1 - o0, o1, o1, d, Ly, G, b, L, sm_bt, n_bt);
+    finish_rows(sm.rr, o1 - o0, o1, o1, d, Ly, k, G, b, L, sm_bt, n_bt);
     return;
   }
   if (sel > 0) {
@@ -1090,7 +1130,7 @@ __device__ __forceinline__ void rank_part(const skv_decode_desc* __restrict__ d,
     constexpr int kPfU = 9;  // 8 threads x 9 tasks cover a 576-channel row (bf16 72 chunks, fp8 40 tasks)
     const bool fp8 = Ly.format == SKV_FMT_FP8;
     const int n_pf = (n_own <= kRankPf) ? n_own : min(n_sure_mine, kRankPf);
-    if (in_lds && n_pf > 0 && Ly.out_entries && entry_tasks<8, kPfU>(d->latent, fp8) <= 8 * kPfU) {  // uniform
+    if (in_lds && n_pf > 0 && Ly.out_entries && entry_tasks<8, kPfU>(Ly.latent, fp8) <= 8 * kPfU) {  // uniform
       const int r = tid / 8;
       int pick = -1, kind = 0;
       const uint8_t* src = nullptr;
@@ -1102,26 +1142,26 @@ __device__ __forceinline__ void rank_part(const skv_decode_desc* __restrict__ d,
         if (kind == 0) kind = 3;
       }
       EntryShare<kPfU> share;
-      entry_share_load<8, kPfU>(share, src, kind, d->latent, fp8, reinterpret_cast<const u32x4*>(d));
+      entry_share_load<8, kPfU>(share, src, kind, Ly.latent, fp8, reinterpret_cast<const u32x4*>(d));
       rank_candidates(sm.rr, lds_key, S, C, sel, part, parts, sm.own_pos, n_pf);
       __syncthreads();
       const int pos = (r < n_pf) ? sm.own_pos[r] : -1;
       if (pos >= 0) {
-        const int64_t out_row = static_cast<int64_t>(d->latent) * 2;
+        const int64_t out_row = static_cast<int64_t>(Ly.latent) * 2;
         if ((tid & 7) == 0) Ly.topk_idx[static_cast<int64_t>(b) * k + pos] = pick;
         entry_share_store<8, kPfU>(share, static_cast<uint8_t*>(Ly.out_entries) +
                                               (static_cast<int64_t>(b) * k + pos) * out_row,
-                                   kind, d->latent, fp8);
+                                   kind, Ly.latent, fp8);
       }
       // the other winners and the fills
-      finish_rows(sm.rr, sm.rr.n_rows, max(o0, sel), o1, d, Ly, G, b, L, sm_bt, n_bt);
+      finish_rows(sm.rr, sm.rr.n_rows, max(o0, sel), o1, d, Ly, k, G, b, L, sm_bt, n_bt);
       return;
     }
     if (in_lds) rank_candidates(sm.rr, lds_key, S, C, sel, part, parts);
     else rank_candidates(sm.rr, global_key, S, C, sel, part, parts);
   }
   __syncthreads();
-  finish_rows(sm.rr, sm.rr.n_rows, max(o0, sel), o1, d, Ly, G, b, L, sm_bt, n_bt);
+  finish_rows(sm.rr, sm.rr.n_rows, max(o0, sel), o1, d, Ly, k, G, b, L, sm_bt, n_bt);
 }
 
 // Blocks of the gather launch: rank part i (parts_max x batch x CSA layers
