@@ -62,6 +62,11 @@ class _PagedRows:
     out; page ids are handed out by the device free stack (skv_reserve).  Rows
     whose size is not a multiple of 16 bytes are stored with the last dim
     zero-padded (the kernels move 16-byte chunks); views hide the padding.
+
+    The gather buffer is a running copy of the pages: an append refreshes it
+    from the page that holds the first new row on (at most block_size - 1
+    earlier rows plus the new ones), so an append costs O(new rows), not
+    O(length), as the reference's slice views cost nothing per append.
     """
 
     def __init__(self, batch: int, max_rows: int, row_shape: tuple[int, ...], dtype: torch.dtype,
@@ -91,7 +96,7 @@ class _PagedRows:
         """(B, max_rows, *row_shape) gather buffer; rows [0, length) are current."""
         return self._out if self.d == self.d_pad else self._out[..., : self.d]
 
-    def append(self, rows: Tensor, gather: bool = True) -> Tensor:
+    def append(self, rows: Tensor) -> Tensor:
         """Append rows (B, n, *row) and return the gathered (B, length, *row)."""
         n = rows.shape[1]
         if n:
@@ -99,10 +104,8 @@ class _PagedRows:
                 rows = torch.nn.functional.pad(rows, (0, self.d_pad - self.d))
             ops.reserve(self.free_stack, self.free_top, self.block_table, self.lens, n,
                         self.block_size, self.status)
-            if gather:
-                ops.append_gather(self.pool, self.block_table, self.lens, rows, n, self._out)
-            else:
-                ops.paged_append(self.pool, self.block_table, self.lens, rows, n)
+            ops.append_gather(self.pool, self.block_table, self.lens, rows, n, self._out,
+                              first_page=self.length // self.block_size)
             self.length += n
         return self.out[:, : self.length]
 
@@ -325,8 +328,10 @@ class _CompressedLayer:
                 ops.compress_append(stream.pool, stream.block_table, state, c, z,
                                     bias.detach().to(torch.float32).contiguous(), lens, n_fold)
             if n_complete > 0:
+                first_page = stream.length // stream.block_size  # the page of the first new entry
                 stream.length += n_complete
-                ops.paged_gather(stream.pool, stream.block_table, stream.lens, stream._out)
+                ops.paged_gather(stream.pool, stream.block_table, stream.lens, stream._out,
+                                 first_page=first_page)
 
     def reset(self) -> None:
         self._sw.reset()

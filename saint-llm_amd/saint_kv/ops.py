@@ -155,24 +155,46 @@ def _dst_args(out: torch.Tensor, rb: int, batch: int,
     return None, seq_stride_bytes // rb, cap
 
 
+def _from_page(block_table: torch.Tensor, seq_lens: torch.Tensor, out: torch.Tensor, bs: int,
+               first_page: int, row_offsets: torch.Tensor | None) -> tuple[int, torch.Tensor, torch.Tensor]:
+    """(table pointer, lengths, out view) that make a gather start at page
+    ``first_page`` of every sequence: the table row from that page on, the
+    lengths less its first row, and out from that row on."""
+    if first_page == 0:
+        return block_table.data_ptr(), seq_lens, out
+    if row_offsets is not None:
+        raise ValueError("first_page needs out as [batch, rows, *row], not packed rows")
+    if not 0 < first_page < block_table.shape[1]:
+        raise ValueError(f"first_page must be in [0, {block_table.shape[1]}); got {first_page}")
+    lens = torch.clamp(seq_lens - first_page * bs, min=0).to(torch.int32)
+    return block_table.data_ptr() + first_page * block_table.element_size(), lens, out[:, first_page * bs:]
+
+
 def paged_gather(pool: torch.Tensor, block_table: torch.Tensor, seq_lens: torch.Tensor,
-                 out: torch.Tensor, row_offsets: torch.Tensor | None = None) -> torch.Tensor:
-    """Copy rows ``[0, seq_lens[b])`` of every sequence, in order, into ``out``."""
+                 out: torch.Tensor, row_offsets: torch.Tensor | None = None,
+                 first_page: int = 0) -> torch.Tensor:
+    """Copy rows ``[0, seq_lens[b])`` of every sequence, in order, into ``out``.
+
+    With ``first_page`` > 0 only rows ``[first_page * block_size, seq_lens[b])``
+    are copied (to the same rows of ``out``); the rows before are left as they
+    are.  A caller that keeps ``out`` as a running copy of the cache refreshes
+    it this way in O(new rows) instead of O(length)."""
     n_pages, bs, rb = _check_pool(pool)
     _require_i32(block_table, "block_table")
     batch, bt_stride = block_table.shape
     _require_i32(seq_lens, "seq_lens", (batch,))
-    off_ptr, seq_rows, cap = _dst_args(out, rb, batch, row_offsets)
-    _lib.call("skv_paged_gather", out.data_ptr(), off_ptr, seq_rows, cap, pool.data_ptr(), rb, bs,
-              n_pages, block_table.data_ptr(), bt_stride, seq_lens.data_ptr(), batch,
-              _lib.stream_handle(pool.device))
+    bt_ptr, lens, out_v = _from_page(block_table, seq_lens, out, bs, first_page, row_offsets)
+    off_ptr, seq_rows, cap = _dst_args(out_v, rb, batch, row_offsets)
+    _lib.call("skv_paged_gather", out_v.data_ptr(), off_ptr, seq_rows, cap, pool.data_ptr(), rb, bs,
+              n_pages, bt_ptr, bt_stride, lens.data_ptr(), batch, _lib.stream_handle(pool.device))
     return out
 
 
 def append_gather(pool: torch.Tensor, block_table: torch.Tensor, seq_lens: torch.Tensor,
                   src: torch.Tensor, n_new: int | torch.Tensor, out: torch.Tensor,
-                  row_offsets: torch.Tensor | None = None) -> torch.Tensor:
-    """Fused decode step: append ``src`` rows to the pool and gather every sequence into ``out``."""
+                  row_offsets: torch.Tensor | None = None, first_page: int = 0) -> torch.Tensor:
+    """Fused decode step: append ``src`` rows to the pool and gather every sequence into ``out``
+    (from page ``first_page`` on, as in ``paged_gather``; the appended rows must lie there)."""
     n_pages, bs, rb = _check_pool(pool)
     _require_i32(block_table, "block_table")
     batch, bt_stride = block_table.shape
@@ -182,9 +204,10 @@ def append_gather(pool: torch.Tensor, block_table: torch.Tensor, seq_lens: torch
         raise ValueError(f"src batch {src.shape[0]} != block_table batch {batch}")
     s_seq, s_row = _row_view_strides(src, rb, "src")
     n_ptr, n_uni = _n_new_args(n_new, batch)
-    off_ptr, seq_rows, cap = _dst_args(out, rb, batch, row_offsets)
-    _lib.call("skv_append_gather", out.data_ptr(), off_ptr, seq_rows, cap, pool.data_ptr(), rb,
-              bs, n_pages, block_table.data_ptr(), bt_stride, seq_lens.data_ptr(), n_ptr, n_uni,
+    bt_ptr, lens, out_v = _from_page(block_table, seq_lens, out, bs, first_page, row_offsets)
+    off_ptr, seq_rows, cap = _dst_args(out_v, rb, batch, row_offsets)
+    _lib.call("skv_append_gather", out_v.data_ptr(), off_ptr, seq_rows, cap, pool.data_ptr(), rb,
+              bs, n_pages, bt_ptr, bt_stride, lens.data_ptr(), n_ptr, n_uni,
               src.data_ptr(), s_seq, s_row, src.shape[1], batch, _lib.stream_handle(pool.device))
     return out
 

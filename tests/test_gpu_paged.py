@@ -169,6 +169,53 @@ def test_append_spanning_pages_and_strided_source(dev) -> None:
         assert torch.equal(out[b, : s.r_lens[b]].cpu(), torch.cat(hist[b]))
 
 
+def test_gather_from_page(dev) -> None:
+    """paged_gather / append_gather with first_page: rows from page first_page
+    on equal the full gather's (oracle), rows before it are left untouched, and
+    the appended rows reach the pool as with a full gather.  Ragged lengths,
+    one sequence shorter than the first page's first row."""
+    g = torch.Generator().manual_seed(5)
+    rng = np.random.default_rng(5)
+    batch, bs, n_pages, max_pages = 4, 16, 64, 12
+    s = _State(dev, batch, n_pages, max_pages, bs, (64,), torch.bfloat16,
+               rng.permutation(n_pages).astype(np.int32))
+    r_pool = torch.zeros(n_pages, bs, 64, dtype=torch.bfloat16)
+    n0 = np.array([70, 33, 100, 40], dtype=np.int32)
+    src = torch.randn(batch, int(n0.max()), 64, generator=g).to(torch.bfloat16)
+    assert s.reserve(n0) == 0
+    s.ops.paged_append(s.pool, s.bt, s.lens, src.to(dev), torch.as_tensor(n0, device=dev))
+    ref.paged_append(r_pool, s.r_bt, s.r_lens, src, n0)
+    for first_page in (0, 1, 2, 6):
+        out = torch.full((batch, max_pages * bs, 64), 7.0, dtype=torch.bfloat16, device=dev)
+        s.ops.paged_gather(s.pool, s.bt, s.lens, out, first_page=first_page)
+        want = ref.paged_gather(r_pool, s.r_bt, s.r_lens, torch.zeros(batch, max_pages * bs, 64,
+                                                                       dtype=torch.bfloat16))
+        got = out.cpu()
+        lo = first_page * bs
+        for b in range(batch):
+            L = int(s.r_lens[b])
+            assert (got[b, :lo] == 7.0).all(), (first_page, b)
+            assert torch.equal(got[b, lo:L], want[b, lo:L]), (first_page, b)
+            assert (got[b, max(L, lo):] == 7.0).all(), (first_page, b)
+    # append 3 rows and refresh from the page of the first new row
+    new = torch.randn(batch, 3, 64, generator=g).to(torch.bfloat16)
+    out = torch.zeros(batch, max_pages * bs, 64, dtype=torch.bfloat16, device=dev)
+    s.ops.paged_gather(s.pool, s.bt, s.lens, out)
+    first_page = int(s.r_lens.min()) // bs
+    assert s.reserve(3) == 0
+    s.ops.append_gather(s.pool, s.bt, s.lens, new.to(dev), 3, out, first_page=first_page)
+    ref.paged_append(r_pool, s.r_bt, s.r_lens, new, 3)
+    s.check_tables()
+    assert torch.equal(s.pool.cpu(), r_pool)
+    want = ref.paged_gather(r_pool, s.r_bt, s.r_lens, torch.zeros(batch, max_pages * bs, 64, dtype=torch.bfloat16))
+    got = out.cpu()
+    for b in range(batch):
+        L = int(s.r_lens[b])
+        assert torch.equal(got[b, :L], want[b, :L]), b
+    with pytest.raises(ValueError, match="first_page"):
+        s.ops.paged_gather(s.pool, s.bt, s.lens, out, first_page=max_pages)
+
+
 def test_empty_batch_and_zero_lengths(dev) -> None:
     from saint_kv import ops
 
