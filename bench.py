@@ -358,7 +358,7 @@ def run_decode_leg(dev, name: str, specs, batch: int, lens0: np.ndarray, steps: 
         warm.release(np.array([True, False]))
         warm.compact()
         del warm
-        ws = torch.zeros(3 * max(g.n_pages for g in cache.groups), dtype=torch.int32, device=dev)
+        ws = torch.zeros(cache.compact_workspace_words(), dtype=torch.int32, device=dev)
         m_dev = torch.as_tensor(mask.astype(np.uint8), device=dev)
         torch.cuda.synchronize()
         # the release and compaction launches recorded in one HIP graph and

@@ -310,8 +310,8 @@ typedef struct skv_pool_ref {
  * n_live+1, ...  workspace: int32 [3*n_pages] whose first n_pages words are
  * zero before the first call and are left zero by every call (the rest is
  * scratch); info: int32 [2] receives {n_live, n_moved}.  Calls that share a
- * workspace must not overlap.  batch * bt_stride < 2^24.  No reference
- * counterpart. */
+ * workspace must not overlap.  n_pages < 2^24, batch * bt_stride < 2^24.  No
+ * reference counterpart. */
 int skv_compact(const skv_pool_ref* pools, int32_t n_pools, int32_t* block_table,
                 int64_t bt_stride, const int32_t* seq_lens, int64_t batch, int64_t block_size,
                 int64_t n_pages, int32_t* free_stack, int32_t* free_top, int32_t* workspace,

@@ -96,6 +96,18 @@ struct PoolRefs {
   int n;
 };
 
+// The plan runs one workgroup per block of kPlanSpan page ids.  A count
+// launch before it writes the live pages of every block (counts: the last
+// n_blocks words of the workspace, which the movers' list never reaches:
+// n_moved <= n / 2), so that each plan workgroup knows how many live pages
+// precede its block without waiting for another workgroup.
+constexpr int kPlanPer = 4;                          // ids per thread: one 16-byte load of marks
+constexpr int kPlanShift = 12;
+constexpr int kPlanSpan = 1 << kPlanShift;           // ids per plan workgroup
+static_assert(kPlanSpan == kEvictThreads * kPlanPer, "a plan workgroup covers its block in one pass");
+
+__host__ __device__ __forceinline__ int64_t plan_blocks(int64_t n) { return (n + kPlanSpan - 1) >> kPlanShift; }
+
 // grid: (ceil(bt_stride / 256), batch)
 __global__ void k_mark_live(const int32_t* __restrict__ bt, int64_t bt_stride,
                             const int32_t* __restrict__ lens, int bs, int64_t n_pages,
@@ -108,100 +120,112 @@ __global__ void k_mark_live(const int32_t* __restrict__ bt, int64_t bt_stride,
   if (p >= 0 && p < n_pages) mark[p] = 1;
 }
 
-// One workgroup: n_live, hole and mover lists, remap, new free stack.
-// ws: [0, n) mark -> remap, [n, 2n) holes, [2n, 3n) movers.  info = {n_live, n_moved}.
-// The marks below n_live are cleared here and the remap of ids at or above
-// n_live holds a mover's hole (cleared by the rewrite that reads it) or 0, so
-// words [0, n) are zero again after the compaction.
-// Each thread takes kPlanRun consecutive ids per pass (four 16-byte loads of
-// the marks), so a pass costs one block scan per kEvictThreads * kPlanRun ids.
-constexpr int kPlanRun = 16;
-
-// The marks of ids [i0, i0 + kPlanRun) (0 past n).
+// The marks of ids [i0, i0 + kPlanPer) (0 past n).
 __device__ __forceinline__ void load_run(const int32_t* mark, int64_t i0, int64_t n, int* v) {
-  if (i0 + kPlanRun <= n) {  // whole run in range: 16-byte loads (i0 is a multiple of 16)
-#pragma unroll
-    for (int q = 0; q < kPlanRun / 4; ++q) {
-      const int4 w = reinterpret_cast<const int4*>(mark + i0)[q];
-      v[4 * q] = w.x;
-      v[4 * q + 1] = w.y;
-      v[4 * q + 2] = w.z;
-      v[4 * q + 3] = w.w;
-    }
+  if (i0 + kPlanPer <= n) {  // whole run in range: one 16-byte load (i0 is a multiple of 4)
+    const int4 w = *reinterpret_cast<const int4*>(mark + i0);
+    v[0] = w.x;
+    v[1] = w.y;
+    v[2] = w.z;
+    v[3] = w.w;
   } else {
 #pragma unroll
-    for (int k = 0; k < kPlanRun; ++k) v[k] = (i0 + k < n) ? mark[i0 + k] : 0;
+    for (int k = 0; k < kPlanPer; ++k) v[k] = (i0 + k < n) ? mark[i0 + k] : 0;
   }
 }
 
+// Workgroup g writes the live pages of ids [g * kPlanSpan, (g + 1) * kPlanSpan).
+__global__ __launch_bounds__(kEvictThreads) void k_count_live(const int32_t* __restrict__ mark, int64_t n,
+                                                              int32_t* __restrict__ counts) {
+  __shared__ int scan_lds[17];
+  const int64_t i0 = static_cast<int64_t>(blockIdx.x) * kPlanSpan + static_cast<int64_t>(threadIdx.x) * kPlanPer;
+  int v[kPlanPer];
+  load_run(mark, i0, n, v);
+  int c = 0;
+#pragma unroll
+  for (int k = 0; k < kPlanPer; ++k) c += (v[k] != 0) ? 1 : 0;
+  c = block_reduce_sum(c, scan_lds);
+  if (threadIdx.x == 0) counts[blockIdx.x] = c;
+}
+
+// Workgroup g: ids [g * kPlanSpan, (g + 1) * kPlanSpan).
+// ws: [0, n) marks -> movers' ranks, [n, 2n) holes, [2n, 3n) movers; counts
+// as above.  A hole's rank is the number of holes before it (its id less the
+// live pages before it); a mover's rank is the number of live pages in
+// [n_live, id), i.e. the live pages before it less those before n_live.
+// A mover's mark becomes its rank, which the copy launch's table rewrite
+// reads and clears; the copy launch also clears the marks below n_live (other
+// plan workgroups read them here), so words [0, n) are zero again after the
+// compaction.  The free stack is rebuilt so that pops return
+// n_live, n_live + 1, ...; info = {n_live, n_moved} (workgroup 0).
 __global__ __launch_bounds__(kEvictThreads) void k_compact_plan(int32_t* __restrict__ ws, int64_t n,
                                                                 int32_t* __restrict__ stack,
                                                                 int32_t* __restrict__ top_ptr,
                                                                 int32_t* __restrict__ info) {
   __shared__ int scan_lds[17];
   const int tid = threadIdx.x;
+  const int g = blockIdx.x;
+  const int n_blocks = static_cast<int>(plan_blocks(n));
   int32_t* mark = ws;
   int32_t* holes = ws + n;
   int32_t* movers = ws + 2 * n;
-  constexpr int64_t kSpan = static_cast<int64_t>(kEvictThreads) * kPlanRun;
-  int v[kPlanRun];
-  int64_t n_live = 0;
-  for (int64_t base = 0; base < n; base += kSpan) {
-    const int64_t i0 = base + static_cast<int64_t>(tid) * kPlanRun;
-    load_run(mark, i0, n, v);
-    int c = 0;
+  const int32_t* counts = ws + 3 * n - n_blocks;
+  // every load of the first round trip: the block counts and this block's marks
+  constexpr int kCntPer = (1 << 24) / kPlanSpan / kEvictThreads;  // n < 2^24 pages
+  int cnt[kCntPer];
 #pragma unroll
-    for (int k = 0; k < kPlanRun; ++k) c += v[k] != 0 ? 1 : 0;
-    n_live += block_reduce_sum(c, scan_lds);
+  for (int k = 0; k < kCntPer; ++k) {
+    const int i = tid + k * kEvictThreads;
+    cnt[k] = (i < n_blocks) ? counts[i] : 0;
   }
-  // holes: the free ids below n_live, ranked in ascending order
-  int carry = 0;
-  for (int64_t base = 0; base < n_live; base += kSpan) {
-    const int64_t i0 = base + static_cast<int64_t>(tid) * kPlanRun;
-    load_run(mark, i0, n_live, v);
-    int c = 0;
+  const int64_t i0 = static_cast<int64_t>(g) * kPlanSpan + static_cast<int64_t>(tid) * kPlanPer;
+  int v[kPlanPer];
+  load_run(mark, i0, n, v);
+  int total = 0, before = 0;
 #pragma unroll
-    for (int k = 0; k < kPlanRun; ++k) c += (i0 + k < n_live && v[k] == 0) ? 1 : 0;
-    int tot;
-    int r = carry + block_exclusive_scan(c, scan_lds, &tot);
-#pragma unroll
-    for (int k = 0; k < kPlanRun; ++k) {
-      if (i0 + k >= n_live) break;
-      if (v[k] == 0) holes[r++] = static_cast<int32_t>(i0 + k);
-      else mark[i0 + k] = 0;
-    }
-    carry += tot;
+  for (int k = 0; k < kCntPer; ++k) {
+    total += cnt[k];
+    before += (tid + k * kEvictThreads < g) ? cnt[k] : 0;
   }
-  __syncthreads();  // holes[] complete before the movers read it
-  const int n_moved = carry;
-  // movers: the live ids at or above n_live, ranked; their remap is the hole
-  // of the same rank, other ids there remap to -1
-  carry = 0;
-  for (int64_t base = n_live; base < n; base += kSpan) {
-    const int64_t i0 = base + static_cast<int64_t>(tid) * kPlanRun;
-    int c = 0;
+  const int64_t n_live = block_reduce_sum(total, scan_lds);
+  before = block_reduce_sum(before, scan_lds);
+  // live pages before n_live: the blocks before its block, then that block up to n_live
+  const int gs = static_cast<int>(n_live >> kPlanShift);
+  int pre = 0;
 #pragma unroll
-    for (int k = 0; k < kPlanRun; ++k) {
-      v[k] = (i0 + k < n) ? mark[i0 + k] : 0;  // n_live need not be a multiple of 16
-      c += v[k] != 0 ? 1 : 0;
-    }
-    int tot;
-    int r = carry + block_exclusive_scan(c, scan_lds, &tot);
+  for (int k = 0; k < kCntPer; ++k) pre += (tid + k * kEvictThreads < gs) ? cnt[k] : 0;
+  int w[kPlanPer];
+  const int64_t j0 = static_cast<int64_t>(gs) * kPlanSpan + static_cast<int64_t>(tid) * kPlanPer;
+  load_run(mark, j0, n_live, w);
 #pragma unroll
-    for (int k = 0; k < kPlanRun; ++k) {
-      if (i0 + k >= n) break;
-      if (v[k] != 0) {  // other ids keep mark 0 (their remap is never read)
-        mark[i0 + k] = holes[r];
-        movers[r] = static_cast<int32_t>(i0 + k);
-        ++r;
+  for (int k = 0; k < kPlanPer; ++k) pre += (w[k] != 0) ? 1 : 0;
+  const int live_below = block_reduce_sum(pre, scan_lds);  // live pages with id < n_live
+  const int n_moved = static_cast<int>(n_live) - live_below;
+  // this block's ids
+  int c = 0;
+#pragma unroll
+  for (int k = 0; k < kPlanPer; ++k) c += (v[k] != 0) ? 1 : 0;
+  int tot;
+  int lb = before + block_exclusive_scan(c, scan_lds, &tot);  // live pages before id i0
+#pragma unroll
+  for (int k = 0; k < kPlanPer; ++k) {
+    const int64_t i = i0 + k;
+    if (i >= n) break;
+    const bool live = v[k] != 0;
+    if (i < n_live) {
+      if (!live) holes[i - lb] = static_cast<int32_t>(i);
+    } else {
+      if (live) {
+        const int r = lb - live_below;
+        movers[r] = static_cast<int32_t>(i);
+        mark[i] = r;
       }
+      stack[n - 1 - i] = static_cast<int32_t>(i);
     }
-    carry += tot;
+    lb += live ? 1 : 0;
   }
-  const int64_t n_free = n - n_live;
-  for (int64_t i = tid; i < n_free; i += kEvictThreads) stack[i] = static_cast<int32_t>(n - 1 - i);
-  if (tid == 0) {
-    *top_ptr = static_cast<int32_t>(n_free);
+  if (g == 0 && tid == 0) {
+    *top_ptr = static_cast<int32_t>(n - n_live);
     info[0] = static_cast<int32_t>(n_live);
     info[1] = n_moved;
   }
@@ -219,10 +243,12 @@ struct CopySlices {
 };
 
 // Persistent grid over 4 KB slices of (mover, pool) pages.  A workgroup takes
-// kCopySlices slices per iteration: one round trip for their hole / mover
-// ids, one for their data (all loads issued before any store).
-// The same grid first rewrites the block tables: every table entry of a
-// live page at or above n_live takes its remap, which it then clears.
+// kCopySlices slices per iteration, all loads issued before any store; the
+// hole / mover ids of its next iteration are loaded before this iteration's
+// stores, so only the first iteration waits for them.  The same grid first
+// rewrites the block tables (every table entry of a live page at or above
+// n_live takes the hole of its rank, which it then clears) and clears the
+// plan's marks below n_live.
 struct TableRef {
   int32_t* bt;
   const int32_t* lens;
@@ -230,6 +256,17 @@ struct TableRef {
   int32_t batch;
   int32_t block_size;
 };
+
+__device__ __forceinline__ void slice_ids(const CopySlices& cs, const int32_t* movers, const int32_t* holes,
+                                          int s0, int total, int32_t* src_id, int32_t* dst_id) {
+#pragma unroll
+  for (int k = 0; k < kCopySlices; ++k) {
+    const int s = min(s0 + k, total - 1);
+    const int r = static_cast<int>(udiv24(s, cs.per_mover));
+    src_id[k] = movers[r];
+    dst_id[k] = holes[r];
+  }
+}
 
 __global__ __launch_bounds__(kCompactCopyThreads) void k_compact_copy(PoolRefs pools, CopySlices cs, TableRef tr,
                                                                      int32_t* __restrict__ ws, int64_t n,
@@ -241,21 +278,26 @@ __global__ __launch_bounds__(kCompactCopyThreads) void k_compact_copy(PoolRefs p
   const int32_t* movers = ws + 2 * n;
   const int total = n_moved * cs.per_mover;  // < 2^24 (checked on the host)
   const int tid = threadIdx.x;
+  const int gtid = blockIdx.x * kCompactCopyThreads + tid;
+  const int gsize = gridDim.x * kCompactCopyThreads;
+  int s0 = blockIdx.x * kCopySlices;
+  int32_t src_id[kCopySlices], dst_id[kCopySlices];
+  if (s0 < total) slice_ids(cs, movers, holes, s0, total, src_id, dst_id);  // in flight during the rewrite
   const int entries = tr.batch * tr.bt_stride;  // < 2^24 (checked on the host)
-  for (int t = blockIdx.x * kCompactCopyThreads + tid; t < entries; t += gridDim.x * kCompactCopyThreads) {
+  for (int t = gtid; t < entries; t += gsize) {
     const int b = static_cast<int>(udiv24(t, tr.bt_stride));
     const int j = t - b * tr.bt_stride;
     const int np = static_cast<int>(min<int64_t>(ceil_div24(max(tr.lens[b], 0), tr.block_size), tr.bt_stride));
     if (j < np) {
       const int32_t p = tr.bt[t];
       if (p >= n_live && p < n) {
-        tr.bt[t] = remap[p];
+        tr.bt[t] = holes[remap[p]];
         remap[p] = 0;
       }
     }
   }
-  for (int s0 = blockIdx.x * kCopySlices; s0 < total; s0 += gridDim.x * kCopySlices) {
-    int32_t src_id[kCopySlices], dst_id[kCopySlices];
+  for (int i = gtid; i < n_live; i += gsize) remap[i] = 0;
+  for (; s0 < total; s0 += gridDim.x * kCopySlices) {
     int q_of[kCopySlices], off[kCopySlices];
 #pragma unroll
     for (int k = 0; k < kCopySlices; ++k) {
@@ -266,8 +308,6 @@ __global__ __launch_bounds__(kCompactCopyThreads) void k_compact_copy(PoolRefs p
       for (int qq = 1; qq < pools.n; ++qq) q += (j >= cs.first[qq]) ? 1 : 0;
       q_of[k] = q;
       off[k] = (j - cs.first[q]) * kCopySlice + tid * 16;
-      src_id[k] = movers[r];
-      dst_id[k] = holes[r];
     }
     u32x4 v[kCopySlices];
 #pragma unroll
@@ -277,6 +317,9 @@ __global__ __launch_bounds__(kCompactCopyThreads) void k_compact_copy(PoolRefs p
       const uint8_t* src = pools.base[q_of[k]] + static_cast<int64_t>(src_id[k]) * pb + (live ? off[k] : 0);
       v[k] = ld_stream(reinterpret_cast<const u32x4*>(src));
     }
+    int32_t next_src[kCopySlices], next_dst[kCopySlices];
+    const int s1 = s0 + gridDim.x * kCopySlices;
+    if (s1 < total) slice_ids(cs, movers, holes, s1, total, next_src, next_dst);
 #pragma unroll
     for (int k = 0; k < kCopySlices; ++k) {
       const int64_t pb = pools.page_bytes[q_of[k]];
@@ -284,6 +327,11 @@ __global__ __launch_bounds__(kCompactCopyThreads) void k_compact_copy(PoolRefs p
         st_stream(reinterpret_cast<u32x4*>(pools.base[q_of[k]] + static_cast<int64_t>(dst_id[k]) * pb + off[k]),
                   v[k]);
       }
+    }
+#pragma unroll
+    for (int k = 0; k < kCopySlices; ++k) {
+      src_id[k] = next_src[k];
+      dst_id[k] = next_dst[k];
     }
   }
 }
@@ -338,7 +386,7 @@ extern "C" int skv_compact(const skv_pool_ref* pools, int32_t n_pools, int32_t* 
     refs.page_bytes[q] = pools[q].page_bytes;
     slices_per_mover += ceil_div(pools[q].page_bytes, kCopySlice);
   }
-  if (n_pages * slices_per_mover >= (1 << 24)) {
+  if (n_pages >= (1 << 24) || n_pages * slices_per_mover >= (1 << 24)) {
     return set_error(SKV_EINVAL, "%s: n_pages x 4 KB slices per page must stay below 2^24", what);
   }
   if (batch * bt_stride >= (1 << 24)) {
@@ -352,7 +400,11 @@ extern "C" int skv_compact(const skv_pool_ref* pools, int32_t n_pools, int32_t* 
                        static_cast<int>(block_size), n_pages, workspace);
     if ((rc = check_launch(what))) return rc;
   }
-  hipLaunchKernelGGL(k_compact_plan, dim3(1), dim3(kEvictThreads), 0, s, workspace, n_pages,
+  const dim3 pgrid(static_cast<unsigned>(plan_blocks(n_pages)));
+  hipLaunchKernelGGL(k_count_live, pgrid, dim3(kEvictThreads), 0, s, workspace, n_pages,
+                     workspace + 3 * n_pages - plan_blocks(n_pages));
+  if ((rc = check_launch(what))) return rc;
+  hipLaunchKernelGGL(k_compact_plan, pgrid, dim3(kEvictThreads), 0, s, workspace, n_pages,
                      free_stack, free_top, info);
   if ((rc = check_launch(what))) return rc;
   CopySlices cs{};

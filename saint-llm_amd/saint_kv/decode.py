@@ -181,10 +181,10 @@ class DecodeCache:
                 m=m, n_pages=n_pages, free_stack=stack, free_top=top,
                 block_table=torch.full((batch, bt_stride), -1, dtype=torch.int32, device=dev),
                 n_entries=torch.zeros(batch, dtype=torch.int32, device=dev)))
-        # compaction buffers: zeroed once, the compaction leaves the marks zero
+        # compaction buffers: zeroed once; each page group has its own slice of
+        # the workspace, whose page marks the compaction leaves zero
         self._compact_info = torch.zeros(max(len(self.groups), 1), 2, dtype=torch.int32, device=dev)
-        self._compact_ws = torch.zeros(3 * max([g.n_pages for g in self.groups] + [1]), dtype=torch.int32,
-                                       device=dev)
+        self._compact_ws = torch.zeros(max(self.compact_workspace_words(), 1), dtype=torch.int32, device=dev)
 
         bf = torch.bfloat16
         self.ring, self.pool, self.state, self.bias = [], [], [], []
@@ -531,15 +531,24 @@ class DecodeCache:
             raise RuntimeError("DecodeCache release refused (" + "; ".join(
                 f"group m={g.m}: status bits {b}" for g, b in zip(self.groups, bad) if b) + ")")
 
+    def compact_workspace_words(self) -> int:
+        """int32 words of the compaction workspace: 3 * n_pages per page group."""
+        return sum(3 * g.n_pages for g in self.groups)
+
     def compact(self, workspace: torch.Tensor | None = None, sync: bool = True):
         """Defragment every page group; returns [(n_live, n_moved)] per group.
 
         With ``sync=False`` nothing waits for the device: the result is an
         int32 device tensor [n_groups, 2] holding the same pairs (reused by the
-        next call).  A caller's ``workspace`` must hold 3 * n_pages int32 of
-        the largest group, its first words zero before the first use (the
-        compaction leaves them zero)."""
+        next call).  A caller's ``workspace`` must hold
+        ``compact_workspace_words()`` int32, zero before its first use; group g
+        uses its own slice (3 * n_pages words), whose first n_pages words (the
+        page marks) every compaction leaves zero."""
         info = self._compact_info
+        ws_all = workspace if workspace is not None else self._compact_ws
+        if ws_all.numel() < self.compact_workspace_words():
+            raise ValueError(f"compaction workspace needs {self.compact_workspace_words()} int32")
+        ws_off = 0
         for gi, g in enumerate(self.groups):
             pools = []
             for i, spec in enumerate(self.layers):
@@ -547,11 +556,10 @@ class DecodeCache:
                     pools.append(self.pool[i])
                     if self.idx_pool[i] is not None:
                         pools.append(self.idx_pool[i])
-            ws = workspace if workspace is not None else self._compact_ws
-            if ws.numel() < 3 * g.n_pages:
-                raise ValueError(f"compaction workspace needs {3 * g.n_pages} int32")
+            ws = ws_all[ws_off: ws_off + 3 * g.n_pages]
+            ws_off += 3 * g.n_pages
             ops.compact(pools, g.block_table, g.n_entries, self.block_size, g.free_stack,
-                        g.free_top, ws[: 3 * g.n_pages], info[gi])
+                        g.free_top, ws, info[gi])
         if not sync:
             return info
         return [tuple(int(v) for v in row) for row in info.cpu()]

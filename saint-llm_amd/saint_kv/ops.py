@@ -614,7 +614,7 @@ def compact(pools: list[torch.Tensor], block_table: torch.Tensor, seq_lens: torc
     """Defragment ``pools`` (sharing ``block_table``) so live pages occupy [0, n_live).
 
     ``workspace`` (int32 [3 * n_pages]): its first n_pages words must be zero
-    before the first call; every call leaves them zero.
+    before the first call; every call leaves them zero (the rest is scratch).
     """
     n_pages = free_stack.numel()
     refs = (_lib.PoolRef * len(pools))()

@@ -494,10 +494,12 @@ def test_release_and_compact(dev) -> None:
 
 
 def test_release_and_compact_multi_pass_plan(dev) -> None:
-    """Compaction of a 40,000-page pool: the planner ranks holes and movers in
-    passes of 16,384 page ids, carrying its counts from pass to pass; n_live is
-    not a multiple of 16 and the movers and holes span all three passes.
-    Tables, stack, counts and page contents equal the oracle's."""
+    """Compaction of a 40,000-page pool: ten plan workgroups of 4096 page ids
+    each rank their block's holes and movers from the live-page counts of the
+    blocks before theirs; n_live is not a multiple of 16 and lies inside a
+    block, and the movers and holes span many blocks.  Tables, stack, counts
+    and page contents equal the oracle's, and the workspace's marks are zero
+    again afterwards."""
     from saint_kv import ops
 
     rng = np.random.default_rng(40)
@@ -533,12 +535,14 @@ def test_release_and_compact_multi_pass_plan(dev) -> None:
     # reach into every 16,384-id pass
     assert n_live % 16 and n_live > 16384
     assert movers.max() >= 32768 and holes.min() < 16384 and holes.max() >= 16384
+    assert n_live % 4096  # inside a plan block
     ws = torch.zeros(3 * n_pages, dtype=torch.int32, device=dev)
     info = torch.zeros(2, dtype=torch.int32, device=dev)
     ops.compact(pools, bt, lens, bs, stack, top, ws, info)
     r_stack, r_top, moved = ref.compact(r_pools, r_bt, r_lens, bs)
     torch.cuda.synchronize()
     assert int(status.item()) == 0
+    assert not _np(ws)[:n_pages].any()
     assert _np(info).tolist() == [n_live, moved] and moved == len(movers)
     assert np.array_equal(_np(bt), r_bt) and np.array_equal(_np(lens), r_lens)
     assert int(top.item()) == r_top and np.array_equal(_np(stack)[:r_top], r_stack[:r_top])

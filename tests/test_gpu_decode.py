@@ -297,6 +297,68 @@ def _check_csa_outputs(cache, i, scores, ctx):
     assert torch.equal(cache.out_entries[i].cpu(), exp_out), ctx
 
 
+def test_decode_compactions_with_groups_of_growing_size(dev) -> None:
+    """Two page groups, the first compacted (m=4) smaller than the second
+    (m=128, given a larger pool), and two release + compaction rounds: each
+    group compacts in its own slice of the workspace, so the larger group never
+    reads the smaller one's scratch as marks or block counts.  Tables, free
+    stacks and entries equal the oracle's replay of release / compact on the
+    same tables."""
+    from saint_kv.decode import DecodeCache, LayerSpec
+
+    specs = [LayerSpec("hca", m=128), LayerSpec("csa", m=4, top_k=16)]
+    B, max_len, bs = 6, 8192, 16
+    cache = DecodeCache(specs, B, max_len, block_size=bs, window=16, device=dev, page_order_seed=4,
+                        pages_per_group={128: 2000})
+    assert cache.groups[0].n_pages < cache.groups[1].n_pages
+    pool_of = {cache.group_of_rate[sp.m]: cache.pool[i] for i, sp in enumerate(specs)}
+    gen = torch.Generator(device=dev).manual_seed(4)
+    rng = np.random.default_rng(4)
+    cache.prefill(rng.integers(500, 8000, size=B), generator=gen)
+    views = {}
+
+    def entries(g, b):
+        e = int(g.n_entries[b])
+        return ref.paged_gather(pool_of[cache.groups.index(g)].cpu(), _np(g.block_table)[b:b + 1],
+                                _np(g.n_entries)[b:b + 1], torch.zeros(1, max(e, 1), 576, dtype=torch.bfloat16))[0, :e]
+
+    for rnd, fin in enumerate(([0, 3], [2])):
+        mask = np.zeros(B, dtype=bool)
+        mask[fin] = True
+        r_tabs = []
+        for g in cache.groups:
+            r_bt, r_ent = _np(g.block_table).copy(), _np(g.n_entries).copy()
+            r_stack, r_top = _np(g.free_stack).copy(), int(g.free_top.item())
+            st, r_top = ref.release(r_stack, r_top, r_bt, r_ent, mask.astype(np.uint8), bs)
+            assert st == 0
+            r_tabs.append((r_bt, r_ent))
+        for b in range(B):
+            if not mask[b] and cache.host_lens[b]:
+                views[b] = [entries(g, b) for g in cache.groups]
+        cache.release(mask)
+        info = cache.compact()
+        for gi, g in enumerate(cache.groups):
+            r_bt, r_ent = r_tabs[gi]
+            pools = [torch.zeros(g.n_pages, 1, 1, dtype=torch.uint8)]
+            r_stack2, r_top2, moved = ref.compact(pools, r_bt, r_ent, bs)
+            assert info[gi][1] == moved, (rnd, gi)
+            assert np.array_equal(_np(g.block_table), r_bt), (rnd, gi)
+            assert int(g.free_top.item()) == r_top2
+            assert np.array_equal(_np(g.free_stack)[:r_top2], r_stack2[:r_top2])
+        for b, vs in views.items():
+            if mask[b] or not cache.host_lens[b]:
+                continue
+            for g, v in zip(cache.groups, vs):
+                assert torch.equal(entries(g, b), v), (rnd, b)
+        off = 0
+        for g in cache.groups:  # the marks of every group's slice are zero again
+            assert not _np(cache._compact_ws[off: off + g.n_pages]).any()
+            off += 3 * g.n_pages
+        views = {}
+        cache.step()
+        cache.check_status()
+
+
 def test_decode_scores_from_cached_indexer_keys(dev) -> None:
     """The indexer scores of each step computed on the GPU from the cache's own
     paged indexer keys (ops.indexer_scores) match the oracle, and the step
