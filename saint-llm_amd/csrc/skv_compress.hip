@@ -54,9 +54,16 @@ __device__ __forceinline__ void fold_tokens(PoolState& st, const CompressArgs& a
                                             int64_t p0, int64_t p1, int lane, int groups) {
   for (int64_t p = p0; p < p1; ++p) {
     const int64_t i = p - first_new;
-    const uint16_t* crow = reinterpret_cast<const uint16_t*>(a.c_new + b * a.in_seq_stride + i * a.in_row_stride);
-    const uint16_t* zrow = reinterpret_cast<const uint16_t*>(a.z_new + b * a.in_seq_stride + i * a.in_row_stride);
-    state_update(st, crow, zrow, a.bias + (p % a.m) * a.channels, lane, groups);
+    const uint8_t* crow = a.c_new + b * a.in_seq_stride + i * a.in_row_stride;
+    const uint8_t* zrow = a.z_new + b * a.in_seq_stride + i * a.in_row_stride;
+    const float* brow = a.bias + (p % a.m) * a.channels;
+    if (a.format == SKV_FMT_F32) {  // uniform: fp32 rows
+      state_update(st, reinterpret_cast<const float*>(crow), reinterpret_cast<const float*>(zrow), brow, lane,
+                   groups);
+    } else {
+      state_update(st, reinterpret_cast<const uint16_t*>(crow), reinterpret_cast<const uint16_t*>(zrow), brow,
+                   lane, groups);
+    }
   }
 }
 
@@ -130,11 +137,12 @@ extern "C" int skv_compress_append(void* pool, int64_t entry_bytes, int64_t bloc
   if (block_size <= 0 || bt_stride <= 0 || batch < 0 || batch > 65535) {
     return set_error(SKV_EINVAL, "%s: bad block_size/bt_stride/batch", what);
   }
-  const int fp8_main = entry_layout(format, channels, entry_bytes);
+  const int fp8_main = (format == SKV_FMT_F32) ? ((entry_bytes == channels * 4) ? 0 : -1)
+                                               : entry_layout(format, channels, entry_bytes);
   if (fp8_main < 0) {
     return set_error(SKV_EINVAL,
                      "%s: entry_bytes %lld does not match format %d with %lld channels (bf16: 2*channels; "
-                     "fp8: channels = 128*q + %d, entry_bytes = %lld)",
+                     "fp32: 4*channels; fp8: channels = 128*q + %d, entry_bytes = %lld)",
                      what, (long long)entry_bytes, format, (long long)channels, SKV_FP8_ROPE_DIMS,
                      (long long)SKV_FP8_ENTRY_BYTES(channels));
   }

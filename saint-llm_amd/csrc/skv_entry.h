@@ -2,6 +2,8 @@
 // channels (groups lane, lane+64, ...) as fp32 already rounded to bf16.
 //
 // bf16 format : the 2*channels bytes of the entry are the bf16 values.
+// fp32 format : the 4*channels bytes of the entry are the fp32 values (the
+//               values are not rounded).
 // fp8 format  : [main e4m3fn codes][main/128 fp32 scales][rope bf16], with
 //               main = channels - SKV_FP8_ROPE_DIMS; each 128-channel block is
 //               16 lanes of the wave.  scale = max(amax / 448, FLT_MIN),
@@ -34,6 +36,19 @@ __device__ __forceinline__ void unpack8_bf16(u32x4 v, float* f) {
 // take part in no shuffle group that matters and store nothing.
 __device__ __forceinline__ void store_entry_group(uint8_t* entry, const float* v, int grp,
                                                   int groups, int format, int fp8_main) {
+  if (format == SKV_FMT_F32) {
+    if (grp < groups) {
+      u32x4 lo, hi;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        lo[j] = __float_as_uint(v[j]);
+        hi[j] = __float_as_uint(v[j + 4]);
+      }
+      *reinterpret_cast<u32x4*>(entry + grp * 32) = lo;
+      *reinterpret_cast<u32x4*>(entry + grp * 32 + 16) = hi;
+    }
+    return;
+  }
   if (format == SKV_FMT_BF16) {
     if (grp < groups) *reinterpret_cast<u32x4*>(entry + grp * 16) = pack8_bf16(v);
     return;

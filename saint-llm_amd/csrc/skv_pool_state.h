@@ -59,17 +59,32 @@ __device__ __forceinline__ void state_store(const PoolState& st, float* base, in
   }
 }
 
-// Fold token (c, z) rows with bias row `brow` into the running state:
-// online softmax over the tokens of the block, per channel.
-__device__ __forceinline__ void state_update(PoolState& st, const uint16_t* crow, const uint16_t* zrow,
+// The 8 channels of group grp of a bf16 (uint16_t) or fp32 token row.
+__device__ __forceinline__ void load8(const uint16_t* row, int grp, float* f) {
+  unpack8_bf16(*reinterpret_cast<const u32x4*>(row + grp * 8), f);
+}
+__device__ __forceinline__ void load8(const float* row, int grp, float* f) {
+  const u32x4 lo = *reinterpret_cast<const u32x4*>(row + grp * 8);
+  const u32x4 hi = *reinterpret_cast<const u32x4*>(row + grp * 8 + 4);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    f[j] = __uint_as_float(lo[j]);
+    f[j + 4] = __uint_as_float(hi[j]);
+  }
+}
+
+// Fold token (c, z) rows (bf16 or fp32) with bias row `brow` into the running
+// state: online softmax over the tokens of the block, per channel.
+template <class Row>
+__device__ __forceinline__ void state_update(PoolState& st, const Row* crow, const Row* zrow,
                                              const float* brow, int lane, int groups) {
 #pragma unroll
   for (int g = 0; g < kMaxGroups; ++g) {
     const int grp = lane + g * kPoolWave;
     if (grp >= groups) break;
     float c[8], z[8];
-    unpack8_bf16(*reinterpret_cast<const u32x4*>(crow + grp * 8), c);
-    unpack8_bf16(*reinterpret_cast<const u32x4*>(zrow + grp * 8), z);
+    load8(crow, grp, c);
+    load8(zrow, grp, z);
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       const float v = z[j] + brow[grp * 8 + j];
@@ -87,7 +102,8 @@ __device__ __forceinline__ void state_update(PoolState& st, const uint16_t* crow
   }
 }
 
-// Write acc/sum (rounded to bf16) as one entry; see store_entry_group.
+// Write acc/sum (rounded to bf16, except for fp32 entries) as one entry; see
+// store_entry_group.
 __device__ __forceinline__ void state_emit_entry(const PoolState& st, uint8_t* entry, int lane, int groups,
                                                  int format, int fp8_main) {
 #pragma unroll
@@ -97,8 +113,10 @@ __device__ __forceinline__ void state_emit_entry(const PoolState& st, uint8_t* e
     float out[8];
 #pragma unroll
     for (int j = 0; j < 8; ++j) out[j] = (grp < groups) ? st.acc[g][j] / st.sum[g][j] : 0.f;
+    if (format != SKV_FMT_F32) {
 #pragma unroll
-    for (int j = 0; j < 8; j += 2) bf16_round2(out[j], out[j + 1]);  // the compressor emits bf16 entries
+      for (int j = 0; j < 8; j += 2) bf16_round2(out[j], out[j + 1]);  // a bf16 compressor's entries
+    }
     store_entry_group(entry, out, grp, groups, format, fp8_main);
   }
 }

@@ -89,6 +89,7 @@ SIGNATURES: dict[str, list] = {
 # Entry formats and the FP8 entry layout (include/saintkv.h).
 SKV_FMT_BF16 = 0
 SKV_FMT_FP8 = 1
+SKV_FMT_F32 = 2  # fp32 entries from fp32 c/z rows (skv_compress_append only)
 SKV_FP8_ROPE_DIMS = 64
 
 

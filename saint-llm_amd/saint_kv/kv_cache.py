@@ -296,8 +296,10 @@ class _CompressedLayer:
         return [*compressed, sw[:, :, 0], sw[:, :, 1]]
 
     def _fast_path(self, compressors: list) -> list | None:
-        """The streams' (w_kv, w_z, bias) when every compressor takes the fast path."""
-        if self.dtype != torch.bfloat16:
+        """The streams' (w_kv, w_z, bias) when every compressor takes the fast path
+        (bf16 caches keep bf16 entries; fp32 caches, the reference's default,
+        keep unrounded fp32 entries)."""
+        if self.dtype not in (torch.bfloat16, torch.float32):
             return None
         out = []
         for comp, stream in zip(compressors, self._streams, strict=True):
@@ -323,8 +325,8 @@ class _CompressedLayer:
             if n_fold > 0:
                 hh = h.to(bias.dtype)  # the module's own dtype, as its forward sees it
                 with torch.no_grad():  # the kernel consumes raw buffers; no autograd graph
-                    c = w_kv(hh).to(torch.bfloat16).contiguous()
-                    z = w_z(hh).to(torch.bfloat16).contiguous()
+                    c = w_kv(hh).to(self.dtype).contiguous()
+                    z = w_z(hh).to(self.dtype).contiguous()
                 ops.compress_append(stream.pool, stream.block_table, state, c, z,
                                     bias.detach().to(torch.float32).contiguous(), lens, n_fold)
             if n_complete > 0:

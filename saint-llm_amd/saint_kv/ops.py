@@ -373,25 +373,31 @@ def compress_append(pool: torch.Tensor, block_table: torch.Tensor, tail_state: t
                     seq_lens: torch.Tensor, n_new: int | torch.Tensor) -> int:
     """Pool every block of m tokens completed by this append into the paged cache.
 
-    ``pool`` is bf16 [n_pages, bs, C] (bf16 entries) or uint8 [n_pages, bs, E]
-    (fp8 entries); ``tail_state`` fp32 [B, 3, C] carries the incomplete block;
-    ``c_new``/``z_new`` bf16 [B, T, C] with identical strides; ``bias`` fp32
-    [m, C] (m = compression rate).  Returns the entry format used.
+    ``pool`` is bf16 [n_pages, bs, C] (bf16 entries), uint8 [n_pages, bs, E]
+    (fp8 entries) or fp32 [n_pages, bs, C] (fp32 entries, unrounded);
+    ``tail_state`` fp32 [B, 3, C] carries the incomplete block;
+    ``c_new``/``z_new`` [B, T, C] with identical strides, bf16 (fp32 for an
+    fp32 pool); ``bias`` fp32 [m, C] (m = compression rate).  Returns the
+    entry format used.
     """
     n_pages, bs, rb = _check_pool(pool)
     _require_i32(block_table, "block_table")
     batch, bt_stride = block_table.shape
     _require_i32(seq_lens, "seq_lens", (batch,))
     channels = c_new.shape[-1]
-    fmt = _entry_format(pool, channels)
+    if pool.dtype == torch.float32 and rb == 4 * channels:
+        fmt = _lib.SKV_FMT_F32
+    else:
+        fmt = _entry_format(pool, channels)
+    in_dtype = torch.float32 if fmt == _lib.SKV_FMT_F32 else torch.bfloat16
     _require_gpu(tail_state, "tail_state")
     if (tail_state.dtype != torch.float32 or tuple(tail_state.shape) != (batch, 3, channels)
             or not tail_state.is_contiguous()):
         raise ValueError(f"tail_state must be contiguous fp32 [{batch}, 3, {channels}]")
     for name, t in (("c_new", c_new), ("z_new", z_new)):
         _require_gpu(t, name)
-        if t.dtype != torch.bfloat16 or t.dim() != 3 or t.shape[0] != batch or t.stride(-1) != 1:
-            raise ValueError(f"{name} must be bf16 [batch, T, channels] with dense rows")
+        if t.dtype != in_dtype or t.dim() != 3 or t.shape[0] != batch or t.stride(-1) != 1:
+            raise ValueError(f"{name} must be {in_dtype} [batch, T, channels] with dense rows")
     if c_new.shape != z_new.shape or c_new.stride() != z_new.stride():
         raise ValueError("c_new and z_new must have the same shape and strides")
     _require_gpu(bias, "bias")
