@@ -724,13 +724,20 @@ __device__ __forceinline__ void entry_share_load(EntryShare<kU>& sh, const uint8
   const bool live = fp8 ? kind == 2 : kind == 1;
 #pragma unroll
   for (int u = 0; u < kU; ++u) {
+    // uniform: tasks past the row's (an fp8 row has 40 of 72) and the scales
+    // of bf16 rows and rope chunks are not loaded; the store reads neither
+    sh.v[u] = u32x4{0u, 0u, 0u, 0u};
+    sh.sc[u] = 0.f;
+    if (u * kTPR >= n) continue;
     const int c = min(sub + u * kTPR, n - 1);
     const bool is_code = fp8 && c < code_chunks;
     const uint8_t* p = !fp8 ? src + c * 16
                             : is_code ? src + c * 16 : src + fp8_main + (fp8_main >> 7) * 4 + (c - code_chunks) * 16;
     sh.v[u] = ld_stream(live ? reinterpret_cast<const u32x4*>(p) : safe4);
-    sh.sc[u] = *(live && is_code ? reinterpret_cast<const float*>(src + fp8_main + (c >> 3) * 4)
-                                 : reinterpret_cast<const float*>(safe4));
+    if (fp8 && u * kTPR < code_chunks) {
+      sh.sc[u] = *(live && is_code ? reinterpret_cast<const float*>(src + fp8_main + (c >> 3) * 4)
+                                   : reinterpret_cast<const float*>(safe4));
+    }
   }
 }
 
@@ -850,8 +857,8 @@ __device__ __forceinline__ void dense_block(const skv_decode_desc* d, const Step
 //    list [S, C), each in the same order in every part.  A part ranks its
 //    candidates p, p + parts, ... of each list within that list (a lane
 //    group per kRankR candidates, each lane comparing a strided share of the
-//    list with all of them), writes every
-//    winner's index and entry at its output position, and gives the
+//    list with all of them; the groups of both lists run side by side),
+//    writes every winner's index and entry at its output position, and gives the
 //    positions in [sel, top_k) it owns index -1 and entry 0 (the reference's
 //    clamp(min=0) before its gather).
 // ---------------------------------------------------------------------------
@@ -891,63 +898,81 @@ __device__ __forceinline__ int rank_lanes(int n_groups) {
   return sub_n;
 }
 
+// Sum of v over an aligned group of sub_n (a power of two <= 64) lanes, by
+// DPP adds: quad exchanges, the half-row and row mirrors (every lane of a
+// group of <= 16 then holds the sum), then row broadcasts of lanes 15 and 31
+// (the group's last lane holds the sum of 32 or 64).  Every lane of the
+// group must be active; no lane reads outside its group.
+__device__ __forceinline__ int lane_group_sum(int v, int sub_n) {
+  if (sub_n >= 2) v += __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, false);   // quad_perm 1,0,3,2
+  if (sub_n >= 4) v += __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xF, 0xF, false);   // quad_perm 2,3,0,1
+  if (sub_n >= 8) v += __builtin_amdgcn_update_dpp(0, v, 0x141, 0xF, 0xF, false);  // row_half_mirror
+  if (sub_n >= 16) v += __builtin_amdgcn_update_dpp(0, v, 0x140, 0xF, 0xF, false); // row_mirror
+  if (sub_n >= 32) v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xA, 0xF, false); // row_bcast15 into rows 1, 3
+  if (sub_n >= 64) v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xC, 0xF, false); // row_bcast31 into rows 2, 3
+  return v;
+}
+
 // The part's first n_pf candidates (its sure ones first, then its ties)
 // get their output position, or -1 for a tie past the winners, in
 // own_pos[j] instead of being collected; the other winners are collected.
+// A candidate's position is its class's first position plus the keys of its
+// class above it (every sure key is above every tie key).
 template <class KeyAt>
 __device__ __forceinline__ void rank_candidates(RankRows& rr, KeyAt ck, int S, int C, int sel, int part, int parts,
                                                 int* own_pos = nullptr, int n_pf = 0) {
   const int n_sure_mine = (part < S) ? static_cast<int>(ceil_div24(S - part, parts)) : 0;
+  const int n_tie_mine = (part < C - S) ? static_cast<int>(ceil_div24(C - S - part, parts)) : 0;
   const int tid = threadIdx.x;
-#pragma unroll 1
-  for (int cls = 0; cls < 2; ++cls) {
+  // the lane groups of both classes (sure candidates against the sure list,
+  // ties against the tie list) run side by side
+  const int ng_sure = (n_sure_mine + kRankR - 1) / kRankR;
+  const int n_groups = ng_sure + (n_tie_mine + kRankR - 1) / kRankR;
+  const int sub_n = rank_lanes(n_groups);  // uniform
+  const int sub = tid & (sub_n - 1);
+  for (int g0 = 0; g0 < n_groups; g0 += kStepThreads / sub_n) {
+    const int g = g0 + tid / sub_n;  // this lane group's group
+    if (g >= n_groups) break;        // uniform over the lane group
+    const int cls = g >= ng_sure;
     const int lo = cls ? S : 0;
     const int hi = cls ? C : S;
-    const int n_mine = (part < hi - lo) ? static_cast<int>(ceil_div24(hi - lo - part, parts)) : 0;
-    const int n_groups = (n_mine + kRankR - 1) / kRankR;
-    const int sub_n = rank_lanes(n_groups);  // uniform
-    const int sub = tid & (sub_n - 1);
-    for (int g0 = 0; g0 < n_groups; g0 += kStepThreads / sub_n) {
-      const int j0 = (g0 + tid / sub_n) * kRankR;  // the group's first candidate
-      uint64_t mine[kRankR];
-      int rank[kRankR];
+    const int n_mine = cls ? n_tie_mine : n_sure_mine;
+    const int j0 = (cls ? g - ng_sure : g) * kRankR;  // the group's first candidate
+    uint64_t mine[kRankR];
+    int rank[kRankR];
+#pragma unroll
+    for (int r = 0; r < kRankR; ++r) {
+      mine[r] = (j0 + r < n_mine) ? ck(lo + part + (j0 + r) * parts) : ~0ull;
+      rank[r] = 0;
+    }
+#pragma unroll 4
+    for (int q = lo + sub; q < hi; q += sub_n) {
+      const uint64_t key = ck(q);
+#pragma unroll
+      for (int r = 0; r < kRankR; ++r) rank[r] += key > mine[r];
+    }
+    // sum over the lane group, two counts (< 2^16: a list holds at most
+    // kTkTieCap keys) per word
+    static_assert(kRankR == 4 && kTkTieCap < (1 << 16), "packed counts");
+    const int p01 = lane_group_sum(rank[0] | (rank[1] << 16), sub_n);
+    const int p23 = lane_group_sum(rank[2] | (rank[3] << 16), sub_n);
+    rank[0] = p01 & 0xffff;
+    rank[1] = p01 >> 16;
+    rank[2] = p23 & 0xffff;
+    rank[3] = p23 >> 16;
+    if (sub == sub_n - 1) {  // the lane that holds the group's sums
 #pragma unroll
       for (int r = 0; r < kRankR; ++r) {
-        mine[r] = (j0 + r < n_mine) ? ck(lo + part + (j0 + r) * parts) : ~0ull;
-        rank[r] = 0;
-      }
-#pragma unroll 4
-      for (int q = lo + sub; q < hi; q += sub_n) {
-        const uint64_t key = ck(q);
-#pragma unroll
-        for (int r = 0; r < kRankR; ++r) rank[r] += key > mine[r];
-      }
-      // sum over the lane group, two counts (< 2^16: a list holds at most
-      // kTkTieCap keys) per word
-      static_assert(kRankR == 4 && kTkTieCap < (1 << 16), "packed counts");
-      int p01 = rank[0] | (rank[1] << 16), p23 = rank[2] | (rank[3] << 16);
-      for (int o = 1; o < sub_n; o <<= 1) {
-        p01 += __shfl_xor(p01, o);
-        p23 += __shfl_xor(p23, o);
-      }
-      rank[0] = p01 & 0xffff;
-      rank[1] = p01 >> 16;
-      rank[2] = p23 & 0xffff;
-      rank[3] = p23 >> 16;
-      if (sub == 0) {
-#pragma unroll
-        for (int r = 0; r < kRankR; ++r) {
-          const int j = j0 + r;
-          if (j >= n_mine) break;
-          const int pos = lo + rank[r];
-          const int own = (cls ? n_sure_mine : 0) + j;
-          if (own < n_pf) {
-            own_pos[own] = (pos < sel) ? pos : -1;
-          } else if (pos < sel) {
-            const uint32_t key = static_cast<uint32_t>(mine[r] >> 32);
-            const int idx = static_cast<int>(~static_cast<uint32_t>(mine[r]));
-            rr.win[atomicAdd(&rr.n_rows, 1)] = make_int2(pos, key_finite(key) ? idx : -1);
-          }
+        const int j = j0 + r;
+        if (j >= n_mine) break;
+        const int pos = lo + rank[r];
+        const int own = (cls ? n_sure_mine : 0) + j;
+        if (own < n_pf) {
+          own_pos[own] = (pos < sel) ? pos : -1;
+        } else if (pos < sel) {
+          const uint32_t key = static_cast<uint32_t>(mine[r] >> 32);
+          const int idx = static_cast<int>(~static_cast<uint32_t>(mine[r]));
+          rr.win[atomicAdd(&rr.n_rows, 1)] = make_int2(pos, key_finite(key) ? idx : -1);
         }
       }
     }
@@ -1196,9 +1221,14 @@ using namespace skv;
 namespace {
 
 constexpr int64_t kLdsPerCu = 160 * 1024;
+// LDS is allocated to a workgroup in 1280-byte granules on MI355X (measured:
+// four workgroups of 40,960 bytes share a CU, three of 53,744 do, three of
+// 54,272 do not); the runtime's occupancy calculator assumes a finer granule.
+constexpr int64_t kLdsGranule = 1280;
 
 // Most LDS bytes a rank workgroup may take while a CU still holds as many of
-// them as it does with `lds` bytes each (the register-limited count caps it).
+// them as it does with `lds` bytes each (the register-limited count caps
+// it), a whole number of granules.
 int64_t rank_lds_budget(int64_t lds) {
   static const int by_regs = [] {
     int n = 0;
@@ -1209,10 +1239,10 @@ int64_t rank_lds_budget(int64_t lds) {
     }
     return n;
   }();
-  int64_t wgs = kLdsPerCu / lds;
+  int64_t wgs = kLdsPerCu / ((lds + kLdsGranule - 1) / kLdsGranule * kLdsGranule);
   if (wgs > by_regs) wgs = by_regs;
   if (wgs < 1) wgs = 1;
-  return kLdsPerCu / wgs;
+  return kLdsPerCu / wgs / kLdsGranule * kLdsGranule;
 }
 
 }  // namespace
