@@ -65,7 +65,7 @@ struct AttnArgs {
   int64_t entry_bytes, pick_stride;
   int32_t kind, fp8_main;  // fp8_main > 0: fp8 entries with that many coded dims
   int32_t block_size, n_pages, bt_stride, m, top_k;
-  int32_t window, H, D, n_hg, n_cu, n_wu;
+  int32_t window, H, D, n_hg, n_cu, n_wu, batch;
   float eps, softcap;  // softcap <= 0: none
 };
 
@@ -199,7 +199,8 @@ __device__ __forceinline__ u32x2 read_tr(const uint16_t* p) {
 // [kD/2 * h, kD/2 * (h+1)) for O; the pair exchanges its block maxima and P
 // through LDS.
 template <int NKS, bool kFp8, bool kComp>
-__device__ __forceinline__ void attn_unit(AtSmem<NKS>& sm, const AttnArgs& a, int b, int s, int ns, int hg) {
+__device__ __forceinline__ void attn_unit(AtSmem<NKS>& sm, const AttnArgs& a, int b, int s, int ns, int hg,
+                                          int64_t unit) {
   constexpr int kD = NKS * 32;
   constexpr int kDbW = kD / 32;  // 16-dim blocks of O per wave
   using TC = TileChunks<NKS>;
@@ -224,10 +225,10 @@ __device__ __forceinline__ void attn_unit(AtSmem<NKS>& sm, const AttnArgs& a, in
   const int t_lo = static_cast<int>((static_cast<int64_t>(s) * n_tiles) / ns);
   const int t_hi = static_cast<int>((static_cast<int64_t>(s + 1) * n_tiles) / ns);
   const int head0 = hg * kAtHeads + hb * 16;  // the pair's first head
-  const int64_t unit = blockIdx.x;
   float* part_ml = a.part + unit * kAtHeads * 2;
+  const int64_t n_units = static_cast<int64_t>(a.batch) * (a.n_cu + a.n_wu) * a.n_hg;
   uint16_t* part_o =  // bf16 outputs after every unit's (max, sum)
-      reinterpret_cast<uint16_t*>(a.part + static_cast<int64_t>(gridDim.x) * kAtHeads * 2) + unit * kAtHeads * a.D;
+      reinterpret_cast<uint16_t*>(a.part + n_units * kAtHeads * 2) + unit * kAtHeads * a.D;
   const int D = a.D;
   // query (times w for the compressed branch) as B operands for this wave's
   // half of the dims: head head0+col, dims 32(ks0 + ks) + 8grp..+7, zero past
@@ -242,8 +243,9 @@ __device__ __forceinline__ void attn_unit(AtSmem<NKS>& sm, const AttnArgs& a, in
     for (int ks = 0; ks < kHalfKs; ++ks) {
       const int d0 = (ks0 + ks) * 32 + grp * 8;
       const bool live = h < a.H && d0 < D;
-      u32x4 v = *reinterpret_cast<const u32x4*>(qrow + (live ? d0 : 0) * 2);
-      v = live ? v : u32x4{0u, 0u, 0u, 0u};
+      // dead lanes read zeros: no select after the load, which would make
+      // the window branch wait for the query before its row lookups
+      u32x4 v = *reinterpret_cast<const u32x4*>(live ? qrow + d0 * 2 : g_zero_row);
       if constexpr (kComp) {
         const float* wp = a.knorm_w + (live ? d0 : 0);
 #pragma unroll
@@ -477,17 +479,31 @@ __device__ __forceinline__ void attn_unit(AtSmem<NKS>& sm, const AttnArgs& a, in
   }
 }
 
+// Blocks go to the XCDs in turn (block i to XCD i % kXcds); the units of
+// sequence b take the blocks of XCD b % kXcds, so the query that every unit
+// of b reads comes from far memory once per sequence and the partial outputs
+// stay in the L2 of the XCD whose merge blocks read them (merge block b runs
+// there too when the batch is a multiple of kXcds).  The grid holds kXcds *
+// ceil(batch / kXcds) * (units per sequence) blocks; blocks past the batch
+// exit.
+constexpr int kXcds = 8;  // MI355X
+
 template <int NKS, bool kFp8>
 __global__ __launch_bounds__(kAtThreads, 1) void k_attn_part(AttnArgs a) {
   __shared__ AtSmem<NKS> sm;
   const int U = a.n_cu + a.n_wu;
-  const int hg = blockIdx.x % a.n_hg;
-  const int bu = blockIdx.x / a.n_hg;
-  const int u = bu % U, b = bu / U;
+  const int per_seq = U * a.n_hg;
+  const int k = static_cast<int>(blockIdx.x) / kXcds;  // this block's turn on its XCD
+  const int sb = k / per_seq;
+  const int b = static_cast<int>(blockIdx.x) % kXcds + kXcds * sb;
+  if (b >= a.batch) return;  // uniform
+  const int r = k - sb * per_seq;
+  const int u = r / a.n_hg, hg = r - u * a.n_hg;
+  const int64_t unit = (static_cast<int64_t>(b) * U + u) * a.n_hg + hg;
   if (u < a.n_cu) {
-    attn_unit<NKS, kFp8, true>(sm, a, b, u, a.n_cu, hg);
+    attn_unit<NKS, kFp8, true>(sm, a, b, u, a.n_cu, hg, unit);
   } else {
-    attn_unit<NKS, false, false>(sm, a, b, u - a.n_cu, a.n_wu, hg);
+    attn_unit<NKS, false, false>(sm, a, b, u - a.n_cu, a.n_wu, hg, unit);
   }
 }
 
@@ -844,10 +860,11 @@ extern "C" int skv_decode_attention(const skv_attention_desc* d, void* workspace
   a.n_hg = p.n_hg;
   a.n_cu = p.n_cu;
   a.n_wu = p.n_wu;
+  a.batch = static_cast<int32_t>(d->batch);
   a.eps = d->eps;
   a.softcap = d->softcap;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  const dim3 grid(static_cast<unsigned>(d->batch * (p.n_cu + p.n_wu) * p.n_hg));
+  const dim3 grid(static_cast<unsigned>(kXcds * ceil_div(d->batch, kXcds) * (p.n_cu + p.n_wu) * p.n_hg));
   if (a.fp8_main > 0) {
     hipLaunchKernelGGL((k_attn_part<18, true>), grid, dim3(kAtThreads), 0, s, a);
   } else if (p.nks == 4) {
