@@ -95,16 +95,47 @@ __device__ __forceinline__ void score_cols(const skv_decode_layer& Ly, int m, in
   score_cols(Ly.score_stride, m, L, n_cols, n_valid);
 }
 
-// Top-k chunk u of a launch: (chunk, sequence, CSA layer), chunk fastest.
+// Blocks go to the XCDs in turn (block i to XCD i % kXcds), each XCD with
+// its own L2.  With `lanes` = kXcds (a batch that is a multiple of kXcds, so
+// that every XCD gets the same work), a region of lanes * ceil(batch / lanes)
+// * per_seq blocks that starts at a multiple of kXcds gives the per_seq items
+// of sequence b to blocks of XCD b % kXcds, in every launch of the step: the
+// scores, candidate lists and block-table row of b that one launch writes or
+// reads, the next one finds in the same L2.  With lanes = 1 (smaller or
+// ragged batches) the items go sequence by sequence to consecutive blocks,
+// spread over every XCD.  Item r of sequence b for block u of the region, or
+// false for a block past the batch.
+constexpr int kXcds = 8;  // MI355X
+
+__host__ __device__ constexpr int xcd_lanes(int batch) { return batch % kXcds == 0 ? kXcds : 1; }
+
+__host__ __device__ constexpr int64_t xcd_region(int batch, int64_t per_seq) {
+  return static_cast<int64_t>(batch) * per_seq;  // lanes divide the batch
+}
+
+__device__ __forceinline__ bool xcd_item(uint32_t u, int per_seq, int batch, int& b, int& r) {
+  const int lanes = xcd_lanes(batch);  // uniform
+  const uint32_t k = u / lanes;  // the block's turn on its XCD
+  const uint32_t sb = udiv24(k, per_seq);
+  b = static_cast<int>(u % lanes + lanes * sb);
+  r = static_cast<int>(k - sb * per_seq);
+  return b < batch;
+}
+
+// Top-k chunk u of a launch's region: (chunk, sequence, CSA layer); ok is
+// false for a block past the batch.
 struct TopkChunk {
   int chunk, b, z;
+  bool ok;
 };
 
 __device__ __forceinline__ TopkChunk topk_chunk(uint32_t u, int n_chunks, const StepMap& map) {
-  const uint32_t ub = udiv24(u, n_chunks);
-  const uint32_t uz = udiv24(ub, map.batch);
-  return TopkChunk{static_cast<int>(u - ub * n_chunks), static_cast<int>(ub - uz * map.batch),
-                   static_cast<int>(uz)};
+  TopkChunk c;
+  int r;
+  c.ok = xcd_item(u, n_chunks * map.n_csa, map.batch, c.b, r);
+  c.z = static_cast<int>(udiv24(r, n_chunks));
+  c.chunk = r - c.z * n_chunks;
+  return c;
 }
 
 // ---------------------------------------------------------------------------
@@ -376,6 +407,7 @@ __device__ __forceinline__ void chunk_cols(const StepMap& map, const TopkChunk& 
 __global__ __launch_bounds__(kTkPartThreads) void k_decode_hist(int n_chunks, StepMap map) {
   __shared__ TopkHistSmem sm;
   const TopkChunk c = topk_chunk(blockIdx.x, n_chunks, map);
+  if (!c.ok) return;
   int32_t* ws = map.topk_ws[c.z] + static_cast<int64_t>(c.b) * kTkWsWords;
   if (c.chunk == 0 && threadIdx.x < 3) ws[kTkWsCnt + threadIdx.x] = 0;
   const int width = map.score_stride[c.z];
@@ -403,6 +435,7 @@ __global__ __launch_bounds__(kIdxThreads, 2) void k_decode_score_hist(int n_tile
   __shared__ IndexerSmem sm;
   __shared__ TopkHistSmem hs;
   const TopkChunk c = topk_chunk(blockIdx.x, n_tiles, map);
+  if (!c.ok) return;
   const int tid = threadIdx.x;
   int32_t* ws = map.topk_ws[c.z] + static_cast<int64_t>(c.b) * kTkWsWords;
   if (c.chunk == 0 && tid < 3) ws[kTkWsCnt + tid] = 0;
@@ -449,11 +482,12 @@ union AppendSmem {
 __global__ __launch_bounds__(kStepThreads) void k_decode_append(const skv_decode_desc* __restrict__ d,
                                                                 int n_chunks, StepMap map) {
   __shared__ AppendSmem sm;
-  const int n_append = map.batch * map.n_layers;
+  const int n_append = static_cast<int>(xcd_region(map.batch, map.n_layers));
   const int tid = threadIdx.x;
   if (static_cast<int>(blockIdx.x) >= n_append) {
     // top-k filter chunk: candidate lists from the complete histogram
     const TopkChunk c = topk_chunk(blockIdx.x - n_append, n_chunks, map);
+    if (!c.ok) return;
     const int width = map.score_stride[c.z];
     topk_filter_chunk_at(
         sm.filter, map.scores[c.z] + static_cast<int64_t>(c.b) * width, width,
@@ -461,8 +495,8 @@ __global__ __launch_bounds__(kStepThreads) void k_decode_append(const skv_decode
         map.topk_ws[c.z] + static_cast<int64_t>(c.b) * kTkWsWords);
     return;
   }
-  const int l = static_cast<int>(udiv24(blockIdx.x, map.batch));
-  const int b = static_cast<int>(blockIdx.x) - l * map.batch;
+  int b, l;
+  if (!xcd_item(blockIdx.x, map.n_layers, map.batch, b, l)) return;  // block 0 is (layer 0, sequence 0)
   const skv_decode_layer& Ly = d->layers[l];
   const bool paged = Ly.kind != SKV_LAYER_SWA;
   const int wave = tid / kWave;
@@ -1189,13 +1223,17 @@ __device__ __forceinline__ void rank_part(const skv_decode_desc* __restrict__ d,
   finish_rows(sm.rr, sm.rr.n_rows, max(o0, sel), o1, d, Ly, k, G, b, L, sm_bt, n_bt);
 }
 
-// Blocks of the gather launch: rank part i (parts_max x batch x CSA layers
-// of them) is block i * period, every other block is the next dense tile.
-// period * n_rank <= n_rank + dense tiles, so every rank block is in the grid.
+// Blocks of the gather launch, in groups of xcd_lanes(batch) blocks (one
+// block per XCD when the lanes are kXcds): group i * period is the i-th group
+// of rank parts (batch * parts_max * CSA layers of them, placed as xcd_item
+// places them), every other group holds the next dense tiles.  period *
+// n_rank_groups <= the groups of the grid, so every rank group is in it;
+// blocks past the dense tiles exit.
 struct GatherGrid {
-  int32_t n_rank;
+  int32_t n_rank_groups;
   int32_t parts_max;
   int32_t period;
+  int32_t n_dense;
 };
 
 __global__ __launch_bounds__(kStepThreads) void k_decode_gather(const skv_decode_desc* __restrict__ d,
@@ -1203,15 +1241,18 @@ __global__ __launch_bounds__(kStepThreads) void k_decode_gather(const skv_decode
                                                                 int ck_cap, StepMap map) {
   extern __shared__ __align__(16) uint8_t rank_lds[];
   const uint32_t u = blockIdx.x;  // grids stay below 2^24 workgroups
-  const uint32_t grp = udiv24(u, gg.period);
-  if (u == grp * gg.period && static_cast<int>(grp) < gg.n_rank) {
-    const uint32_t rest = udiv24(grp, gg.parts_max);
-    const uint32_t z = udiv24(rest, map.batch);
-    rank_part(d, map, rank_lds, static_cast<int>(grp - rest * gg.parts_max),
-              static_cast<int>(rest - z * map.batch), static_cast<int>(z), rank_out, bt_lds, ck_cap);
+  const int lanes = xcd_lanes(map.batch);
+  const uint32_t g = u / lanes;  // the block's group
+  const uint32_t i = udiv24(g, gg.period);
+  if (g == i * gg.period && static_cast<int>(i) < gg.n_rank_groups) {
+    int b, r;
+    if (!xcd_item(i * lanes + u % lanes, gg.parts_max * map.n_csa, map.batch, b, r)) return;
+    const int z = static_cast<int>(udiv24(r, gg.parts_max));
+    rank_part(d, map, rank_lds, r - z * gg.parts_max, b, z, rank_out, bt_lds, ck_cap);
     return;
   }
-  dense_block(d, map, static_cast<int>(u) - min(static_cast<int>(ceil_div24(u, gg.period)), gg.n_rank));
+  const int dense = static_cast<int>(u) - lanes * min(static_cast<int>(ceil_div24(g, gg.period)), gg.n_rank_groups);
+  if (dense < gg.n_dense) dense_block(d, map, dense);
 }
 
 }  // namespace skv
@@ -1397,17 +1438,17 @@ extern "C" int skv_decode_step(const skv_decode_desc* h, const skv_decode_desc* 
   }
   if (h->batch == 0 || h->n_layers == 0) return SKV_OK;
   const int n_chunks = static_cast<int>(ceil_div(max_score_cols, kTkChunk));
-  const int64_t n_append = static_cast<int64_t>(h->batch) * h->n_layers +
-                           static_cast<int64_t>(n_chunks) * h->batch * n_csa;
-  const int64_t n_hist = static_cast<int64_t>(n_chunks) * h->batch * n_csa;
+  const int64_t n_append = xcd_region(h->batch, h->n_layers) + xcd_region(h->batch, static_cast<int64_t>(n_chunks) * n_csa);
+  const int64_t n_hist = xcd_region(h->batch, static_cast<int64_t>(n_chunks) * n_csa);
   // smaller parts when the rows alone would leave most CUs idle
   int rank_out = kRankOut;
   while (rank_out > kRankOutMin && static_cast<int64_t>(h->batch) * n_csa * ceil_div(max_top_k, rank_out) < 512) {
     rank_out >>= 1;
   }
   const int64_t parts_max = ceil_div(max_top_k, rank_out);
-  const int64_t n_rank = parts_max * h->batch * n_csa;
-  const int64_t n_gather = n_rank + n_tiles;
+  const int lanes = xcd_lanes(h->batch);
+  const int64_t n_rank_groups = xcd_region(h->batch, parts_max * n_csa) / lanes;
+  const int64_t n_gather = lanes * ceil_div(lanes * n_rank_groups + n_tiles, lanes);
   if (n_append >= (1 << 24) || n_gather >= (1 << 24)) {
     return set_error(SKV_EINVAL, "%s: score_stride/out_rows give a grid of 2^24 workgroups or more", what);
   }
@@ -1415,7 +1456,7 @@ extern "C" int skv_decode_step(const skv_decode_desc* h, const skv_decode_desc* 
   int rc;
   if (n_hist > 0 && n_scored > 0) {
     const int n_score_tiles = static_cast<int>(ceil_div(max_score_cols, kIdxTile));
-    const int64_t n_score = static_cast<int64_t>(n_score_tiles) * h->batch * n_csa;
+    const int64_t n_score = xcd_region(h->batch, static_cast<int64_t>(n_score_tiles) * n_csa);
     if (n_score >= (1 << 24)) return set_error(SKV_EINVAL, "%s: score grid of 2^24 workgroups or more", what);
     hipLaunchKernelGGL(k_decode_score_hist, dim3(static_cast<unsigned>(n_score)), dim3(kIdxThreads), 0, s,
                        n_score_tiles, map, sc);
@@ -1429,9 +1470,10 @@ extern "C" int skv_decode_step(const skv_decode_desc* h, const skv_decode_desc* 
                      n_chunks, map);
   if ((rc = check_launch(what))) return rc;
   GatherGrid gg;
-  gg.n_rank = static_cast<int32_t>(n_rank);
+  gg.n_rank_groups = static_cast<int32_t>(n_rank_groups);
   gg.parts_max = static_cast<int32_t>(parts_max);
-  gg.period = n_rank > 0 ? static_cast<int32_t>(n_gather / n_rank) : 1;
+  gg.period = n_rank_groups > 0 ? static_cast<int32_t>(n_gather / lanes / n_rank_groups) : 1;
+  gg.n_dense = static_cast<int32_t>(n_tiles);
   int bt = 1, ck_cap = 0;
   int64_t lds = 0;
   if (n_csa > 0) {

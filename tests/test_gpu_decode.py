@@ -102,6 +102,16 @@ def test_decode_step_matches_oracle(dev, score_cols) -> None:
                                LayerSpec("hca", m=128), LayerSpec("swa")], score_cols)
 
 
+# a batch that is a multiple of 8: each sequence's blocks of every launch of
+# the step run on one XCD
+def test_decode_step_matches_oracle_batch_of_8(dev) -> None:
+    from saint_kv.decode import LayerSpec
+
+    _decode_oracle_steps(dev, [LayerSpec("csa", m=4, top_k=64, fp8=True), LayerSpec("csa", m=4, top_k=64),
+                               LayerSpec("hca", m=128), LayerSpec("swa")], None,
+                         lens0=[0, 1, 130, 511, 1300, 64, 900, 2000])
+
+
 # steps without a CSA layer: no top-k launches, gather launch of dense tiles
 # only; the SWA-only stack has no page group at all
 @pytest.mark.parametrize("kinds", [("hca-fp8", "swa"), ("swa", "swa"), ("hca",)])
@@ -113,10 +123,10 @@ def test_decode_step_without_csa_layers(dev, kinds) -> None:
     _decode_oracle_steps(dev, specs, None)
 
 
-def _decode_oracle_steps(dev, specs, score_cols) -> None:
+def _decode_oracle_steps(dev, specs, score_cols, lens0=(0, 1, 130, 511, 1300)) -> None:
     from saint_kv.decode import DecodeCache
 
-    B, max_len, bs, W, C, CI = 5, 2048, 16, 32, 576, 128
+    B, max_len, bs, W, C, CI = len(lens0), 2048, 16, 32, 576, 128
     seed = 3
     cache = DecodeCache(specs, B, max_len, block_size=bs, window=W, device=dev, page_order_seed=seed,
                         score_cols=score_cols)
@@ -132,7 +142,7 @@ def _decode_oracle_steps(dev, specs, score_cols) -> None:
             cache.bias[i].copy_(bias[i])
         if ibias[i] is not None:
             cache.idx_bias[i].copy_(ibias[i])
-    lens0 = np.array([0, 1, 130, 511, 1300], dtype=np.int64)
+    lens0 = np.array(lens0, dtype=np.int64)
     pre = _rand_data(g, specs, B, int(lens0.max()), C, CI)
     cache.prefill(lens0, data=[{k: v.to(dev) for k, v in d.items()} for d in pre])
     orc.append(lens0, pre, bias, ibias)
@@ -514,21 +524,23 @@ def test_decode_refused_step_changes_nothing(dev) -> None:
 
 # the step computes its own scores (LayerSpec.idx_heads): the scores it writes
 # equal skv_indexer_scores over the entries before the step, bit for bit, and
-# its top-k and gathered entries equal the oracle's on those scores
-def test_decode_step_computes_scores(dev) -> None:
+# its top-k and gathered entries equal the oracle's on those scores; a batch
+# of 8 places every sequence's blocks on one XCD, a batch of 5 spreads them
+@pytest.mark.parametrize("lens0", [[0, 3, 4, 2051, 3000], [0, 3, 4, 2051, 3000, 17, 1024, 4000]])
+def test_decode_step_computes_scores(dev, lens0) -> None:
     from saint_kv import ops
     from saint_kv.decode import DecodeCache, LayerSpec
 
     specs = [LayerSpec("csa", m=4, top_k=64, idx_heads=64), LayerSpec("hca", m=128),
              LayerSpec("csa", m=4, top_k=24, fp8=True, idx_heads=20)]
-    B, max_len, bs, C = 5, 4096, 16, 576
+    B, max_len, bs, C = len(lens0), 4096, 16, 576
     cache = DecodeCache(specs, B, max_len, block_size=bs, window=32, device=dev, page_order_seed=7)
     gen = torch.Generator(device=dev).manual_seed(7)
     for i in range(len(specs)):
         for t in (cache.bias[i], cache.idx_bias[i]):
             if t is not None:
                 t.normal_(generator=gen)
-    cache.prefill(np.array([0, 3, 4, 2051, 3000]), generator=gen)
+    cache.prefill(np.array(lens0), generator=gen)
     for step in range(9):
         for i in range(len(specs)):
             for v in cache.inputs[i].values():
