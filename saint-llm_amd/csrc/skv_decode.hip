@@ -1115,9 +1115,13 @@ __device__ __forceinline__ void rank_part(const skv_decode_desc* __restrict__ d,
     sh[u] = sure_list[tid + u * kStepThreads];
     th[u] = tie_list[tid + u * kStepThreads];
   }
+  // the row's slices only (uniform bound): short rows issue one load, not 16
   int32_t btv[kRankBt / kStepThreads];
 #pragma unroll
-  for (int u = 0; u < kRankBt / kStepThreads; ++u) btv[u] = bt_row[min(tid + u * kStepThreads, n_bt - 1)];
+  for (int u = 0; u < kRankBt / kStepThreads; ++u) {
+    if (u * kStepThreads >= n_bt) break;
+    btv[u] = bt_row[min(tid + u * kStepThreads, n_bt - 1)];
+  }
   hold_fields(Ly, false);
   const int k = map.top_k[z];
   const int parts = static_cast<int>(ceil_div24(k, rank_out));
@@ -1132,6 +1136,7 @@ __device__ __forceinline__ void rank_part(const skv_decode_desc* __restrict__ d,
   const int sel = topk_sel(k, n_cols, n_valid);
 #pragma unroll
   for (int u = 0; u < kRankBt / kStepThreads; ++u) {
+    if (u * kStepThreads >= n_bt) break;
     if (tid + u * kStepThreads < n_bt) sm_bt[tid + u * kStepThreads] = btv[u];
   }
   if (tid == 0) sm.rr.n_rows = 0;
@@ -1171,8 +1176,8 @@ __device__ __forceinline__ void rank_part(const skv_decode_desc* __restrict__ d,
 #pragma unroll
           for (int u = 0; u < kLoad; ++u) {
             const int c = c0 + u * kStepThreads;
-            const bool head = c < S ? c < kRankHead : c - S < kRankHead;
-            if (c < C && !head) sm_ck[c] = order_key(v[u]);
+            const bool in_head = c < S ? c < kRankHead : c - S < kRankHead;
+            if (c < C && !in_head) sm_ck[c] = order_key(v[u]);
           }
         }
       }
