@@ -174,19 +174,28 @@ __device__ __forceinline__ OwnPlan step_plan(PlanSmem& sm, const StepMap& map, i
   const int ng = map.n_groups;
   OwnPlan P{0, map.tok_lens[b], 0, 0, 0, 0};
   if (ng == 0) return P;  // uniform: no page group, nothing to plan
-  // every load first (clamped indices), so they are all in flight together
-  int len1[kPerT];
-  int cur[kPerT][SKV_MAX_GROUPS];
+  // every load first (clamped indices), so they are all in flight together;
+  // the bounds (batch slices, groups) are uniform, so a small batch or a
+  // single group issues one load of each kind, not kPerT * SKV_MAX_GROUPS
+  int len1[kPerT] = {};
+  int cur[kPerT][SKV_MAX_GROUPS] = {};
 #pragma unroll
   for (int j = 0; j < kPerT; ++j) {
+    if (j * kStepThreads >= batch) break;
     const int s = min(tid + j * kStepThreads, batch - 1);
     len1[j] = map.tok_lens[s] + 1;
 #pragma unroll
-    for (int g = 0; g < SKV_MAX_GROUPS; ++g) cur[j][g] = map.n_entries[min(g, ng - 1)][s];
+    for (int g = 0; g < SKV_MAX_GROUPS; ++g) {
+      if (g >= ng) break;
+      cur[j][g] = map.n_entries[g][s];
+    }
   }
-  int top[SKV_MAX_GROUPS];
+  int top[SKV_MAX_GROUPS] = {};
 #pragma unroll
-  for (int g = 0; g < SKV_MAX_GROUPS; ++g) top[g] = *map.free_top[min(g, ng - 1)];
+  for (int g = 0; g < SKV_MAX_GROUPS; ++g) {
+    if (g >= ng) break;
+    top[g] = *map.free_top[g];
+  }
   const int own_cur = map.n_entries[min(max(g_own, 0), ng - 1)][b];
   early(P.len);
   if (tid == 0) {
