@@ -1077,7 +1077,6 @@ struct RankHead {
 };
 struct RankFallback {
   TopkSmemT<kStepThreads> full;
-  int32_t order[kMaxTopK];
 };
 
 __host__ __device__ constexpr int64_t align16(int64_t x) { return (x + 15) & ~static_cast<int64_t>(15); }
@@ -1152,11 +1151,12 @@ __device__ __forceinline__ void rank_part(const skv_decode_desc* __restrict__ d,
   const int o0 = part * rank_out;
   const int o1 = min(k, o0 + rank_out);
   if (sel > 0 && flag) {
-    // tie bin over the list capacity: full select of the row, then this part's positions
-    topk_row<kStepThreads>(fb.full, nullptr, map.scores[z] + static_cast<int64_t>(b) * map.score_stride[z],
-                           n_cols, n_valid, k, fb.order);
-    __syncthreads();
-    if (tid < o1 - o0) sm.rr.win[tid] = make_int2(o0 + tid, fb.order[o0 + tid]);
+    // tie bin over the list capacity: full select of the row, keeping this
+    // part's positions (each is emitted once)
+    topk_row_emit<kStepThreads>(fb.full, nullptr, map.scores[z] + static_cast<int64_t>(b) * map.score_stride[z],
+                                n_cols, n_valid, k, [&](int j, int v) {
+                                  if (j >= o0 && j < o1) sm.rr.win[j - o0] = make_int2(j, v);
+                                });
     __syncthreads();
     finish_rows(sm.rr, o1 - o0, o1, o1, d, Ly, k, G, b, L, sm_bt, n_bt);
     return;

@@ -45,14 +45,15 @@ struct TopkSmemT {
 };
 using TopkSmem = TopkSmemT<kTopkThreads>;
 
-// out[0, k): the sel = min(k, n_cols, n_valid) best of row[0, n_valid) in
-// (score desc, index asc) order, -1 for non-finite picks and ranks >= sel.
-// `keys` (kLdsKeys words of LDS) stages short rows; nullptr reads global
-// memory on every pass.  Every thread of the kThreads-thread workgroup
-// (kThreads >= 256) must call it.
-template <int kThreads = kTopkThreads>
-__device__ __forceinline__ void topk_row(TopkSmemT<kThreads>& sm, uint32_t* keys, const float* row,
-                                         int n_cols, int n_valid, int k, int32_t* out) {
+// emit(j, v) for every output position j in [0, k), once each: the sel =
+// min(k, n_cols, n_valid) best of row[0, n_valid) in (score desc, index asc)
+// order, -1 for non-finite picks and ranks >= sel.  `keys` (kLdsKeys words
+// of LDS) stages short rows; nullptr reads global memory on every pass.
+// Every thread of the kThreads-thread workgroup (kThreads >= 256) must call
+// it.
+template <int kThreads, class Emit>
+__device__ __forceinline__ void topk_row_emit(TopkSmemT<kThreads>& sm, uint32_t* keys, const float* row,
+                                              int n_cols, int n_valid, int k, Emit emit) {
   static_assert(kThreads >= 256 && kThreads % kWave == 0, "topk_row needs >= 256 threads");
   constexpr int kWaves = kThreads / kWave;
   const int tid = threadIdx.x;
@@ -61,7 +62,7 @@ __device__ __forceinline__ void topk_row(TopkSmemT<kThreads>& sm, uint32_t* keys
   n_valid = max(0, min(n_valid, n_cols));
   const int k_eff = min(k, n_cols);
   const int sel = min(k_eff, n_valid);
-  for (int j = sel + tid; j < k; j += kThreads) out[j] = -1;
+  for (int j = sel + tid; j < k; j += kThreads) emit(j, -1);
   if (sel == 0) return;
   const bool in_lds = keys != nullptr && n_valid <= kLdsKeys;
   if (in_lds) {
@@ -152,8 +153,15 @@ __device__ __forceinline__ void topk_row(TopkSmemT<kThreads>& sm, uint32_t* keys
       const uint32_t kj = sm.cand_key[j];
       rank += (kj > kc) || (kj == kc && sm.cand_idx[j] < ic);
     }
-    out[rank] = key_finite(kc) ? ic : -1;
+    emit(rank, key_finite(kc) ? ic : -1);
   }
+}
+
+// out[0, k) as topk_row_emit gives it.
+template <int kThreads = kTopkThreads>
+__device__ __forceinline__ void topk_row(TopkSmemT<kThreads>& sm, uint32_t* keys, const float* row,
+                                         int n_cols, int n_valid, int k, int32_t* out) {
+  topk_row_emit<kThreads>(sm, keys, row, n_cols, n_valid, k, [&](int j, int v) { out[j] = v; });
 }
 
 // ===========================================================================
