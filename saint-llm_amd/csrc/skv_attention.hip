@@ -82,6 +82,7 @@ struct AtSmem {
   int64_t row[kAtRun];                       // byte offset of each key's source row in the run, -1 masked
   f32x4 sx[kAtWaves][2][kWave];              // per wave: its half-dims S^T partial per key block
   float ssx[2][2][16];                       // per half of the dims: the keys' sums of squares
+  float w[kAtMaxD];                          // k_norm weight (compressed branch)
 };
 
 // Zero bytes that dead chunks (masked keys, dims past D) are read from: no
@@ -235,6 +236,26 @@ __device__ __forceinline__ void attn_unit(AtSmem<NKS>& sm, const AttnArgs& a, in
   // H and D
   constexpr int kHalfKs = NKS / 2;
   const int ks0 = half * kHalfKs;
+  // The prologue's loads, in this order (vector loads complete in order):
+  // a CSA unit's first pick and the entry count; the k_norm weight, one or
+  // two elements per thread, for LDS (per-lane loads of each 32-dim step's 8
+  // weights would add 18 load instructions per wave, which the CU's address
+  // unit works through one after another); the query; then the pick's
+  // block-table entry, which waits for the pick only.  The pick -> block
+  // table chain overlaps the query's round trip, and q * w waits for the
+  // query.  Every load is unconditional (a branch around a load waits for it
+  // where the branch ends); lanes without a key read the zero row.
+  int32_t pick0 = 0, ne0 = 0;
+  float w_lo = 0.f, w_hi = 0.f;
+  if constexpr (kComp) {
+    const bool csa = a.kind == SKV_LAYER_CSA && n_keys > 0;
+    pick0 = *(csa ? a.picks + static_cast<int64_t>(b) * a.pick_stride + min(t_lo * kAtTile + tid, n_keys - 1)
+                  : reinterpret_cast<const int32_t*>(g_zero_row));
+    ne0 = a.n_entries[b];
+    w_lo = a.knorm_w[min(tid, D - 1)];
+    w_hi = a.knorm_w[min(tid + kAtThreads, D - 1)];
+  }
+  __builtin_amdgcn_sched_barrier(0);
   u32x4 qreg[kHalfKs];
   {
     const int h = head0 + col;
@@ -245,13 +266,34 @@ __device__ __forceinline__ void attn_unit(AtSmem<NKS>& sm, const AttnArgs& a, in
       const bool live = h < a.H && d0 < D;
       // dead lanes read zeros: no select after the load, which would make
       // the window branch wait for the query before its row lookups
-      u32x4 v = *reinterpret_cast<const u32x4*>(live ? qrow + d0 * 2 : g_zero_row);
-      if constexpr (kComp) {
-        const float* wp = a.knorm_w + (live ? d0 : 0);
+      qreg[ks] = *reinterpret_cast<const u32x4*>(live ? qrow + d0 * 2 : g_zero_row);
+    }
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  int e0 = -1, pi0 = 0;
+  int32_t page0 = -1;
+  if constexpr (kComp) {
+    e0 = (pick0 < max(ne0, 0)) ? pick0 : -1;
+    pi0 = e0 >= 0 ? static_cast<int>(udiv24(e0, a.block_size)) : 0;
+    if (pi0 >= a.bt_stride) e0 = -1;
+    page0 = *(e0 >= 0 ? a.block_table + static_cast<int64_t>(b) * a.bt_stride + pi0
+                      : reinterpret_cast<const int32_t*>(g_zero_row));
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  if constexpr (kComp) {
+    if (tid < D) sm.w[tid] = w_lo;
+    if (tid + kAtThreads < D) sm.w[tid + kAtThreads] = w_hi;
+    lds_barrier();
+    const int h = head0 + col;
 #pragma unroll
-        for (int t = 0; t < 4; ++t) {
-          v[t] = bf16_pack2(__uint_as_float(v[t] << 16) * wp[2 * t], __uint_as_float(v[t] & 0xffff0000u) * wp[2 * t + 1]);
-        }
+    for (int ks = 0; ks < kHalfKs; ++ks) {
+      const int d0 = (ks0 + ks) * 32 + grp * 8;
+      const bool live = h < a.H && d0 < D;
+      const float* wp = sm.w + (live ? d0 : 0);
+      u32x4 v = qreg[ks];
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        v[t] = bf16_pack2(__uint_as_float(v[t] << 16) * wp[2 * t], __uint_as_float(v[t] & 0xffff0000u) * wp[2 * t + 1]);
       }
       qreg[ks] = v;
     }
@@ -282,8 +324,15 @@ __device__ __forceinline__ void attn_unit(AtSmem<NKS>& sm, const AttnArgs& a, in
         } else {
           int e = j;
           if (a.kind == SKV_LAYER_CSA) {
-            e = a.picks[static_cast<int64_t>(b) * a.pick_stride + j];
-            if (e >= max(a.n_entries[b], 0)) e = -1;
+            if (k_lo == t_lo * kAtTile) {  // uniform: the first run's rows come from the prologue
+              e = -1;
+              if (e0 >= 0 && page0 >= 0 && page0 < a.n_pages) {
+                row = (static_cast<int64_t>(page0) * a.block_size + (e0 - pi0 * a.block_size)) * row_bytes;
+              }
+            } else {
+              e = a.picks[static_cast<int64_t>(b) * a.pick_stride + j];
+              if (e >= max(a.n_entries[b], 0)) e = -1;
+            }
           }
           if (e >= 0) {
             const int pi = static_cast<int>(udiv24(e, a.block_size));
