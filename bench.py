@@ -435,14 +435,17 @@ def cpu_baseline_decode(seconds: float = 5.0, seed: int = 0) -> dict:
 
 def run_layer_seq_leg(dev, n_layers: int = 8, batch: int = 16, L: int = 65536, steps: int = 100,
                       per_graph: int = 10, heads: int = 64, window: int = 128, seed: int = 8,
-                      materialize: bool = False) -> dict:
+                      mode: str = "fused") -> dict:
     """What a model's decode step sees at 64k context: n_layers CSA layers
     (m=4, top-k 512, W=128), one after another, each layer's cache step
     followed by its decode attention over the step's picks and window (the
     next layer's inputs come from that attention, so the layers cannot be
     stepped together).  Each layer has its own cache and input sets; the
     sequence of layers is replayed from HIP graphs of ``per_graph`` model
-    steps.  The steps write no gathered copies unless ``materialize``: the
+    steps.  ``mode``: "fused", one skv_decode_step_attend per layer (the
+    attention launch ranks the picks itself, in place of the step's gather
+    launch); "separate", skv_decode_step then skv_decode_attention;
+    "materialize", the same with the step's gathered copies written.  The
     attention reads the picks' entries and the window rows in place."""
     from saint_kv.decode import DecodeCache, LayerSpec
 
@@ -451,7 +454,7 @@ def run_layer_seq_leg(dev, n_layers: int = 8, batch: int = 16, L: int = 65536, s
     caches, qs, knorm, outs = [], [], [], []
     for li in range(n_layers):
         c = DecodeCache([LayerSpec("csa", m=4, top_k=512)], batch, max_len, window=window, device=dev,
-                        page_order_seed=seed + li, input_sets=per_graph, materialize=materialize)
+                        page_order_seed=seed + li, input_sets=per_graph, materialize=mode == "materialize")
         c.bias[0].normal_(generator=gen)
         c.idx_bias[0].normal_(generator=gen)
         for k in range(per_graph):
@@ -463,16 +466,22 @@ def run_layer_seq_leg(dev, n_layers: int = 8, batch: int = 16, L: int = 65536, s
         qs.append(torch.empty(batch, heads, 576, dtype=torch.bfloat16, device=dev).normal_(generator=gen))
         knorm.append(torch.empty(576, dtype=torch.float32, device=dev).uniform_(0.5, 1.5, generator=gen))
         outs.append(torch.empty(batch, heads, 576, dtype=torch.float32, device=dev))
+    def layer(li, c, s):
+        if mode == "fused":
+            c._launch_step_attend(s % c.n_input_sets, qs[li], knorm[li], None, None, None, 1.0e-6, outs[li])
+        else:
+            c._launch_step(s % c.n_input_sets)
+            c.attention(0, qs[li], knorm[li], out=outs[li])
+
     for li, c in enumerate(caches):  # warm-up: kernel loads and each layer's attention workspace
-        c.step()
-        c.attention(0, qs[li], knorm[li], out=outs[li])
+        layer(li, c, 0)
+        c.host_lens += 1
     torch.cuda.synchronize()
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph):
         for s in range(per_graph):
             for li, c in enumerate(caches):
-                c._launch_step(s % c.n_input_sets)
-                c.attention(0, qs[li], knorm[li], out=outs[li])
+                layer(li, c, s)
     graph.replay()  # warm-up replay
     for c in caches:
         c.host_lens += per_graph
@@ -494,11 +503,12 @@ def run_layer_seq_leg(dev, n_layers: int = 8, batch: int = 16, L: int = 65536, s
                     f"one decode step, then its decode attention ({heads} heads x 576) over the picks",
         "model_steps": reps * per_graph, "us_per_model_step": round(us, 2),
         "us_per_layer": round(us / n_layers, 2),
-        "launches_per_layer": caches[0].step_launches() + 2,
-        "gathered_copies": materialize,
+        "mode": mode,
+        "launches_per_layer": caches[0].step_launches() + (1 if mode == "fused" else 2),
+        "gathered_copies": mode == "materialize",
         "kv_tokens_per_s": round(n_layers * batch * (512 + window) / (us * 1e-6), 1),
     }
-    log(f"layer_seq_64k: {rec['us_per_model_step']} us per {n_layers}-layer model step, "
+    log(f"layer_seq_64k ({mode}): {rec['us_per_model_step']} us per {n_layers}-layer model step, "
         f"{rec['us_per_layer']} us per layer (step + attention)")
     del caches
     torch.cuda.empty_cache()
@@ -804,8 +814,9 @@ def main() -> int:
 
     layer_seq = None
     if "layer_seq_64k" in wanted:
-        layer_seq = run_layer_seq_leg(dev)
-        layer_seq["with_gathered_copies"] = run_layer_seq_leg(dev, materialize=True)
+        layer_seq = run_layer_seq_leg(dev, mode="fused")
+        layer_seq["separate"] = run_layer_seq_leg(dev, mode="separate")
+        layer_seq["with_gathered_copies"] = run_layer_seq_leg(dev, mode="materialize")
     indexer = None if args.no_indexer else run_indexer_leg(dev, 16, 16384, 64, 128, 200)
     state_io = None if args.no_state else run_state_leg(dev)
     attention = {}

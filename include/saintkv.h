@@ -483,6 +483,33 @@ int64_t skv_attention_workspace(const skv_attention_desc* desc);
 int64_t skv_attention_desc_size(void);
 int skv_decode_attention(const skv_attention_desc* desc, void* workspace, int64_t ws_bytes, void* stream);
 
+/* One decode step of a one-layer stack followed by that layer's decode
+ * attention, in the launches of skv_decode_step with its gather launch
+ * replaced by the attention's: what one layer of a model's cached forward
+ * does (model.py:294-315: the block's attention appends to its cache layer,
+ * csa.py:299-373 / hca.py:110-169 / swa.py:107-137, then attends over it).
+ *   hist, append : as skv_decode_step;
+ *   attention    : per (sequence, split, 64 heads) units as
+ *                  skv_decode_attention's; a CSA unit ranks its share of the
+ *                  row's top-k candidates (the ordering of skv_decode_step's
+ *                  gather launch), writes those positions of topk_idx and
+ *                  attends over its picks in place; the step's lengths, entry
+ *                  counts and tops are committed;
+ *   merge        : as skv_decode_attention's.
+ * The results equal skv_decode_step followed by skv_decode_attention over
+ * the cache (topk_idx, lengths, pages and rings bit for bit; the attention
+ * output up to its partial sums' order).  The layer writes no gathered
+ * copies (out_entries and out_window NULL).  `attn` supplies q, out,
+ * knorm_w (HCA/CSA), eps, softcap, sink, win_v (NULL: the layer's ring),
+ * n_heads, head_dim (= latent), batch (= the step's), max_entries and
+ * splits; the cache fields (kind, format, lens, pool, block table, entry
+ * counts, m, picks, top_k, win_k, window) are taken from the step's
+ * descriptor.  skv_decode_step_attend_workspace returns the workspace bytes
+ * (16-byte aligned, as skv_decode_attention's), or -1 on bad descriptors. */
+int64_t skv_decode_step_attend_workspace(const skv_decode_desc* host_desc, const skv_attention_desc* attn);
+int skv_decode_step_attend(const skv_decode_desc* host_desc, const skv_decode_desc* device_desc,
+                           const skv_attention_desc* attn, void* workspace, int64_t ws_bytes, void* stream);
+
 /* sizeof(skv_decode_desc), sizeof(skv_decode_layer), sizeof(skv_page_group)
  * written to out[0..2], so bindings can check their struct layout. */
 int skv_decode_desc_sizes(int64_t* out);

@@ -35,6 +35,7 @@
 
 #include "skv_common.h"
 #include "skv_entry.h"
+#include "skv_step.h"
 
 namespace skv {
 
@@ -67,6 +68,7 @@ struct AttnArgs {
   int32_t block_size, n_pages, bt_stride, m, top_k;
   int32_t window, H, D, n_hg, n_cu, n_wu, batch;
   float eps, softcap;  // softcap <= 0: none
+  int32_t fused;       // 1: the decode step's last launch (lens are the step's new lengths)
 };
 
 __device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
@@ -194,37 +196,50 @@ __device__ __forceinline__ u32x2 read_tr(const uint16_t* p) {
   return __builtin_bit_cast(u32x2, v);
 }
 
+// The keys of a unit: the picks of a top-k row (CSA), the visible entries
+// (HCA) or the window, split by tiles over the units of the branch.
+struct NoRank {
+  static constexpr bool kOn = false;
+};
+
 // Unit s of ns of one branch (kComp: compressed entries, else the window).
 // Waves 2hb and 2hb+1 share heads 16hb..16hb+15 of the group: wave half h
 // multiplies key block h (keys 16h..16h+15) for S^T and dims
 // [kD/2 * h, kD/2 * (h+1)) for O; the pair exchanges its block maxima and P
-// through LDS.
-template <int NKS, bool kFp8, bool kComp>
+// through LDS.  With a ranking Rank (Rank::kOn), a CSA unit's keys are the
+// picks Rank finds (its share of the row's top-k, in output order) once the
+// query's loads are in flight; they resolve to pool rows through Rank::row.
+template <int NKS, bool kFp8, bool kComp, class Rank = NoRank>
 __device__ __forceinline__ void attn_unit(AtSmem<NKS>& sm, const AttnArgs& a, int b, int s, int ns, int hg,
-                                          int64_t unit) {
+                                          int64_t unit, Rank&& rk = Rank{}) {
   constexpr int kD = NKS * 32;
   constexpr int kDbW = kD / 32;  // 16-dim blocks of O per wave
+  constexpr bool kRanked = std::remove_reference_t<Rank>::kOn;
+  static_assert(!kRanked || kComp, "ranked keys are compressed entries");
   using TC = TileChunks<NKS>;
   const int tid = threadIdx.x;
   const int wave = tid / kWave, lane = tid % kWave;
   const int hb = wave >> 1, half = wave & 1;
   const int col = lane & 15, grp = lane >> 4;
   const int L = min(max(a.lens[b], 0), (1 << 24) - 1);
-  // keys of this branch for sequence b
-  int n_keys;
+  // keys of this branch for sequence b (ranked: known after the ranking)
+  int n_keys = 0;
   if constexpr (!kComp) {
     n_keys = min(L, a.window);
-  } else {
+  } else if constexpr (!kRanked) {
     if (a.kind == SKV_LAYER_CSA) {
       n_keys = a.top_k;
     } else {
+      // in the step's launch the visible count (L-1)/m is what the entry
+      // count committed beside it bounds it by
       const int q_pos = max(L - 1, 0);
-      n_keys = min(static_cast<int>(udiv24(q_pos, a.m)), max(a.n_entries[b], 0));
+      n_keys = a.fused ? static_cast<int>(udiv24(q_pos, a.m))
+                       : min(static_cast<int>(udiv24(q_pos, a.m)), max(a.n_entries[b], 0));
     }
   }
-  const int n_tiles = (n_keys + kAtTile - 1) / kAtTile;
-  const int t_lo = static_cast<int>((static_cast<int64_t>(s) * n_tiles) / ns);
-  const int t_hi = static_cast<int>((static_cast<int64_t>(s + 1) * n_tiles) / ns);
+  int n_tiles = (n_keys + kAtTile - 1) / kAtTile;
+  int t_lo = static_cast<int>((static_cast<int64_t>(s) * n_tiles) / ns);
+  int t_hi = static_cast<int>((static_cast<int64_t>(s + 1) * n_tiles) / ns);
   const int head0 = hg * kAtHeads + hb * 16;  // the pair's first head
   float* part_ml = a.part + unit * kAtHeads * 2;
   const int64_t n_units = static_cast<int64_t>(a.batch) * (a.n_cu + a.n_wu) * a.n_hg;
@@ -245,9 +260,14 @@ __device__ __forceinline__ void attn_unit(AtSmem<NKS>& sm, const AttnArgs& a, in
   // table chain overlaps the query's round trip, and q * w waits for the
   // query.  Every load is unconditional (a branch around a load waits for it
   // where the branch ends); lanes without a key read the zero row.
+  // A ranked unit's first loads are its ranking's (they return first).
   int32_t pick0 = 0, ne0 = 0;
   float w_lo = 0.f, w_hi = 0.f;
-  if constexpr (kComp) {
+  if constexpr (kRanked) {
+    rk.load();
+    w_lo = a.knorm_w[min(tid, D - 1)];
+    w_hi = a.knorm_w[min(tid + kAtThreads, D - 1)];
+  } else if constexpr (kComp) {
     const bool csa = a.kind == SKV_LAYER_CSA && n_keys > 0;
     pick0 = *(csa ? a.picks + static_cast<int64_t>(b) * a.pick_stride + min(t_lo * kAtTile + tid, n_keys - 1)
                   : reinterpret_cast<const int32_t*>(g_zero_row));
@@ -269,10 +289,11 @@ __device__ __forceinline__ void attn_unit(AtSmem<NKS>& sm, const AttnArgs& a, in
       qreg[ks] = *reinterpret_cast<const u32x4*>(live ? qrow + d0 * 2 : g_zero_row);
     }
   }
+  if constexpr (kRanked) rk.load_bt();
   __builtin_amdgcn_sched_barrier(0);
   int e0 = -1, pi0 = 0;
   int32_t page0 = -1;
-  if constexpr (kComp) {
+  if constexpr (kComp && !kRanked) {
     e0 = (pick0 < max(ne0, 0)) ? pick0 : -1;
     pi0 = e0 >= 0 ? static_cast<int>(udiv24(e0, a.block_size)) : 0;
     if (pi0 >= a.bt_stride) e0 = -1;
@@ -284,6 +305,13 @@ __device__ __forceinline__ void attn_unit(AtSmem<NKS>& sm, const AttnArgs& a, in
     if (tid < D) sm.w[tid] = w_lo;
     if (tid + kAtThreads < D) sm.w[tid + kAtThreads] = w_hi;
     lds_barrier();
+    if constexpr (kRanked) {
+      // the ranking waits for its own loads only; q * w below waits for the query
+      n_keys = rk.rank(sm);
+      n_tiles = (n_keys + kAtTile - 1) / kAtTile;
+      t_lo = 0;
+      t_hi = n_tiles;
+    }
     const int h = head0 + col;
 #pragma unroll
     for (int ks = 0; ks < kHalfKs; ++ks) {
@@ -321,6 +349,9 @@ __device__ __forceinline__ void attn_unit(AtSmem<NKS>& sm, const AttnArgs& a, in
         if constexpr (!kComp) {
           const int pos = L - n_keys + j;
           row = (static_cast<int64_t>(b) * a.window + static_cast<int>(umod24(pos, a.window))) * row_bytes;
+        } else if constexpr (kRanked) {
+          const int64_t r = rk.row(j);
+          row = r >= 0 ? r * row_bytes : -1;
         } else {
           int e = j;
           if (a.kind == SKV_LAYER_CSA) {
@@ -517,6 +548,7 @@ __device__ __forceinline__ void attn_unit(AtSmem<NKS>& sm, const AttnArgs& a, in
     part_ml[2 * hl] = m_run;
     part_ml[2 * hl + 1] = l_run;
   }
+  if constexpr (kRanked) rk.finish(sm);
   if (!__ballot(m_run != -__builtin_huge_valf())) return;  // no live key: O is not read
 #pragma unroll
   for (int db = 0; db < kDbW; ++db) {
@@ -535,7 +567,6 @@ __device__ __forceinline__ void attn_unit(AtSmem<NKS>& sm, const AttnArgs& a, in
 // there too when the batch is a multiple of kXcds).  The grid holds kXcds *
 // ceil(batch / kXcds) * (units per sequence) blocks; blocks past the batch
 // exit.
-constexpr int kXcds = 8;  // MI355X
 
 template <int NKS, bool kFp8>
 __global__ __launch_bounds__(kAtThreads, 1) void k_attn_part(AttnArgs a) {
@@ -852,6 +883,420 @@ int attn_plan(const skv_attention_desc* d, AttnPlan& p) {
   return SKV_OK;
 }
 
+// The merge launch of a part launch's units (k_attn_merge_q for sequences
+// of at most kMergeChunkQ units).
+int launch_merge(const AttnArgs& a, const AttnPlan& p, int kind, const float* knorm_w, const float* sink,
+                 float* out, hipStream_t s, const char* what) {
+  MergeArgs mg;
+  mg.part = a.part;
+  mg.out = out;
+  mg.knorm_w = knorm_w;
+  mg.sink = sink;
+  mg.H = a.H;
+  mg.D = a.D;
+  mg.n_hg = p.n_hg;
+  mg.n_cu = p.n_cu;
+  mg.n_wu = p.n_wu;
+  mg.sink_comp = kind == SKV_LAYER_HCA;
+  if (p.n_cu + p.n_wu <= kMergeChunkQ) {
+    hipLaunchKernelGGL(k_attn_merge_q,
+                       dim3(static_cast<unsigned>(a.batch), static_cast<unsigned>(ceil_div(a.H, 4)),
+                            static_cast<unsigned>(ceil_div(a.D / 4, kWave))),
+                       dim3(256), 0, s, mg);
+  } else {
+    hipLaunchKernelGGL(k_attn_merge,
+                       dim3(static_cast<unsigned>(a.batch), static_cast<unsigned>(ceil_div(a.H, 4)), 2),
+                       dim3(256), 0, s, mg);
+  }
+  return check_launch(what);
+}
+
+
+// ---------------------------------------------------------------------------
+// The decode step's last launch with the attention fused in
+// (skv_decode_step_attend, one layer).  It takes the place of the step's
+// gather launch: a CSA unit ranks its share of the row's top-k candidates
+// (the lists the step's filter chunks wrote), writes those positions of the
+// top-k row and attends over its picks, read in place through the block
+// table; HCA and window units are the attention's own.  The gather launch's
+// other work happens here as well: the first window unit of a sequence
+// commits the step (lengths, entry counts, free-stack tops) and CSA unit 0
+// clears the row's top-k histogram for the next step.  No unit reads what
+// the commit writes: lengths come from the step's scratch (a.lens is
+// step_lens) and an HCA unit's visible count from the length alone.
+// ---------------------------------------------------------------------------
+
+// A CSA unit's ranking works in the LDS of the key tiles, which it is done
+// with before the first tile is stored: kr holds the candidates' order keys
+// (or the full-select fallback's state); vs, which compressed units do not
+// use otherwise, holds the compaction's per-wave counts, the unit's picks by
+// output position, its keys in output order and the block-table row.
+template <int NKS>
+struct RankLds {
+  static constexpr int kKr = sizeof(AtSmem<NKS>::kr);
+  static constexpr int kVs = sizeof(AtSmem<NKS>::vs);
+  static constexpr int kCkCap = kKr / 8;  // order keys held in LDS
+  static constexpr int kScan = 16;
+  static constexpr int kBtCap = (kVs - 4 * (kScan + 2 * kMaxTopK)) / 4;  // block-table entries held in LDS
+  static_assert(sizeof(TopkSmemT<kAtThreads>) <= kKr, "full-select fallback state fits the key tile");
+  static_assert(kBtCap >= 1024, "block-table row in LDS");
+};
+
+constexpr int kPosEmpty = -2147483647 - 1;  // an output position another unit owns
+
+// Ranking of CSA unit `part` of `parts` of sequence b, over the one layer of
+// a step: its candidates are the lists' entries part, part + parts, ...;
+// positions [part * out, (part + 1) * out), out = ceil(k / parts), are its
+// share of the fills (and of the fallback's positions).
+template <int NKS>
+struct StepRank {
+  static constexpr bool kOn = true;
+  using RL = RankLds<NKS>;
+  static constexpr int kBtPer = (RL::kBtCap + kAtThreads - 1) / kAtThreads;
+  const StepMap& map;
+  int32_t* topk_idx;
+  int b, part, parts;
+  bool lead;  // head group 0: writes the top-k row and clears the histogram
+  // the first round trip
+  int status = 0, L = 0, cnt0 = 0, cnt1 = 0, flag = 0, n_bt = 0;
+  int word = 0;  // lane 0: status, 1: length, 2-4: the lists' counters and tie-overflow flag
+  int2 sh, th;
+  int32_t btv[kBtPer];
+  const int32_t* bt_row = nullptr;
+  int32_t* ws = nullptr;
+  // LDS, from rank()
+  const int* keys = nullptr;
+  const int32_t* bt_lds = nullptr;
+
+  __device__ StepRank(const StepMap& m_, int32_t* idx, int b_, int part_, int parts_, bool lead_)
+      : map(m_), topk_idx(idx), b(b_), part(part_), parts(parts_), lead(lead_) {}
+
+  // The ranking's loads, unconditional (clamped indices), ahead of the
+  // query's: the heads of both lists, and the status, length and list
+  // counters as one load whose lanes read different words.  Loaded as
+  // uniform values they would go to scalar registers right after their
+  // loads, behind a wait that would hold back the query's loads; read out of
+  // lanes in rank(), they are waited for there.
+  __device__ __forceinline__ void load() {
+    const int tid = threadIdx.x;
+    const int gi = map.group[0];
+    ws = map.topk_ws[0] + static_cast<int64_t>(b) * kTkWsWords;
+    bt_row = map.block_table[gi] + static_cast<int64_t>(b) * map.bt_stride[gi];
+    n_bt = min(map.bt_stride[gi], RL::kBtCap);
+    static_assert(kAtThreads <= kMaxTopK && kAtThreads <= kTkTieCap, "list heads within the lists");
+    sh = reinterpret_cast<const int2*>(ws + kTkWsSure)[tid];
+    th = reinterpret_cast<const int2*>(ws + kTkWsTie)[tid];
+    const int lane = tid % kWave;
+    word = *(lane == 1 ? map.step_lens + b : (lane >= 2 && lane <= 4) ? ws + kTkWsCnt + (lane - 2) : map.status);
+  }
+
+  // The row's block-table slices, after the query's loads: they are first
+  // needed when the ranking is done, and registers held from the start
+  // would be reused (and waited for) by the query's address arithmetic.
+  __device__ __forceinline__ void load_bt() {
+    const int tid = threadIdx.x;
+#pragma unroll
+    for (int u = 0; u < kBtPer; ++u) {
+      if (u * kAtThreads >= n_bt) break;  // uniform: the row's slices only
+      btv[u] = bt_row[min(tid + u * kAtThreads, n_bt - 1)];
+    }
+  }
+
+  // Ranks the unit's candidates and writes its positions of the top-k row;
+  // returns its key count (picks >= 0, in output order).  Every thread calls
+  // it; the result is uniform.  Its barriers order LDS only, so the query's
+  // loads stay in flight through the ranking.
+  __device__ __forceinline__ int rank(AtSmem<NKS>& sm) {
+    const int tid = threadIdx.x;
+    int* scan = reinterpret_cast<int*>(&sm.vs[0][0]);
+    int* at_pos = scan + RL::kScan;
+    int* key_list = at_pos + kMaxTopK;
+    int32_t* bt = key_list + kMaxTopK;
+    keys = key_list;
+    bt_lds = bt;
+    uint64_t* ck = reinterpret_cast<uint64_t*>(&sm.kr[0][0]);
+    const int k = map.top_k[0];
+    // Every value of the first round trip is used here, by every wave: a
+    // load whose only use sits in a branch that some waves skip stays
+    // pending in the compiler's count, and the next write of its register
+    // then waits for every load in flight, the query's among them.
+    const uint64_t key_sh = order_key(sh), key_th = order_key(th);
+    status = __builtin_amdgcn_readlane(word, 0);
+    L = __builtin_amdgcn_readlane(word, 1);
+    cnt0 = __builtin_amdgcn_readlane(word, 2);
+    cnt1 = __builtin_amdgcn_readlane(word, 3);
+    flag = __builtin_amdgcn_readlane(word, 4);
+    for (int i = tid; i < k; i += kAtThreads) at_pos[i] = kPosEmpty;
+    if (status) return 0;  // refused step
+    const int gi = map.group[0];
+    int n_cols, n_valid;
+    score_cols(map.score_stride[0], map.m[gi], L, n_cols, n_valid);
+    const int sel = topk_sel(k, n_cols, n_valid);
+    const int out = static_cast<int>(ceil_div24(k, parts));
+    const int o0 = min(k, part * out), o1 = min(k, o0 + out);
+    lds_barrier();
+    if (sel > 0 && flag) {
+      // tie bin over the list capacity: full select of the row, keeping this
+      // unit's positions
+      auto& fb = *reinterpret_cast<TopkSmemT<kAtThreads>*>(ck);
+      topk_row_emit<kAtThreads>(fb, nullptr, map.scores[0] + static_cast<int64_t>(b) * map.score_stride[0], n_cols,
+                                n_valid, k, [&](int j, int v) {
+                                  if (j >= o0 && j < o1) at_pos[j] = v;
+                                });
+    } else if (sel > 0) {
+      const int S = min(cnt0, kMaxTopK);
+      const int T = min(cnt1, kTkTieCap);
+      const int C = S + T;
+      const int2* sure_list = reinterpret_cast<const int2*>(ws + kTkWsSure);
+      const int2* tie_list = reinterpret_cast<const int2*>(ws + kTkWsTie);
+      const bool in_lds = C <= RL::kCkCap;  // uniform
+      if (in_lds) {
+        if (tid < S) ck[tid] = key_sh;
+        if (tid < T) ck[S + tid] = key_th;
+        if (S > kAtThreads || T > kAtThreads) {  // uniform: the rest of the lists
+          constexpr int kLoad = 4;  // list loads in flight per thread
+          for (int c0 = tid; c0 < C; c0 += kAtThreads * kLoad) {
+            int2 v[kLoad];
+#pragma unroll
+            for (int u = 0; u < kLoad; ++u) {
+              const int c = min(c0 + u * kAtThreads, C - 1);  // unconditional: C >= sel > 0
+              v[u] = (c < S ? sure_list : tie_list - S)[c];
+            }
+#pragma unroll
+            for (int u = 0; u < kLoad; ++u) {
+              const int c = c0 + u * kAtThreads;
+              const bool in_head = c < S ? c < kAtThreads : c - S < kAtThreads;
+              // keyed unconditionally: a load used only under a branch that a
+              // wave may skip stays pending in the compiler's count, and later
+              // register reuse would then wait for every load in flight
+              const uint64_t key = order_key(v[u]);
+              asm volatile("" ::"v"(key));
+              if (c < C && !in_head) ck[c] = key;
+            }
+          }
+        }
+      }
+      lds_barrier();
+      const auto put = [&](int pos, int idx) { at_pos[pos] = idx; };
+      if (in_lds) {
+        rank_candidates<kAtThreads, 4>(put, [&](int q) { return ck[q]; }, S, C, sel, part, parts);
+      } else {
+        rank_candidates<kAtThreads>(put, [&](int q) { return order_key(q < S ? sure_list[q] : tie_list[q - S]); },
+                                    S, C, sel, part, parts);
+      }
+    }
+    for (int j = max(o0, sel) + tid; j < o1; j += kAtThreads) at_pos[j] = -1;  // the fills
+    lds_barrier();
+    // its picks >= 0 become the unit's keys, in output order (4 consecutive
+    // positions per thread, counts summed over the wave, then over the waves)
+    static_assert(4 * kAtThreads >= kMaxTopK, "positions per thread");
+    int v[4], cnt = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int pos = 4 * tid + i;
+      v[i] = pos < k ? at_pos[pos] : kPosEmpty;
+      cnt += v[i] >= 0;
+    }
+    const int lane = tid % kWave, wave = tid / kWave;
+    int incl = cnt;
+#pragma unroll
+    for (int off = 1; off < kWave; off <<= 1) {
+      const int o = __shfl_up(incl, off);
+      if (lane >= off) incl += o;
+    }
+    if (lane == kWave - 1) scan[wave] = incl;
+    lds_barrier();
+    int base = 0, total = 0;
+#pragma unroll
+    for (int w = 0; w < kAtWaves; ++w) {
+      const int c = scan[w];
+      base += w < wave ? c : 0;
+      total += c;
+    }
+    int at = base + incl - cnt;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      if (v[i] >= 0) key_list[at++] = v[i];
+    }
+#pragma unroll
+    for (int u = 0; u < kBtPer; ++u) {
+      if (u * kAtThreads >= n_bt) break;
+      if (tid + u * kAtThreads < n_bt) bt[tid + u * kAtThreads] = btv[u];
+    }
+    lds_barrier();
+    return total;
+  }
+
+  // The unit's global stores, after its last loads: every position it owns
+  // goes to the top-k row, and unit 0 clears the row's histogram for the
+  // next step (also after a refusal).  Stores issued while loads are in
+  // flight would make every later wait for a load wait for all of them (the
+  // compiler cannot count on a mix of loads and stores completing in order).
+  __device__ __forceinline__ void finish(AtSmem<NKS>& sm) {
+    if (!lead) return;
+    const int tid = threadIdx.x;
+    const int k = map.top_k[0];
+    if (part == 0) {
+      for (int i = tid; i < kTkBins; i += kAtThreads) ws[kTkWsHist + i] = 0;
+    }
+    if (status) return;
+    const int* at_pos = reinterpret_cast<const int*>(&sm.vs[0][0]) + RL::kScan;
+    for (int pos = tid; pos < k; pos += kAtThreads) {
+      const int v = at_pos[pos];
+      if (v != kPosEmpty) topk_idx[static_cast<int64_t>(b) * k + pos] = v;
+    }
+  }
+
+  // Pool row (page * block_size + slot) of key j, or -1.
+  __device__ __forceinline__ int64_t row(int j) const {
+    const int gi = map.group[0];
+    const int bs = map.block_size[gi];
+    const int e = keys[j];
+    if (e < 0 || e >= static_cast<int>(udiv24(static_cast<uint32_t>(max(L, 0)), map.m[gi]))) return -1;
+    const int pi = static_cast<int>(udiv24(e, bs));
+    if (pi >= map.bt_stride[gi]) return -1;
+    const int32_t page = pi < n_bt ? bt_lds[pi] : bt_row[pi];
+    if (page < 0 || page >= map.n_pages[gi]) return -1;
+    return static_cast<int64_t>(page) * bs + (e - pi * bs);
+  }
+};
+
+// The step's commit for sequence b (after a refusal: nothing).
+__device__ __forceinline__ void step_commit(const StepMap& map, int b) {
+  if (*map.status) return;
+  const int L = map.step_lens[b];
+  map.tok_lens[b] = L;
+  for (int g = 0; g < map.n_groups; ++g) map.n_entries[g][b] = udiv24(static_cast<uint32_t>(L), map.m[g]);
+  if (b == 0) {
+    for (int g = 0; g < map.n_groups; ++g) *map.free_top[g] = map.step_top[g];
+  }
+}
+
+// Units as k_attn_part places them.
+template <int NKS, bool kFp8>
+__global__ __launch_bounds__(kAtThreads, 1) void k_decode_attend(AttnArgs a, StepMap map, int32_t* topk_idx) {
+  __shared__ AtSmem<NKS> sm;
+  const int U = a.n_cu + a.n_wu;
+  const int per_seq = U * a.n_hg;
+  const int k = static_cast<int>(blockIdx.x) / kXcds;
+  const int sb = k / per_seq;
+  const int b = static_cast<int>(blockIdx.x) % kXcds + kXcds * sb;
+  if (b >= a.batch) return;  // uniform
+  const int r = k - sb * per_seq;
+  const int u = r / a.n_hg, hg = r - u * a.n_hg;
+  const int64_t unit = (static_cast<int64_t>(b) * U + u) * a.n_hg + hg;
+  if (u < a.n_cu) {
+    if constexpr (NKS >= 16) {  // the host refuses a CSA layer of head_dim <= 128
+      if (a.kind == SKV_LAYER_CSA) {
+        attn_unit<NKS, kFp8, true>(sm, a, b, 0, 1, hg, unit, StepRank<NKS>(map, topk_idx, b, u, a.n_cu, hg == 0));
+        return;
+      }
+    }
+    attn_unit<NKS, kFp8, true>(sm, a, b, u, a.n_cu, hg, unit);
+  } else {
+    if (u == a.n_cu && hg == 0 && threadIdx.x == 0) step_commit(map, b);
+    attn_unit<NKS, false, false>(sm, a, b, u - a.n_cu, a.n_wu, hg, unit);
+  }
+}
+
+int decode_attend(const skv_attention_desc* d, const skv_decode_desc* h, const StepMap* map, void* workspace,
+                  int64_t ws_bytes, hipStream_t s, int64_t* ws_need, bool call) {
+  const char* what = "skv_decode_step_attend";
+  if (!d) return set_error(SKV_EINVAL, "%s: NULL attention descriptor", what);
+  if (h->n_layers != 1) return set_error(SKV_EINVAL, "%s: the step must have exactly one layer", what);
+  const skv_decode_layer& Ly = h->layers[0];
+  if (Ly.out_entries || Ly.out_window) {
+    return set_error(SKV_EINVAL, "%s: the layer must not write gathered copies (out_entries / out_window)", what);
+  }
+  if (d->head_dim != h->latent || d->batch != h->batch) {
+    return set_error(SKV_EINVAL, "%s: head_dim must equal the step's latent and batch its batch", what);
+  }
+  const bool comp = Ly.kind != SKV_LAYER_SWA;
+  if (comp && (Ly.group < 0 || Ly.group >= h->n_groups)) return set_error(SKV_EINVAL, "%s: layer group out of range", what);
+  if (Ly.kind == SKV_LAYER_CSA && d->head_dim <= 128) {
+    return set_error(SKV_EINVAL, "%s: a CSA layer needs head_dim > 128", what);
+  }
+  // the attention over the step's own cache
+  skv_attention_desc x = *d;
+  x.kind = Ly.kind;
+  x.format = Ly.format;
+  x.lens = h->step_lens;
+  x.win_k = Ly.ring;
+  if (!x.win_v) x.win_v = Ly.ring;
+  x.window = h->window;
+  if (comp) {
+    const skv_page_group& G = h->groups[Ly.group];
+    x.pool = Ly.pool;
+    x.entry_bytes = Ly.entry_bytes;
+    x.block_size = G.block_size;
+    x.n_pages = G.n_pages;
+    x.block_table = G.block_table;
+    x.bt_stride = G.bt_stride;
+    x.n_entries = G.n_entries;
+    x.m = G.m;
+    if (Ly.kind == SKV_LAYER_CSA) {
+      x.picks = Ly.topk_idx;
+      x.pick_stride = Ly.top_k;
+      x.top_k = Ly.top_k;
+    }
+  }
+  AttnPlan p;
+  int rc = attn_plan(&x, p);
+  if (rc != SKV_OK) return rc;
+  if (ws_need) *ws_need = p.ws_bytes;
+  if (!call) return SKV_OK;
+  if (!x.q || !x.out || (comp && !x.knorm_w)) return set_error(SKV_EINVAL, "%s: NULL q/out/knorm_w", what);
+  if (!workspace || ws_bytes < p.ws_bytes) {
+    return set_error(SKV_EINVAL, "%s: workspace of %lld bytes needed", what, (long long)p.ws_bytes);
+  }
+  if (reinterpret_cast<uintptr_t>(workspace) & 15) {
+    return set_error(SKV_EINVAL, "%s: workspace must be 16-byte aligned", what);
+  }
+  if (!map) return SKV_OK;
+  AttnArgs a;
+  a.q = static_cast<const uint8_t*>(x.q);
+  a.part = static_cast<float*>(workspace);
+  a.lens = x.lens;
+  a.pool = static_cast<const uint8_t*>(x.pool);
+  a.block_table = x.block_table;
+  a.n_entries = x.n_entries;
+  a.picks = x.picks;
+  a.knorm_w = x.knorm_w;
+  a.win_k = static_cast<const uint8_t*>(x.win_k);
+  a.win_v = static_cast<const uint8_t*>(x.win_v);
+  a.entry_bytes = comp ? x.entry_bytes : 0;
+  a.pick_stride = x.pick_stride;
+  a.kind = x.kind;
+  a.fp8_main = comp && x.format == SKV_FMT_FP8 ? entry_layout(x.format, x.head_dim, x.entry_bytes) : 0;
+  a.block_size = static_cast<int32_t>(comp ? x.block_size : 1);
+  a.n_pages = static_cast<int32_t>(comp ? x.n_pages : 1);
+  a.bt_stride = static_cast<int32_t>(comp ? x.bt_stride : 1);
+  a.m = static_cast<int32_t>(x.kind == SKV_LAYER_HCA ? x.m : 1);
+  a.top_k = static_cast<int32_t>(x.kind == SKV_LAYER_CSA ? x.top_k : 0);
+  a.window = static_cast<int32_t>(x.window);
+  a.H = static_cast<int32_t>(x.n_heads);
+  a.D = static_cast<int32_t>(x.head_dim);
+  a.n_hg = p.n_hg;
+  a.n_cu = p.n_cu;
+  a.n_wu = p.n_wu;
+  a.batch = static_cast<int32_t>(x.batch);
+  a.eps = x.eps;
+  a.softcap = x.softcap;
+  a.fused = 1;
+  const dim3 grid(static_cast<unsigned>(kXcds * ceil_div(x.batch, kXcds) * (p.n_cu + p.n_wu) * p.n_hg));
+  int32_t* idx = Ly.kind == SKV_LAYER_CSA ? Ly.topk_idx : nullptr;
+  if (a.fp8_main > 0) {
+    hipLaunchKernelGGL((k_decode_attend<18, true>), grid, dim3(kAtThreads), 0, s, a, *map, idx);
+  } else if (p.nks == 4) {
+    hipLaunchKernelGGL((k_decode_attend<4, false>), grid, dim3(kAtThreads), 0, s, a, *map, idx);
+  } else if (p.nks == 16) {
+    hipLaunchKernelGGL((k_decode_attend<16, false>), grid, dim3(kAtThreads), 0, s, a, *map, idx);
+  } else {
+    hipLaunchKernelGGL((k_decode_attend<18, false>), grid, dim3(kAtThreads), 0, s, a, *map, idx);
+  }
+  if ((rc = check_launch(what))) return rc;
+  return launch_merge(a, p, x.kind, comp ? x.knorm_w : nullptr, x.sink, x.out, s, what);
+}
 }  // namespace skv
 
 using namespace skv;
@@ -912,6 +1357,7 @@ extern "C" int skv_decode_attention(const skv_attention_desc* d, void* workspace
   a.batch = static_cast<int32_t>(d->batch);
   a.eps = d->eps;
   a.softcap = d->softcap;
+  a.fused = 0;
   hipStream_t s = static_cast<hipStream_t>(stream);
   const dim3 grid(static_cast<unsigned>(kXcds * ceil_div(d->batch, kXcds) * (p.n_cu + p.n_wu) * p.n_hg));
   if (a.fp8_main > 0) {
@@ -924,26 +1370,5 @@ extern "C" int skv_decode_attention(const skv_attention_desc* d, void* workspace
     hipLaunchKernelGGL((k_attn_part<18, false>), grid, dim3(kAtThreads), 0, s, a);
   }
   if ((rc = check_launch(what))) return rc;
-  MergeArgs mg;
-  mg.part = a.part;
-  mg.out = d->out;
-  mg.knorm_w = comp ? d->knorm_w : nullptr;
-  mg.sink = d->sink;
-  mg.H = a.H;
-  mg.D = a.D;
-  mg.n_hg = p.n_hg;
-  mg.n_cu = p.n_cu;
-  mg.n_wu = p.n_wu;
-  mg.sink_comp = d->kind == SKV_LAYER_HCA;
-  if (p.n_cu + p.n_wu <= kMergeChunkQ) {
-    hipLaunchKernelGGL(k_attn_merge_q,
-                       dim3(static_cast<unsigned>(d->batch), static_cast<unsigned>(ceil_div(d->n_heads, 4)),
-                            static_cast<unsigned>(ceil_div(d->head_dim / 4, kWave))),
-                       dim3(256), 0, s, mg);
-  } else {
-    hipLaunchKernelGGL(k_attn_merge,
-                       dim3(static_cast<unsigned>(d->batch), static_cast<unsigned>(ceil_div(d->n_heads, 4)), 2),
-                       dim3(256), 0, s, mg);
-  }
-  return check_launch(what);
+  return launch_merge(a, p, d->kind, comp ? d->knorm_w : nullptr, d->sink, d->out, s, what);
 }

@@ -82,6 +82,8 @@ SIGNATURES: dict[str, list] = {
     "skv_decode_desc_sizes": [_P],
     "skv_attention_workspace": [_P],
     "skv_decode_attention": [_P, _P, _I64, _P],
+    "skv_decode_step_attend_workspace": [_P, _P],
+    "skv_decode_step_attend": [_P, _P, _P, _P, _I64, _P],
     "skv_attention_desc_size": [],
     "skv_compact": [ctypes.c_void_p, _I32, _P, _I64, _P, _I64, _I64, _I64, _P, _P, _P, _P, _P],
 }
@@ -104,7 +106,8 @@ class PoolRef(ctypes.Structure):
     _fields_ = [("base", ctypes.c_void_p), ("page_bytes", ctypes.c_int64)]
 
 # entry points returning a size rather than a status code
-INT64_RESULTS = {"skv_topk_workspace_words", "skv_attention_workspace", "skv_attention_desc_size"}
+INT64_RESULTS = {"skv_topk_workspace_words", "skv_attention_workspace", "skv_attention_desc_size",
+                 "skv_decode_step_attend_workspace"}
 
 _lib: ctypes.CDLL | None = None
 

@@ -170,6 +170,51 @@ def decode_attention(q: torch.Tensor, kind: str, lens: torch.Tensor, win_k: torc
 _LAST_WS: torch.Tensor | None = None
 
 
+def step_attention_desc(q: torch.Tensor, kind: str, window: int, *, knorm_w: torch.Tensor | None = None,
+                        eps: float = 1.0e-6, sink: torch.Tensor | None = None, softcap: float | None = None,
+                        win_v: torch.Tensor | None = None, out: torch.Tensor | None = None,
+                        max_entries: int = 0, splits: int = 0) -> tuple[AttentionDesc, torch.Tensor]:
+    """The caller's fields of skv_decode_step_attend's attention descriptor:
+    q (bf16 [B, H, D]), out (fp32 [B, H, D], allocated when None), knorm_w
+    (fp32 [D], "csa"/"hca"), eps, sink (fp32 [H] or None), softcap, win_v
+    (bf16 [B, window, D] value ring, or None for the layer's own ring: K = V)
+    and the split bounds.  The cache's fields come from the step's descriptor.
+    Returns (descriptor, out)."""
+    _check_layout()
+    if kind not in KIND:
+        raise ValueError(f"kind must be one of {sorted(KIND)}; got {kind!r}")
+    _require_gpu(q, "q")
+    if q.dtype != torch.bfloat16 or q.dim() != 3 or not q.is_contiguous():
+        raise ValueError("q must be a contiguous bf16 [B, H, D] tensor")
+    batch, heads, dim = q.shape
+    d = AttentionDesc()
+    d.kind = KIND[kind]
+    d.batch, d.n_heads, d.head_dim = batch, heads, dim
+    d.q = q.data_ptr()
+    d.eps = eps
+    if softcap is not None and softcap <= 0:
+        raise ValueError("softcap must be positive (or None)")
+    d.softcap = 0.0 if softcap is None else float(softcap)
+    if sink is not None:
+        _f32_vec(sink, "sink", heads)
+        d.sink = sink.data_ptr()
+    if win_v is not None:
+        _bf16_rows(win_v, "win_v", (batch, window, dim))
+        d.win_v = win_v.data_ptr()
+    if kind != "swa":
+        if knorm_w is None:
+            raise ValueError(f"{kind} attention needs knorm_w")
+        _f32_vec(knorm_w, "knorm_w", dim)
+        d.knorm_w = knorm_w.data_ptr()
+    d.max_entries, d.splits = int(max_entries), int(splits)
+    if out is None:
+        out = torch.empty(batch, heads, dim, dtype=torch.float32, device=q.device)
+    elif out.dtype != torch.float32 or tuple(out.shape) != (batch, heads, dim) or not out.is_contiguous():
+        raise ValueError(f"out must be a contiguous fp32 [{batch}, {heads}, {dim}] tensor")
+    d.out = out.data_ptr()
+    return d, out
+
+
 def last_workspace() -> torch.Tensor | None:
     """The workspace the last decode_attention call used (allocated by it when
     none was passed), for callers that keep it for later calls."""

@@ -320,6 +320,51 @@ class DecodeCache:
         d, d_dev = self._descs[input_set]
         _lib.call("skv_decode_step", ctypes.addressof(d), d_dev.data_ptr(), _lib.stream_handle(self.device))
 
+    def step_attend(self, q: torch.Tensor, knorm_w: torch.Tensor | None = None,
+                    sink: torch.Tensor | None = None, softcap: float | None = None,
+                    v_ring: torch.Tensor | None = None, eps: float = 1.0e-6,
+                    out: torch.Tensor | None = None, input_set: int = 0) -> torch.Tensor:
+        """One decode step of this one-layer cache followed by the layer's
+        attention for the new token's query q (bf16 [batch, H, latent]), as
+        ``step(input_set)`` then ``attention(0, q, ...)`` give them, in one
+        call of skv_decode_step_attend: the attention launch ranks the top-k
+        picks itself (writing ``topk_idx``) and takes the place of the step's
+        gather launch.  Needs ``materialize=False`` (no gathered copies).
+        Returns the fp32 [batch, H, latent] output (``out`` when given).  After
+        a refused step (``check_status`` raises) the output is undefined."""
+        if (self.host_lens + 1 > self.max_len).any():
+            raise RuntimeError(f"DecodeCache overflow: a sequence would exceed max_len={self.max_len}")
+        out = self._launch_step_attend(input_set, q, knorm_w, sink, softcap, v_ring, eps, out)
+        self.host_lens += 1
+        return out
+
+    def _launch_step_attend(self, input_set: int, q: torch.Tensor, knorm_w: torch.Tensor | None,
+                            sink: torch.Tensor | None, softcap: float | None, v_ring: torch.Tensor | None,
+                            eps: float, out: torch.Tensor | None) -> torch.Tensor:
+        from saint_kv.attention import step_attention_desc
+
+        if len(self.layers) != 1:
+            raise ValueError("step_attend needs a one-layer cache")
+        if self.out_window[0] is not None or self.out_entries[0] is not None:
+            raise ValueError("step_attend needs a cache built with materialize=False")
+        spec = self.layers[0]
+        if q.shape[0] != self.batch or q.dim() != 3 or q.shape[2] != self.latent:
+            raise ValueError(f"q must be bf16 [{self.batch}, H, {self.latent}]")
+        ad, out = step_attention_desc(q, spec.kind, self.window, knorm_w=knorm_w, eps=eps, sink=sink,
+                                      softcap=softcap, win_v=v_ring, out=out)
+        d, d_dev = self._descs[input_set]
+        lib = _lib.load()
+        need = int(lib.skv_decode_step_attend_workspace(ctypes.addressof(d), ctypes.byref(ad)))
+        if need < 0:
+            _lib.check(-1, "skv_decode_step_attend_workspace")
+        ws = self._attn_ws.get("step")
+        if ws is None or ws.numel() * 4 < need:  # allocated once (not while a graph is captured)
+            ws = torch.empty(max(need, 4) // 4 + 1, dtype=torch.float32, device=self.device)
+            self._attn_ws["step"] = ws
+        _lib.call("skv_decode_step_attend", ctypes.addressof(d), d_dev.data_ptr(), ctypes.byref(ad),
+                  ws.data_ptr(), ws.numel() * 4, _lib.stream_handle(self.device))
+        return out
+
     def capture(self, steps: int, before_step=None) -> "CapturedSteps":
         """Capture ``steps`` decode steps in one HIP graph (see CapturedSteps);
         step s reads input set s % input_sets.  ``before_step()`` (optional)

@@ -165,3 +165,60 @@ def test_decode_step_score_fields_checked_on_host() -> None:
     no_stream.layers[1].idx_q, no_stream.layers[1].idx_w, no_stream.layers[1].idx_heads = fake, fake, 8
     no_stream.layers[1].idx_pool = None
     assert step(no_stream) == _lib.SKV_EINVAL
+
+
+def test_step_attend_checked_on_host() -> None:
+    """skv_decode_step_attend's workspace query and argument checks run on the
+    host before any device work: one layer, no gathered copies, head_dim equal
+    to the latent, the batch of the step, a workspace large enough.  Pointers
+    are placeholders, never dereferenced on these paths."""
+    import ctypes
+
+    from saint_kv import _lib
+    from saint_kv.attention import KIND, AttentionDesc
+    from saint_kv.decode import DecodeDescC
+
+    lib = _lib.load()
+    fake = 0x1000
+    d = DecodeDescC()
+    d.batch, d.n_layers, d.n_groups = 16, 1, 1
+    d.latent, d.c_indexer, d.window = 576, 128, 128
+    d.tok_lens = d.status = d.step_lens = d.step_top = fake
+    G = d.groups[0]
+    G.free_stack = G.free_top = G.block_table = G.n_entries = fake
+    G.n_pages, G.bt_stride, G.m, G.block_size = 4096, 256, 4, 64
+    Ly = d.layers[0]
+    Ly.kind, Ly.group, Ly.format, Ly.top_k = KIND["csa"], 0, _lib.SKV_FMT_BF16, 512
+    Ly.ring = Ly.kv_new = Ly.pool = Ly.state = Ly.bias = fake
+    Ly.c_new = Ly.z_new = Ly.scores = Ly.topk_idx = Ly.topk_ws = fake
+    Ly.entry_bytes, Ly.score_stride = 1152, 16384
+    Ly.idx_pool = Ly.idx_state = Ly.idx_bias = Ly.ci_new = Ly.zi_new = fake
+    a = AttentionDesc()
+    a.batch, a.n_heads, a.head_dim = 16, 64, 576
+    a.q = a.out = a.knorm_w = fake
+    ws = lib.skv_decode_step_attend_workspace(ctypes.byref(d), ctypes.byref(a))
+    # the same units as skv_decode_attention over the layer: a multiple of the batch
+    per_unit = 64 * (8 + 2 * 576)
+    assert ws > 0 and ws % (16 * per_unit) == 0
+
+    def call(desc, attn, ws_bytes=ws):
+        return lib.skv_decode_step_attend(ctypes.byref(desc), ctypes.c_void_p(fake), ctypes.byref(attn),
+                                          ctypes.c_void_p(fake), ws_bytes, None)
+
+    assert call(d, a, ws - 16) == _lib.SKV_EINVAL and "workspace" in _lib.last_error()
+    two = DecodeDescC.from_buffer_copy(d)
+    two.n_layers = 2
+    two.layers[1] = d.layers[0]
+    assert call(two, a) == _lib.SKV_EINVAL and "one layer" in _lib.last_error()
+    assert lib.skv_decode_step_attend_workspace(ctypes.byref(two), ctypes.byref(a)) == -1
+    copies = DecodeDescC.from_buffer_copy(d)
+    copies.layers[0].out_window = fake
+    assert call(copies, a) == _lib.SKV_EINVAL and "gathered copies" in _lib.last_error()
+    for field, value in (("head_dim", 512), ("batch", 8)):
+        bad = AttentionDesc.from_buffer_copy(a)
+        setattr(bad, field, value)
+        assert call(d, bad) == _lib.SKV_EINVAL and "head_dim" in _lib.last_error()
+    no_q = AttentionDesc.from_buffer_copy(a)
+    no_q.q = None
+    assert call(d, no_q) == _lib.SKV_EINVAL
+    assert lib.skv_decode_step_attend(ctypes.byref(d), ctypes.c_void_p(fake), None, None, 0, None) == _lib.SKV_EINVAL
