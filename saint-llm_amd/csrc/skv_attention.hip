@@ -968,8 +968,20 @@ struct StepRank {
   const int* keys = nullptr;
   const int32_t* bt_lds = nullptr;
 
+  // the layer's group fields, read from the kernel arguments once, at the
+  // unit's start (read where they are used, a computed index into the
+  // arguments makes them dependent scalar loads on the unit's path)
+  int k = 0, m = 1, bs = 1, bt_stride = 1, n_pages = 1;
+
   __device__ StepRank(const StepMap& m_, int32_t* idx, int b_, int part_, int parts_, bool lead_)
-      : map(m_), topk_idx(idx), b(b_), part(part_), parts(parts_), lead(lead_) {}
+      : map(m_), topk_idx(idx), b(b_), part(part_), parts(parts_), lead(lead_) {
+    const int gi = map.group[0];
+    k = map.top_k[0];
+    m = map.m[gi];
+    bs = map.block_size[gi];
+    bt_stride = map.bt_stride[gi];
+    n_pages = map.n_pages[gi];
+  }
 
   // The ranking's loads, unconditional (clamped indices), ahead of the
   // query's: the heads of both lists, and the status, length and list
@@ -981,8 +993,8 @@ struct StepRank {
     const int tid = threadIdx.x;
     const int gi = map.group[0];
     ws = map.topk_ws[0] + static_cast<int64_t>(b) * kTkWsWords;
-    bt_row = map.block_table[gi] + static_cast<int64_t>(b) * map.bt_stride[gi];
-    n_bt = min(map.bt_stride[gi], RL::kBtCap);
+    bt_row = map.block_table[gi] + static_cast<int64_t>(b) * bt_stride;
+    n_bt = min(bt_stride, RL::kBtCap);
     static_assert(kAtThreads <= kMaxTopK && kAtThreads <= kTkTieCap, "list heads within the lists");
     sh = reinterpret_cast<const int2*>(ws + kTkWsSure)[tid];
     th = reinterpret_cast<const int2*>(ws + kTkWsTie)[tid];
@@ -1015,7 +1027,6 @@ struct StepRank {
     keys = key_list;
     bt_lds = bt;
     uint64_t* ck = reinterpret_cast<uint64_t*>(&sm.kr[0][0]);
-    const int k = map.top_k[0];
     // Every value of the first round trip is used here, by every wave: a
     // load whose only use sits in a branch that some waves skip stays
     // pending in the compiler's count, and the next write of its register
@@ -1028,9 +1039,8 @@ struct StepRank {
     flag = __builtin_amdgcn_readlane(word, 4);
     for (int i = tid; i < k; i += kAtThreads) at_pos[i] = kPosEmpty;
     if (status) return 0;  // refused step
-    const int gi = map.group[0];
     int n_cols, n_valid;
-    score_cols(map.score_stride[0], map.m[gi], L, n_cols, n_valid);
+    score_cols(map.score_stride[0], m, L, n_cols, n_valid);
     const int sel = topk_sel(k, n_cols, n_valid);
     const int out = static_cast<int>(ceil_div24(k, parts));
     const int o0 = min(k, part * out), o1 = min(k, o0 + out);
@@ -1135,7 +1145,6 @@ struct StepRank {
   __device__ __forceinline__ void finish(AtSmem<NKS>& sm) {
     if (!lead) return;
     const int tid = threadIdx.x;
-    const int k = map.top_k[0];
     if (part == 0) {
       for (int i = tid; i < kTkBins; i += kAtThreads) ws[kTkWsHist + i] = 0;
     }
@@ -1149,14 +1158,12 @@ struct StepRank {
 
   // Pool row (page * block_size + slot) of key j, or -1.
   __device__ __forceinline__ int64_t row(int j) const {
-    const int gi = map.group[0];
-    const int bs = map.block_size[gi];
     const int e = keys[j];
-    if (e < 0 || e >= static_cast<int>(udiv24(static_cast<uint32_t>(max(L, 0)), map.m[gi]))) return -1;
+    if (e < 0 || e >= static_cast<int>(udiv24(static_cast<uint32_t>(max(L, 0)), m))) return -1;
     const int pi = static_cast<int>(udiv24(e, bs));
-    if (pi >= map.bt_stride[gi]) return -1;
+    if (pi >= bt_stride) return -1;
     const int32_t page = pi < n_bt ? bt_lds[pi] : bt_row[pi];
-    if (page < 0 || page >= map.n_pages[gi]) return -1;
+    if (page < 0 || page >= n_pages) return -1;
     return static_cast<int64_t>(page) * bs + (e - pi * bs);
   }
 };
