@@ -205,16 +205,18 @@ def cpu_baseline(seconds: float = 10.0, seed: int = 0) -> dict:
 # Decode-step legs: heterogeneous compressed cache (CSA / HCA / SWA layers)
 # ---------------------------------------------------------------------------
 def decode_step_bytes(specs, lens_after: np.ndarray, window: int, latent: int = 576,
-                      c_indexer: int = 128, bs: int = 64) -> int:
+                      c_indexer: int = 128, bs: int = 64, copies: bool = True) -> int:
     """Compulsory HBM bytes of one fused decode step, for the sequences'
     token counts after the step: reads + writes of every row, entry, state,
-    score and index the step touches (the formula is stated in the design notes)."""
+    score and index the step touches (the formula is stated in the design notes).
+    ``copies=False``: a step that writes no gathered copies (the picks' and
+    window's rows are then the attention's reads, not the step's)."""
     L = lens_after.astype(np.int64)
     p = L - 1
     E = latent * 2
     total = 0
     for s in specs:
-        cnt = np.minimum(L, window)
+        cnt = np.minimum(L, window) if copies else np.zeros_like(L)
         total += int((2 * E + 2 * cnt * E).sum())  # token in + ring write; window read + write
         if s.kind == "swa":
             continue
@@ -235,8 +237,9 @@ def decode_step_bytes(specs, lens_after: np.ndarray, window: int, latent: int = 
             total += int((n_valid * 4 + s.top_k * 4).sum())  # scores read, indices written
             if s.idx_heads:  # scores computed in the step: indexer keys, query and weights read, scores written
                 total += int((n_valid * (c_indexer * 2 + 4) + s.idx_heads * (c_indexer * 2 + 4)).sum())
-            total += int((k_eff * (ent_bytes + E + 8) + (s.top_k - k_eff) * E).sum())
-        else:
+            if copies:
+                total += int((k_eff * (ent_bytes + E + 8) + (s.top_k - k_eff) * E).sum())
+        elif copies:
             total += int((n_ent * (ent_bytes + E) + (-(-n_ent // bs)) * 4).sum())
     return total
 
@@ -435,7 +438,8 @@ def cpu_baseline_decode(seconds: float = 5.0, seed: int = 0) -> dict:
 
 def run_layer_seq_leg(dev, n_layers: int = 8, batch: int = 16, L: int = 65536, steps: int = 100,
                       per_graph: int = 10, heads: int = 64, window: int = 128, seed: int = 8,
-                      mode: str = "fused") -> dict:
+                      mode: str = "fused", kinds: list | None = None, lens: np.ndarray | None = None,
+                      name: str = "layer_seq_64k") -> dict:
     """What a model's decode step sees at 64k context: n_layers CSA layers
     (m=4, top-k 512, W=128), one after another, each layer's cache step
     followed by its decode attention over the step's picks and window (the
@@ -446,22 +450,30 @@ def run_layer_seq_leg(dev, n_layers: int = 8, batch: int = 16, L: int = 65536, s
     attention launch ranks the picks itself, in place of the step's gather
     launch); "separate", skv_decode_step then skv_decode_attention;
     "materialize", the same with the step's gathered copies written.  The
-    attention reads the picks' entries and the window rows in place."""
+    attention reads the picks' entries and the window rows in place.
+    ``kinds`` (default all "csa") alternates CSA (m=4, top-k 512) and HCA
+    (m=128) layers; ``lens`` gives ragged lengths (default L each)."""
     from saint_kv.decode import DecodeCache, LayerSpec
 
-    max_len = L + steps + 2 * per_graph + 8
+    kinds = kinds or ["csa"] * n_layers
+    n_layers = len(kinds)
+    lens = np.full(batch, L, dtype=np.int64) if lens is None else np.asarray(lens, dtype=np.int64)
+    specs = [LayerSpec("csa", m=4, top_k=512) if kd == "csa" else LayerSpec("hca", m=128) for kd in kinds]
+    max_len = int(lens.max()) + steps + 2 * per_graph + 8
     gen = torch.Generator(device=dev).manual_seed(seed)
     caches, qs, knorm, outs = [], [], [], []
-    for li in range(n_layers):
-        c = DecodeCache([LayerSpec("csa", m=4, top_k=512)], batch, max_len, window=window, device=dev,
-                        page_order_seed=seed + li, input_sets=per_graph, materialize=mode == "materialize")
+    for li, spec in enumerate(specs):
+        c = DecodeCache([spec], batch, max_len, window=window, device=dev, page_order_seed=seed + li,
+                        input_sets=per_graph, materialize=mode == "materialize")
         c.bias[0].normal_(generator=gen)
-        c.idx_bias[0].normal_(generator=gen)
+        if c.idx_bias[0] is not None:
+            c.idx_bias[0].normal_(generator=gen)
         for k in range(per_graph):
             for v in c.inputs_by_set[k][0].values():
                 v.normal_(generator=gen)
-            c.scores_by_set[k][0].normal_(generator=gen)
-        c.prefill(np.full(batch, L), generator=gen)
+            if c.scores_by_set[k][0] is not None:
+                c.scores_by_set[k][0].normal_(generator=gen)
+        c.prefill(lens, generator=gen)
         caches.append(c)
         qs.append(torch.empty(batch, heads, 576, dtype=torch.bfloat16, device=dev).normal_(generator=gen))
         knorm.append(torch.empty(576, dtype=torch.float32, device=dev).uniform_(0.5, 1.5, generator=gen))
@@ -498,18 +510,41 @@ def run_layer_seq_leg(dev, n_layers: int = 8, batch: int = 16, L: int = 65536, s
         c.host_lens += reps * per_graph
         c.check_status()
     us = e0.elapsed_time(e1) * 1e3 / (reps * per_graph)
+    # bytes of the layers: their steps (gathered copies only when
+    # materialized) and their attention's reads of the picked or visible
+    # entries, the K/V window, the query, the pick rows and block-table
+    # slots, and its output
+    lens_after = lens + 1
+    cnt = np.minimum(lens_after, window)
+    model_bytes = 0
+    for spec in specs:
+        if spec.kind == "csa":
+            keys = np.minimum(lens_after // spec.m, spec.top_k)
+            meta = batch * spec.top_k * 4 + int(keys.sum()) * 4
+        else:
+            keys = (lens_after - 1) // spec.m
+            meta = int((-(-keys // 64)).sum()) * 4
+        model_bytes += (int(keys.sum()) * 576 * 2 + int(cnt.sum()) * 576 * 4 + batch * heads * 576 * 6
+                        + meta + batch * 8)
+        model_bytes += decode_step_bytes([spec], lens_after, window, copies=mode == "materialize")
+    layer_bytes = model_bytes / n_layers
+    gbs = model_bytes / (us * 1e-6) / 1e9
+    what = (f"{n_layers} CSA layers (m=4, top-k 512, W=128)" if all(kd == "csa" for kd in kinds) else
+            f"{n_layers} layers alternating CSA (m=4, top-k 512) and HCA (m=128), each with W=128")
     rec = {
-        "workload": f"{n_layers} CSA layers (m=4, top-k 512, W=128) in sequence, B={batch}, L={L}: per layer "
-                    f"one decode step, then its decode attention ({heads} heads x 576) over the picks",
+        "workload": f"{what} in sequence, B={batch}, L in [{int(lens.min())}, {int(lens.max())}]: per layer "
+                    f"one decode step, then its decode attention ({heads} heads x 576) over its picks or entries",
         "model_steps": reps * per_graph, "us_per_model_step": round(us, 2),
         "us_per_layer": round(us / n_layers, 2),
         "mode": mode,
         "launches_per_layer": caches[0].step_launches() + (1 if mode == "fused" else 2),
         "gathered_copies": mode == "materialize",
-        "kv_tokens_per_s": round(n_layers * batch * (512 + window) / (us * 1e-6), 1),
+        "kv_tokens_per_s": round(sum(decode_kv_tokens([sp], lens_after, window) for sp in specs) / (us * 1e-6), 1),
+        "alg_bytes_per_layer": int(layer_bytes), "gbs": round(gbs, 1),
+        "pct_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 2),
     }
-    log(f"layer_seq_64k ({mode}): {rec['us_per_model_step']} us per {n_layers}-layer model step, "
-        f"{rec['us_per_layer']} us per layer (step + attention)")
+    log(f"{name} ({mode}): {rec['us_per_model_step']} us per {n_layers}-layer model step, "
+        f"{rec['us_per_layer']} us per layer (step + attention), {rec['gbs']} GB/s ({rec['pct_hbm_peak']}%)")
     del caches
     torch.cuda.empty_cache()
     return rec
@@ -708,7 +743,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
-    ap.add_argument("--legs", default="csa_64k,csa_64k_b256,csa_64k_idx,mixed_8layer,fp8_1m,layer_seq_64k",
+    ap.add_argument("--legs", default="csa_64k,csa_64k_b256,csa_64k_idx,mixed_8layer,fp8_1m,layer_seq_64k,"
+                    "layer_seq_mixed",
                     help="comma list of decode-step legs to run after the headline ('' for none)")
     ap.add_argument("--leg-steps", type=int, default=200)
     ap.add_argument("--no-indexer", action="store_true", help="skip the indexer-score leg")
@@ -817,6 +853,15 @@ def main() -> int:
         layer_seq = run_layer_seq_leg(dev, mode="fused")
         layer_seq["separate"] = run_layer_seq_leg(dev, mode="separate")
         layer_seq["with_gathered_copies"] = run_layer_seq_leg(dev, mode="materialize")
+    layer_seq_mixed = None
+    if "layer_seq_mixed" in wanted:
+        # the 8-layer CSA/HCA stack of mixed_8layer (B=32, L~U[32k,128k]) as a model steps it
+        mixed_lens = np.random.default_rng(4).integers(32768, 131073, size=32)
+        kinds = ["csa", "hca"] * 4
+        layer_seq_mixed = run_layer_seq_leg(dev, batch=32, mode="fused", kinds=kinds, lens=mixed_lens,
+                                            name="layer_seq_mixed")
+        layer_seq_mixed["separate"] = run_layer_seq_leg(dev, batch=32, mode="separate", kinds=kinds,
+                                                        lens=mixed_lens, name="layer_seq_mixed")
     indexer = None if args.no_indexer else run_indexer_leg(dev, 16, 16384, 64, 128, 200)
     state_io = None if args.no_state else run_state_leg(dev)
     attention = {}
@@ -879,6 +924,7 @@ def main() -> int:
         "decode_kv_tokens_per_s_64k": legs.get("csa_64k", {}).get("kv_tokens_per_s"),
         "decode_legs": legs,
         "layer_seq_64k": layer_seq,
+        "layer_seq_mixed": layer_seq_mixed,
         "indexer_64k": indexer,
         "attention": attention or None,
         "state_64k": state_io,
