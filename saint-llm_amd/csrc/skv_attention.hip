@@ -872,6 +872,12 @@ int attn_plan(const skv_attention_desc* d, AttnPlan& p) {
       }
     }
   }
+  if (d->splits <= 0 && d->kind == SKV_LAYER_CSA && n_wu > 1) {
+    // a CSA unit resolves its picks (or ranks them) before its tiles, so
+    // window units of two tiles still end before it; fewer units leave the
+    // merge fewer partial outputs
+    n_wu = std::max<int64_t>(1, std::min<int64_t>(n_wu, ceil_div(tiles_w, 2)));
+  }
   if (n_cu + n_wu > kMergeUnits) {
     return set_error(SKV_EINVAL, "%s: at most %d splits per sequence", what, kMergeUnits);
   }
@@ -1250,14 +1256,6 @@ int decode_attend(const skv_attention_desc* d, const skv_decode_desc* h, const S
   AttnPlan p;
   int rc = attn_plan(&x, p);
   if (rc != SKV_OK) return rc;
-  if (Ly.kind == SKV_LAYER_CSA && x.splits <= 0 && p.n_wu > 1) {
-    // a CSA unit ranks before its tiles, so window units of two tiles still
-    // end before it; fewer units leave the merge fewer partial outputs
-    const int64_t tiles_w = ceil_div(x.window, kAtTile);
-    p.n_wu = static_cast<int>(std::max<int64_t>(1, std::min<int64_t>(p.n_wu, ceil_div(tiles_w, 2))));
-    p.ws_bytes = x.batch * (p.n_cu + p.n_wu) * p.n_hg * kAtHeads *
-                 (2 * static_cast<int64_t>(sizeof(float)) + x.head_dim * 2);
-  }
   if (ws_need) *ws_need = p.ws_bytes;
   if (!call) return SKV_OK;
   if (!x.q || !x.out || (comp && !x.knorm_w)) return set_error(SKV_EINVAL, "%s: NULL q/out/knorm_w", what);
