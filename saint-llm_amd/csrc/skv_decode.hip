@@ -928,9 +928,9 @@ __host__ __device__ constexpr int64_t rank_lds_bytes(int bt_lds, int ck_cap) {
 // longer than the launch's LDS holds, on the lists in global memory), page
 // lookups read the LDS table, and the entry copy is the last round trip.
 template <bool kWB>
-__device__ __forceinline__ void rank_part(const skv_decode_desc* __restrict__ d, const StepMap& map,
-                                          uint8_t* rank_lds, int part, int b, int z, int rank_out, int bt_lds,
-                                          int ck_cap) {
+__device__ __forceinline__ void rank_part_body(const skv_decode_desc* __restrict__ d, const StepMap& map,
+                                               uint8_t* rank_lds, int part, int b, int z, int rank_out, int bt_lds,
+                                               int ck_cap) {
   RankHead& sm = *reinterpret_cast<RankHead*>(rank_lds);
   int32_t* sm_bt = reinterpret_cast<int32_t*>(rank_lds + align16(sizeof(RankHead)));
   uint8_t* region = rank_lds + align16(sizeof(RankHead)) + align16(static_cast<int64_t>(bt_lds) * 4);
@@ -967,9 +967,6 @@ __device__ __forceinline__ void rank_part(const skv_decode_desc* __restrict__ d,
   const int parts = static_cast<int>(ceil_div24(k, rank_out));
   if (part >= parts) return;  // the grid is sized for the largest top_k
   const GroupRef G = group_ref(map, gi);
-  if (part == 0) {
-    for (int i = tid; i < kTkBins; i += kStepThreads) ws[kTkWsHist + i] = 0;
-  }
   if (status) return;  // refused step
   int n_cols, n_valid;
   score_cols(map.score_stride[z], G.m, L, n_cols, n_valid);
@@ -1073,6 +1070,22 @@ __device__ __forceinline__ void rank_part(const skv_decode_desc* __restrict__ d,
   }
   __syncthreads();
   finish_rows<kWB>(sm.rr, sm.rr.n_rows, max(o0, sel), o1, d, Ly, k, G, b, L, sm_bt, n_bt);
+}
+
+// A rank part; part 0 then clears the row's histogram for the next step
+// (also after a refusal).  The clear comes last: stores issued while the
+// part's loads are in flight would make every later wait for a load wait for
+// all of them (the compiler cannot count on a mix of loads and stores
+// completing in order).
+template <bool kWB>
+__device__ __forceinline__ void rank_part(const skv_decode_desc* __restrict__ d, const StepMap& map,
+                                          uint8_t* rank_lds, int part, int b, int z, int rank_out, int bt_lds,
+                                          int ck_cap) {
+  rank_part_body<kWB>(d, map, rank_lds, part, b, z, rank_out, bt_lds, ck_cap);
+  if (part == 0) {
+    int32_t* ws = map.topk_ws[z] + static_cast<int64_t>(b) * kTkWsWords;
+    for (int i = static_cast<int>(threadIdx.x); i < kTkBins; i += kStepThreads) ws[kTkWsHist + i] = 0;
+  }
 }
 
 // Blocks of the gather launch, in groups of xcd_lanes(batch) blocks (one

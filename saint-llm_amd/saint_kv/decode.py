@@ -158,7 +158,7 @@ class DecodeCache:
         # calls (a later group's success must not hide an earlier refusal)
         self.group_status = torch.zeros(MAX_GROUPS, dtype=torch.int32, device=dev)
         self.host_lens = np.zeros(batch, dtype=np.int64)
-        self._attn_ws: dict[int, torch.Tensor] = {}
+        self._attn_ws: dict[int | str, torch.Tensor] = {}  # per layer, and "step" for step_attend
 
         # page groups: one per compression rate
         rates = sorted({s.m for s in layers if s.kind in ("csa", "hca")})

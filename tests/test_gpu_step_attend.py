@@ -148,6 +148,23 @@ def test_step_attend_xcd_batch_many_heads(dev) -> None:
     _run_pair(caches, spec, 3, dev, torch.Generator().manual_seed(8), H=128)
 
 
+def test_step_attend_partial_head_group_latent_512(dev) -> None:
+    """40 heads (a partial head group) over a 512-channel latent."""
+    from saint_kv.decode import DecodeCache, LayerSpec
+
+    spec = LayerSpec("csa", m=4, top_k=96)
+    caches = []
+    for _ in range(2):
+        c = DecodeCache([spec], 3, 4096, latent=512, window=32, block_size=16, device=dev, page_order_seed=5,
+                        materialize=False)
+        gen = torch.Generator(device=dev).manual_seed(5)
+        c.bias[0].normal_(generator=gen)
+        c.idx_bias[0].normal_(generator=gen)
+        c.prefill(np.array([1500, 77, 3001]), generator=gen)
+        caches.append(c)
+    _run_pair(caches, spec, 3, dev, torch.Generator().manual_seed(6), H=40)
+
+
 def test_step_attend_tie_overflow_full_select(dev) -> None:
     """Equal scores over 5,000 entries put every entry in one tie bin, past
     the candidate lists' capacity: the units fall back to the full select."""
