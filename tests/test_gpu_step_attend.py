@@ -181,6 +181,25 @@ def test_step_attend_tie_overflow_full_select(dev) -> None:
         assert np.array_equal(idx[b], np.arange(min(512, n_valid)))
 
 
+def test_step_attend_long_lists_rank_from_global(dev) -> None:
+    """top-k 2048 over 2,000 sure candidates and a 3,000-key tie bin: 5,000
+    candidates, more than a unit holds in LDS, so the units rank from the
+    lists in global memory."""
+    from saint_kv.decode import LayerSpec
+
+    spec = LayerSpec("csa", m=4, top_k=2048)
+    caches = _pair([spec], 2, 24064, [24000, 24000], dev)
+    cols = caches[0].scores[0].shape[1]
+    g = torch.Generator().manual_seed(12)
+    row = -torch.rand(cols, generator=g)  # below the ties
+    row[:2000] = 10.0 + torch.rand(2000, generator=g)  # sure
+    row[2000:5000] = 1.0  # one tie bin
+    scores = torch.stack([row, row.flip(0).roll(5000)])
+    _run_pair(caches, spec, 1, dev, g, scores=scores)
+    idx = caches[1].topk_idx[0].cpu().numpy()
+    assert set(idx[0][:2000]) == set(range(2000)) and np.array_equal(idx[0][2000:], np.arange(2000, 2048))
+
+
 def test_step_attend_config3_shape(dev) -> None:
     """B=16 at 64k context, CSA m=4, top-k 512, W=128, block size 64 (the
     64k decode workload), two steps."""
