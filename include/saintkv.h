@@ -52,6 +52,8 @@ extern "C" {
                         * per 128 main dims, then SKV_FP8_ROPE_DIMS bf16 dims */
 #define SKV_FMT_F32 2  /* entry = channels fp32 values (4*channels bytes), with fp32
                         * c/z rows: skv_compress_append only (fp32 caches) */
+#define SKV_FMT_IN_F32 0x100 /* or'd into skv_compress_append's format: the c/z rows
+                              * are fp32 (pooled unrounded) for bf16 or fp8 entries */
 #define SKV_FP8_ROPE_DIMS 64
 #define SKV_FP8_ENTRY_BYTES(channels) \
   (((channels) - SKV_FP8_ROPE_DIMS) + ((channels) - SKV_FP8_ROPE_DIMS) / 128 * 4 + 2 * SKV_FP8_ROPE_DIMS)
@@ -200,7 +202,10 @@ int skv_ring_read(void* dst, int64_t dst_seq_stride_rows, int64_t dst_capacity_r
  * (bias fp32 [m, channels]; fp32 math, rounded to bf16), and written as entry
  * floor(p/m) of the paged compressed cache (format SKV_FMT_BF16 or
  * SKV_FMT_FP8, quantized on write).  With SKV_FMT_F32 the c/z rows are fp32
- * and the entries the unrounded fp32 results (fp32 caches).  The incomplete block is carried in
+ * and the entries the unrounded fp32 results (fp32 caches); SKV_FMT_IN_F32
+ * or'd into a bf16 or fp8 format takes fp32 c/z rows (an fp32 compressor
+ * module feeding a bf16 cache: the entry is rounded once, as the
+ * reference's copy into its cache rounds it).  The incomplete block is carried in
  * tail_state (fp32 [batch, 3, channels]: running max, sum of weights and
  * weighted sum of its tokens' online softmax), so a block split over several
  * calls pools to the same value as one call.  Pages for the new entries must

@@ -372,6 +372,25 @@ def pooling_bound(c: Tensor, z: Tensor, bias: Tensor) -> Tensor:
     return POOL_REL * out.abs() + POOL_CANCEL * (w * c.float().abs()).sum(dim=-2)
 
 
+BF16_ULP = 2.0 ** -8  # one unit in the last place of bf16, relative (round to nearest: half of it)
+
+
+def pooling_bound_rounded_inputs(c: Tensor, z: Tensor, bias: Tensor, u: float = BF16_ULP) -> Tensor:
+    """pooling_bound widened for projections c, z that the pooled side holds
+    rounded to a format of relative precision u (bf16 GEMM outputs), while
+    c, z here are the exact (fp32) projections.  With w = softmax(z + bias)
+    and out = sum_i w_i c_i, the first-order change of out is
+    d out = sum_i w_i dc_i + sum_i w_i (c_i - out) dz_i, so |dc_i| <= u |c_i|
+    and |dz_i| <= u |z_i| move out by at most
+    u * (sum_i w_i |c_i| + sum_i w_i |c_i - out| |z_i|); twice that is added
+    for the second-order terms."""
+    w = torch.softmax(z.float() + bias.float(), dim=-2)
+    cf = c.float()
+    out = (w * cf).sum(dim=-2, keepdim=True)
+    drift = (w * cf.abs()).sum(dim=-2) + (w * (cf - out).abs() * z.float().abs()).sum(dim=-2)
+    return pooling_bound(c, z, bias) + 2.0 * u * drift
+
+
 def compress_append(pool: Tensor, block_table: np.ndarray, tail_c: Tensor, tail_z: Tensor,
                     c_new: Tensor, z_new: Tensor, bias: Tensor, seq_lens: np.ndarray,
                     n_new: np.ndarray | int, fp8: bool = False,

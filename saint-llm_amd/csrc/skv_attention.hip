@@ -69,6 +69,7 @@ struct AttnArgs {
   int32_t window, H, D, n_hg, n_cu, n_wu, batch;
   float eps, softcap;  // softcap <= 0: none
   int32_t fused;       // 1: the decode step's last launch (lens are the step's new lengths)
+  int32_t xcds;        // the device's XCDs (unit placement)
 };
 
 __device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
@@ -560,22 +561,22 @@ __device__ __forceinline__ void attn_unit(AtSmem<NKS>& sm, const AttnArgs& a, in
   }
 }
 
-// Blocks go to the XCDs in turn (block i to XCD i % kXcds); the units of
-// sequence b take the blocks of XCD b % kXcds, so the query that every unit
-// of b reads comes from far memory once per sequence and the partial outputs
-// stay in the L2 of the XCD whose merge blocks read them (merge block b runs
-// there too when the batch is a multiple of kXcds).  The grid holds kXcds *
-// ceil(batch / kXcds) * (units per sequence) blocks; blocks past the batch
-// exit.
+// Blocks go to the XCDs in turn (block i to XCD i % X on a device of X =
+// a.xcds XCDs); the units of sequence b take the blocks of XCD b % X, so the
+// query that every unit of b reads comes from far memory once per sequence
+// and the partial outputs stay in the L2 of the XCD whose merge blocks read
+// them (merge block b runs there too when the batch is a multiple of X).
+// The grid holds X * ceil(batch / X) * (units per sequence) blocks; blocks
+// past the batch exit.
 
 template <int NKS, bool kFp8>
 __global__ __launch_bounds__(kAtThreads, 1) void k_attn_part(AttnArgs a) {
   __shared__ AtSmem<NKS> sm;
   const int U = a.n_cu + a.n_wu;
   const int per_seq = U * a.n_hg;
-  const int k = static_cast<int>(blockIdx.x) / kXcds;  // this block's turn on its XCD
+  const int k = static_cast<int>(blockIdx.x) / a.xcds;  // this block's turn on its XCD
   const int sb = k / per_seq;
-  const int b = static_cast<int>(blockIdx.x) % kXcds + kXcds * sb;
+  const int b = static_cast<int>(blockIdx.x) % a.xcds + a.xcds * sb;
   if (b >= a.batch) return;  // uniform
   const int r = k - sb * per_seq;
   const int u = r / a.n_hg, hg = r - u * a.n_hg;
@@ -601,7 +602,6 @@ struct MergeArgs {
 // of both branches), the wave reduces them per branch; then every lane loads
 // its dims of 16 units' outputs at a time and sums them with the weights.
 constexpr int kMergeUnits = 64;  // units per sequence the merge takes (one per lane)
-constexpr int kAttnCUs = 256;    // MI355X compute units
 constexpr int kMergeChunk = 16;  // units whose outputs are loaded at once
 
 __global__ __launch_bounds__(256) void k_attn_merge(MergeArgs a) {
@@ -858,9 +858,10 @@ int attn_plan(const skv_attention_desc* d, AttnPlan& p) {
     n_wu = std::max<int64_t>(1, std::min(std::min(w, tiles_w), kMergeUnits - n_cu));
   } else {
     // split the branch with the most tiles per unit (a window tile reads K
-    // and V) while the grid is short of one workgroup per CU (a CU holds
-    // one) and units keep at least 2 tiles' worth of reads
-    while (d->batch * p.n_hg * (n_cu + n_wu) < kAttnCUs && n_cu + n_wu < kMergeUnits) {
+    // and V) while the grid is short of one workgroup per CU of the device
+    // (a CU holds one) and units keep at least 2 tiles' worth of reads
+    const int cus = device_cus();
+    while (d->batch * p.n_hg * (n_cu + n_wu) < cus && n_cu + n_wu < kMergeUnits) {
       const double pc = n_cu ? static_cast<double>(tiles_c) / n_cu : 0.0;
       const double pw = 2.0 * tiles_w / n_wu;
       if (pc >= pw && pc >= 2.0) {
@@ -951,9 +952,13 @@ struct RankLds {
 constexpr int kPosEmpty = -2147483647 - 1;  // an output position another unit owns
 
 // Ranking of CSA unit `part` of `parts` of sequence b, over the one layer of
-// a step: its candidates are the lists' entries part, part + parts, ...;
-// positions [part * out, (part + 1) * out), out = ceil(k / parts), are its
-// share of the fills (and of the fallback's positions).
+// a step: its candidates are the entries e with e % parts == part (lists
+// held in LDS; lists ranked from global memory: the lists' entries part,
+// part + parts, ...), so that which picks a unit attends over, and with them
+// its partial output, do not depend on the order in which the filter chunks
+// appended to the lists; positions [part * out, (part + 1) * out), out =
+// ceil(k / parts), are its share of the fills (and of the fallback's
+// positions).
 template <int NKS>
 struct StepRank {
   static constexpr bool kOn = true;
@@ -1095,7 +1100,26 @@ struct StepRank {
       lds_barrier();
       const auto put = [&](int pos, int idx) { at_pos[pos] = idx; };
       if (in_lds) {
-        rank_candidates<kAtThreads, 4>(put, [&](int q) { return ck[q]; }, S, C, sel, part, parts);
+        // the unit's own candidates by entry index, sure ones from the front
+        // of the (not yet filled) block-table area, ties from its back; their
+        // order there is immaterial: each one's position is its rank
+        static_assert(RL::kBtCap >= RL::kCkCap, "own candidates fit the block-table area");
+        int* own = bt;
+        int* own_cnt = scan;  // [0] sure, [1] ties
+        if (tid < 2) own_cnt[tid] = 0;
+        lds_barrier();
+        for (int c = tid; c < C; c += kAtThreads) {
+          const uint32_t e = ~static_cast<uint32_t>(ck[c]);
+          if (umod24(e, parts) == static_cast<uint32_t>(part)) {
+            if (c < S) own[atomicAdd(&own_cnt[0], 1)] = c;
+            else own[RL::kBtCap - 1 - atomicAdd(&own_cnt[1], 1)] = c;
+          }
+        }
+        lds_barrier();
+        const int n_os = own_cnt[0], n_ot = own_cnt[1];
+        rank_candidates_of<kAtThreads, 4>(
+            put, [&](int q) { return ck[q]; },
+            [&](int cls, int j) { return cls ? own[RL::kBtCap - 1 - j] : own[j]; }, n_os, n_ot, S, C, sel);
       } else {
         rank_candidates<kAtThreads>(put, [&](int q) { return order_key(q < S ? sure_list[q] : tie_list[q - S]); },
                                     S, C, sel, part, parts);
@@ -1191,9 +1215,9 @@ __global__ __launch_bounds__(kAtThreads, 1) void k_decode_attend(AttnArgs a, Ste
   __shared__ AtSmem<NKS> sm;
   const int U = a.n_cu + a.n_wu;
   const int per_seq = U * a.n_hg;
-  const int k = static_cast<int>(blockIdx.x) / kXcds;
+  const int k = static_cast<int>(blockIdx.x) / a.xcds;
   const int sb = k / per_seq;
-  const int b = static_cast<int>(blockIdx.x) % kXcds + kXcds * sb;
+  const int b = static_cast<int>(blockIdx.x) % a.xcds + a.xcds * sb;
   if (b >= a.batch) return;  // uniform
   const int r = k - sb * per_seq;
   const int u = r / a.n_hg, hg = r - u * a.n_hg;
@@ -1296,7 +1320,8 @@ int decode_attend(const skv_attention_desc* d, const skv_decode_desc* h, const S
   a.eps = x.eps;
   a.softcap = x.softcap;
   a.fused = 1;
-  const dim3 grid(static_cast<unsigned>(kXcds * ceil_div(x.batch, kXcds) * (p.n_cu + p.n_wu) * p.n_hg));
+  a.xcds = device_xcds();
+  const dim3 grid(static_cast<unsigned>(a.xcds * ceil_div(x.batch, a.xcds) * (p.n_cu + p.n_wu) * p.n_hg));
   int32_t* idx = Ly.kind == SKV_LAYER_CSA ? Ly.topk_idx : nullptr;
   if (a.fp8_main > 0) {
     hipLaunchKernelGGL((k_decode_attend<18, true>), grid, dim3(kAtThreads), 0, s, a, *map, idx);
@@ -1371,8 +1396,9 @@ extern "C" int skv_decode_attention(const skv_attention_desc* d, void* workspace
   a.eps = d->eps;
   a.softcap = d->softcap;
   a.fused = 0;
+  a.xcds = device_xcds();
   hipStream_t s = static_cast<hipStream_t>(stream);
-  const dim3 grid(static_cast<unsigned>(kXcds * ceil_div(d->batch, kXcds) * (p.n_cu + p.n_wu) * p.n_hg));
+  const dim3 grid(static_cast<unsigned>(a.xcds * ceil_div(d->batch, a.xcds) * (p.n_cu + p.n_wu) * p.n_hg));
   if (a.fp8_main > 0) {
     hipLaunchKernelGGL((k_attn_part<18, true>), grid, dim3(kAtThreads), 0, s, a);
   } else if (p.nks == 4) {

@@ -25,6 +25,10 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 // ---------------------------------------------------------------------------
 int set_error(int code, const char* fmt, ...);
 int check_launch(const char* what);
+// The current device's compute units and XCDs (hipDeviceGetAttribute, read
+// once per device): launch shapes and XCD-affine block placement follow them.
+int device_cus();
+int device_xcds();
 
 // ---------------------------------------------------------------------------
 // Streaming loads/stores.  Page copies touch every byte exactly once, so they

@@ -38,6 +38,7 @@ struct CompressArgs {
   int channels;
   int format;
   int fp8_main;  // main (quantized) channels in FP8 format
+  int in_f32;    // c/z rows are fp32
 };
 
 __device__ __forceinline__ void state_emit(const PoolState& st, const CompressArgs& a, int b, int64_t e,
@@ -57,7 +58,7 @@ __device__ __forceinline__ void fold_tokens(PoolState& st, const CompressArgs& a
     const uint8_t* crow = a.c_new + b * a.in_seq_stride + i * a.in_row_stride;
     const uint8_t* zrow = a.z_new + b * a.in_seq_stride + i * a.in_row_stride;
     const float* brow = a.bias + (p % a.m) * a.channels;
-    if (a.format == SKV_FMT_F32) {  // uniform: fp32 rows
+    if (a.in_f32) {  // uniform: fp32 rows
       state_update(st, reinterpret_cast<const float*>(crow), reinterpret_cast<const float*>(zrow), brow, lane,
                    groups);
     } else {
@@ -129,6 +130,8 @@ extern "C" int skv_compress_append(void* pool, int64_t entry_bytes, int64_t bloc
                                    int32_t n_new_uniform, int64_t m, int64_t channels,
                                    int32_t format, int64_t batch, void* stream) {
   const char* what = "skv_compress_append";
+  const bool in_f32 = (format & SKV_FMT_IN_F32) || (format & ~SKV_FMT_IN_F32) == SKV_FMT_F32;
+  format &= ~SKV_FMT_IN_F32;
   if (m <= 0 || m > 4096) return set_error(SKV_EINVAL, "%s: compression_rate must be in [1, 4096]; got %lld", what, (long long)m);
   if (channels <= 0 || (channels & 7) || channels > kPoolWave * 8 * kMaxGroups) {
     return set_error(SKV_EINVAL, "%s: channels must be a multiple of 8 in [8, %d]; got %lld", what,
@@ -175,6 +178,7 @@ extern "C" int skv_compress_append(void* pool, int64_t entry_bytes, int64_t bloc
   a.channels = static_cast<int>(channels);
   a.format = format;
   a.fp8_main = fp8_main;
+  a.in_f32 = in_f32 ? 1 : 0;
   // at most floor((in_len + m - 1) / m) + 1 blocks complete in one call
   const int64_t units = (in_len + m - 1) / m + 1;
   if (units > INT32_MAX) return set_error(SKV_EINVAL, "%s: in_len too large", what);

@@ -42,7 +42,7 @@ struct TopkChunk {
 __device__ __forceinline__ TopkChunk topk_chunk(uint32_t u, int n_chunks, const StepMap& map) {
   TopkChunk c;
   int r;
-  c.ok = xcd_item(u, n_chunks * map.n_csa, map.batch, c.b, r);
+  c.ok = xcd_item(u, n_chunks * map.n_csa, map.batch, map.lanes, c.b, r);
   c.z = static_cast<int>(udiv24(r, n_chunks));
   c.chunk = r - c.z * n_chunks;
   return c;
@@ -415,7 +415,7 @@ __global__ __launch_bounds__(kStepThreads) void k_decode_append(const skv_decode
     return;
   }
   int b, l;
-  if (!xcd_item(blockIdx.x, map.n_layers, map.batch, b, l)) return;  // block 0 is (layer 0, sequence 0)
+  if (!xcd_item(blockIdx.x, map.n_layers, map.batch, map.lanes, b, l)) return;  // block 0 is (layer 0, sequence 0)
   const skv_decode_layer& Ly = d->layers[l];
   const bool paged = Ly.kind != SKV_LAYER_SWA;
   const int wave = tid / kWave;
@@ -1088,8 +1088,8 @@ __device__ __forceinline__ void rank_part(const skv_decode_desc* __restrict__ d,
   }
 }
 
-// Blocks of the gather launch, in groups of xcd_lanes(batch) blocks (one
-// block per XCD when the lanes are kXcds): group i * period is the i-th group
+// Blocks of the gather launch, in groups of map.lanes blocks (one block per
+// XCD when the lanes are the XCDs): group i * period is the i-th group
 // of rank parts (batch * parts_max * CSA layers of them, placed as xcd_item
 // places them), every other group holds the next dense tiles.  period *
 // n_rank_groups <= the groups of the grid, so every rank group is in it;
@@ -1107,12 +1107,12 @@ __global__ __launch_bounds__(kStepThreads) void k_decode_gather(const skv_decode
                                                                 int ck_cap, StepMap map) {
   extern __shared__ __align__(16) uint8_t rank_lds[];
   const uint32_t u = blockIdx.x;  // grids stay below 2^24 workgroups
-  const int lanes = xcd_lanes(map.batch);
+  const int lanes = map.lanes;
   const uint32_t g = u / lanes;  // the block's group
   const uint32_t i = udiv24(g, gg.period);
   if (g == i * gg.period && static_cast<int>(i) < gg.n_rank_groups) {
     int b, r;
-    if (!xcd_item(i * lanes + u % lanes, gg.parts_max * map.n_csa, map.batch, b, r)) return;
+    if (!xcd_item(i * lanes + u % lanes, gg.parts_max * map.n_csa, map.batch, lanes, b, r)) return;
     const int z = static_cast<int>(udiv24(r, gg.parts_max));
     rank_part<kWB>(d, map, rank_lds, r - z * gg.parts_max, b, z, rank_out, bt_lds, ck_cap);
     return;
@@ -1210,6 +1210,7 @@ int decode_step(const skv_decode_desc* h, const skv_decode_desc* dd, void* strea
   }
   StepMap map{};
   map.batch = h->batch;
+  map.lanes = xcd_lanes(h->batch);
   map.n_layers = h->n_layers;
   map.n_groups = h->n_groups;
   map.tok_lens = h->tok_lens;
@@ -1328,7 +1329,7 @@ int decode_step(const skv_decode_desc* h, const skv_decode_desc* dd, void* strea
     rank_out >>= 1;
   }
   const int64_t parts_max = ceil_div(max_top_k, rank_out);
-  const int lanes = xcd_lanes(h->batch);
+  const int lanes = map.lanes;
   const int64_t n_rank_groups = xcd_region(h->batch, parts_max * n_csa) / lanes;
   const int64_t n_gather = lanes * ceil_div(lanes * n_rank_groups + n_tiles, lanes);
   if (n_append >= (1 << 24) || n_gather >= (1 << 24)) {

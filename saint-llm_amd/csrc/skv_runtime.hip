@@ -24,6 +24,45 @@ int check_launch(const char* what) {
   return SKV_OK;
 }
 
+namespace {
+
+// Per device, read once: compute units and XCDs (XCCs).  A device whose
+// query fails counts as one XCD of 256 compute units.
+struct Topology {
+  int cus = 0;
+  int xcds = 0;
+};
+
+Topology topology() {
+  static Topology topo[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) {
+    (void)hipGetLastError();
+    return Topology{256, 1};
+  }
+  Topology& t = topo[dev];
+  if (t.cus <= 0) {
+    int cus = 0, xcds = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) {
+      (void)hipGetLastError();
+      cus = 256;
+    }
+    if (hipDeviceGetAttribute(&xcds, hipDeviceAttributeNumberOfXccs, dev) != hipSuccess || xcds <= 0) {
+      (void)hipGetLastError();
+      xcds = 1;
+    }
+    t.xcds = xcds;
+    t.cus = cus;
+  }
+  return t;
+}
+
+}  // namespace
+
+int device_cus() { return topology().cus; }
+
+int device_xcds() { return topology().xcds; }
+
 }  // namespace skv
 
 extern "C" int skv_abi_version(void) { return SKV_ABI_VERSION; }

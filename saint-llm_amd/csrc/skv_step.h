@@ -22,6 +22,7 @@ static_assert(kTkPartThreads == kStepThreads, "top-k chunk workgroups are step w
 // walks the descriptor's layer list through dependent loads to find it.
 struct StepMap {
   int32_t batch;
+  int32_t lanes;  // xcd_lanes(batch)
   int32_t n_layers;
   int32_t n_csa;
   uint32_t hca_mask;                  // bit l: layer l is an HCA layer
@@ -71,26 +72,27 @@ __device__ __forceinline__ void score_cols(int64_t score_stride, int m, int L, i
   n_valid = Lc > 0 ? static_cast<int>(min<int64_t>(udiv24(Lc - 1, m), score_stride)) : 0;
 }
 
-// Blocks go to the XCDs in turn (block i to XCD i % kXcds), each XCD with
-// its own L2.  With `lanes` = kXcds (a batch that is a multiple of kXcds, so
-// that every XCD gets the same work), a region of lanes * ceil(batch / lanes)
-// * per_seq blocks that starts at a multiple of kXcds gives the per_seq items
-// of sequence b to blocks of XCD b % kXcds, in every launch of the step: the
-// scores, candidate lists and block-table row of b that one launch writes or
-// reads, the next one finds in the same L2.  With lanes = 1 (smaller or
-// ragged batches) the items go sequence by sequence to consecutive blocks,
-// spread over every XCD.  Item r of sequence b for block u of the region, or
-// false for a block past the batch.
-constexpr int kXcds = 8;  // MI355X
-
-__host__ __device__ constexpr int xcd_lanes(int batch) { return batch % kXcds == 0 ? kXcds : 1; }
+// Blocks go to the XCDs in turn (block i to XCD i % X on a device of X
+// XCDs, each with its own L2).  With `lanes` = X (a batch that is a multiple
+// of X, so that every XCD gets the same work), a region of lanes *
+// ceil(batch / lanes) * per_seq blocks that starts at a multiple of X gives
+// the per_seq items of sequence b to blocks of XCD b % X, in every launch of
+// the step: the scores, candidate lists and block-table row of b that one
+// launch writes or reads, the next one finds in the same L2.  With lanes = 1
+// (one XCD, or smaller or ragged batches) the items go sequence by sequence
+// to consecutive blocks, spread over every XCD.  Item r of sequence b for
+// block u of the region, or false for a block past the batch.
+inline int xcd_lanes(int batch) {
+  const int x = device_xcds();
+  return (x > 1 && batch % x == 0) ? x : 1;
+}
 
 __host__ __device__ constexpr int64_t xcd_region(int batch, int64_t per_seq) {
   return static_cast<int64_t>(batch) * per_seq;  // lanes divide the batch
 }
 
-__device__ __forceinline__ bool xcd_item(uint32_t u, int per_seq, int batch, int& b, int& r) {
-  const int lanes = xcd_lanes(batch);  // uniform
+// lanes: xcd_lanes(batch) of the launch (a kernel argument).
+__device__ __forceinline__ bool xcd_item(uint32_t u, int per_seq, int batch, int lanes, int& b, int& r) {
   const uint32_t k = u / lanes;  // the block's turn on its XCD
   const uint32_t sb = udiv24(k, per_seq);
   b = static_cast<int>(u % lanes + lanes * sb);
@@ -130,20 +132,20 @@ __device__ __forceinline__ int lane_group_sum(int v, int sub_n) {
   return v;
 }
 
-// The part's first n_pf candidates (its sure ones first, then its ties)
-// get their output position, or -1 for a tie past the winners, in
-// own_pos[j] instead of being collected; every other winner is handed to
-// win(position, index) (index -1 for a non-finite key), by one lane.  NT
-// threads of the workgroup (threads 0..NT-1) take part.  KU: list keys a
-// lane reads at once (1: a loop over its own keys, which needs the fewest
-// registers).
+// Ranks a part's own candidates: cand(cls, j) is the list index (sure list
+// [0, S), tie list [S, C)) of its j-th own candidate of class cls (0 sure,
+// 1 tie), n_sure_mine and n_tie_mine of them.  The part's first n_pf
+// candidates (its sure ones first, then its ties) get their output
+// position, or -1 for a tie past the winners, in own_pos[j] instead of being
+// collected; every other winner is handed to win(position, index) (index -1
+// for a non-finite key), by one lane.  NT threads of the workgroup (threads
+// 0..NT-1) take part.  KU: list keys a lane reads at once (1: a loop over its
+// own keys, which needs the fewest registers).
 // A candidate's position is its class's first position plus the keys of its
 // class above it (every sure key is above every tie key).
-template <int NT, int KU = 1, class KeyAt, class Win>
-__device__ __forceinline__ void rank_candidates(Win win, KeyAt ck, int S, int C, int sel, int part, int parts,
-                                                int* own_pos = nullptr, int n_pf = 0) {
-  const int n_sure_mine = (part < S) ? static_cast<int>(ceil_div24(S - part, parts)) : 0;
-  const int n_tie_mine = (part < C - S) ? static_cast<int>(ceil_div24(C - S - part, parts)) : 0;
+template <int NT, int KU = 1, class KeyAt, class Win, class Cand>
+__device__ __forceinline__ void rank_candidates_of(Win win, KeyAt ck, Cand cand, int n_sure_mine, int n_tie_mine,
+                                                   int S, int C, int sel, int* own_pos = nullptr, int n_pf = 0) {
   const int tid = threadIdx.x;
   // the lane groups of both classes (sure candidates against the sure list,
   // ties against the tie list) run side by side
@@ -163,7 +165,7 @@ __device__ __forceinline__ void rank_candidates(Win win, KeyAt ck, int S, int C,
     int rank[kRankR];
 #pragma unroll
     for (int r = 0; r < kRankR; ++r) {
-      mine[r] = (j0 + r < n_mine) ? ck(lo + part + (j0 + r) * parts) : ~0ull;
+      mine[r] = (j0 + r < n_mine) ? ck(cand(cls, j0 + r)) : ~0ull;
       rank[r] = 0;
     }
     if constexpr (KU == 1) {
@@ -216,6 +218,18 @@ __device__ __forceinline__ void rank_candidates(Win win, KeyAt ck, int S, int C,
       }
     }
   }
+}
+
+// rank_candidates_of with the part's own candidates at list positions part,
+// part + parts, ... of each class.
+template <int NT, int KU = 1, class KeyAt, class Win>
+__device__ __forceinline__ void rank_candidates(Win win, KeyAt ck, int S, int C, int sel, int part, int parts,
+                                                int* own_pos = nullptr, int n_pf = 0) {
+  const int n_sure_mine = (part < S) ? static_cast<int>(ceil_div24(S - part, parts)) : 0;
+  const int n_tie_mine = (part < C - S) ? static_cast<int>(ceil_div24(C - S - part, parts)) : 0;
+  rank_candidates_of<NT, KU>(
+      win, ck, [&](int cls, int j) { return (cls ? S : 0) + part + j * parts; }, n_sure_mine, n_tie_mine, S, C, sel,
+      own_pos, n_pf);
 }
 
 // The attention launches that end skv_decode_step_attend, after the step's

@@ -92,6 +92,7 @@ SIGNATURES: dict[str, list] = {
 SKV_FMT_BF16 = 0
 SKV_FMT_FP8 = 1
 SKV_FMT_F32 = 2  # fp32 entries from fp32 c/z rows (skv_compress_append only)
+SKV_FMT_IN_F32 = 0x100  # skv_compress_append: fp32 c/z rows into bf16 or fp8 entries
 SKV_FP8_ROPE_DIMS = 64
 
 

@@ -117,11 +117,34 @@ class _PagedRows:
         self.length = 0
 
 
+def _reference_forward(comp: object) -> bool:
+    """Whether calling ``comp`` runs TokenLevelCompressor.forward itself
+    (csa.py:66-88) and nothing around it: a torch module whose class has a
+    ``TokenLevelCompressor`` on its MRO whose ``forward`` is the one the
+    module resolves (no subclass overrides it, e.g. with the overlapping a/b
+    pooling that csa.py:78-79 leaves for later), with no forward hooks or
+    pre-hooks of its own or global ones."""
+    if not isinstance(comp, torch.nn.Module):
+        return False
+    cls = next((k for k in type(comp).__mro__ if k.__name__ == "TokenLevelCompressor"), None)
+    if cls is None or "forward" not in vars(cls) or type(comp).forward is not vars(cls)["forward"]:
+        return False
+    if comp._forward_hooks or comp._forward_pre_hooks:
+        return False
+    from torch.nn.modules import module as _module
+
+    return not (_module._global_forward_hooks or _module._global_forward_pre_hooks)
+
+
 def _fast_compressor(comp: object, m: int, c: int) -> tuple | None:
-    """(w_b_kv, w_b_z, bias_b) of a TokenLevelCompressor-shaped module with
-    this cache's compression rate and channels (csa.py:59-64): the b-branch
-    projections and positional bias its forward pools with (csa.py:73-87; the
-    a-branch is computed there but unused).  None for any other callable."""
+    """(w_b_kv, w_b_z, bias_b) of a TokenLevelCompressor module with this
+    cache's compression rate and channels (csa.py:59-64) whose forward is the
+    reference's own (_reference_forward): the b-branch projections and
+    positional bias that forward pools with (csa.py:73-87; the a-branch is
+    computed there but unused).  None for any other callable, which is then
+    called as the reference calls it."""
+    if not _reference_forward(comp):
+        return None
     w_kv, w_z, bias = (getattr(comp, n, None) for n in ("w_b_kv", "w_b_z", "bias_b"))
     if not (callable(w_kv) and callable(w_z) and isinstance(bias, Tensor)):
         return None
@@ -250,9 +273,10 @@ class _CompressedLayer:
         # 1) SW branch K/V (kv_cache.py:167-168)
         rows = torch.stack([sw_k_new.to(self.dtype), sw_v_new.to(self.dtype)], dim=2)
         sw = self._sw.append(rows)
-        # 2) combine the buffered h with the new chunk (kv_cache.py:171-179)
+        # 2) combine the buffered h with the new chunk (kv_cache.py:171-179;
+        # torch.cat promotes the cache-dtype buffer and h_new as there)
         if self.h_buf_count > 0:
-            combined = torch.cat([self.h_buffer[:, : self.h_buf_count], h_new.to(self.dtype)], dim=1)
+            combined = torch.cat([self.h_buffer[:, : self.h_buf_count], h_new], dim=1)
         else:
             combined = h_new
         total = self.h_buf_count + n
@@ -268,8 +292,16 @@ class _CompressedLayer:
                 )
             # the tokens the state has not folded yet: the new ones, or the
             # buffered ones too after a compressor call left them out
-            fold = (h_new, n) if self._tail_folded else (combined, total)
-            self._fold(fast, *fold, n_complete, self.n_blocks * self.compression_rate + total)
+            h_fold, n_fold = (h_new, n) if self._tail_folded else (combined, total)
+            # the reference hands a token to its compressor from h_new when the
+            # token's block completes in the same call, else from h_buffer,
+            # i.e. rounded to the cache dtype: fold the leftover tokens so
+            leftover = total - n_consumed
+            if leftover > 0 and h_fold.dtype != self.dtype:
+                k = min(leftover, n_fold)
+                h_fold = torch.cat([h_fold[:, : n_fold - k], h_fold[:, n_fold - k:].to(self.dtype).to(h_fold.dtype)],
+                                   dim=1)
+            self._fold(fast, h_fold, n_fold, n_complete, self.n_blocks * self.compression_rate + total)
             self.fast_appends += 1
         # 3) emit complete blocks through the caller's compressors (kv_cache.py:182-189)
         elif n_complete > 0:
@@ -325,8 +357,13 @@ class _CompressedLayer:
             if n_fold > 0:
                 hh = h.to(bias.dtype)  # the module's own dtype, as its forward sees it
                 with torch.no_grad():  # the kernel consumes raw buffers; no autograd graph
-                    c = w_kv(hh).to(self.dtype).contiguous()
-                    z = w_z(hh).to(self.dtype).contiguous()
+                    # the projections as the module computes them: a bf16
+                    # module's bf16 values, otherwise fp32 (pooled unrounded
+                    # into a bf16 cache's entries, which round once)
+                    pdt = torch.bfloat16 if (bias.dtype == torch.bfloat16 and self.dtype == torch.bfloat16) \
+                        else torch.float32
+                    c = w_kv(hh).to(pdt).contiguous()
+                    z = w_z(hh).to(pdt).contiguous()
                 ops.compress_append(stream.pool, stream.block_table, state, c, z,
                                     bias.detach().to(torch.float32).contiguous(), lens, n_fold)
             if n_complete > 0:

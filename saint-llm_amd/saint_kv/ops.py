@@ -166,7 +166,10 @@ def _from_page(block_table: torch.Tensor, seq_lens: torch.Tensor, out: torch.Ten
         raise ValueError("first_page needs out as [batch, rows, *row], not packed rows")
     if not 0 < first_page < block_table.shape[1]:
         raise ValueError(f"first_page must be in [0, {block_table.shape[1]}); got {first_page}")
-    lens = torch.clamp(seq_lens - first_page * bs, min=0).to(torch.int32)
+    # the shifted table row holds bt_stride - first_page pages: clamp there, so
+    # that no length reaches past it into the next sequence's row
+    lens = torch.clamp(seq_lens - first_page * bs, min=0,
+                       max=(block_table.shape[1] - first_page) * bs).to(torch.int32)
     return block_table.data_ptr() + first_page * block_table.element_size(), lens, out[:, first_page * bs:]
 
 
@@ -376,9 +379,10 @@ def compress_append(pool: torch.Tensor, block_table: torch.Tensor, tail_state: t
     ``pool`` is bf16 [n_pages, bs, C] (bf16 entries), uint8 [n_pages, bs, E]
     (fp8 entries) or fp32 [n_pages, bs, C] (fp32 entries, unrounded);
     ``tail_state`` fp32 [B, 3, C] carries the incomplete block;
-    ``c_new``/``z_new`` [B, T, C] with identical strides, bf16 (fp32 for an
-    fp32 pool); ``bias`` fp32 [m, C] (m = compression rate).  Returns the
-    entry format used.
+    ``c_new``/``z_new`` [B, T, C] with identical strides, bf16 or fp32 (fp32
+    for an fp32 pool; fp32 rows into a bf16 or fp8 pool are pooled unrounded
+    and the entry is rounded once); ``bias`` fp32 [m, C] (m = compression
+    rate).  Returns the entry format used.
     """
     n_pages, bs, rb = _check_pool(pool)
     _require_i32(block_table, "block_table")
@@ -389,7 +393,10 @@ def compress_append(pool: torch.Tensor, block_table: torch.Tensor, tail_state: t
         fmt = _lib.SKV_FMT_F32
     else:
         fmt = _entry_format(pool, channels)
-    in_dtype = torch.float32 if fmt == _lib.SKV_FMT_F32 else torch.bfloat16
+    in_dtype = torch.float32 if fmt == _lib.SKV_FMT_F32 else c_new.dtype
+    if in_dtype not in (torch.float32, torch.bfloat16):
+        raise ValueError(f"c_new/z_new must be bf16 or fp32; got {c_new.dtype}")
+    in_flag = _lib.SKV_FMT_IN_F32 if (in_dtype == torch.float32 and fmt != _lib.SKV_FMT_F32) else 0
     _require_gpu(tail_state, "tail_state")
     if (tail_state.dtype != torch.float32 or tuple(tail_state.shape) != (batch, 3, channels)
             or not tail_state.is_contiguous()):
@@ -410,7 +417,7 @@ def compress_append(pool: torch.Tensor, block_table: torch.Tensor, tail_state: t
     _lib.call("skv_compress_append", pool.data_ptr(), rb, bs, n_pages, block_table.data_ptr(),
               bt_stride, tail_state.data_ptr(), c_new.data_ptr(), z_new.data_ptr(),
               c_new.stride(0) * es, c_new.stride(1) * es, c_new.shape[1], bias.data_ptr(),
-              seq_lens.data_ptr(), n_ptr, n_uni, m, channels, fmt, batch,
+              seq_lens.data_ptr(), n_ptr, n_uni, m, channels, fmt | in_flag, batch,
               _lib.stream_handle(pool.device))
     return fmt
 

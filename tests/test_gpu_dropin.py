@@ -300,3 +300,68 @@ def test_compressor_fast_path_matches_reference_formula(dev, dtype) -> None:
             with torch.no_grad():
                 mod = comps[si](hh.to(bf).to(dev)).float().cpu()
             assert float((got - mod).norm() / mod.norm()) < (1e-5 if fp32 else 1e-2)
+
+
+def test_compressor_fast_path_only_for_the_reference_forward(dev) -> None:
+    """The fast path runs only when calling the module would run
+    TokenLevelCompressor.forward and nothing else: a subclass that overrides
+    forward, or a module with a forward hook, is called as the reference
+    calls it (kv_cache.py:182-189), and its own outputs become the entries."""
+    from saint_kv.kv_cache import HCAKVCacheLayer
+
+    class Doubled(ref.TokenLevelCompressor):
+        def forward(self, h):
+            return 2.0 * super().forward(h)
+
+    g = torch.Generator().manual_seed(4)
+    H, D, m, B = 32, 16, 4, 2
+    plain = ref.TokenLevelCompressor(H, D, m)
+    hooked = ref.TokenLevelCompressor(H, D, m)
+    hooked.register_forward_hook(lambda mod, args, out: out + 1.0)
+    for comp, scale, shift in ((Doubled(H, D, m), 2.0, 0.0), (hooked, 1.0, 1.0)):
+        comp.load_state_dict(plain.state_dict())
+        comp = comp.to(dev)
+        layer = HCAKVCacheLayer(max_seq_len=64, hidden_dim=H, head_dim=D, compression_rate=m, batch_size=B,
+                                device=dev)
+        h = torch.randn(B, 12, H, generator=g)
+        out, _, _ = layer.append(h.to(dev), torch.zeros(B, 12, D, device=dev), torch.zeros(B, 12, D, device=dev),
+                                 compressor=comp)
+        assert layer.fast_appends == 0
+        with torch.no_grad():
+            want = scale * plain(h) + shift
+        torch.testing.assert_close(out.cpu(), want, rtol=1e-5, atol=1e-5)
+
+
+def test_compressor_fast_path_fp32_module_into_bf16_cache(dev) -> None:
+    """An fp32 TokenLevelCompressor feeding a bf16 cache, one token per append
+    (every block spans appends): the reference pools in fp32, sees buffered
+    tokens rounded to bf16 (its h_buffer) and rounds the entry once when it
+    copies it into its cache.  The fast path pools the fp32 projections of
+    the same token values: every entry within the pooling bound of the
+    oracle's pooling of those projections, elementwise."""
+    from saint_kv.kv_cache import HCAKVCacheLayer
+
+    g = torch.Generator().manual_seed(6)
+    H, D, m, B, T = 48, 32, 4, 3, 22
+    comp = ref.TokenLevelCompressor(H, D, m)
+    with torch.no_grad():
+        comp.bias_b.copy_(torch.randn(m, D, generator=g))
+    layer = HCAKVCacheLayer(max_seq_len=64, hidden_dim=H, head_dim=D, compression_rate=m, batch_size=B,
+                            device=dev, dtype=torch.bfloat16)
+    mod = comp.to(dev)
+    h = torch.randn(B, T, H, generator=g)
+    for i in range(T):
+        out, _, _ = layer.append(h[:, i:i + 1].to(dev), torch.zeros(B, 1, D, device=dev),
+                                 torch.zeros(B, 1, D, device=dev), compressor=mod)
+    assert layer.fast_appends == T
+    nb = T // m
+    # the token values the reference's compressor sees: every token but the
+    # last of its block was buffered (bf16), the last came in h_new (fp32)
+    seen = h[:, : nb * m].clone().view(B, nb, m, H)
+    seen[:, :, : m - 1] = seen[:, :, : m - 1].to(torch.bfloat16).float()
+    with torch.no_grad():
+        cz, zz = comp.cpu().w_b_kv(seen), comp.w_b_z(seen)
+        want = ref.compress_pool(cz, zz, comp.bias_b)
+        bound = ref.pooling_bound(cz, zz, comp.bias_b)
+    got = out[:, :nb].float().cpu()
+    assert ((got - want).abs() <= bound).all(), float((got - want).abs().max())

@@ -333,6 +333,33 @@ def test_pooling_bound_covers_reordering_and_catches_a_dropped_term() -> None:
             assert ((bad - want).abs() > bound).float().mean() > 0.5
 
 
+def test_pooling_bound_rounded_inputs_covers_bf16_projections() -> None:
+    """ref.pooling_bound_rounded_inputs holds the pooling of projections
+    rounded to bf16 (and of ones pushed a whole bf16 ulp either way, as a
+    GEMM that sums in another order may round them), measured against the
+    pooling of the exact fp32 projections, elementwise; a planted mistake (the
+    bias ignored; at m <= 8 a dropped token, which at m = 128 moves an entry
+    by about a 128th of a term) still violates it on most channels."""
+    g = torch.Generator().manual_seed(5)
+    for m in (2, 8, 128):
+        c = torch.randn(32, m, 64, generator=g) * 3
+        z = torch.randn(32, m, 64, generator=g)
+        bias = torch.randn(m, 64, generator=g).to(torch.bfloat16).float()
+        want = ref.compress_pool(c, z, bias)
+        bound = ref.pooling_bound_rounded_inputs(c, z, bias)
+        cb, zb = c.to(torch.bfloat16).float(), z.to(torch.bfloat16).float()
+        ulp = lambda t: t.abs() * ref.BF16_ULP  # noqa: E731
+        sign = lambda: torch.randint(0, 2, c.shape, generator=g).float() * 2 - 1  # noqa: E731
+        for cc, zz in ((cb, zb), (cb + sign() * ulp(cb), zb + sign() * ulp(zb))):
+            got = ref.compress_pool(cc, zz, bias).to(torch.bfloat16).float()
+            assert ((got - want).abs() <= bound).all(), m
+        w = torch.softmax(z + bias, dim=-2)
+        dropped = (w[:, 1:] * c[:, 1:]).sum(dim=-2)
+        no_bias = ref.compress_pool(c, z, torch.zeros_like(bias))
+        for bad in ((dropped, no_bias) if m <= 8 else (no_bias,)):
+            assert ((bad - want).abs() > bound).float().mean() > 0.5, m
+
+
 def test_token_level_compressor_restatement_pools_its_b_branch() -> None:
     """The oracle TokenLevelCompressor equals compress_pool of its own b-branch
     projections (the formula the fast path of the drop-in uses), ignores its
