@@ -39,6 +39,7 @@ import torch  # noqa: E402
 HBM_PEAK_GBS = 8000.0  # MI355X HBM3E peak, 8 TB/s
 TRAFFIC_FILE = ROOT / "profiles" / "hbm_traffic_k_copy_slices_b64_L1k-32k.json"
 DECODE_TRAFFIC_FILE = ROOT / "profiles" / "hbm_traffic_decode_legs.json"
+ATTN_TRAFFIC_FILE = ROOT / "profiles" / "hbm_traffic_attention_layer_seq.json"
 
 
 def committed_traffic(path: Path, key: str | None, alg_bytes: float) -> tuple[int | None, str | None]:
@@ -543,6 +544,14 @@ def run_layer_seq_leg(dev, n_layers: int = 8, batch: int = 16, L: int = 65536, s
         "alg_bytes_per_layer": int(layer_bytes), "gbs": round(gbs, 1),
         "pct_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 2),
     }
+    traffic, source = committed_traffic(ATTN_TRAFFIC_FILE, f"{name}_{mode}", layer_bytes)
+    rec["roofline"] = {
+        "bound": "hbm",
+        "kernel": f"one layer: decode step + attention ({rec['launches_per_layer']} launches; the layer as the unit)",
+        "achieved": rec["gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+        "frac": round(rec["gbs"] / HBM_PEAK_GBS, 4), "traffic": traffic, "traffic_source": source,
+        "alg_bytes_per_launch": int(layer_bytes), "avg_launch_us": rec["us_per_layer"],
+    }
     log(f"{name} ({mode}): {rec['us_per_model_step']} us per {n_layers}-layer model step, "
         f"{rec['us_per_layer']} us per layer (step + attention), {rec['gbs']} GB/s ({rec['pct_hbm_peak']}%)")
     del caches
@@ -592,6 +601,14 @@ def run_indexer_leg(dev, batch: int, n_ent: int, heads: int, channels: int, laun
         "launches": launches, "us_per_launch": round(us, 2), "alg_bytes_per_launch": int(alg),
         "gbs": round(gbs, 1), "pct_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 2),
         "mfma_tflops": round(flops / (us * 1e-6) / 1e12, 1),
+    }
+    traffic, source = committed_traffic(ATTN_TRAFFIC_FILE, name, alg)
+    rec["roofline"] = {
+        "bound": "hbm",
+        "kernel": "skv_decode_attention (k_attn_part, then the merge; the layer call as the unit)",
+        "achieved": rec["gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+        "frac": round(rec["gbs"] / HBM_PEAK_GBS, 4), "traffic": traffic, "traffic_source": source,
+        "alg_bytes_per_launch": alg, "avg_launch_us": rec["us_per_launch"],
     }
     log(f"indexer_64k: {rec['us_per_launch']} us/launch, {rec['gbs']} GB/s ({rec['pct_hbm_peak']}%), "
         f"{rec['mfma_tflops']} TFLOP/s bf16")
@@ -691,6 +708,14 @@ def run_attention_leg(dev, name: str, kind: str, batch: int, lens: np.ndarray, l
         "gbs": round(gbs, 1), "pct_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 2),
         "mfma_tflops": round(flops / (us * 1e-6) / 1e12, 1),
     }
+    traffic, source = committed_traffic(ATTN_TRAFFIC_FILE, name, alg)
+    rec["roofline"] = {
+        "bound": "hbm",
+        "kernel": "skv_decode_attention (k_attn_part, then the merge; the layer call as the unit)",
+        "achieved": rec["gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+        "frac": round(rec["gbs"] / HBM_PEAK_GBS, 4), "traffic": traffic, "traffic_source": source,
+        "alg_bytes_per_launch": alg, "avg_launch_us": rec["us_per_launch"],
+    }
     log(f"{name}: {rec['us_per_launch']} us/launch, {rec['gbs']} GB/s ({rec['pct_hbm_peak']}%), "
         f"{rec['mfma_tflops']} TFLOP/s bf16")
     del sets, ws, graph
@@ -747,6 +772,9 @@ def main() -> int:
                     "layer_seq_mixed",
                     help="comma list of decode-step legs to run after the headline ('' for none)")
     ap.add_argument("--leg-steps", type=int, default=200)
+    ap.add_argument("--layer-steps", type=int, default=100, help="timed model steps of the layer-sequential legs")
+    ap.add_argument("--layer-modes", default="fused,separate,materialize",
+                    help="comma list of the layer-sequential legs' modes to run")
     ap.add_argument("--no-indexer", action="store_true", help="skip the indexer-score leg")
     ap.add_argument("--no-attention", action="store_true", help="skip the decode-attention legs")
     ap.add_argument("--no-state", action="store_true", help="skip the request save/load leg")
@@ -848,20 +876,29 @@ def main() -> int:
             rng.integers(262144, 1048577, size=4), args.leg_steps, seed=5, outlier_frac=0.01,
             evict_frac=0.3)
 
+    layer_modes = [x for x in args.layer_modes.split(",") if x]
+
+    def layer_seq_modes(modes, **kw):
+        """The fused mode's record with the other modes' records under their keys."""
+        rec = {}
+        for mode, key in (("fused", None), ("separate", "separate"), ("materialize", "with_gathered_copies")):
+            if mode in modes and mode in layer_modes:
+                r = run_layer_seq_leg(dev, mode=mode, steps=args.layer_steps, **kw)
+                if key is None:
+                    rec.update(r)
+                else:
+                    rec[key] = r
+        return rec or None
+
     layer_seq = None
     if "layer_seq_64k" in wanted:
-        layer_seq = run_layer_seq_leg(dev, mode="fused")
-        layer_seq["separate"] = run_layer_seq_leg(dev, mode="separate")
-        layer_seq["with_gathered_copies"] = run_layer_seq_leg(dev, mode="materialize")
+        layer_seq = layer_seq_modes(("fused", "separate", "materialize"))
     layer_seq_mixed = None
     if "layer_seq_mixed" in wanted:
         # the 8-layer CSA/HCA stack of mixed_8layer (B=32, L~U[32k,128k]) as a model steps it
         mixed_lens = np.random.default_rng(4).integers(32768, 131073, size=32)
-        kinds = ["csa", "hca"] * 4
-        layer_seq_mixed = run_layer_seq_leg(dev, batch=32, mode="fused", kinds=kinds, lens=mixed_lens,
-                                            name="layer_seq_mixed")
-        layer_seq_mixed["separate"] = run_layer_seq_leg(dev, batch=32, mode="separate", kinds=kinds,
-                                                        lens=mixed_lens, name="layer_seq_mixed")
+        layer_seq_mixed = layer_seq_modes(("fused", "separate"), batch=32, kinds=["csa", "hca"] * 4,
+                                          lens=mixed_lens, name="layer_seq_mixed")
     indexer = None if args.no_indexer else run_indexer_leg(dev, 16, 16384, 64, 128, 200)
     state_io = None if args.no_state else run_state_leg(dev)
     attention = {}

@@ -69,7 +69,7 @@ struct AttnArgs {
   int32_t window, H, D, n_hg, n_cu, n_wu, batch;
   float eps, softcap;  // softcap <= 0: none
   int32_t fused;       // 1: the decode step's last launch (lens are the step's new lengths)
-  int32_t xcds;        // the device's XCDs (unit placement)
+  int32_t xcds;        // the device's XCDs, a power of two (unit placement)
 };
 
 __device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
@@ -574,9 +574,10 @@ __global__ __launch_bounds__(kAtThreads, 1) void k_attn_part(AttnArgs a) {
   __shared__ AtSmem<NKS> sm;
   const int U = a.n_cu + a.n_wu;
   const int per_seq = U * a.n_hg;
-  const int k = static_cast<int>(blockIdx.x) / a.xcds;  // this block's turn on its XCD
+  const int xs = __builtin_ctz(static_cast<uint32_t>(a.xcds));  // a.xcds is a power of two
+  const int k = static_cast<int>(blockIdx.x) >> xs;             // this block's turn on its XCD
   const int sb = k / per_seq;
-  const int b = static_cast<int>(blockIdx.x) % a.xcds + a.xcds * sb;
+  const int b = (static_cast<int>(blockIdx.x) & (a.xcds - 1)) + (sb << xs);
   if (b >= a.batch) return;  // uniform
   const int r = k - sb * per_seq;
   const int u = r / a.n_hg, hg = r - u * a.n_hg;
@@ -952,13 +953,17 @@ struct RankLds {
 constexpr int kPosEmpty = -2147483647 - 1;  // an output position another unit owns
 
 // Ranking of CSA unit `part` of `parts` of sequence b, over the one layer of
-// a step: its candidates are the entries e with e % parts == part (lists
-// held in LDS; lists ranked from global memory: the lists' entries part,
-// part + parts, ...), so that which picks a unit attends over, and with them
-// its partial output, do not depend on the order in which the filter chunks
-// appended to the lists; positions [part * out, (part + 1) * out), out =
-// ceil(k / parts), are its share of the fills (and of the fallback's
-// positions).
+// a step: its candidates are the entries at positions part, part + parts,
+// ... of each list in canonical order, the list's entries sorted by entry
+// index (restored through the run table the filter chunks write), so that
+// which picks a unit attends over, and with them its partial output, do not
+// depend on the order in which the filter chunks appended to the lists, and
+// every unit holds the same share of the sure candidates.  With more filter
+// chunks than the run table holds, its candidates are the entries e with
+// e % parts == part; with lists longer than LDS holds, the lists' positions
+// part, part + parts, ... as written (not reproducible).  Positions
+// [part * out, (part + 1) * out), out = ceil(k / parts), are its share of
+// the fills (and of the fallback's positions).
 template <int NKS>
 struct StepRank {
   static constexpr bool kOn = true;
@@ -972,6 +977,7 @@ struct StepRank {
   int status = 0, L = 0, cnt0 = 0, cnt1 = 0, flag = 0, n_bt = 0;
   int word = 0;  // lane 0: status, 1: length, 2-4: the lists' counters and tie-overflow flag
   int2 sh, th;
+  int4 run;  // the row's run table entry of filter chunk `lane`
   int32_t btv[kBtPer];
   const int32_t* bt_row = nullptr;
   int32_t* ws = nullptr;
@@ -1010,6 +1016,8 @@ struct StepRank {
     sh = reinterpret_cast<const int2*>(ws + kTkWsSure)[tid];
     th = reinterpret_cast<const int2*>(ws + kTkWsTie)[tid];
     const int lane = tid % kWave;
+    static_assert(kTkRunCap == kWave, "one run table entry per lane");
+    run = reinterpret_cast<const int4*>(ws + kTkWsRuns)[lane];
     word = *(lane == 1 ? map.step_lens + b : (lane >= 2 && lane <= 4) ? ws + kTkWsCnt + (lane - 2) : map.status);
   }
 
@@ -1071,12 +1079,58 @@ struct StepRank {
       const int2* sure_list = reinterpret_cast<const int2*>(ws + kTkWsSure);
       const int2* tie_list = reinterpret_cast<const int2*>(ws + kTkWsTie);
       const bool in_lds = C <= RL::kCkCap;  // uniform
+      // Canonical order of a list: its entries sorted by entry index.  Filter
+      // chunk c (entries [c * kTkChunk, (c + 1) * kTkChunk)) writes its
+      // candidates to one run of slots of each list, sorted by entry index,
+      // and records the run's first slot and length in the row's run table;
+      // the runs follow each other in the order the chunks reserved them.
+      // Slot p of chunk c's run is therefore at canonical position p - first(c)
+      // + (the list's entries in the chunks before c); every wave holds that
+      // difference of chunk `lane` for both lists, as two 16-bit halves (a
+      // scan of the run lengths, both lists' in one word: a list holds fewer
+      // than 2^15 entries).
+      const int n_ch = static_cast<int>(ceil_div24(static_cast<uint32_t>(n_valid), kTkChunk));
+      const bool canon = in_lds && n_ch <= kTkRunCap;  // uniform
+      static_assert(kMaxTopK < (1 << 15) && kTkTieCap < (1 << 15), "16-bit run sums and differences");
+      int d_pack = 0;
+      if (canon) {
+        const int lane = tid % kWave;
+        const int n2 = lane < n_ch ? (run.y | (run.w << 16)) : 0;
+        const int before = wave_prefix_sum(n2) - n2;
+        const int d_sure = (before & 0xffff) - run.x, d_tie = (before >> 16) - run.z;
+        d_pack = static_cast<int>((static_cast<uint32_t>(d_sure) & 0xffffu) | (static_cast<uint32_t>(d_tie) << 16));
+      }
+      // canonical position -> slot, each class at its own offset (sure
+      // [0, S), ties [S, C)), in the (not yet filled) block-table area
+      static_assert(RL::kBtCap >= RL::kCkCap, "canonical map fits the block-table area");
+      int* slot_at = bt;
+      // the canonical position of slot c holding `key`; every lane of the
+      // wave takes part (the lookup reads other lanes' registers)
+      const auto canon_pos = [&](int c, uint64_t key) {
+        const int ch = static_cast<int>((~static_cast<uint32_t>(key)) / kTkChunk) & (kWave - 1);
+        const int d = __shfl(d_pack, ch);
+        return c + (c < S ? static_cast<int>(static_cast<int16_t>(d & 0xffff)) : (d >> 16));
+      };
+      const auto put_slot = [&](int c, int q) {
+        if (c < S ? static_cast<unsigned>(q) < static_cast<unsigned>(S)
+                  : static_cast<unsigned>(q - S) < static_cast<unsigned>(T)) {
+          slot_at[q] = c;
+        }
+      };
       if (in_lds) {
         if (tid < S) ck[tid] = key_sh;
         if (tid < T) ck[S + tid] = key_th;
+        if (canon) {
+          const int qs = canon_pos(tid, key_sh), qt = canon_pos(S + tid, key_th);
+          if (tid < S) put_slot(tid, qs);
+          if (tid < T) put_slot(S + tid, qt);
+        }
         if (S > kAtThreads || T > kAtThreads) {  // uniform: the rest of the lists
           constexpr int kLoad = 4;  // list loads in flight per thread
-          for (int c0 = tid; c0 < C; c0 += kAtThreads * kLoad) {
+          const int lane = tid % kWave;
+          // the trip count is the wave's: canon_pos needs the whole wave
+          for (int w0 = tid - lane; w0 < C; w0 += kAtThreads * kLoad) {
+            const int c0 = w0 + lane;
             int2 v[kLoad];
 #pragma unroll
             for (int u = 0; u < kLoad; ++u) {
@@ -1092,18 +1146,32 @@ struct StepRank {
               // register reuse would then wait for every load in flight
               const uint64_t key = order_key(v[u]);
               asm volatile("" ::"v"(key));
-              if (c < C && !in_head) ck[c] = key;
+              const int q = canon ? canon_pos(c, key) : 0;
+              if (c < C && !in_head) {
+                ck[c] = key;
+                if (canon) put_slot(c, q);
+              }
             }
           }
         }
       }
       lds_barrier();
       const auto put = [&](int pos, int idx) { at_pos[pos] = idx; };
-      if (in_lds) {
-        // the unit's own candidates by entry index, sure ones from the front
-        // of the (not yet filled) block-table area, ties from its back; their
-        // order there is immaterial: each one's position is its rank
-        static_assert(RL::kBtCap >= RL::kCkCap, "own candidates fit the block-table area");
+      if (canon) {
+        // canonical positions part, part + parts, ... of each list: the same
+        // share of the sure candidates for every unit
+        const int n_os = part < S ? static_cast<int>(ceil_div24(S - part, parts)) : 0;
+        const int n_ot = part < T ? static_cast<int>(ceil_div24(T - part, parts)) : 0;
+        rank_candidates_of<kAtThreads, 4>(
+            put, [&](int q) { return ck[q]; },
+            [&](int cls, int j) { return min(max(slot_at[(cls ? S : 0) + part + j * parts], 0), C - 1); }, n_os,
+            n_ot, S, C, sel);
+      } else if (in_lds) {
+        // more filter chunks than the run table holds: the unit's candidates
+        // are the entries e with e % parts == part (its share of the sure
+        // candidates then varies), sure ones from the front of the block-table
+        // area, ties from its back; their order there is immaterial: each
+        // one's position is its rank
         int* own = bt;
         int* own_cnt = scan;  // [0] sure, [1] ties
         if (tid < 2) own_cnt[tid] = 0;
@@ -1215,9 +1283,10 @@ __global__ __launch_bounds__(kAtThreads, 1) void k_decode_attend(AttnArgs a, Ste
   __shared__ AtSmem<NKS> sm;
   const int U = a.n_cu + a.n_wu;
   const int per_seq = U * a.n_hg;
-  const int k = static_cast<int>(blockIdx.x) / a.xcds;
+  const int xs = __builtin_ctz(static_cast<uint32_t>(a.xcds));  // a.xcds is a power of two
+  const int k = static_cast<int>(blockIdx.x) >> xs;
   const int sb = k / per_seq;
-  const int b = static_cast<int>(blockIdx.x) % a.xcds + a.xcds * sb;
+  const int b = (static_cast<int>(blockIdx.x) & (a.xcds - 1)) + (sb << xs);
   if (b >= a.batch) return;  // uniform
   const int r = k - sb * per_seq;
   const int u = r / a.n_hg, hg = r - u * a.n_hg;

@@ -26,7 +26,8 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 int set_error(int code, const char* fmt, ...);
 int check_launch(const char* what);
 // The current device's compute units and XCDs (hipDeviceGetAttribute, read
-// once per device): launch shapes and XCD-affine block placement follow them.
+// once per device; the XCD count is a power of two): launch shapes and
+// XCD-affine block placement follow them.
 int device_cus();
 int device_xcds();
 

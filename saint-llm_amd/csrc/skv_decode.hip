@@ -1107,12 +1107,12 @@ __global__ __launch_bounds__(kStepThreads) void k_decode_gather(const skv_decode
                                                                 int ck_cap, StepMap map) {
   extern __shared__ __align__(16) uint8_t rank_lds[];
   const uint32_t u = blockIdx.x;  // grids stay below 2^24 workgroups
-  const int lanes = map.lanes;
-  const uint32_t g = u / lanes;  // the block's group
+  const int lanes = map.lanes;  // a power of two
+  const uint32_t g = u >> __builtin_ctz(static_cast<uint32_t>(lanes));  // the block's group
   const uint32_t i = udiv24(g, gg.period);
   if (g == i * gg.period && static_cast<int>(i) < gg.n_rank_groups) {
     int b, r;
-    if (!xcd_item(i * lanes + u % lanes, gg.parts_max * map.n_csa, map.batch, lanes, b, r)) return;
+    if (!xcd_item(i * lanes + (u & (lanes - 1)), gg.parts_max * map.n_csa, map.batch, lanes, b, r)) return;
     const int z = static_cast<int>(udiv24(r, gg.parts_max));
     rank_part<kWB>(d, map, rank_lds, r - z * gg.parts_max, b, z, rank_out, bt_lds, ck_cap);
     return;

@@ -27,7 +27,9 @@ int check_launch(const char* what) {
 namespace {
 
 // Per device, read once: compute units and XCDs (XCCs).  A device whose
-// query fails counts as one XCD of 256 compute units.
+// query fails counts as one XCD of 256 compute units; an XCD count that is
+// not a power of two counts as one (placement then ignores the XCDs, and
+// kernels place blocks with shifts and masks).
 struct Topology {
   int cus = 0;
   int xcds = 0;
@@ -51,6 +53,7 @@ Topology topology() {
       (void)hipGetLastError();
       xcds = 1;
     }
+    if (xcds & (xcds - 1)) xcds = 1;
     t.xcds = xcds;
     t.cus = cus;
   }

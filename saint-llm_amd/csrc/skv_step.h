@@ -22,7 +22,7 @@ static_assert(kTkPartThreads == kStepThreads, "top-k chunk workgroups are step w
 // walks the descriptor's layer list through dependent loads to find it.
 struct StepMap {
   int32_t batch;
-  int32_t lanes;  // xcd_lanes(batch)
+  int32_t lanes;  // xcd_lanes(batch), a power of two
   int32_t n_layers;
   int32_t n_csa;
   uint32_t hca_mask;                  // bit l: layer l is an HCA layer
@@ -91,11 +91,12 @@ __host__ __device__ constexpr int64_t xcd_region(int batch, int64_t per_seq) {
   return static_cast<int64_t>(batch) * per_seq;  // lanes divide the batch
 }
 
-// lanes: xcd_lanes(batch) of the launch (a kernel argument).
+// lanes: xcd_lanes(batch) of the launch (a kernel argument, a power of two).
 __device__ __forceinline__ bool xcd_item(uint32_t u, int per_seq, int batch, int lanes, int& b, int& r) {
-  const uint32_t k = u / lanes;  // the block's turn on its XCD
+  const int sh = __builtin_ctz(static_cast<uint32_t>(lanes));
+  const uint32_t k = u >> sh;  // the block's turn on its XCD
   const uint32_t sb = udiv24(k, per_seq);
-  b = static_cast<int>(u % lanes + lanes * sb);
+  b = static_cast<int>((u & (lanes - 1)) + (sb << sh));
   r = static_cast<int>(k - sb * per_seq);
   return b < batch;
 }
@@ -129,6 +130,19 @@ __device__ __forceinline__ int lane_group_sum(int v, int sub_n) {
   if (sub_n >= 16) v += __builtin_amdgcn_update_dpp(0, v, 0x140, 0xF, 0xF, false); // row_mirror
   if (sub_n >= 32) v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xA, 0xF, false); // row_bcast15 into rows 1, 3
   if (sub_n >= 64) v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xC, 0xF, false); // row_bcast31 into rows 2, 3
+  return v;
+}
+
+// Inclusive prefix sum over the 64 lanes of a wave (lane i: the values of
+// lanes 0..i): shifts by 1, 2, 4 and 8 within each row of 16 lanes, then each
+// row's last lane added to the rows after it.  Every lane must be active.
+__device__ __forceinline__ int wave_prefix_sum(int v) {
+  v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xF, 0xF, false);  // row_shr:1
+  v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xF, 0xF, false);  // row_shr:2
+  v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xF, 0xF, false);  // row_shr:4
+  v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xF, 0xF, false);  // row_shr:8
+  v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xA, 0xF, false);  // row_bcast15 into rows 1, 3
+  v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xC, 0xF, false);  // row_bcast31 into rows 2, 3
   return v;
 }
 

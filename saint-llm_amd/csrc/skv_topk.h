@@ -192,7 +192,13 @@ constexpr int kTkWsCnt = kTkBins;       // n_sure, n_tie, tie-overflow flag, (sp
 constexpr int kTkWsFlag = kTkWsCnt + 2;
 constexpr int kTkWsSure = kTkWsCnt + 4; // (key, idx) pairs, kMaxTopK of them
 constexpr int kTkWsTie = kTkWsSure + 2 * kMaxTopK;
-constexpr int kTkWsWords = kTkWsTie + 2 * kTkTieCap;
+// filter chunk c < kTkRunCap: (first slot, count) of its run in the sure
+// list, then in the tie list, so that a reader can put the lists in entry
+// order without sorting them
+constexpr int kTkRunCap = 64;
+constexpr int kTkWsRuns = kTkWsTie + 2 * kTkTieCap;
+constexpr int kTkWsWords = kTkWsRuns + 4 * kTkRunCap;
+static_assert(kTkWsRuns % 4 == 0 && kTkWsWords % 4 == 0, "16-byte run entries in 16-byte aligned rows");
 
 __device__ __forceinline__ int topk_sel(int k, int n_cols, int n_valid) {
   n_cols = max(n_cols, 0);
@@ -307,8 +313,9 @@ struct TopkFilterSmem {
 
 // The chunk's keys stay in registers: a first ballot pass counts each wave's
 // sure and tie candidates, one global atomic per list reserves the chunk's
-// slots, and a second ballot pass writes every candidate to its slot (waves in
-// order, lanes in order, so each list is index-sorted within a chunk).  The
+// slots (recorded in the row's run table), and a second ballot pass writes
+// every candidate to its slot (waves in order, lanes in order, so each list
+// is index-sorted within a chunk).  The
 // scores are loaded before the histogram is read, so the two memory
 // latencies overlap.  A tie bin above kTkTieCap is flagged in ws[kTkWsFlag]
 // by chunk 0 and no list is written.
@@ -368,7 +375,12 @@ __device__ __forceinline__ void topk_filter_chunk_at(TopkFilterSmem& sm, const f
     int tot = 0;
 #pragma unroll
     for (int w = 0; w < kWaves; ++w) tot += sm.wcnt[tid][w];
-    sm.base[tid] = tot ? atomicAdd(&ws[kTkWsCnt + tid], tot) : 0;
+    const int base = tot ? atomicAdd(&ws[kTkWsCnt + tid], tot) : 0;
+    sm.base[tid] = base;
+    if (chunk < kTkRunCap) {
+      ws[kTkWsRuns + 4 * chunk + 2 * tid] = base;
+      ws[kTkWsRuns + 4 * chunk + 2 * tid + 1] = tot;
+    }
   }
   __syncthreads();
   int ps = sm.base[0], pt = sm.base[1];
