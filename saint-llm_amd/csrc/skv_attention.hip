@@ -219,7 +219,12 @@ __device__ __forceinline__ void attn_unit(AtSmem<NKS>& sm, const AttnArgs& a, in
   static_assert(!kRanked || kComp, "ranked keys are compressed entries");
   using TC = TileChunks<NKS>;
   const int tid = threadIdx.x;
-  const int wave = tid / kWave, lane = tid % kWave;
+  // a ranked unit takes the wave's index as a scalar (uniform) value: the
+  // values derived from it then stay out of the vector registers, which its
+  // tile loop fills (spill stores ahead of the loop would hold its first
+  // wait on the vector memory count); the other units keep the allocation
+  // that spills least for them
+  const int wave = (kRanked ? __builtin_amdgcn_readfirstlane(tid) : tid) / kWave, lane = tid % kWave;
   const int hb = wave >> 1, half = wave & 1;
   const int col = lane & 15, grp = lane >> 4;
   const int L = min(max(a.lens[b], 0), (1 << 24) - 1);
@@ -1057,14 +1062,14 @@ struct StepRank {
     cnt1 = __builtin_amdgcn_readlane(word, 3);
     flag = __builtin_amdgcn_readlane(word, 4);
     for (int i = tid; i < k; i += kAtThreads) at_pos[i] = kPosEmpty;
-    if (status) return 0;  // refused step
+    if (__builtin_expect(status != 0, 0)) return 0;  // refused step
     int n_cols, n_valid;
     score_cols(map.score_stride[0], m, L, n_cols, n_valid);
     const int sel = topk_sel(k, n_cols, n_valid);
     const int out = static_cast<int>(ceil_div24(k, parts));
     const int o0 = min(k, part * out), o1 = min(k, o0 + out);
     lds_barrier();
-    if (sel > 0 && flag) {
+    if (__builtin_expect(sel > 0 && flag, 0)) {
       // tie bin over the list capacity: full select of the row, keeping this
       // unit's positions
       auto& fb = *reinterpret_cast<TopkSmemT<kAtThreads>*>(ck);
@@ -1125,7 +1130,7 @@ struct StepRank {
           if (tid < S) put_slot(tid, qs);
           if (tid < T) put_slot(S + tid, qt);
         }
-        if (S > kAtThreads || T > kAtThreads) {  // uniform: the rest of the lists
+        if (__builtin_expect(S > kAtThreads || T > kAtThreads, 0)) {  // uniform: the rest of the lists
           constexpr int kLoad = 4;  // list loads in flight per thread
           const int lane = tid % kWave;
           // the trip count is the wave's: canon_pos needs the whole wave
@@ -1157,7 +1162,7 @@ struct StepRank {
       }
       lds_barrier();
       const auto put = [&](int pos, int idx) { at_pos[pos] = idx; };
-      if (canon) {
+      if (__builtin_expect(canon, 1)) {
         // canonical positions part, part + parts, ... of each list: the same
         // share of the sure candidates for every unit
         const int n_os = part < S ? static_cast<int>(ceil_div24(S - part, parts)) : 0;

@@ -109,6 +109,7 @@ __device__ __forceinline__ uint64_t order_key(int2 v) {
 
 constexpr int kRankR = 4;  // candidates a lane compares with each key it reads
 
+
 // Lanes that share a group of kRankR candidates: the largest power of two
 // in [1, 64] that still gives every group of the round its lanes.
 template <int NT>
@@ -192,9 +193,23 @@ __device__ __forceinline__ void rank_candidates_of(Win win, KeyAt ck, Cand cand,
     } else {
       // KU key reads in flight per lane: the trip count is the lane group's
       // (a lane's own count makes the loop divergent, and each read is then
-      // waited for before the next is issued); reads past the list are
-      // clamped to its last key and not counted
-      for (int q0 = lo; q0 < hi; q0 += KU * sub_n) {
+      // waited for before the next is issued).  Whole chunks of KU * sub_n
+      // keys first, every read inside the list and every compare counted (a
+      // per-key mask would put a scalar AND between each compare and its
+      // add); then the chunk the list ends in, its reads clamped to the
+      // list's last key and not counted past the end
+      int q0 = lo;
+      for (; q0 + KU * sub_n <= hi; q0 += KU * sub_n) {
+        uint64_t key[KU];
+#pragma unroll
+        for (int u = 0; u < KU; ++u) key[u] = ck(q0 + sub + u * sub_n);
+#pragma unroll
+        for (int u = 0; u < KU; ++u) {
+#pragma unroll
+          for (int r = 0; r < kRankR; ++r) rank[r] += key[u] > mine[r];
+        }
+      }
+      if (q0 < hi) {  // uniform over the lane group
         uint64_t key[KU];
 #pragma unroll
         for (int u = 0; u < KU; ++u) key[u] = ck(min(q0 + sub + u * sub_n, hi - 1));
