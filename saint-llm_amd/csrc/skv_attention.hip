@@ -1167,10 +1167,10 @@ struct StepRank {
         // share of the sure candidates for every unit
         const int n_os = part < S ? static_cast<int>(ceil_div24(S - part, parts)) : 0;
         const int n_ot = part < T ? static_cast<int>(ceil_div24(T - part, parts)) : 0;
-        rank_candidates_of<kAtThreads, 4>(
-            put, [&](int q) { return ck[q]; },
-            [&](int cls, int j) { return min(max(slot_at[(cls ? S : 0) + part + j * parts], 0), C - 1); }, n_os,
-            n_ot, S, C, sel);
+        const auto own_slot = [&](int cls, int j) {
+          return min(max(slot_at[(cls ? S : 0) + part + j * parts], 0), C - 1);
+        };
+        rank_candidates_of<kAtThreads, 4>(put, [&](int q) { return ck[q]; }, own_slot, n_os, n_ot, S, C, sel);
       } else if (in_lds) {
         // more filter chunks than the run table holds: the unit's candidates
         // are the entries e with e % parts == part (its share of the sure

@@ -176,13 +176,21 @@ __device__ __forceinline__ void rank_candidates_of(Win win, KeyAt ck, Cand cand,
     const int hi = cls ? C : S;
     const int n_mine = cls ? n_tie_mine : n_sure_mine;
     const int j0 = (cls ? g - ng_sure : g) * kRankR;  // the group's first candidate
+    // the group's candidates: their list indices first, clamped into the
+    // group (n_mine >= 1 here), so that every read is issued before any is
+    // waited for, then their keys; a candidate past the group never counts
     uint64_t mine[kRankR];
     int rank[kRankR];
+    int ci[kRankR];
+#pragma unroll
+    for (int r = 0; r < kRankR; ++r) ci[r] = cand(cls, min(j0 + r, n_mine - 1));
 #pragma unroll
     for (int r = 0; r < kRankR; ++r) {
-      mine[r] = (j0 + r < n_mine) ? ck(cand(cls, j0 + r)) : ~0ull;
+      mine[r] = ck(ci[r]);
       rank[r] = 0;
     }
+#pragma unroll
+    for (int r = 0; r < kRankR; ++r) mine[r] = (j0 + r < n_mine) ? mine[r] : ~0ull;
     if constexpr (KU == 1) {
 #pragma unroll 4
       for (int q = lo + sub; q < hi; q += sub_n) {
@@ -198,16 +206,28 @@ __device__ __forceinline__ void rank_candidates_of(Win win, KeyAt ck, Cand cand,
       // per-key mask would put a scalar AND between each compare and its
       // add); then the chunk the list ends in, its reads clamped to the
       // list's last key and not counted past the end
-      int q0 = lo;
-      for (; q0 + KU * sub_n <= hi; q0 += KU * sub_n) {
-        uint64_t key[KU];
-#pragma unroll
-        for (int u = 0; u < KU; ++u) key[u] = ck(q0 + sub + u * sub_n);
+      // the next chunk's keys are read before this chunk's are compared
+      const auto count = [&](const uint64_t(&key)[KU]) {
 #pragma unroll
         for (int u = 0; u < KU; ++u) {
 #pragma unroll
           for (int r = 0; r < kRankR; ++r) rank[r] += key[u] > mine[r];
         }
+      };
+      int q0 = lo;
+      if (q0 + KU * sub_n <= hi) {
+        uint64_t key[KU];
+#pragma unroll
+        for (int u = 0; u < KU; ++u) key[u] = ck(q0 + sub + u * sub_n);
+        for (q0 += KU * sub_n; q0 + KU * sub_n <= hi; q0 += KU * sub_n) {
+          uint64_t nxt[KU];
+#pragma unroll
+          for (int u = 0; u < KU; ++u) nxt[u] = ck(q0 + sub + u * sub_n);
+          count(key);
+#pragma unroll
+          for (int u = 0; u < KU; ++u) key[u] = nxt[u];
+        }
+        count(key);
       }
       if (q0 < hi) {  // uniform over the lane group
         uint64_t key[KU];
