@@ -434,23 +434,33 @@ int skv_decode_step(const skv_decode_desc* host_desc, const skv_decode_desc* dev
                     void* stream);
 int skv_decode_step_launches(const skv_decode_desc* host_desc);
 
-/* Decode attention of one layer over the paged cache (one query token per
+/* Decode attention of one layer over the paged cache (T query tokens per
  * sequence, MQA: one K/V head, n_heads query heads of head_dim), the gather
  * fused in: replaces the cached-step attention of CSA.forward
  * (csa.py:324-373: sparse branch over the top-k picks + window branch),
  * HCA.forward (hca.py:126-169: dense branch over the visible entries + window
  * branch) and SWAttention.forward (swa.py:115-137: window branch), with
  * scaled_dot_product / softmax_with_sink / RMSNorm of common.py:12-124.
- *   out[b,h,:] = compressed(b,h) + window(b,h), each its own softmax with
- *   scores q.k / sqrt(head_dim):
+ * Query token t of sequence b (q, out: [batch, T, n_heads, head_dim]; T = 1
+ * is [batch, n_heads, head_dim]) is the cache's position q_pos = lens[b] - T
+ * + t: the T tokens were appended last, as the cached forward of csa.py:276-
+ * 281 and hca.py:127-131 sees them (cache_offset = lens[b] - T).  It sees the
+ * first L_t = q_pos + 1 positions:
+ *   out[b,t,h,:] = compressed(b,t,h) + window(b,t,h), each its own softmax
+ *   with scores q.k / sqrt(head_dim):
  *   compressed: K = V = k_norm(entry) = knorm_w * e * rsqrt(mean(e^2) + eps);
- *     CSA: the picks picks[b, j] >= 0 (j < top_k; picks >= n_entries[b] are
- *     masked), no sink; HCA: entries s < floor((lens[b]-1)/m) (s*m + m-1 <
- *     q_pos), with the sink; SWA: none.  No live key: adds 0.
- *   window: keys win_k and values win_v of positions [L - min(W, L), L),
- *     L = lens[b], ring slot pos % W ([batch, window, head_dim] bf16, keys
- *     already normed and roped as the reference caches them), the sink, and
- *     the softcap c*tanh(s/c) when softcap > 0.
+ *     CSA: the picks picks[b, t, j] >= 0 (rows of pick_stride; j < top_k;
+ *     picks >= n_entries[b] are masked), no sink; HCA: entries s <
+ *     floor(q_pos/m) (s*m + m-1 < q_pos, hca.py:128-130), at most
+ *     n_entries[b], with the sink; SWA: none.  No live key: adds 0.
+ *   window: keys win_k and values win_v of positions [L_t - min(W, L_t),
+ *     L_t) (k_pos <= q_pos and q_pos - k_pos < W, swa.py:121-124), ring slot
+ *     pos % ring ([batch, ring, head_dim] bf16, keys already normed and roped
+ *     as the reference caches them), the sink, and the softcap c*tanh(s/c)
+ *     when softcap > 0.  The ring must hold the last min(W + T - 1,
+ *     lens[b]) positions: a ring of W + T - 1 slots or more always does, and
+ *     so does a contiguous cache of the sequence's whole capacity (slot pos
+ *     = pos), such as SWAKVCacheLayer's.
  * The pool's entries are bf16 or fp8 (dequantized to bf16 as the gathers
  * do).  Two launches: per (sequence, split, 64 heads) partial softmax
  * statistics and outputs into `workspace` (16-byte aligned), then the merge
@@ -477,10 +487,14 @@ typedef struct skv_attention_desc {
   float eps;
   float softcap;            /* <= 0: none */
   const float* sink;        /* [n_heads] or NULL */
-  const void* win_k;        /* [batch, window, head_dim] bf16 */
-  const void* win_v;        /* [batch, window, head_dim] bf16 (may equal win_k) */
+  const void* win_k;        /* [batch, ring] slots of head_dim bf16, win_stride apart */
+  const void* win_v;        /* the same for values (may equal win_k) */
   int64_t window;
   int64_t splits;           /* 0: chosen by the library */
+  int64_t n_queries;        /* query tokens per sequence, T (0: 1; at most 4096) */
+  int64_t ring;             /* window slots per sequence (0: window), >= window; see above */
+  int64_t win_stride;       /* bytes from one window slot to the next (0: head_dim * 2; a
+                               multiple of 16), e.g. 4 * head_dim for [K | V] rows */
 } skv_attention_desc;
 
 int64_t skv_attention_workspace(const skv_attention_desc* desc);

@@ -47,6 +47,7 @@ constexpr int kAtWaves = kAtThreads / 64;
 constexpr int kAtHeads = 64;  // query heads per workgroup: 16 per pair of waves
 constexpr int kAtTile = 32;   // keys per tile
 constexpr int kAtMaxD = 576;
+constexpr int kAtMaxQueries = 4096;  // query tokens per sequence of one call
 constexpr int kAtRun = 512;   // keys whose source rows are resolved at once
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr int kAhead = 4;  // LDS operand reads in flight ahead of the products
@@ -66,7 +67,11 @@ struct AttnArgs {
   int64_t entry_bytes, pick_stride;
   int32_t kind, fp8_main;  // fp8_main > 0: fp8 entries with that many coded dims
   int32_t block_size, n_pages, bt_stride, m, top_k;
-  int32_t window, H, D, n_hg, n_cu, n_wu, batch;
+  int32_t window, H, D, n_hg, n_cu, n_wu;
+  int32_t batch;       // query rows: sequences x n_q
+  int32_t n_q;         // query tokens per sequence (row b: sequence b / n_q, token b % n_q)
+  int32_t ring;        // window slots per sequence of win_k / win_v
+  int64_t win_row;     // bytes from one window slot to the next
   float eps, softcap;  // softcap <= 0: none
   int32_t fused;       // 1: the decode step's last launch (lens are the step's new lengths)
   int32_t xcds;        // the device's XCDs, a power of two (unit placement)
@@ -227,8 +232,11 @@ __device__ __forceinline__ void attn_unit(AtSmem<NKS>& sm, const AttnArgs& a, in
   const int wave = (kRanked ? __builtin_amdgcn_readfirstlane(tid) : tid) / kWave, lane = tid % kWave;
   const int hb = wave >> 1, half = wave & 1;
   const int col = lane & 15, grp = lane >> 4;
-  const int L = min(max(a.lens[b], 0), (1 << 24) - 1);
-  // keys of this branch for sequence b (ranked: known after the ranking)
+  // query row b is token t of sequence cb, position L - n_q + t of its L
+  // tokens: it sees the first L - n_q + t + 1 of them
+  const int cb = b / a.n_q, t_q = b - cb * a.n_q;
+  const int L = min(max(a.lens[cb] - (a.n_q - 1 - t_q), 0), (1 << 24) - 1);
+  // keys of this branch for query row b (ranked: known after the ranking)
   int n_keys = 0;
   if constexpr (!kComp) {
     n_keys = min(L, a.window);
@@ -240,7 +248,7 @@ __device__ __forceinline__ void attn_unit(AtSmem<NKS>& sm, const AttnArgs& a, in
       // count committed beside it bounds it by
       const int q_pos = max(L - 1, 0);
       n_keys = a.fused ? static_cast<int>(udiv24(q_pos, a.m))
-                       : min(static_cast<int>(udiv24(q_pos, a.m)), max(a.n_entries[b], 0));
+                       : min(static_cast<int>(udiv24(q_pos, a.m)), max(a.n_entries[cb], 0));
     }
   }
   int n_tiles = (n_keys + kAtTile - 1) / kAtTile;
@@ -277,7 +285,7 @@ __device__ __forceinline__ void attn_unit(AtSmem<NKS>& sm, const AttnArgs& a, in
     const bool csa = a.kind == SKV_LAYER_CSA && n_keys > 0;
     pick0 = *(csa ? a.picks + static_cast<int64_t>(b) * a.pick_stride + min(t_lo * kAtTile + tid, n_keys - 1)
                   : reinterpret_cast<const int32_t*>(g_zero_row));
-    ne0 = a.n_entries[b];
+    ne0 = a.n_entries[cb];
     w_lo = a.knorm_w[min(tid, D - 1)];
     w_hi = a.knorm_w[min(tid + kAtThreads, D - 1)];
   }
@@ -303,7 +311,7 @@ __device__ __forceinline__ void attn_unit(AtSmem<NKS>& sm, const AttnArgs& a, in
     e0 = (pick0 < max(ne0, 0)) ? pick0 : -1;
     pi0 = e0 >= 0 ? static_cast<int>(udiv24(e0, a.block_size)) : 0;
     if (pi0 >= a.bt_stride) e0 = -1;
-    page0 = *(e0 >= 0 ? a.block_table + static_cast<int64_t>(b) * a.bt_stride + pi0
+    page0 = *(e0 >= 0 ? a.block_table + static_cast<int64_t>(cb) * a.bt_stride + pi0
                       : reinterpret_cast<const int32_t*>(g_zero_row));
   }
   __builtin_amdgcn_sched_barrier(0);
@@ -338,7 +346,7 @@ __device__ __forceinline__ void attn_unit(AtSmem<NKS>& sm, const AttnArgs& a, in
   const bool capped = !kComp && a.softcap > 0.f;
   const float inv_cap = capped ? 1.f / a.softcap : 0.f;
   const float cap_log2e = a.softcap * kLog2e;
-  const int64_t row_bytes = kComp ? a.entry_bytes : static_cast<int64_t>(D) * 2;
+  const int64_t row_bytes = kComp ? a.entry_bytes : a.win_row;
   const uint8_t* kbase = kComp ? a.pool : a.win_k;
   float m_run = -__builtin_huge_valf(), l_run = 0.f;
   f32x4 acc_o[kDbW];
@@ -354,7 +362,7 @@ __device__ __forceinline__ void attn_unit(AtSmem<NKS>& sm, const AttnArgs& a, in
       if (j < n_keys) {
         if constexpr (!kComp) {
           const int pos = L - n_keys + j;
-          row = (static_cast<int64_t>(b) * a.window + static_cast<int>(umod24(pos, a.window))) * row_bytes;
+          row = (static_cast<int64_t>(cb) * a.ring + static_cast<int>(umod24(pos, a.ring))) * row_bytes;
         } else if constexpr (kRanked) {
           const int64_t r = rk.row(j);
           row = r >= 0 ? r * row_bytes : -1;
@@ -368,13 +376,13 @@ __device__ __forceinline__ void attn_unit(AtSmem<NKS>& sm, const AttnArgs& a, in
               }
             } else {
               e = a.picks[static_cast<int64_t>(b) * a.pick_stride + j];
-              if (e >= max(a.n_entries[b], 0)) e = -1;
+              if (e >= max(a.n_entries[cb], 0)) e = -1;
             }
           }
           if (e >= 0) {
             const int pi = static_cast<int>(udiv24(e, a.block_size));
             if (pi < a.bt_stride) {
-              const int32_t page = a.block_table[static_cast<int64_t>(b) * a.bt_stride + pi];
+              const int32_t page = a.block_table[static_cast<int64_t>(cb) * a.bt_stride + pi];
               if (page >= 0 && page < a.n_pages) {
                 row = (static_cast<int64_t>(page) * a.block_size + (e - pi * a.block_size)) * row_bytes;
               }
@@ -812,6 +820,8 @@ __global__ __launch_bounds__(256) void k_attn_merge_q(MergeArgs a) {
 
 struct AttnPlan {
   int n_cu, n_wu, n_hg, nks;
+  int64_t rows;  // query rows: batch x query tokens per sequence
+  int64_t nq, ring, win_row;
   int64_t ws_bytes;
 };
 
@@ -829,6 +839,20 @@ int attn_plan(const skv_attention_desc* d, AttnPlan& p) {
     return set_error(SKV_EINVAL, "%s: head_dim must be a multiple of 32 in [32, %d]", what, kAtMaxD);
   }
   if (d->window < 1 || d->window >= (1 << 24)) return set_error(SKV_EINVAL, "%s: window must be in [1, 2^24)", what);
+  p.nq = d->n_queries > 0 ? d->n_queries : 1;
+  p.ring = d->ring > 0 ? d->ring : d->window;
+  if (d->n_queries < 0 || p.nq > kAtMaxQueries) {
+    return set_error(SKV_EINVAL, "%s: n_queries must be in [0, %d]", what, kAtMaxQueries);
+  }
+  if (d->ring < 0 || p.ring >= (1 << 24) || p.ring < d->window) {
+    return set_error(SKV_EINVAL, "%s: ring must be in [window, 2^24)", what);
+  }
+  p.win_row = d->win_stride > 0 ? d->win_stride : d->head_dim * 2;
+  if (d->win_stride < 0 || (d->win_stride > 0 && (d->win_stride < d->head_dim * 2 || d->win_stride % 16))) {
+    return set_error(SKV_EINVAL, "%s: win_stride must be 0 or a multiple of 16 of at least head_dim * 2", what);
+  }
+  p.rows = d->batch * p.nq;
+  if (p.rows >= (1 << 24)) return set_error(SKV_EINVAL, "%s: batch x n_queries must be < 2^24", what);
   const bool comp = d->kind != SKV_LAYER_SWA;
   int64_t comp_keys = 0;
   if (comp) {
@@ -867,7 +891,7 @@ int attn_plan(const skv_attention_desc* d, AttnPlan& p) {
     // and V) while the grid is short of one workgroup per CU of the device
     // (a CU holds one) and units keep at least 2 tiles' worth of reads
     const int cus = device_cus();
-    while (d->batch * p.n_hg * (n_cu + n_wu) < cus && n_cu + n_wu < kMergeUnits) {
+    while (p.rows * p.n_hg * (n_cu + n_wu) < cus && n_cu + n_wu < kMergeUnits) {
       const double pc = n_cu ? static_cast<double>(tiles_c) / n_cu : 0.0;
       const double pw = 2.0 * tiles_w / n_wu;
       if (pc >= pw && pc >= 2.0) {
@@ -890,7 +914,7 @@ int attn_plan(const skv_attention_desc* d, AttnPlan& p) {
   }
   p.n_cu = static_cast<int>(n_cu);
   p.n_wu = static_cast<int>(n_wu);
-  const int64_t units = d->batch * (n_cu + n_wu) * p.n_hg;
+  const int64_t units = p.rows * (n_cu + n_wu) * p.n_hg;
   if (units >= (1 << 30)) return set_error(SKV_EINVAL, "%s: too many workgroups", what);
   p.ws_bytes = units * kAtHeads * (2 * static_cast<int64_t>(sizeof(float)) + d->head_dim * 2);  // (max, sum) fp32, O bf16
   return SKV_OK;
@@ -1335,6 +1359,12 @@ int decode_attend(const skv_attention_desc* d, const skv_decode_desc* h, const S
   x.win_k = Ly.ring;
   if (!x.win_v) x.win_v = Ly.ring;
   x.window = h->window;
+  if (d->n_queries > 1 || d->ring > 0 || d->win_stride > 0) {
+    return set_error(SKV_EINVAL, "%s: one query token per sequence over the layer's ring (n_queries 0 or 1, "
+                     "ring and win_stride 0)", what);
+  }
+  x.n_queries = 1;
+  x.ring = h->window;
   if (comp) {
     const skv_page_group& G = h->groups[Ly.group];
     x.pool = Ly.pool;
@@ -1391,6 +1421,9 @@ int decode_attend(const skv_attention_desc* d, const skv_decode_desc* h, const S
   a.n_cu = p.n_cu;
   a.n_wu = p.n_wu;
   a.batch = static_cast<int32_t>(x.batch);
+  a.n_q = 1;
+  a.ring = static_cast<int32_t>(x.window);
+  a.win_row = x.head_dim * 2;
   a.eps = x.eps;
   a.softcap = x.softcap;
   a.fused = 1;
@@ -1466,13 +1499,16 @@ extern "C" int skv_decode_attention(const skv_attention_desc* d, void* workspace
   a.n_hg = p.n_hg;
   a.n_cu = p.n_cu;
   a.n_wu = p.n_wu;
-  a.batch = static_cast<int32_t>(d->batch);
+  a.batch = static_cast<int32_t>(p.rows);
+  a.n_q = static_cast<int32_t>(p.nq);
+  a.ring = static_cast<int32_t>(p.ring);
+  a.win_row = p.win_row;
   a.eps = d->eps;
   a.softcap = d->softcap;
   a.fused = 0;
   a.xcds = device_xcds();
   hipStream_t s = static_cast<hipStream_t>(stream);
-  const dim3 grid(static_cast<unsigned>(a.xcds * ceil_div(d->batch, a.xcds) * (p.n_cu + p.n_wu) * p.n_hg));
+  const dim3 grid(static_cast<unsigned>(a.xcds * ceil_div(p.rows, a.xcds) * (p.n_cu + p.n_wu) * p.n_hg));
   if (a.fp8_main > 0) {
     hipLaunchKernelGGL((k_attn_part<18, true>), grid, dim3(kAtThreads), 0, s, a);
   } else if (p.nks == 4) {

@@ -9,7 +9,7 @@ C-ABI call.
 """
 
 from saint_kv import ops
-from saint_kv.attention import decode_attention
+from saint_kv.attention import cached_attention, decode_attention
 from saint_kv.decode import CapturedSteps, DecodeCache, LayerSpec
 from saint_kv.kv_cache import CSAKVCacheLayer, HCAKVCacheLayer, KVCacheBundle, SWAKVCacheLayer
 
@@ -21,6 +21,7 @@ __all__ = [
     "KVCacheBundle",
     "LayerSpec",
     "SWAKVCacheLayer",
+    "cached_attention",
     "decode_attention",
     "ops",
 ]

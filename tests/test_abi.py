@@ -111,6 +111,19 @@ def test_attention_descriptor_and_workspace() -> None:
     bad = AttentionDesc.from_buffer_copy(d)
     bad.kind, bad.m = KIND["hca"], 0
     assert lib.skv_attention_workspace(ctypes.byref(bad)) == -1 and "m >= 1" in _lib.last_error()
+    # T query tokens per sequence: units per query row (a multiple of the 64
+    # rows), and the window's ring and slot stride
+    multi = AttentionDesc.from_buffer_copy(d)
+    multi.n_queries, multi.ring, multi.win_stride = 4, 131, 4 * 576
+    ws_multi = lib.skv_attention_workspace(ctypes.byref(multi))
+    assert ws_multi > 0 and ws_multi % (64 * per_unit) == 0
+    for field, value, msg in (("n_queries", -1, "n_queries"), ("n_queries", 5000, "n_queries"),
+                              ("ring", 100, "ring"), ("win_stride", 1000, "win_stride"),
+                              ("win_stride", 1160, "win_stride")):
+        bad = AttentionDesc.from_buffer_copy(multi)
+        setattr(bad, field, value)
+        assert lib.skv_attention_workspace(ctypes.byref(bad)) == -1
+        assert msg in _lib.last_error()
 
 
 def test_single_hip_runtime_mapped() -> None:
