@@ -401,7 +401,7 @@ union AppendSmem {
 __global__ __launch_bounds__(kStepThreads) void k_decode_append(const skv_decode_desc* __restrict__ d,
                                                                 int n_chunks, StepMap map) {
   __shared__ AppendSmem sm;
-  const int n_append = static_cast<int>(xcd_region(map.batch, map.n_layers));
+  const int n_append = map.n_own;
   const int tid = threadIdx.x;
   if (static_cast<int>(blockIdx.x) >= n_append) {
     // top-k filter chunk: candidate lists from the complete histogram
@@ -1211,6 +1211,14 @@ int decode_step(const skv_decode_desc* h, const skv_decode_desc* dd, void* strea
   StepMap map{};
   map.batch = h->batch;
   map.lanes = xcd_lanes(h->batch);
+  // the append launch's filter chunk i runs on the XCD (block index mod XCDs)
+  // that ran histogram chunk i, and re-reads its scores from that XCD's L2:
+  // the (layer, sequence) blocks before the chunks fill whole rounds of XCDs
+  // (with lanes = XCDs they already do; the extra blocks exit at once)
+  {
+    const int64_t own = xcd_region(h->batch, h->n_layers), x = device_xcds();
+    map.n_own = static_cast<int32_t>(map.lanes == 1 && x > 1 ? ceil_div(own, x) * x : own);
+  }
   map.n_layers = h->n_layers;
   map.n_groups = h->n_groups;
   map.tok_lens = h->tok_lens;
@@ -1321,7 +1329,7 @@ int decode_step(const skv_decode_desc* h, const skv_decode_desc* dd, void* strea
   }
   if (h->batch == 0 || h->n_layers == 0) return SKV_OK;
   const int n_chunks = static_cast<int>(ceil_div(max_score_cols, kTkChunk));
-  const int64_t n_append = xcd_region(h->batch, h->n_layers) + xcd_region(h->batch, static_cast<int64_t>(n_chunks) * n_csa);
+  const int64_t n_append = map.n_own + xcd_region(h->batch, static_cast<int64_t>(n_chunks) * n_csa);
   const int64_t n_hist = xcd_region(h->batch, static_cast<int64_t>(n_chunks) * n_csa);
   // smaller parts when the rows alone would leave most CUs idle
   int rank_out = kRankOut;

@@ -23,6 +23,7 @@ static_assert(kTkPartThreads == kStepThreads, "top-k chunk workgroups are step w
 struct StepMap {
   int32_t batch;
   int32_t lanes;  // xcd_lanes(batch), a power of two
+  int32_t n_own;  // the append launch's (layer, sequence) blocks, before its filter chunks
   int32_t n_layers;
   int32_t n_csa;
   uint32_t hca_mask;                  // bit l: layer l is an HCA layer
