@@ -85,13 +85,26 @@ __device__ __forceinline__ int slot_key(int a, int j) { return (j < 4) ? 4 * a +
 template <int NKS>
 struct AtSmem {
   static constexpr int kD = NKS * 32;
-  alignas(16) uint16_t kr[kAtTile][kD + 8];  // row-major keys (16 bytes of pad per row)
-  alignas(16) uint16_t vs[kAtTile][kD + 8];  // row-major window values
+  // keys and window values: kAtTile rows of kD elements (32 bytes of pad
+  // per row) in swizzled 16-byte chunks (tile_chunk)
+  alignas(16) uint16_t kr[kAtTile][kD + 16];
+  alignas(16) uint16_t vs[kAtTile][kD + 16];
   int64_t row[kAtRun];                       // byte offset of each key's source row in the run, -1 masked
   f32x4 sx[kAtWaves][2][kWave];              // per wave: its half-dims S^T partial per key block
   float ssx[2][2][16];                       // per half of the dims: the keys' sums of squares
   float w[kAtMaxD];                          // k_norm weight (compressed branch)
 };
+
+// A tile row's 16-byte chunk c (dims 8c..8c+7) sits at chunk c ^ ((r/4) % 2)
+// of its LDS row; rows are kD + 16 elements apart.  The LDS has 32 banks of 4
+// bytes, 8 chunks per bank round, and a row starts 2 chunks further round
+// than the one before.  The 8 lanes of one cycle of a 16-byte operand read
+// (rows r..r+7, one chunk c) then take chunks c + 2i (rows r + i, i < 4) and
+// (c ^ 1) + 2i (the next 4), every position of the round once; the 16 lanes of
+// one cycle of a transposing read (rows 4g..4g+3, an aligned pair of chunks
+// each) take 4 different pairs.  (Rows of kD + 8 elements, one chunk round
+// apart, put two of those rows' pairs on the same banks.)
+__device__ __forceinline__ int tile_chunk(int r, int c) { return c ^ ((r >> 2) & 1); }
 
 // Zero bytes that dead chunks (masked keys, dims past D) are read from: no
 // select follows a load, so the loaded registers are first used when they are
@@ -128,13 +141,14 @@ __device__ __forceinline__ void load_tile(RawBf16<NKS>& r, const int64_t* rows, 
 }
 
 template <int NKS>
-__device__ __forceinline__ void store_tile(uint16_t (*dst)[NKS * 32 + 8], const RawBf16<NKS>& r) {
+__device__ __forceinline__ void store_tile(uint16_t* dst, const RawBf16<NKS>& r) {
   using TC = TileChunks<NKS>;
 #pragma unroll
   for (int k = 0; k < TC::kPer; ++k) {
     const int q = static_cast<int>(threadIdx.x) + k * kAtThreads;
     if (TC::kTotal % kAtThreads == 0 || q < TC::kTotal) {
-      *reinterpret_cast<u32x4*>(&dst[q / TC::kChunks][8 * (q % TC::kChunks)]) = r.v[k];
+      const int row = q / TC::kChunks;
+      *reinterpret_cast<u32x4*>(dst + row * (NKS * 32 + 16) + 8 * tile_chunk(row, q % TC::kChunks)) = r.v[k];
     }
   }
 }
@@ -171,7 +185,7 @@ __device__ __forceinline__ void load_tile(RawFp8& r, const int64_t* rows, const 
   r.rope = *reinterpret_cast<const u32x4*>(p + kFp8Main + (kFp8Main >> 7) * 4 + (qr % kFp8RopeChunks) * 16);
 }
 
-__device__ __forceinline__ void store_tile(uint16_t (*dst)[kAtMaxD + 8], const RawFp8& r) {
+__device__ __forceinline__ void store_tile(uint16_t* dst, const RawFp8& r) {
   const int tid = threadIdx.x;
 #pragma unroll
   for (int k = 0; k < kFp8CodePer; ++k) {
@@ -182,10 +196,13 @@ __device__ __forceinline__ void store_tile(uint16_t (*dst)[kAtMaxD + 8], const R
     u32x4 o;
 #pragma unroll
     for (int h = 0; h < 4; ++h) o[h] = bf16_pack2(f[2 * h] * r.scale[k], f[2 * h + 1] * r.scale[k]);
-    *reinterpret_cast<u32x4*>(&dst[q / kFp8CodeChunks][8 * (q % kFp8CodeChunks)]) = o;
+    const int row = q / kFp8CodeChunks;
+    *reinterpret_cast<u32x4*>(dst + row * (kAtMaxD + 16) + 8 * tile_chunk(row, q % kFp8CodeChunks)) = o;
   }
   if (tid < kAtTile * kFp8RopeChunks) {
-    *reinterpret_cast<u32x4*>(&dst[tid / kFp8RopeChunks][kFp8Main + 8 * (tid % kFp8RopeChunks)]) = r.rope;
+    const int row = tid / kFp8RopeChunks;
+    *reinterpret_cast<u32x4*>(dst + row * (kAtMaxD + 16) +
+                              8 * tile_chunk(row, kFp8CodeChunks + tid % kFp8RopeChunks)) = r.rope;
   }
 }
 
@@ -353,6 +370,17 @@ __device__ __forceinline__ void attn_unit(AtSmem<NKS>& sm, const AttnArgs& a, in
 #pragma unroll
   for (int db = 0; db < kDbW; ++db) acc_o[db] = f32x4{0.f, 0.f, 0.f, 0.f};
 
+  // LDS element offsets of the tile operands (tile_chunk's layout; the swizzle
+  // flips bit 0 of the chunk index, so chunk 4m + grp and pair 2X move by
+  // whole steps of m and X).  K (S^T's A operand): lane (col, grp) reads
+  // chunk 4m + grp, m = ks0 + ks, of rows col and 16 + col.  V (O's B operand,
+  // transposing reads): lane (col, grp) reads dims 4(col % 4).. of 16-dim
+  // block X = half * kDbW + db in rows 4grp + col/4 and 16 more, chunk
+  // 2X + (col % 4) / 2.
+  constexpr int kRow = kD + 16;
+  const int koff = col * kRow + 8 * tile_chunk(col, grp) + 32 * ks0;
+  const int voff = (4 * grp + (col >> 2)) * kRow + 8 * tile_chunk(4 * grp + (col >> 2), (col & 3) >> 1) +
+                   4 * (col & 1) + 16 * half * kDbW;
   for (int k_lo = t_lo * kAtTile; k_lo < t_hi * kAtTile; k_lo += kAtRun) {
     const int k_hi = min(t_hi * kAtTile, k_lo + kAtRun);
     lds_barrier();  // the previous run's rows are no longer read
@@ -409,9 +437,9 @@ __device__ __forceinline__ void attn_unit(AtSmem<NKS>& sm, const AttnArgs& a, in
       lds_barrier();  // the previous tile's LDS reads are done
       if constexpr (kComp) {
         if constexpr (kFp8) {
-          store_tile(sm.kr, raw);
+          store_tile(&sm.kr[0][0], raw);
         } else {
-          store_tile<NKS>(sm.kr, raw);
+          store_tile<NKS>(&sm.kr[0][0], raw);
         }
         // the next tile's rows are in flight while this one is multiplied
         if (t + 1 < n_run_tiles) load(raw, rows + kAtTile, kbase);
@@ -419,8 +447,8 @@ __device__ __forceinline__ void attn_unit(AtSmem<NKS>& sm, const AttnArgs& a, in
         RawBf16<NKS> rk, rv;
         load_tile<NKS>(rk, rows, kbase, D);  // keys and values in flight together
         load_tile<NKS>(rv, rows, a.win_v, D);
-        store_tile<NKS>(sm.kr, rk);
-        store_tile<NKS>(sm.vs, rv);
+        store_tile<NKS>(&sm.kr[0][0], rk);
+        store_tile<NKS>(&sm.vs[0][0], rv);
       }
       lds_barrier();
       // which keys of the tile are live (bits 0..31)
@@ -433,7 +461,7 @@ __device__ __forceinline__ void attn_unit(AtSmem<NKS>& sm, const AttnArgs& a, in
       constexpr int kOps = 2 * kHalfKs;
       u32x4 kv[kOps];
       auto read_k = [&](int o) {
-        kv[o] = *reinterpret_cast<const u32x4*>(&sm.kr[16 * (o & 1) + col][(ks0 + (o >> 1)) * 32 + grp * 8]);
+        kv[o] = *reinterpret_cast<const u32x4*>(&sm.kr[0][0] + koff + 32 * (o >> 1) + (o & 1) * 16 * kRow);
       };
 #pragma unroll
       for (int o = 0; o < kAhead; ++o) read_k(o);
@@ -535,11 +563,11 @@ __device__ __forceinline__ void attn_unit(AtSmem<NKS>& sm, const AttnArgs& a, in
       // operand of lane (n, grp) is dim 16db + n of the slot group's keys
       // 4grp..4grp+3 and 16+4grp..16+4grp+3, read transposed from the rows
       u32x4 vv[kDbW];
-      const uint16_t(*vrows)[kD + 8] = kComp ? sm.kr : sm.vs;
+      const uint16_t* vrows = kComp ? &sm.kr[0][0] : &sm.vs[0][0];
       auto read_v = [&](int db) {
-        const int c = 16 * (half * kDbW + db) + 4 * (col & 3);
-        const u32x2 lo = read_tr(&vrows[4 * grp + (col >> 2)][c]);
-        const u32x2 hi = read_tr(&vrows[16 + 4 * grp + (col >> 2)][c]);
+        const uint16_t* v = vrows + voff + 16 * db;
+        const u32x2 lo = read_tr(v);
+        const u32x2 hi = read_tr(v + 16 * kRow);
         vv[db] = u32x4{lo[0], lo[1], hi[0], hi[1]};
       };
 #pragma unroll
