@@ -40,6 +40,7 @@ HBM_PEAK_GBS = 8000.0  # MI355X HBM3E peak, 8 TB/s
 TRAFFIC_FILE = ROOT / "profiles" / "hbm_traffic_k_copy_slices_b64_L1k-32k.json"
 DECODE_TRAFFIC_FILE = ROOT / "profiles" / "hbm_traffic_decode_legs.json"
 ATTN_TRAFFIC_FILE = ROOT / "profiles" / "hbm_traffic_attention_layer_seq.json"
+INDEXER_TRAFFIC_FILE = ROOT / "profiles" / "hbm_traffic_indexer_scores.json"
 
 
 def committed_traffic(path: Path, key: str | None, alg_bytes: float) -> tuple[int | None, str | None]:
@@ -602,13 +603,13 @@ def run_indexer_leg(dev, batch: int, n_ent: int, heads: int, channels: int, laun
         "gbs": round(gbs, 1), "pct_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 2),
         "mfma_tflops": round(flops / (us * 1e-6) / 1e12, 1),
     }
-    traffic, source = committed_traffic(ATTN_TRAFFIC_FILE, name, alg)
+    traffic, source = committed_traffic(INDEXER_TRAFFIC_FILE, "indexer_64k", alg)
     rec["roofline"] = {
         "bound": "hbm",
-        "kernel": "skv_decode_attention (k_attn_part, then the merge; the layer call as the unit)",
+        "kernel": "k_indexer_scores (skv_indexer_scores)",
         "achieved": rec["gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
         "frac": round(rec["gbs"] / HBM_PEAK_GBS, 4), "traffic": traffic, "traffic_source": source,
-        "alg_bytes_per_launch": alg, "avg_launch_us": rec["us_per_launch"],
+        "alg_bytes_per_launch": int(alg), "avg_launch_us": rec["us_per_launch"],
     }
     log(f"indexer_64k: {rec['us_per_launch']} us/launch, {rec['gbs']} GB/s ({rec['pct_hbm_peak']}%), "
         f"{rec['mfma_tflops']} TFLOP/s bf16")
