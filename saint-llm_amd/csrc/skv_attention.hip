@@ -1020,7 +1020,9 @@ constexpr int kPosEmpty = -2147483647 - 1;  // an output position another unit o
 // e % parts == part; with lists longer than LDS holds, the lists' positions
 // part, part + parts, ... as written (not reproducible).  Positions
 // [part * out, (part + 1) * out), out = ceil(k / parts), are its share of
-// the fills (and of the fallback's positions).
+// the fills (and of the fallback's positions).  On the canonical path a
+// unit ranks only its ties (every sure candidate wins); the sure
+// candidates' positions come from the layer's window units (sure_positions).
 template <int NKS>
 struct StepRank {
   static constexpr bool kOn = true;
@@ -1041,6 +1043,9 @@ struct StepRank {
   // LDS, from rank()
   const int* keys = nullptr;
   const int32_t* bt_lds = nullptr;
+  // sure candidates among the unit's keys whose positions the window units
+  // write (the canonical path), ahead of the ranked ones
+  int n_sure_keys = 0;
 
   // the layer's group fields, read from the kernel arguments once, at the
   // unit's start (read where they are used, a computed index into the
@@ -1090,8 +1095,10 @@ struct StepRank {
     }
   }
 
-  // Ranks the unit's candidates and writes its positions of the top-k row;
-  // returns its key count (picks >= 0, in output order).  Every thread calls
+  // Ranks the unit's candidates and writes its positions of the top-k row
+  // (on the canonical path its tie winners' only); returns its key count
+  // (its sure candidates first on that path, then its picks >= 0 in output
+  // order).  Every thread calls
   // it; the result is uniform.  Its barriers order LDS only, so the query's
   // loads stay in flight through the ranking.
   __device__ __forceinline__ int rank(AtSmem<NKS>& sm) {
@@ -1216,13 +1223,21 @@ struct StepRank {
       const auto put = [&](int pos, int idx) { at_pos[pos] = idx; };
       if (__builtin_expect(canon, 1)) {
         // canonical positions part, part + parts, ... of each list: the same
-        // share of the sure candidates for every unit
+        // share of the sure candidates for every unit.  A sure candidate
+        // always wins, so only the ties are ranked here; the sure candidates
+        // are the unit's first keys, in canonical order, and the window units
+        // write their positions of the top-k row (sure_positions).
         const int n_os = part < S ? static_cast<int>(ceil_div24(S - part, parts)) : 0;
         const int n_ot = part < T ? static_cast<int>(ceil_div24(T - part, parts)) : 0;
         const auto own_slot = [&](int cls, int j) {
           return min(max(slot_at[(cls ? S : 0) + part + j * parts], 0), C - 1);
         };
-        rank_candidates_of<kAtThreads, 4>(put, [&](int q) { return ck[q]; }, own_slot, n_os, n_ot, S, C, sel);
+        for (int j = tid; j < n_os; j += kAtThreads) {
+          const uint64_t key = ck[own_slot(0, j)];
+          key_list[j] = key_finite(static_cast<uint32_t>(key >> 32)) ? static_cast<int>(~static_cast<uint32_t>(key)) : -1;
+        }
+        n_sure_keys = n_os;
+        rank_candidates_of<kAtThreads, 4>(put, [&](int q) { return ck[q]; }, own_slot, 0, n_ot, S, C, sel);
       } else if (in_lds) {
         // more filter chunks than the run table holds: the unit's candidates
         // are the entries e with e % parts == part (its share of the sure
@@ -1252,8 +1267,9 @@ struct StepRank {
     }
     for (int j = max(o0, sel) + tid; j < o1; j += kAtThreads) at_pos[j] = -1;  // the fills
     lds_barrier();
-    // its picks >= 0 become the unit's keys, in output order (4 consecutive
-    // positions per thread, counts summed over the wave, then over the waves)
+    // its picks >= 0 become the unit's keys, in output order, after its sure
+    // candidates on the canonical path (4 consecutive positions per thread,
+    // counts summed over the wave, then over the waves)
     static_assert(4 * kAtThreads >= kMaxTopK, "positions per thread");
     int v[4], cnt = 0;
 #pragma unroll
@@ -1278,7 +1294,7 @@ struct StepRank {
       base += w < wave ? c : 0;
       total += c;
     }
-    int at = base + incl - cnt;
+    int at = n_sure_keys + base + incl - cnt;  // after the sure keys the ranking left in place
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       if (v[i] >= 0) key_list[at++] = v[i];
@@ -1289,7 +1305,7 @@ struct StepRank {
       if (tid + u * kAtThreads < n_bt) bt[tid + u * kAtThreads] = btv[u];
     }
     lds_barrier();
-    return total;
+    return n_sure_keys + total;
   }
 
   // The unit's global stores, after its last loads: every position it owns
@@ -1322,6 +1338,42 @@ struct StepRank {
     return static_cast<int64_t>(page) * bs + (e - pi * bs);
   }
 };
+
+// The positions of a CSA row's sure candidates in its top-k row, written by
+// window unit w of n_w of sequence b once its own output is done: its share
+// is the sure list's slots w, w + n_w, ...; a sure candidate's position is
+// the count of sure keys above it.  Only where StepRank::rank takes its
+// canonical path (the same conditions from the same loads), on which the
+// CSA units rank their ties alone.
+template <int NKS>
+__device__ __forceinline__ void sure_positions(AtSmem<NKS>& sm, const StepMap& map, int32_t* topk_idx, int b,
+                                               int w, int n_w) {
+  using RL = RankLds<NKS>;
+  const int tid = threadIdx.x;
+  const int32_t* ws = map.topk_ws[0] + static_cast<int64_t>(b) * kTkWsWords;
+  const int status = *map.status;
+  const int L = map.step_lens[b];
+  const int cnt0 = ws[kTkWsCnt], cnt1 = ws[kTkWsCnt + 1], flag = ws[kTkWsCnt + 2];
+  const int k = map.top_k[0];
+  const int m = map.m[map.group[0]];
+  lds_barrier();  // the unit's tile reads are done
+  if (status != 0 || flag != 0) return;
+  int n_cols, n_valid;
+  score_cols(map.score_stride[0], m, L, n_cols, n_valid);
+  const int sel = topk_sel(k, n_cols, n_valid);
+  if (sel == 0) return;
+  const int S = min(cnt0, kMaxTopK), T = min(cnt1, kTkTieCap);
+  const int n_ch = static_cast<int>(ceil_div24(static_cast<uint32_t>(n_valid), kTkChunk));
+  if (S + T > RL::kCkCap || n_ch > kTkRunCap) return;  // the CSA units rank every candidate
+  uint64_t* ck = reinterpret_cast<uint64_t*>(&sm.kr[0][0]);
+  const int2* sure_list = reinterpret_cast<const int2*>(ws + kTkWsSure);
+  for (int c = tid; c < S; c += kAtThreads) ck[c] = order_key(sure_list[c]);
+  lds_barrier();
+  const int n_own = w < S ? static_cast<int>(ceil_div24(S - w, n_w)) : 0;
+  int32_t* row = topk_idx + static_cast<int64_t>(b) * k;
+  rank_candidates_of<kAtThreads, 4>([&](int pos, int idx) { row[pos] = idx; }, [&](int q) { return ck[q]; },
+                                     [&](int, int j) { return w + j * n_w; }, n_own, 0, S, S, sel);
+}
 
 // The step's commit for sequence b (after a refusal: nothing).
 __device__ __forceinline__ void step_commit(const StepMap& map, int b) {
@@ -1359,6 +1411,9 @@ __global__ __launch_bounds__(kAtThreads, 1) void k_decode_attend(AttnArgs a, Ste
   } else {
     if (u == a.n_cu && hg == 0 && threadIdx.x == 0) step_commit(map, b);
     attn_unit<NKS, false, false>(sm, a, b, u - a.n_cu, a.n_wu, hg, unit);
+    if constexpr (NKS >= 16) {
+      if (a.kind == SKV_LAYER_CSA && hg == 0) sure_positions<NKS>(sm, map, topk_idx, b, u - a.n_cu, a.n_wu);
+    }
   }
 }
 
