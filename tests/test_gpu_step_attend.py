@@ -183,6 +183,21 @@ def test_step_attend_tie_overflow_full_select(dev) -> None:
         assert np.array_equal(idx[b], np.arange(min(512, n_valid)))
 
 
+def test_step_attend_rows_past_the_run_table(dev) -> None:
+    """One launch over a row of 135,000 entries (66 filter chunks, more than
+    the run table holds: its units rank every candidate, by entry index mod
+    the unit count, and write every position) and a row of 75,000 entries
+    (37 chunks: its units rank their ties and the window units write the sure
+    candidates' positions).  Two steps; the top-k rows bit for bit against
+    the separate path."""
+    from saint_kv.decode import LayerSpec
+
+    spec = LayerSpec("csa", m=4, top_k=512)
+    caches = _pair([spec], 2, 540064, [540000, 300000], dev, window=128, block_size=64)
+    assert caches[0].scores[0].shape[1] > 64 * 2048  # past the run table
+    _run_pair(caches, spec, 2, dev, torch.Generator().manual_seed(13), W=128, oracle=False)
+
+
 def test_step_attend_long_lists_rank_from_global(dev) -> None:
     """top-k 2048 over 2,000 sure candidates and a 3,000-key tie bin: 5,000
     candidates, more than a unit holds in LDS, so the units rank from the
