@@ -294,6 +294,17 @@ __device__ __forceinline__ void attn_unit(AtSmem<NKS>& sm, const AttnArgs& a, in
   // A ranked unit's first loads are its ranking's (they return first).
   int32_t pick0 = 0, ne0 = 0;
   float w_lo = 0.f, w_hi = 0.f;
+  using Raw = std::conditional_t<kFp8, RawFp8, RawBf16<NKS>>;
+  Raw raw;                 // a compressed tile's rows in flight
+  bool raw_early = false;  // the first tile's loads were issued by the ranking
+  auto load_raw = [&](Raw& r, const int64_t* rows, const uint8_t* base) {
+    if constexpr (kFp8) {
+      load_tile(r, rows, base);
+    } else {
+      load_tile<NKS>(r, rows, base, D);
+    }
+  };
+
   if constexpr (kRanked) {
     rk.load();
     w_lo = a.knorm_w[min(tid, D - 1)];
@@ -337,8 +348,18 @@ __device__ __forceinline__ void attn_unit(AtSmem<NKS>& sm, const AttnArgs& a, in
     if (tid + kAtThreads < D) sm.w[tid + kAtThreads] = w_hi;
     lds_barrier();
     if constexpr (kRanked) {
-      // the ranking waits for its own loads only; q * w below waits for the query
-      n_keys = rk.rank(sm);
+      // the ranking waits for its own loads only; q * w below waits for the query.
+      // Where the unit's first tile is all sure keys, the ranking resolves
+      // their rows and issues the tile's loads before it ranks the ties.
+      n_keys = rk.rank(sm, [&]() {
+        for (int j = tid; j < kAtTile; j += kAtThreads) {
+          const int64_t r = rk.row(j);
+          sm.row[j] = r >= 0 ? r * a.entry_bytes : -1;
+        }
+        lds_barrier();
+        load_raw(raw, sm.row, a.pool);
+        raw_early = true;
+      });
       n_tiles = (n_keys + kAtTile - 1) / kAtTile;
       t_lo = 0;
       t_hi = n_tiles;
@@ -422,16 +443,9 @@ __device__ __forceinline__ void attn_unit(AtSmem<NKS>& sm, const AttnArgs& a, in
     }
     lds_barrier();
     const int n_run_tiles = (k_hi - k_lo) / kAtTile;
-    using Raw = std::conditional_t<kFp8, RawFp8, RawBf16<NKS>>;
-    Raw raw;
-    auto load = [&](Raw& r, const int64_t* rows, const uint8_t* base) {
-      if constexpr (kFp8) {
-        load_tile(r, rows, base);
-      } else {
-        load_tile<NKS>(r, rows, base, D);
-      }
-    };
-    if constexpr (kComp) load(raw, sm.row, kbase);
+    if constexpr (kComp) {
+      if (!(raw_early && k_lo == 0)) load_raw(raw, sm.row, kbase);  // uniform
+    }
     for (int t = 0; t < n_run_tiles; ++t) {
       const int64_t* rows = sm.row + t * kAtTile;
       lds_barrier();  // the previous tile's LDS reads are done
@@ -442,7 +456,7 @@ __device__ __forceinline__ void attn_unit(AtSmem<NKS>& sm, const AttnArgs& a, in
           store_tile<NKS>(&sm.kr[0][0], raw);
         }
         // the next tile's rows are in flight while this one is multiplied
-        if (t + 1 < n_run_tiles) load(raw, rows + kAtTile, kbase);
+        if (t + 1 < n_run_tiles) load_raw(raw, rows + kAtTile, kbase);
       } else {
         RawBf16<NKS> rk, rv;
         load_tile<NKS>(rk, rows, kbase, D);  // keys and values in flight together
@@ -1022,7 +1036,7 @@ constexpr int kPosEmpty = -2147483647 - 1;  // an output position another unit o
 // [part * out, (part + 1) * out), out = ceil(k / parts), are its share of
 // the fills (and of the fallback's positions).  On the canonical path a
 // unit ranks only its ties (every sure candidate wins); the sure
-// candidates' positions come from the layer's window units (sure_positions).
+// candidates' positions come from the sequence's positions unit (sure_positions).
 template <int NKS>
 struct StepRank {
   static constexpr bool kOn = true;
@@ -1043,9 +1057,20 @@ struct StepRank {
   // LDS, from rank()
   const int* keys = nullptr;
   const int32_t* bt_lds = nullptr;
-  // sure candidates among the unit's keys whose positions the window units
-  // write (the canonical path), ahead of the ranked ones
+  // sure candidates among the unit's keys whose positions the positions
+  // unit writes (the canonical path), ahead of the ranked ones
   int n_sure_keys = 0;
+  bool early_bt = false;  // the block-table row went to LDS before the ranking
+
+  // the row's block-table slices (load_bt) into LDS
+  __device__ __forceinline__ void put_bt(int32_t* bt) const {
+    const int tid = threadIdx.x;
+#pragma unroll
+    for (int u = 0; u < kBtPer; ++u) {
+      if (u * kAtThreads >= n_bt) break;
+      if (tid + u * kAtThreads < n_bt) bt[tid + u * kAtThreads] = btv[u];
+    }
+  }
 
   // the layer's group fields, read from the kernel arguments once, at the
   // unit's start (read where they are used, a computed index into the
@@ -1098,10 +1123,16 @@ struct StepRank {
   // Ranks the unit's candidates and writes its positions of the top-k row
   // (on the canonical path its tie winners' only); returns its key count
   // (its sure candidates first on that path, then its picks >= 0 in output
-  // order).  Every thread calls
-  // it; the result is uniform.  Its barriers order LDS only, so the query's
-  // loads stay in flight through the ranking.
-  __device__ __forceinline__ int rank(AtSmem<NKS>& sm) {
+  // order).  Every thread calls it; the result is uniform.  Its barriers
+  // order LDS only, so the query's loads stay in flight through the ranking.
+  // On the canonical path, when the unit has a tile's worth of sure
+  // candidates and the canonical map fits in the key tile beside the keys,
+  // every thread calls early() once the block-table row and the sure
+  // candidates are in LDS, before the ties are ranked: the caller resolves
+  // the first tile's rows (row()) and issues its loads, which then overlap
+  // the ranking.
+  template <class Early>
+  __device__ __forceinline__ int rank(AtSmem<NKS>& sm, Early&& early) {
     const int tid = threadIdx.x;
     int* scan = reinterpret_cast<int*>(&sm.vs[0][0]);
     int* at_pos = scan + RL::kScan;
@@ -1165,9 +1196,13 @@ struct StepRank {
         d_pack = static_cast<int>((static_cast<uint32_t>(d_sure) & 0xffffu) | (static_cast<uint32_t>(d_tie) << 16));
       }
       // canonical position -> slot, each class at its own offset (sure
-      // [0, S), ties [S, C)), in the (not yet filled) block-table area
+      // [0, S), ties [S, C)): in the key tile after the keys where it fits
+      // (the block-table row then goes to LDS before the ranking, and the
+      // first tile of sure keys can be loaded while the ties are ranked),
+      // else in the (not yet filled) block-table area
       static_assert(RL::kBtCap >= RL::kCkCap, "canonical map fits the block-table area");
-      int* slot_at = bt;
+      early_bt = canon && C * 12 <= static_cast<int>(sizeof(sm.kr));  // uniform
+      int* slot_at = early_bt ? reinterpret_cast<int*>(ck + C) : bt;
       // the canonical position of slot c holding `key`; every lane of the
       // wave takes part (the lookup reads other lanes' registers)
       const auto canon_pos = [&](int c, uint64_t key) {
@@ -1219,14 +1254,15 @@ struct StepRank {
           }
         }
       }
+      if (early_bt) put_bt(bt);
       lds_barrier();
       const auto put = [&](int pos, int idx) { at_pos[pos] = idx; };
       if (__builtin_expect(canon, 1)) {
         // canonical positions part, part + parts, ... of each list: the same
         // share of the sure candidates for every unit.  A sure candidate
         // always wins, so only the ties are ranked here; the sure candidates
-        // are the unit's first keys, in canonical order, and the window units
-        // write their positions of the top-k row (sure_positions).
+        // are the unit's first keys, in canonical order, and the positions unit
+        // writes their positions of the top-k row (sure_positions).
         const int n_os = part < S ? static_cast<int>(ceil_div24(S - part, parts)) : 0;
         const int n_ot = part < T ? static_cast<int>(ceil_div24(T - part, parts)) : 0;
         const auto own_slot = [&](int cls, int j) {
@@ -1237,6 +1273,7 @@ struct StepRank {
           key_list[j] = key_finite(static_cast<uint32_t>(key >> 32)) ? static_cast<int>(~static_cast<uint32_t>(key)) : -1;
         }
         n_sure_keys = n_os;
+        if (early_bt && n_os >= kAtTile) early();  // uniform; key j of the first tile is this thread's own write
         rank_candidates_of<kAtThreads, 4>(put, [&](int q) { return ck[q]; }, own_slot, 0, n_ot, S, C, sel);
       } else if (in_lds) {
         // more filter chunks than the run table holds: the unit's candidates
@@ -1299,11 +1336,7 @@ struct StepRank {
     for (int i = 0; i < 4; ++i) {
       if (v[i] >= 0) key_list[at++] = v[i];
     }
-#pragma unroll
-    for (int u = 0; u < kBtPer; ++u) {
-      if (u * kAtThreads >= n_bt) break;
-      if (tid + u * kAtThreads < n_bt) bt[tid + u * kAtThreads] = btv[u];
-    }
+    if (!early_bt) put_bt(bt);
     lds_barrier();
     return n_sure_keys + total;
   }
@@ -1340,9 +1373,10 @@ struct StepRank {
 };
 
 // The positions of a CSA row's sure candidates in its top-k row, written by
-// window unit w of n_w of sequence b once its own output is done: its share
-// is the sure list's slots w, w + n_w, ...; a sure candidate's position is
-// the count of sure keys above it.  Only where StepRank::rank takes its
+// positions unit w of n_w of sequence b (one block per sequence beside the
+// layer's units, on a CU the attention leaves free; the lists are complete
+// when the launch starts): its share is the sure list's slots w, w + n_w,
+// ...; a sure candidate's position is the count of sure keys above it.  Only where StepRank::rank takes its
 // canonical path (the same conditions from the same loads), on which the
 // CSA units rank their ties alone.
 template <int NKS>
@@ -1356,7 +1390,6 @@ __device__ __forceinline__ void sure_positions(AtSmem<NKS>& sm, const StepMap& m
   const int cnt0 = ws[kTkWsCnt], cnt1 = ws[kTkWsCnt + 1], flag = ws[kTkWsCnt + 2];
   const int k = map.top_k[0];
   const int m = map.m[map.group[0]];
-  lds_barrier();  // the unit's tile reads are done
   if (status != 0 || flag != 0) return;
   int n_cols, n_valid;
   score_cols(map.score_stride[0], m, L, n_cols, n_valid);
@@ -1391,13 +1424,20 @@ template <int NKS, bool kFp8>
 __global__ __launch_bounds__(kAtThreads, 1) void k_decode_attend(AttnArgs a, StepMap map, int32_t* topk_idx) {
   __shared__ AtSmem<NKS> sm;
   const int U = a.n_cu + a.n_wu;
-  const int per_seq = U * a.n_hg;
+  // a CSA layer's sequences have one more block: the positions unit
+  const int per_seq = U * a.n_hg + (a.kind == SKV_LAYER_CSA ? 1 : 0);
   const int xs = __builtin_ctz(static_cast<uint32_t>(a.xcds));  // a.xcds is a power of two
   const int k = static_cast<int>(blockIdx.x) >> xs;
   const int sb = k / per_seq;
   const int b = (static_cast<int>(blockIdx.x) & (a.xcds - 1)) + (sb << xs);
   if (b >= a.batch) return;  // uniform
   const int r = k - sb * per_seq;
+  if constexpr (NKS >= 16) {
+    if (r == U * a.n_hg) {  // the positions unit (CSA layers only)
+      sure_positions<NKS>(sm, map, topk_idx, b, 0, 1);
+      return;
+    }
+  }
   const int u = r / a.n_hg, hg = r - u * a.n_hg;
   const int64_t unit = (static_cast<int64_t>(b) * U + u) * a.n_hg + hg;
   if (u < a.n_cu) {
@@ -1411,9 +1451,6 @@ __global__ __launch_bounds__(kAtThreads, 1) void k_decode_attend(AttnArgs a, Ste
   } else {
     if (u == a.n_cu && hg == 0 && threadIdx.x == 0) step_commit(map, b);
     attn_unit<NKS, false, false>(sm, a, b, u - a.n_cu, a.n_wu, hg, unit);
-    if constexpr (NKS >= 16) {
-      if (a.kind == SKV_LAYER_CSA && hg == 0) sure_positions<NKS>(sm, map, topk_idx, b, u - a.n_cu, a.n_wu);
-    }
   }
 }
 
@@ -1511,7 +1548,8 @@ int decode_attend(const skv_attention_desc* d, const skv_decode_desc* h, const S
   a.softcap = x.softcap;
   a.fused = 1;
   a.xcds = device_xcds();
-  const dim3 grid(static_cast<unsigned>(a.xcds * ceil_div(x.batch, a.xcds) * (p.n_cu + p.n_wu) * p.n_hg));
+  const dim3 grid(static_cast<unsigned>(a.xcds * ceil_div(x.batch, a.xcds) *
+                                        ((p.n_cu + p.n_wu) * p.n_hg + (x.kind == SKV_LAYER_CSA ? 1 : 0))));
   int32_t* idx = Ly.kind == SKV_LAYER_CSA ? Ly.topk_idx : nullptr;
   if (a.fp8_main > 0) {
     hipLaunchKernelGGL((k_decode_attend<18, true>), grid, dim3(kAtThreads), 0, s, a, *map, idx);
