@@ -997,9 +997,10 @@ int launch_merge(const AttnArgs& a, const AttnPlan& p, int kind, const float* kn
 // gather launch: a CSA unit ranks its share of the row's top-k candidates
 // (the lists the step's filter chunks wrote), writes those positions of the
 // top-k row and attends over its picks, read in place through the block
-// table; HCA and window units are the attention's own.  The gather launch's
-// other work happens here as well: the first window unit of a sequence
-// commits the step (lengths, entry counts, free-stack tops) and CSA unit 0
+// table; HCA and window units are the attention's own, and a CSA layer has
+// one positions unit per sequence besides.  The gather launch's other work
+// happens here as well: the first window unit of a sequence commits the
+// step (lengths, entry counts, free-stack tops) and the positions unit
 // clears the row's top-k histogram for the next step.  No unit reads what
 // the commit writes: lengths come from the step's scratch (a.lens is
 // step_lens) and an HCA unit's visible count from the length alone.
@@ -1036,7 +1037,7 @@ constexpr int kPosEmpty = -2147483647 - 1;  // an output position another unit o
 // [part * out, (part + 1) * out), out = ceil(k / parts), are its share of
 // the fills (and of the fallback's positions).  On the canonical path a
 // unit ranks only its ties (every sure candidate wins); the sure
-// candidates' positions come from the sequence's positions unit (sure_positions).
+// candidates' positions come from the sequence's positions unit (positions_unit).
 template <int NKS>
 struct StepRank {
   static constexpr bool kOn = true;
@@ -1262,7 +1263,7 @@ struct StepRank {
         // share of the sure candidates for every unit.  A sure candidate
         // always wins, so only the ties are ranked here; the sure candidates
         // are the unit's first keys, in canonical order, and the positions unit
-        // writes their positions of the top-k row (sure_positions).
+        // writes their positions of the top-k row (positions_unit).
         const int n_os = part < S ? static_cast<int>(ceil_div24(S - part, parts)) : 0;
         const int n_ot = part < T ? static_cast<int>(ceil_div24(T - part, parts)) : 0;
         const auto own_slot = [&](int cls, int j) {
@@ -1342,16 +1343,12 @@ struct StepRank {
   }
 
   // The unit's global stores, after its last loads: every position it owns
-  // goes to the top-k row, and unit 0 clears the row's histogram for the
-  // next step (also after a refusal).  Stores issued while loads are in
-  // flight would make every later wait for a load wait for all of them (the
-  // compiler cannot count on a mix of loads and stores completing in order).
+  // goes to the top-k row.  Stores issued while loads are in flight would
+  // make every later wait for a load wait for all of them (the compiler
+  // cannot count on a mix of loads and stores completing in order).
   __device__ __forceinline__ void finish(AtSmem<NKS>& sm) {
     if (!lead) return;
     const int tid = threadIdx.x;
-    if (part == 0) {
-      for (int i = tid; i < kTkBins; i += kAtThreads) ws[kTkWsHist + i] = 0;
-    }
     if (status) return;
     const int* at_pos = reinterpret_cast<const int*>(&sm.vs[0][0]) + RL::kScan;
     for (int pos = tid; pos < k; pos += kAtThreads) {
@@ -1376,12 +1373,12 @@ struct StepRank {
 // positions unit w of n_w of sequence b (one block per sequence beside the
 // layer's units, on a CU the attention leaves free; the lists are complete
 // when the launch starts): its share is the sure list's slots w, w + n_w,
-// ...; a sure candidate's position is the count of sure keys above it.  Only where StepRank::rank takes its
-// canonical path (the same conditions from the same loads), on which the
-// CSA units rank their ties alone.
+// ...; a sure candidate's position is the count of sure keys above it.  Only
+// where StepRank::rank takes its canonical path (the same conditions from
+// the same loads), on which the CSA units rank their ties alone.
 template <int NKS>
-__device__ __forceinline__ void sure_positions(AtSmem<NKS>& sm, const StepMap& map, int32_t* topk_idx, int b,
-                                               int w, int n_w) {
+__device__ __forceinline__ void sure_positions_of(AtSmem<NKS>& sm, const StepMap& map, int32_t* topk_idx, int b,
+                                                  int w, int n_w) {
   using RL = RankLds<NKS>;
   const int tid = threadIdx.x;
   const int32_t* ws = map.topk_ws[0] + static_cast<int64_t>(b) * kTkWsWords;
@@ -1406,6 +1403,16 @@ __device__ __forceinline__ void sure_positions(AtSmem<NKS>& sm, const StepMap& m
   int32_t* row = topk_idx + static_cast<int64_t>(b) * k;
   rank_candidates_of<kAtThreads, 4>([&](int pos, int idx) { row[pos] = idx; }, [&](int q) { return ck[q]; },
                                      [&](int, int j) { return w + j * n_w; }, n_own, 0, S, S, sel);
+}
+
+// The positions unit of sequence b: the sure candidates' positions, then
+// (also after a refusal, and after its last loads) the row's histogram
+// cleared for the next step; nothing in the launch reads the histogram.
+template <int NKS>
+__device__ __forceinline__ void positions_unit(AtSmem<NKS>& sm, const StepMap& map, int32_t* topk_idx, int b) {
+  sure_positions_of<NKS>(sm, map, topk_idx, b, 0, 1);
+  int32_t* ws = map.topk_ws[0] + static_cast<int64_t>(b) * kTkWsWords;
+  for (int i = threadIdx.x; i < kTkBins; i += kAtThreads) ws[kTkWsHist + i] = 0;
 }
 
 // The step's commit for sequence b (after a refusal: nothing).
@@ -1434,7 +1441,7 @@ __global__ __launch_bounds__(kAtThreads, 1) void k_decode_attend(AttnArgs a, Ste
   const int r = k - sb * per_seq;
   if constexpr (NKS >= 16) {
     if (r == U * a.n_hg) {  // the positions unit (CSA layers only)
-      sure_positions<NKS>(sm, map, topk_idx, b, 0, 1);
+      positions_unit<NKS>(sm, map, topk_idx, b);
       return;
     }
   }
